@@ -1,0 +1,193 @@
+/*
+ * soinfer_amd.h -- C ABI of the MI355X (gfx950) quantized decode hot path.
+ *
+ * Library: sparse-offload-infer_amd/soinfer/libsoinfer_hip.so
+ *
+ * Every entry point takes plain pointers and sizes, launches asynchronously
+ * on `stream` (a hipStream_t passed as void*; NULL = the legacy default
+ * stream) and returns a soi_status (0 = success). Device pointers must be HIP
+ * device allocations on the current device. binary16 data crosses this
+ * interface as uint16_t bit patterns. No entry point allocates device memory
+ * except where it says so; scratch space is passed in by the caller as a
+ * `workspace` argument sized by the matching *_workspace_bytes() query.
+ *
+ * Each declaration cites the reference interface it replaces (file:line in
+ * the sparse-offload-infer repository). The soinfer._C extension
+ * (csrc/bindings.cpp in this package) is a thin torch wrapper over exactly
+ * these functions.
+ */
+#ifndef SOINFER_AMD_H_
+#define SOINFER_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum soi_status {
+    SOI_OK = 0,
+    SOI_ERR_INVALID_ARGUMENT = 1, /* a size, shape or pointer precondition failed; nothing launched */
+    SOI_ERR_WORKSPACE = 2,        /* workspace missing or smaller than *_workspace_bytes() */
+    SOI_ERR_HIP = 3,              /* a HIP runtime call or kernel launch failed */
+    SOI_ERR_UNSUPPORTED = 4       /* arguments valid but outside what this build implements */
+} soi_status;
+
+/* Human-readable text for a status code, and the detail of the last error
+ * raised on the calling thread (which check failed, or the HIP error). */
+const char* soi_status_string(int status);
+const char* soi_last_error(void);
+
+/* Library version string and the GPU architecture it was compiled for. */
+const char* soi_version(void);
+
+/* --------------------------------------------------------------------------
+ * INT4 group-quantized GEMV, y[N] = dequant(Wq, scale) @ x.
+ * Wq: uint8 [N, ceil(K/8)*4], AWQ nibble order (layout.h:19-45);
+ * scale: fp32 [N, num_groups], num_groups == ceil(K/group_size);
+ * group_size: positive multiple of 8; x: fp16 [K]; y: fp16 [N].
+ *   soi_gemv_w4a16_group       replaces launch_gemv_w4a16_group
+ *                              (csrc/kernels/gemv_w4a16_group.cu:64-70;
+ *                               binding csrc/bindings.cpp:300-303)
+ *   soi_gemv_w4a16_group_lop3  replaces launch_gemv_w4a16_group_lop3
+ *                              (gemv_w4a16_group.cu:129-134; bindings.cpp:305-309)
+ * The two differ only in how nibbles become binary16 (per-nibble extract vs.
+ * three-input bitwise construction); both are exact, share one accumulation
+ * order and return bit-identical results.
+ * ------------------------------------------------------------------------ */
+int soi_gemv_w4a16_group(const uint8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N,
+                         int64_t K, int64_t group_size, int64_t num_groups, void* stream);
+int soi_gemv_w4a16_group_lop3(const uint8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N,
+                              int64_t K, int64_t group_size, int64_t num_groups, void* stream);
+
+/* --------------------------------------------------------------------------
+ * INT8 GEMV, y[N] = sum_k scale[n*scale_row_stride + k/group_size] * Wq[n,k] * x[k].
+ * Wq: int8 [N, K]; scale: fp32 [N or 1, num_groups]; scale_row_stride is 0
+ * for a per-tensor [1, G] scale, else num_groups. group_size % 4 == 0 when
+ * num_groups > 1. Replaces launch_gemv_w8a16 (csrc/kernels/gemv_w8a16.cu:64-70;
+ * binding csrc/bindings.cpp:239-262).
+ * ------------------------------------------------------------------------ */
+int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N, int64_t K,
+                   int64_t group_size, int64_t num_groups, int64_t scale_row_stride, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Deterministic threshold top-k over non-negative values (Dynamic Input
+ * Pruning channel selection). Replaces launch_topk_threshold_select
+ * (csrc/kernels/topk_select.cu:98-102; binding csrc/bindings.cpp:507-518).
+ * Semantics are the reference's: tau = the 24-step fp32 bisection of
+ * topk_select.cu:19-61 (lo=0, hi=max+1e-3f, mid=0.5f*(lo+hi),
+ * lo=mid iff count(v>=mid)>=k), then out_indices = the first k indices in
+ * ascending order with v >= tau, *out_count = the number written.
+ * 1 <= k <= n. One workgroup; bit-identical output on every call.
+ * ------------------------------------------------------------------------ */
+int soi_topk_threshold_select(const float* abs_g, int64_t n, int64_t k, int32_t* out_indices, int32_t* out_count,
+                              void* stream);
+
+/* --------------------------------------------------------------------------
+ * Row gather from pinned host memory into device memory.
+ * matrix: pinned host bytes [num_rows, row_nbytes]; indices: host int64 [k],
+ * each in [0, num_rows) (checked; the reference leaves this unchecked).
+ *   soi_gather_rows_staged: host memcpy of the k rows into pinned `staging`
+ *     (>= k*row_nbytes), then ONE hipMemcpyAsync H2D into gpu_dst.
+ *     Replaces launch_gather_rows_staged (csrc/kernels/gather_rows.cu:6-13;
+ *     binding csrc/bindings.cpp:538-549).
+ *   soi_gather_rows_naive: one hipMemcpyAsync per row.
+ *     Replaces launch_gather_rows_naive (gather_rows.cu:15-21; bindings.cpp:551-559).
+ * Both return once the copies are queued; gpu_dst is valid after `stream`
+ * reaches them.
+ * ------------------------------------------------------------------------ */
+int soi_gather_rows_staged(const uint8_t* matrix, int64_t num_rows, int64_t row_nbytes, const int64_t* indices,
+                           int64_t k, uint8_t* staging, uint8_t* gpu_dst, void* stream);
+int soi_gather_rows_naive(const uint8_t* matrix, int64_t num_rows, int64_t row_nbytes, const int64_t* indices,
+                          int64_t k, uint8_t* gpu_dst, void* stream);
+
+/* Device-resident row gather (rows already in HBM): dst[j,:] = src[indices[j],:].
+ * indices: device int32 [k]; an index outside [0, num_rows) writes a zero row.
+ * No reference counterpart: on MI355X the weights stay resident in HBM. */
+int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
+                           int64_t k, uint8_t* dst, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Sparse down projection over k gathered rows of down_proj^T:
+ * y[H] = sum_{j<k} h_sel[j] * dequant(Wq_sel[j,:], scale_sel[j,:]).
+ * Wq_sel: uint8 [k, ceil(H/8)*4]; scale_sel: fp32 [k, ceil(H/group_size)];
+ * h_sel: fp16 [k]; y: fp16 [H]. Split over rows across workgroups, partial
+ * sums combined in a fixed order (deterministic, no float atomics).
+ * Replaces launch_gemv_w4a16_sparse_accumulate
+ * (csrc/kernels/gemv_sparse_accumulate.cu:40-47; binding csrc/bindings.cpp:311-339).
+ * ------------------------------------------------------------------------ */
+size_t soi_sparse_accumulate_workspace_bytes(int64_t H, int64_t k);
+int soi_gemv_w4a16_sparse_accumulate(const uint8_t* Wq_sel, const float* scale_sel, const uint16_t* h_sel,
+                                     uint16_t* y, int64_t H, int64_t k, int64_t group_size, int64_t num_groups,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Hot-channel cache descriptors. desc[j] = slot_of[sel[j]] when >= 0 (cache
+ * row), else (m | 0x80000000) where m numbers the misses in ascending j;
+ * miss_channels[m] = sel[j]; *miss_count = number of misses. A channel
+ * outside [0, num_channels) is treated as a miss. Replaces
+ * launch_build_dip_descriptors (csrc/kernels/gemv_dip_fused.cu:35-42; binding
+ * csrc/bindings.cpp:341-359), whose miss numbering is atomic-order dependent;
+ * here it is deterministic.
+ * ------------------------------------------------------------------------ */
+int soi_build_dip_descriptors(const int32_t* sel, int64_t k, const int32_t* slot_of, int64_t num_channels,
+                              int32_t* desc, int32_t* miss_channels, int32_t* miss_count, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Descriptor-driven fused GEMVs: row j of the logical selected matrix comes
+ * from cache row desc[j] (top bit clear) or staging row desc[j]&0x7fffffff
+ * (top bit set). cache_rows / staging_rows bound the offsets; an offset out
+ * of range yields NaN for that row instead of a read.
+ *   soi_gemv_dip_fused_up: y[k] = rows @ x; bit-identical to
+ *     soi_gemv_w4a16_group_lop3 on the same logical rows. Replaces
+ *     launch_gemv_dip_fused_up (gemv_dip_fused.cu:104-111; bindings.cpp:388-408).
+ *   soi_gemv_dip_fused_down: y[H] = sum_j h_sel[j] * row_j; bit-identical to
+ *     soi_gemv_w4a16_sparse_accumulate on the same logical rows. Replaces
+ *     launch_gemv_dip_fused_down (gemv_dip_fused.cu:156-164; bindings.cpp:410-432).
+ * ------------------------------------------------------------------------ */
+int soi_gemv_dip_fused_up(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                          const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
+                          const int32_t* desc, int64_t k, const uint16_t* x, uint16_t* y, int64_t K,
+                          int64_t group_size, int64_t num_groups, void* stream);
+int soi_gemv_dip_fused_down(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                            const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
+                            const int32_t* desc, int64_t k, const uint16_t* h_sel, uint16_t* y, int64_t H,
+                            int64_t group_size, int64_t num_groups, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* --------------------------------------------------------------------------
+ * Index-driven sparse GEMVs over weights resident in HBM (no gather): row j
+ * is row idx[j] of the full matrix. Bit-identical to gathering the rows
+ * first and calling soi_gemv_w4a16_group_lop3 / soi_gemv_w4a16_sparse_accumulate.
+ * An index outside [0, num_rows) yields NaN for that row. No reference
+ * counterpart (the reference must offload); used by the resident DIP layer.
+ * ------------------------------------------------------------------------ */
+int soi_gemv_w4a16_indexed(const uint8_t* Wq, const float* scale, int64_t num_rows, const int32_t* idx, int64_t k,
+                           const uint16_t* x, uint16_t* y, int64_t K, int64_t group_size, int64_t num_groups,
+                           void* stream);
+int soi_gemv_w4a16_indexed_accumulate(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
+                                      const int32_t* idx, int64_t k, const uint16_t* h_sel, uint16_t* y, int64_t H,
+                                      int64_t group_size, int64_t num_groups, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Batch-1 GQA decode attention:
+ * out[h,:] = softmax_t(q[h,:].k[kvh,t,:] / sqrt(head_dim)) @ v[kvh,t,:],
+ * kvh = h / (NQ/NKV), t < cur_len. q: fp16 [NQ, hd]; k_cache, v_cache:
+ * fp16 [NKV, max_seq, hd]; out: fp16 [NQ, hd]; 1 <= cur_len <= max_seq,
+ * NQ % NKV == 0. `scale` is the score multiplier (the binding passes
+ * 1/sqrt(hd)). Split over the KV sequence with a fixed-order combine.
+ * Replaces launch_decode_attention (csrc/kernels/decode_attention.cu:57-63;
+ * binding csrc/bindings.cpp:468-488).
+ * ------------------------------------------------------------------------ */
+size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len);
+int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                         int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, int64_t cur_len, float scale,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOINFER_AMD_H_ */

@@ -1,0 +1,484 @@
+// soinfer._C -- thin PyTorch-ROCm binding over the C ABI in include/soinfer_amd.h.
+//
+// Function names, argument order, dtypes, output allocation and the
+// validation rules (TORCH_CHECK -> Python RuntimeError) follow the
+// reference's operator surface, csrc/bindings.cpp:26-610 (hot-path subset:
+// gemv_w8a16 239-262, gemv_w4a16_group{,_lop3} 266-309,
+// gemv_w4a16_sparse_accumulate 311-339, build_dip_descriptors 341-359,
+// gemv_dip_fused_{up,down} 363-432, decode_attention 468-488,
+// topk_threshold_select 507-518, gather_rows_{staged,naive} 522-559).
+// Kernels are launched on the current HIP stream of the input's device; a
+// C-ABI failure raises RuntimeError carrying the library's error text
+// (the reference aborts the process instead, common.cuh:18-26).
+#include <torch/extension.h>
+
+#include <ATen/hip/HIPContext.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+#include <tuple>
+
+#include "../../include/soinfer_amd.h"
+
+namespace {
+
+void* cur_stream(const torch::Tensor& t) {
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_status(int status, const char* name) {
+    TORCH_CHECK(status == SOI_OK, name, ": ", soi_status_string(status), ": ", soi_last_error());
+}
+
+void check_f32_cuda_contiguous(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, ": input must be a CUDA tensor");
+    TORCH_CHECK(t.scalar_type() == torch::kFloat32, name, ": only float32 is supported");
+    TORCH_CHECK(t.is_contiguous(), name, ": input must be contiguous");
+}
+
+void check_f16_cuda_contiguous(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, ": input must be a CUDA tensor");
+    TORCH_CHECK(t.scalar_type() == torch::kFloat16, name, ": only float16 is supported");
+    TORCH_CHECK(t.is_contiguous(), name, ": input must be contiguous");
+}
+
+void check_same_device(const torch::Tensor& a, const torch::Tensor& b, const char* name) {
+    TORCH_CHECK(a.device() == b.device(), name, ": all CUDA tensors must be on the same device");
+}
+
+const uint16_t* h16(const torch::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr<at::Half>()); }
+uint16_t* h16m(torch::Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr<at::Half>()); }
+
+int64_t expected_num_groups(int64_t k_dim, int64_t group_size) { return (k_dim + group_size - 1) / group_size; }
+
+torch::Tensor workspace(const torch::Tensor& like, size_t bytes) {
+    return torch::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(torch::kUInt8));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// INT8 / INT4 dense GEMV
+// ---------------------------------------------------------------------------
+
+torch::Tensor gemv_w8a16(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x, int64_t group_size) {
+    TORCH_CHECK(Wq.is_cuda(), "gemv_w8a16(Wq): must be a CUDA tensor");
+    TORCH_CHECK(Wq.scalar_type() == torch::kInt8, "gemv_w8a16(Wq): must be int8");
+    TORCH_CHECK(Wq.is_contiguous(), "gemv_w8a16(Wq): must be contiguous");
+    TORCH_CHECK(Wq.dim() == 2, "gemv_w8a16(Wq): must be 2D [N, K]");
+    check_f16_cuda_contiguous(x, "gemv_w8a16(x)");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == Wq.size(1), "gemv_w8a16: x must be 1D [K] matching Wq's K");
+    TORCH_CHECK(group_size >= 1, "gemv_w8a16: group_size must be >= 1");
+    check_f32_cuda_contiguous(scale, "gemv_w8a16(scale)");
+    const int64_t N = Wq.size(0), K = Wq.size(1);
+    TORCH_CHECK(scale.dim() == 2, "gemv_w8a16: scale must be 2D [N or 1, num_groups]");
+    TORCH_CHECK(scale.size(0) == N || scale.size(0) == 1,
+                "gemv_w8a16: scale.size(0) must be N (per-channel/group) or 1 (per-tensor broadcast)");
+    const int64_t num_groups = scale.size(1);
+    const int64_t stride = (scale.size(0) == 1) ? 0 : num_groups;
+    TORCH_CHECK(num_groups == 1 || group_size % 4 == 0,
+                "gemv_w8a16: group_size must be a multiple of 4 when num_groups > 1");
+    TORCH_CHECK(num_groups == 1 || num_groups == expected_num_groups(K, group_size),
+                "gemv_w8a16: scale's num_groups must be 1 (per-tensor broadcast) or ceil(K/group_size) for the given "
+                "K and group_size, got ", num_groups, " but expected ", expected_num_groups(K, group_size));
+    check_same_device(Wq, x, "gemv_w8a16");
+    check_same_device(Wq, scale, "gemv_w8a16");
+    const at::DeviceGuard guard(x.device());
+    auto y = torch::empty({N}, x.options());
+    check_status(soi_gemv_w8a16(Wq.data_ptr<int8_t>(), scale.data_ptr<float>(), h16(x), h16m(y), N, K, group_size,
+                                num_groups, stride, cur_stream(x)),
+                 "gemv_w8a16");
+    return y;
+}
+
+namespace {
+
+using Int4Fn = int (*)(const uint8_t*, const float*, const uint16_t*, uint16_t*, int64_t, int64_t, int64_t, int64_t,
+                       void*);
+
+torch::Tensor gemv_w4a16_group_impl(torch::Tensor Wq_packed, torch::Tensor scale, torch::Tensor x, int64_t K,
+                                    int64_t group_size, const char* name, Int4Fn fn) {
+    TORCH_CHECK(Wq_packed.is_cuda(), name, "(Wq_packed): must be a CUDA tensor");
+    TORCH_CHECK(Wq_packed.scalar_type() == torch::kUInt8, name, "(Wq_packed): must be uint8 (AWQ-packed int4)");
+    TORCH_CHECK(Wq_packed.is_contiguous(), name, "(Wq_packed): must be contiguous");
+    TORCH_CHECK(Wq_packed.dim() == 2, name, "(Wq_packed): must be 2D [N, ceil(K/8)*4]");
+    check_f16_cuda_contiguous(x, "x");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == K, name, ": x must be 1D [K]");
+    TORCH_CHECK(K >= 1, name, ": K must be >= 1");
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    const int64_t N = Wq_packed.size(0);
+    TORCH_CHECK(Wq_packed.size(1) == ((K + 7) / 8) * 4, name, ": Wq_packed.size(1) must be ceil(K/8)*4 for the given K");
+    TORCH_CHECK(scale.is_cuda(), name, ": scale must be a CUDA tensor");
+    TORCH_CHECK(scale.scalar_type() == torch::kFloat32, name, ": scale must be float32");
+    TORCH_CHECK(scale.is_contiguous(), name, ": scale must be contiguous");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == N, name,
+                ": scale must be 2D [N, num_groups] (grouped int4 has no per-tensor broadcast)");
+    const int64_t num_groups = scale.size(1);
+    TORCH_CHECK(num_groups == expected_num_groups(K, group_size), name, ": scale's num_groups must be "
+                "ceil(K/group_size) for the given K and group_size, got ", num_groups, " but expected ",
+                expected_num_groups(K, group_size));
+    check_same_device(Wq_packed, x, name);
+    check_same_device(Wq_packed, scale, name);
+    const at::DeviceGuard guard(x.device());
+    auto y = torch::empty({N}, x.options());
+    check_status(fn(Wq_packed.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), h16m(y), N, K, group_size,
+                    num_groups, cur_stream(x)),
+                 name);
+    return y;
+}
+
+}  // namespace
+
+torch::Tensor gemv_w4a16_group(torch::Tensor Wq_packed, torch::Tensor scale, torch::Tensor x, int64_t K,
+                               int64_t group_size) {
+    return gemv_w4a16_group_impl(Wq_packed, scale, x, K, group_size, "gemv_w4a16_group", soi_gemv_w4a16_group);
+}
+
+torch::Tensor gemv_w4a16_group_lop3(torch::Tensor Wq_packed, torch::Tensor scale, torch::Tensor x, int64_t K,
+                                    int64_t group_size) {
+    return gemv_w4a16_group_impl(Wq_packed, scale, x, K, group_size, "gemv_w4a16_group_lop3",
+                                 soi_gemv_w4a16_group_lop3);
+}
+
+// ---------------------------------------------------------------------------
+// sparse down accumulate
+// ---------------------------------------------------------------------------
+
+torch::Tensor gemv_w4a16_sparse_accumulate(torch::Tensor Wq_selected, torch::Tensor scale_selected,
+                                           torch::Tensor h_selected, int64_t H, int64_t group_size) {
+    const char* name = "gemv_w4a16_sparse_accumulate";
+    TORCH_CHECK(Wq_selected.is_cuda() && Wq_selected.scalar_type() == torch::kUInt8 && Wq_selected.is_contiguous(),
+                name, "(Wq_selected): must be a contiguous CUDA uint8 tensor");
+    TORCH_CHECK(Wq_selected.dim() == 2, name, "(Wq_selected): must be 2D [k, ceil(H/8)*4]");
+    TORCH_CHECK(H >= 1, name, ": H must be >= 1");
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    const int64_t k = Wq_selected.size(0);
+    TORCH_CHECK(Wq_selected.size(1) == ((H + 7) / 8) * 4, name,
+                ": Wq_selected.size(1) must be ceil(H/8)*4 for the given H");
+    TORCH_CHECK(scale_selected.is_cuda() && scale_selected.scalar_type() == torch::kFloat32 &&
+                    scale_selected.is_contiguous(),
+                name, "(scale_selected): must be a contiguous CUDA float32 tensor");
+    TORCH_CHECK(scale_selected.dim() == 2 && scale_selected.size(0) == k, name,
+                ": scale_selected must be 2D [k, num_groups]");
+    check_f16_cuda_contiguous(h_selected, "gemv_w4a16_sparse_accumulate(h_selected)");
+    TORCH_CHECK(h_selected.dim() == 1 && h_selected.size(0) == k, name, ": h_selected must be 1D [k]");
+    const int64_t num_groups = scale_selected.size(1);
+    TORCH_CHECK(num_groups == expected_num_groups(H, group_size), name, ": scale_selected's num_groups must be "
+                "ceil(H/group_size) for the given H and group_size, got ", num_groups, " but expected ",
+                expected_num_groups(H, group_size));
+    check_same_device(Wq_selected, h_selected, name);
+    check_same_device(Wq_selected, scale_selected, name);
+    const at::DeviceGuard guard(h_selected.device());
+    auto y = torch::empty({H}, h_selected.options());
+    const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
+    auto ws = workspace(h_selected, wsb);
+    check_status(soi_gemv_w4a16_sparse_accumulate(Wq_selected.data_ptr<uint8_t>(), scale_selected.data_ptr<float>(),
+                                                  h16(h_selected), h16m(y), H, k, group_size, num_groups,
+                                                  ws.data_ptr<uint8_t>(), wsb, cur_stream(h_selected)),
+                 name);
+    return y;
+}
+
+// ---------------------------------------------------------------------------
+// hot-cache descriptors and fused GEMVs
+// ---------------------------------------------------------------------------
+
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> build_dip_descriptors(torch::Tensor selected_indices,
+                                                                              torch::Tensor slot_of) {
+    const char* name = "build_dip_descriptors";
+    TORCH_CHECK(selected_indices.is_cuda() && selected_indices.scalar_type() == torch::kInt32 &&
+                    selected_indices.dim() == 1 && selected_indices.is_contiguous(),
+                name, "(selected_indices): must be a contiguous 1D int32 CUDA tensor");
+    TORCH_CHECK(slot_of.is_cuda() && slot_of.scalar_type() == torch::kInt32 && slot_of.dim() == 1 &&
+                    slot_of.is_contiguous(),
+                name, "(slot_of): must be a contiguous 1D int32 CUDA tensor");
+    check_same_device(selected_indices, slot_of, name);
+    const at::DeviceGuard guard(selected_indices.device());
+    const int64_t k = selected_indices.size(0);
+    auto descriptors = torch::empty({k}, selected_indices.options());
+    auto miss_channels = torch::empty({k}, selected_indices.options());
+    auto miss_count = torch::empty({1}, selected_indices.options());
+    check_status(soi_build_dip_descriptors(selected_indices.data_ptr<int32_t>(), k, slot_of.data_ptr<int32_t>(),
+                                           slot_of.size(0), descriptors.data_ptr<int32_t>(),
+                                           miss_channels.data_ptr<int32_t>(), miss_count.data_ptr<int32_t>(),
+                                           cur_stream(selected_indices)),
+                 name);
+    return {descriptors, miss_channels, miss_count};
+}
+
+namespace {
+
+void check_dip_fused_common(const torch::Tensor& cache_Wq, const torch::Tensor& cache_scale,
+                            const torch::Tensor& staging_Wq, const torch::Tensor& staging_scale,
+                            const torch::Tensor& descriptors, int64_t row_dim, const char* name) {
+    const int64_t expected_bytes = ((row_dim + 7) / 8) * 4;
+    TORCH_CHECK(cache_Wq.is_cuda() && cache_Wq.scalar_type() == torch::kUInt8 && cache_Wq.dim() == 2 &&
+                    cache_Wq.is_contiguous() && cache_Wq.size(1) == expected_bytes,
+                name, "(cache_Wq): must be a contiguous 2D uint8 CUDA tensor [C, ceil(row_dim/8)*4]");
+    TORCH_CHECK(staging_Wq.is_cuda() && staging_Wq.scalar_type() == torch::kUInt8 && staging_Wq.dim() == 2 &&
+                    staging_Wq.is_contiguous() && staging_Wq.size(1) == expected_bytes,
+                name, "(staging_Wq): must be a contiguous 2D uint8 CUDA tensor [M, ceil(row_dim/8)*4]");
+    TORCH_CHECK(cache_scale.is_cuda() && cache_scale.scalar_type() == torch::kFloat32 && cache_scale.dim() == 2 &&
+                    cache_scale.is_contiguous(),
+                name, "(cache_scale): must be a contiguous 2D float32 CUDA tensor [C, num_groups]");
+    TORCH_CHECK(staging_scale.is_cuda() && staging_scale.scalar_type() == torch::kFloat32 &&
+                    staging_scale.dim() == 2 && staging_scale.is_contiguous(),
+                name, "(staging_scale): must be a contiguous 2D float32 CUDA tensor [M, num_groups]");
+    TORCH_CHECK(cache_scale.size(1) == staging_scale.size(1), name,
+                ": cache_scale and staging_scale must have the same num_groups");
+    TORCH_CHECK(descriptors.is_cuda() && descriptors.scalar_type() == torch::kInt32 && descriptors.dim() == 1 &&
+                    descriptors.is_contiguous(),
+                name, "(descriptors): must be a contiguous 1D int32 CUDA tensor");
+    // Row counts of each source bound the descriptor offsets inside the kernel.
+    TORCH_CHECK(cache_scale.size(0) >= cache_Wq.size(0) || cache_Wq.size(0) == 0, name,
+                ": cache_scale must have a row per cache_Wq row");
+    TORCH_CHECK(staging_scale.size(0) >= staging_Wq.size(0) || staging_Wq.size(0) == 0, name,
+                ": staging_scale must have a row per staging_Wq row");
+    check_same_device(descriptors, cache_Wq, name);
+    check_same_device(descriptors, staging_Wq, name);
+    check_same_device(descriptors, cache_scale, name);
+    check_same_device(descriptors, staging_scale, name);
+}
+
+}  // namespace
+
+torch::Tensor gemv_dip_fused_up(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor staging_Wq,
+                                torch::Tensor staging_scale, torch::Tensor descriptors, torch::Tensor x, int64_t K,
+                                int64_t group_size) {
+    const char* name = "gemv_dip_fused_up";
+    check_dip_fused_common(cache_Wq, cache_scale, staging_Wq, staging_scale, descriptors, K, name);
+    check_f16_cuda_contiguous(x, "gemv_dip_fused_up(x)");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == K, name, ": x must be 1D [K]");
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    const int64_t k = descriptors.size(0);
+    const int64_t num_groups = cache_scale.size(1);
+    TORCH_CHECK(num_groups == expected_num_groups(K, group_size), name, ": cache_scale/staging_scale's num_groups "
+                "must be ceil(K/group_size) for the given K and group_size, got ", num_groups, " but expected ",
+                expected_num_groups(K, group_size));
+    check_same_device(descriptors, x, name);
+    const at::DeviceGuard guard(x.device());
+    auto y = torch::empty({k}, x.options());
+    const int64_t C = std::min(cache_Wq.size(0), cache_scale.size(0));
+    const int64_t M = std::min(staging_Wq.size(0), staging_scale.size(0));
+    check_status(soi_gemv_dip_fused_up(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), C,
+                                       staging_Wq.data_ptr<uint8_t>(), staging_scale.data_ptr<float>(), M,
+                                       descriptors.data_ptr<int32_t>(), k, h16(x), h16m(y), K, group_size, num_groups,
+                                       cur_stream(x)),
+                 name);
+    return y;
+}
+
+torch::Tensor gemv_dip_fused_down(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor staging_Wq,
+                                  torch::Tensor staging_scale, torch::Tensor descriptors, torch::Tensor h_selected,
+                                  int64_t H, int64_t group_size) {
+    const char* name = "gemv_dip_fused_down";
+    check_dip_fused_common(cache_Wq, cache_scale, staging_Wq, staging_scale, descriptors, H, name);
+    check_f16_cuda_contiguous(h_selected, "gemv_dip_fused_down(h_selected)");
+    const int64_t k = descriptors.size(0);
+    TORCH_CHECK(h_selected.dim() == 1 && h_selected.size(0) == k, name, ": h_selected must be 1D [k]");
+    TORCH_CHECK(H >= 1, name, ": H must be >= 1");
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    const int64_t num_groups = cache_scale.size(1);
+    TORCH_CHECK(num_groups == expected_num_groups(H, group_size), name, ": cache_scale/staging_scale's num_groups "
+                "must be ceil(H/group_size) for the given H and group_size, got ", num_groups, " but expected ",
+                expected_num_groups(H, group_size));
+    check_same_device(descriptors, h_selected, name);
+    const at::DeviceGuard guard(h_selected.device());
+    auto y = torch::empty({H}, h_selected.options());
+    const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
+    auto ws = workspace(h_selected, wsb);
+    const int64_t C = std::min(cache_Wq.size(0), cache_scale.size(0));
+    const int64_t M = std::min(staging_Wq.size(0), staging_scale.size(0));
+    check_status(soi_gemv_dip_fused_down(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), C,
+                                         staging_Wq.data_ptr<uint8_t>(), staging_scale.data_ptr<float>(), M,
+                                         descriptors.data_ptr<int32_t>(), k, h16(h_selected), h16m(y), H, group_size,
+                                         num_groups, ws.data_ptr<uint8_t>(), wsb, cur_stream(h_selected)),
+                 name);
+    return y;
+}
+
+// ---------------------------------------------------------------------------
+// resident-weight (index-driven) sparse GEMVs and device gather
+// ---------------------------------------------------------------------------
+
+torch::Tensor gemv_w4a16_indexed(torch::Tensor Wq_packed, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
+                                 int64_t K, int64_t group_size) {
+    const char* name = "gemv_w4a16_indexed";
+    TORCH_CHECK(Wq_packed.is_cuda() && Wq_packed.scalar_type() == torch::kUInt8 && Wq_packed.is_contiguous() &&
+                    Wq_packed.dim() == 2,
+                name, "(Wq_packed): must be a contiguous 2D CUDA uint8 tensor [N, ceil(K/8)*4]");
+    TORCH_CHECK(Wq_packed.size(1) == ((K + 7) / 8) * 4, name, ": Wq_packed.size(1) must be ceil(K/8)*4");
+    check_f32_cuda_contiguous(scale, "gemv_w4a16_indexed(scale)");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq_packed.size(0), name, ": scale must be 2D [N, num_groups]");
+    TORCH_CHECK(idx.is_cuda() && idx.scalar_type() == torch::kInt32 && idx.dim() == 1 && idx.is_contiguous(), name,
+                "(idx): must be a contiguous 1D int32 CUDA tensor");
+    check_f16_cuda_contiguous(x, "gemv_w4a16_indexed(x)");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == K, name, ": x must be 1D [K]");
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    TORCH_CHECK(scale.size(1) == expected_num_groups(K, group_size), name,
+                ": scale's num_groups must be ceil(K/group_size)");
+    check_same_device(Wq_packed, x, name);
+    check_same_device(Wq_packed, idx, name);
+    check_same_device(Wq_packed, scale, name);
+    const at::DeviceGuard guard(x.device());
+    const int64_t k = idx.size(0);
+    auto y = torch::empty({k}, x.options());
+    check_status(soi_gemv_w4a16_indexed(Wq_packed.data_ptr<uint8_t>(), scale.data_ptr<float>(), Wq_packed.size(0),
+                                        idx.data_ptr<int32_t>(), k, h16(x), h16m(y), K, group_size, scale.size(1),
+                                        cur_stream(x)),
+                 name);
+    return y;
+}
+
+torch::Tensor gemv_w4a16_indexed_accumulate(torch::Tensor Wq_T, torch::Tensor scale_T, torch::Tensor idx,
+                                            torch::Tensor h_selected, int64_t H, int64_t group_size) {
+    const char* name = "gemv_w4a16_indexed_accumulate";
+    TORCH_CHECK(Wq_T.is_cuda() && Wq_T.scalar_type() == torch::kUInt8 && Wq_T.is_contiguous() && Wq_T.dim() == 2,
+                name, "(Wq_T): must be a contiguous 2D CUDA uint8 tensor [I, ceil(H/8)*4]");
+    TORCH_CHECK(Wq_T.size(1) == ((H + 7) / 8) * 4, name, ": Wq_T.size(1) must be ceil(H/8)*4");
+    check_f32_cuda_contiguous(scale_T, "gemv_w4a16_indexed_accumulate(scale_T)");
+    TORCH_CHECK(scale_T.dim() == 2 && scale_T.size(0) == Wq_T.size(0), name, ": scale_T must be 2D [I, num_groups]");
+    TORCH_CHECK(idx.is_cuda() && idx.scalar_type() == torch::kInt32 && idx.dim() == 1 && idx.is_contiguous(), name,
+                "(idx): must be a contiguous 1D int32 CUDA tensor");
+    check_f16_cuda_contiguous(h_selected, "gemv_w4a16_indexed_accumulate(h_selected)");
+    TORCH_CHECK(h_selected.dim() == 1 && h_selected.size(0) == idx.size(0), name, ": h_selected must be 1D [k]");
+    TORCH_CHECK(H >= 1 && group_size >= 1 && group_size % 8 == 0, name, ": bad H or group_size");
+    TORCH_CHECK(scale_T.size(1) == expected_num_groups(H, group_size), name,
+                ": scale_T's num_groups must be ceil(H/group_size)");
+    check_same_device(Wq_T, h_selected, name);
+    check_same_device(Wq_T, idx, name);
+    check_same_device(Wq_T, scale_T, name);
+    const at::DeviceGuard guard(h_selected.device());
+    const int64_t k = idx.size(0);
+    auto y = torch::empty({H}, h_selected.options());
+    const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
+    auto ws = workspace(h_selected, wsb);
+    check_status(soi_gemv_w4a16_indexed_accumulate(Wq_T.data_ptr<uint8_t>(), scale_T.data_ptr<float>(), Wq_T.size(0),
+                                                   idx.data_ptr<int32_t>(), k, h16(h_selected), h16m(y), H, group_size,
+                                                   scale_T.size(1), ws.data_ptr<uint8_t>(), wsb,
+                                                   cur_stream(h_selected)),
+                 name);
+    return y;
+}
+
+void gather_rows_device(torch::Tensor src, torch::Tensor idx, torch::Tensor dst) {
+    const char* name = "gather_rows_device";
+    TORCH_CHECK(src.is_cuda() && src.scalar_type() == torch::kUInt8 && src.dim() == 2 && src.is_contiguous(), name,
+                "(src): must be a contiguous 2D CUDA uint8 tensor");
+    TORCH_CHECK(idx.is_cuda() && idx.scalar_type() == torch::kInt32 && idx.dim() == 1 && idx.is_contiguous(), name,
+                "(idx): must be a contiguous 1D int32 CUDA tensor");
+    TORCH_CHECK(dst.is_cuda() && dst.scalar_type() == torch::kUInt8 && dst.is_contiguous(), name,
+                "(dst): must be a contiguous CUDA uint8 tensor");
+    TORCH_CHECK(dst.numel() >= idx.size(0) * src.size(1), name, "(dst): too small for k * row_nbytes bytes");
+    check_same_device(src, idx, name);
+    check_same_device(src, dst, name);
+    const at::DeviceGuard guard(src.device());
+    check_status(soi_gather_rows_device(src.data_ptr<uint8_t>(), src.size(0), src.size(1), idx.data_ptr<int32_t>(),
+                                        idx.size(0), dst.data_ptr<uint8_t>(), cur_stream(src)),
+                 name);
+}
+
+// ---------------------------------------------------------------------------
+// attention, top-k, host gathers
+// ---------------------------------------------------------------------------
+
+torch::Tensor decode_attention(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, int64_t cur_len) {
+    check_f16_cuda_contiguous(q, "decode_attention(q)");
+    check_f16_cuda_contiguous(k_cache, "decode_attention(k_cache)");
+    check_f16_cuda_contiguous(v_cache, "decode_attention(v_cache)");
+    TORCH_CHECK(q.dim() == 2, "decode_attention: q must be 2D [num_q_heads, head_dim]");
+    TORCH_CHECK(k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes(),
+                "decode_attention: k_cache/v_cache must be 3D [num_kv_heads, max_seq_len, head_dim] and same shape");
+    TORCH_CHECK(q.size(1) == k_cache.size(2), "decode_attention: q's head_dim must match the cache's head_dim");
+    const int64_t NQ = q.size(0), NKV = k_cache.size(0), S = k_cache.size(1), hd = k_cache.size(2);
+    TORCH_CHECK(NKV >= 1 && NQ % NKV == 0, "decode_attention: num_q_heads must be a multiple of num_kv_heads");
+    TORCH_CHECK(cur_len >= 1 && cur_len <= S, "decode_attention: cur_len out of range for max_seq_len");
+    TORCH_CHECK(hd >= 1 && hd <= 1024, "decode_attention: head_dim must be in [1, 1024]");
+    check_same_device(q, k_cache, "decode_attention");
+    check_same_device(q, v_cache, "decode_attention");
+    const at::DeviceGuard guard(q.device());
+    auto out = torch::empty({NQ, hd}, q.options());
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    const size_t wsb = soi_decode_attention_workspace_bytes(NQ, NKV, hd, cur_len);
+    auto ws = workspace(q, wsb);
+    check_status(soi_decode_attention(h16(q), h16(k_cache), h16(v_cache), h16m(out), NQ, NKV, S, hd, cur_len, scale,
+                                      ws.data_ptr<uint8_t>(), wsb, cur_stream(q)),
+                 "decode_attention");
+    return out;
+}
+
+std::tuple<torch::Tensor, torch::Tensor> topk_threshold_select(torch::Tensor abs_g, int64_t k) {
+    check_f32_cuda_contiguous(abs_g, "topk_threshold_select(abs_g)");
+    TORCH_CHECK(abs_g.dim() == 1, "topk_threshold_select: abs_g must be 1D [I]");
+    TORCH_CHECK(k >= 1 && k <= abs_g.size(0), "topk_threshold_select: k must be in [1, I]");
+    const at::DeviceGuard guard(abs_g.device());
+    const int64_t n = abs_g.size(0);
+    auto out_indices = torch::empty({k}, abs_g.options().dtype(torch::kInt32));
+    auto out_count = torch::empty({1}, abs_g.options().dtype(torch::kInt32));
+    check_status(soi_topk_threshold_select(abs_g.data_ptr<float>(), n, k, out_indices.data_ptr<int32_t>(),
+                                           out_count.data_ptr<int32_t>(), cur_stream(abs_g)),
+                 "topk_threshold_select");
+    return {out_indices, out_count};
+}
+
+namespace {
+
+void check_gather_rows_common(const torch::Tensor& matrix, const torch::Tensor& indices, const torch::Tensor& gpu_dst,
+                              const char* name) {
+    TORCH_CHECK(matrix.is_cpu() && matrix.is_pinned(), name, "(matrix): must be pinned host memory");
+    TORCH_CHECK(matrix.scalar_type() == torch::kUInt8 && matrix.dim() == 2 && matrix.is_contiguous(), name,
+                "(matrix): must be a contiguous 2D uint8 tensor [num_rows, row_nbytes]");
+    TORCH_CHECK(indices.is_cpu() && indices.scalar_type() == torch::kInt64 && indices.dim() == 1, name,
+                "(indices): must be a 1D int64 CPU tensor");
+    TORCH_CHECK(gpu_dst.is_cuda() && gpu_dst.scalar_type() == torch::kUInt8 && gpu_dst.is_contiguous(), name,
+                "(gpu_dst): must be a contiguous CUDA uint8 tensor");
+    TORCH_CHECK(gpu_dst.numel() >= indices.size(0) * matrix.size(1), name,
+                "(gpu_dst): too small for k * row_nbytes bytes");
+}
+
+}  // namespace
+
+void gather_rows_staged(torch::Tensor matrix, torch::Tensor indices, torch::Tensor staging, torch::Tensor gpu_dst) {
+    check_gather_rows_common(matrix, indices, gpu_dst, "gather_rows_staged");
+    TORCH_CHECK(staging.is_cpu() && staging.is_pinned() && staging.scalar_type() == torch::kUInt8,
+                "gather_rows_staged(staging): must be pinned host uint8 memory");
+    TORCH_CHECK(staging.is_contiguous(), "gather_rows_staged(staging): must be contiguous");
+    const int64_t k = indices.size(0), row_nbytes = matrix.size(1);
+    TORCH_CHECK(staging.numel() >= k * row_nbytes, "gather_rows_staged(staging): too small for k * row_nbytes bytes");
+    auto idx = indices.contiguous();
+    const at::DeviceGuard guard(gpu_dst.device());
+    check_status(soi_gather_rows_staged(matrix.data_ptr<uint8_t>(), matrix.size(0), row_nbytes,
+                                        idx.data_ptr<int64_t>(), k, staging.data_ptr<uint8_t>(),
+                                        gpu_dst.data_ptr<uint8_t>(), cur_stream(gpu_dst)),
+                 "gather_rows_staged");
+}
+
+void gather_rows_naive(torch::Tensor matrix, torch::Tensor indices, torch::Tensor gpu_dst) {
+    check_gather_rows_common(matrix, indices, gpu_dst, "gather_rows_naive");
+    auto idx = indices.contiguous();
+    const at::DeviceGuard guard(gpu_dst.device());
+    check_status(soi_gather_rows_naive(matrix.data_ptr<uint8_t>(), matrix.size(0), matrix.size(1),
+                                       idx.data_ptr<int64_t>(), idx.size(0), gpu_dst.data_ptr<uint8_t>(),
+                                       cur_stream(gpu_dst)),
+                 "gather_rows_naive");
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "soinfer MI355X (gfx950) quantized decode hot path";
+    m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
+    m.def("gemv_w4a16_group", &gemv_w4a16_group, "INT4 group GEMV (scalar nibble dequant)");
+    m.def("gemv_w4a16_group_lop3", &gemv_w4a16_group_lop3, "INT4 group GEMV (bitfield dequant)");
+    m.def("gemv_w4a16_sparse_accumulate", &gemv_w4a16_sparse_accumulate, "sparse down-proj accumulate");
+    m.def("build_dip_descriptors", &build_dip_descriptors, "hot-cache descriptors");
+    m.def("gemv_dip_fused_up", &gemv_dip_fused_up, "descriptor-driven up GEMV");
+    m.def("gemv_dip_fused_down", &gemv_dip_fused_down, "descriptor-driven down accumulate");
+    m.def("gemv_w4a16_indexed", &gemv_w4a16_indexed, "index-driven up GEMV over resident weights");
+    m.def("gemv_w4a16_indexed_accumulate", &gemv_w4a16_indexed_accumulate,
+          "index-driven down accumulate over resident weights");
+    m.def("gather_rows_device", &gather_rows_device, "device-resident row gather");
+    m.def("decode_attention", &decode_attention, "batch-1 GQA decode attention");
+    m.def("topk_threshold_select", &topk_threshold_select, "deterministic threshold top-k");
+    m.def("gather_rows_staged", &gather_rows_staged, "pinned-host row gather, staged");
+    m.def("gather_rows_naive", &gather_rows_naive, "pinned-host row gather, per row");
+    m.def("version", []() { return std::string(soi_version()); });
+}

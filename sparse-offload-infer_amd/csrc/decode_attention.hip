@@ -1,0 +1,313 @@
+// Batch-1 GQA decode attention on gfx950.
+//
+// Restates csrc/kernels/decode_attention.cu:17-55 (binding scale =
+// 1/sqrt(head_dim), bindings.cpp:482): for each query head h with KV head
+// kvh = h / (NQ/NKV), out[h] = sum_t softmax_t(scale * q_h . k_t) v_t over
+// t < cur_len, fp32 softmax state, fp16 output.
+//
+// The reference runs one block per query head and two block barriers per
+// timestep. Here (fast path, head_dim % 8 == 0, head_dim <= 512, <= 8 query
+// heads per KV head):
+//   * workgroup (kvh, split) = 4 waves streaming one KV head over a
+//     contiguous range of timesteps; every query head that shares the KV head
+//     is processed from the same K/V loads (each K/V byte is read once);
+//   * a timestep row of head_dim fp16 is read by head_dim/8 lanes with 16-byte
+//     loads, so one wave instruction reads 64*16 contiguous bytes;
+//   * scores: v_dot2 over the lane's 8 dims, then a butterfly over the row's
+//     lanes; softmax runs in the log2 domain (scores pre-multiplied by
+//     scale*log2(e), v_exp_f32) with the online max/sum recurrence of the
+//     reference (m0 = -1e30);
+//   * lane groups, then waves (in wave order), then splits (in split order)
+//     are merged with the standard (m, l, acc) rescaling. Fixed order:
+//     deterministic.
+// Other shapes use a simple one-wave-per-head kernel with the same math.
+#include "soi_device.h"
+#include "soi_host.h"
+
+namespace soi {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr float kNegBig = -1e30f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int mask = 1; mask < LPR; mask <<= 1) v += __shfl_xor(v, mask, kWave);
+    return v;
+}
+
+// Partial state layout per (query head, split): [m, l, acc[hd]] in fp32.
+template <int LPR, int REP>
+__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const uint16_t* __restrict__ q,
+                                                                   const uint16_t* __restrict__ kc,
+                                                                   const uint16_t* __restrict__ vc,
+                                                                   float* __restrict__ part, int rep, int S, int L,
+                                                                   int tps, int nsplit, float scale_log2) {
+    constexpr int HD = LPR * 8;
+    constexpr int RPI = kWave / LPR;  // timesteps per wave instruction
+    __shared__ float s_state[kAttnWaves][REP][HD + 2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane / LPR, u = lane % LPR;
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int t0 = split * tps;
+    const int t1 = min(L, t0 + tps);
+
+    f16x2 qv[REP][4];
+#pragma unroll
+    for (int hh = 0; hh < REP; ++hh) {
+        const int h = kvh * rep + (hh < rep ? hh : 0);
+        const u32x4 t = reinterpret_cast<const u32x4*>(q + static_cast<int64_t>(h) * HD)[u];
+        qv[hh][0] = as_f16x2(t.x);
+        qv[hh][1] = as_f16x2(t.y);
+        qv[hh][2] = as_f16x2(t.z);
+        qv[hh][3] = as_f16x2(t.w);
+    }
+    float m[REP], l[REP], acc[REP][8];
+#pragma unroll
+    for (int hh = 0; hh < REP; ++hh) {
+        m[hh] = kNegBig;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[hh][d] = 0.0f;
+    }
+
+    const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * S * HD;
+    const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * S * HD;
+    for (int tb = t0 + wave * RPI; tb < t1; tb += kAttnWaves * RPI) {
+        const int t = tb + g;
+        const bool valid = t < t1;
+        const int tl = valid ? t : t1 - 1;
+        const u32x4 kk = reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(tl) * HD)[u];
+        const u32x4 vv = reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(tl) * HD)[u];
+        const f16x2 k0 = as_f16x2(kk.x), k1 = as_f16x2(kk.y), k2 = as_f16x2(kk.z), k3 = as_f16x2(kk.w);
+        const f16x2 v2[4] = {as_f16x2(vv.x), as_f16x2(vv.y), as_f16x2(vv.z), as_f16x2(vv.w)};
+#pragma unroll
+        for (int hh = 0; hh < REP; ++hh) {
+            if (hh >= rep) break;
+            float part = dot2(qv[hh][0], k0, 0.0f);
+            part = dot2(qv[hh][1], k1, part);
+            part = dot2(qv[hh][2], k2, part);
+            part = dot2(qv[hh][3], k3, part);
+            float sc = group_sum<LPR>(part) * scale_log2;  // every lane of the group takes part
+            if (!valid) sc = -__builtin_inff();
+            const float mn = fmaxf(m[hh], sc);
+            const float corr = fast_exp2(m[hh] - mn);
+            const float p = fast_exp2(sc - mn);
+            l[hh] = fmaf(l[hh], corr, p);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[hh][2 * e] = fmaf(acc[hh][2 * e], corr, p * static_cast<float>(v2[e].x));
+                acc[hh][2 * e + 1] = fmaf(acc[hh][2 * e + 1], corr, p * static_cast<float>(v2[e].y));
+            }
+            m[hh] = mn;
+        }
+    }
+
+    // merge lane groups (same u, different timesteps) inside the wave
+#pragma unroll
+    for (int mask = LPR; mask < kWave; mask <<= 1) {
+#pragma unroll
+        for (int hh = 0; hh < REP; ++hh) {
+            if (hh >= rep) break;
+            const float mo = __shfl_xor(m[hh], mask, kWave);
+            const float lo = __shfl_xor(l[hh], mask, kWave);
+            const float mn = fmaxf(m[hh], mo);
+            const float ca = fast_exp2(m[hh] - mn), cb = fast_exp2(mo - mn);
+            l[hh] = l[hh] * ca + lo * cb;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const float ao = __shfl_xor(acc[hh][d], mask, kWave);
+                acc[hh][d] = acc[hh][d] * ca + ao * cb;
+            }
+            m[hh] = mn;
+        }
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int hh = 0; hh < REP; ++hh) {
+            if (hh >= rep) break;
+            if (u == 0) {
+                s_state[wave][hh][0] = m[hh];
+                s_state[wave][hh][1] = l[hh];
+            }
+#pragma unroll
+            for (int d = 0; d < 8; ++d) s_state[wave][hh][2 + 8 * u + d] = acc[hh][d];
+        }
+    }
+    __syncthreads();
+    // merge the waves in order; thread i handles element i of [m, l, acc...]
+    for (int hh = 0; hh < rep; ++hh) {
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, s_state[w][hh][0]);
+        float* out = part + (static_cast<int64_t>(kvh * rep + hh) * nsplit + split) * (HD + 2);
+        for (int i = threadIdx.x; i < HD + 2; i += kAttnThreads) {
+            float v = 0.0f;
+            if (i == 0) {
+                v = M;
+            } else {
+#pragma unroll
+                for (int w = 0; w < kAttnWaves; ++w) v += s_state[w][hh][i] * fast_exp2(s_state[w][hh][0] - M);
+            }
+            out[i] = v;
+        }
+    }
+}
+
+// out[h,d] = (sum_s acc_s[d] 2^(m_s-M)) / (sum_s l_s 2^(m_s-M)), s ascending
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, uint16_t* __restrict__ out,
+                                                            int hd, int nsplit) {
+    const int h = blockIdx.x;
+    const float* ph = part + static_cast<int64_t>(h) * nsplit * (hd + 2);
+    float M = kNegBig;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ph[s * (hd + 2)]);
+    float Lsum = 0.0f;
+    for (int s = 0; s < nsplit; ++s) Lsum += ph[s * (hd + 2) + 1] * fast_exp2(ph[s * (hd + 2)] - M);
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float a = 0.0f;
+        for (int s = 0; s < nsplit; ++s) a += ph[s * (hd + 2) + 2 + d] * fast_exp2(ph[s * (hd + 2)] - M);
+        out[static_cast<int64_t>(h) * hd + d] = f32_to_f16_bits(a / Lsum);
+    }
+}
+
+// General shapes: one wave per query head, lanes over dims, online softmax.
+__global__ __launch_bounds__(64) void attn_simple_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                          const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+                                                          int rep, int S, int hd, int L, float scale_log2) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int kvh = h / rep;
+    const uint16_t* kb = kc + static_cast<int64_t>(kvh) * S * hd;
+    const uint16_t* vb = vc + static_cast<int64_t>(kvh) * S * hd;
+    const uint16_t* qh = q + static_cast<int64_t>(h) * hd;
+    constexpr int kMaxPer = 16;  // head_dim <= 1024
+    float accd[kMaxPer];
+    float qd[kMaxPer];
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int d = lane + 64 * i;
+        accd[i] = 0.0f;
+        qd[i] = d < hd ? f16_bits_to_f32(qh[d]) : 0.0f;
+    }
+    float m = kNegBig, l = 0.0f;
+    for (int t = 0; t < L; ++t) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int d = lane + 64 * i;
+            if (d < hd) part = fmaf(qd[i], f16_bits_to_f32(kb[static_cast<int64_t>(t) * hd + d]), part);
+        }
+        const float sc = wave_sum_bcast(part) * scale_log2;
+        const float mn = fmaxf(m, sc);
+        const float corr = fast_exp2(m - mn), p = fast_exp2(sc - mn);
+        l = fmaf(l, corr, p);
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int d = lane + 64 * i;
+            if (d < hd) accd[i] = fmaf(accd[i], corr, p * f16_bits_to_f32(vb[static_cast<int64_t>(t) * hd + d]));
+        }
+        m = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int d = lane + 64 * i;
+        if (d < hd) out[static_cast<int64_t>(h) * hd + d] = f32_to_f16_bits(accd[i] / l);
+    }
+}
+
+struct AttnPlan {
+    bool fast;
+    int lpr, rep_t, tps, nsplit;
+};
+
+static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
+    AttnPlan p{false, 0, 0, 0, 0};
+    const int64_t rep = NQ / NKV;
+    const int64_t lpr = hd / 8;
+    const bool pow2 = lpr >= 1 && (lpr & (lpr - 1)) == 0;
+    if (hd % 8 == 0 && pow2 && lpr <= 64 && rep <= 8) {
+        p.fast = true;
+        p.lpr = static_cast<int>(lpr);
+        p.rep_t = rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
+        const int64_t step = (kWave / lpr) * kAttnWaves;  // timesteps per workgroup iteration
+        // aim for ~256 workgroups over the whole KV cache
+        int64_t tps = ceil_div64(L * NKV, 256);
+        tps = ceil_div64(tps, step) * step;
+        if (tps < step) tps = step;
+        p.tps = static_cast<int>(tps);
+        p.nsplit = static_cast<int>(ceil_div64(L, tps));
+    }
+    return p;
+}
+
+}  // namespace soi
+
+using namespace soi;
+
+extern "C" size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len) {
+    if (NQ <= 0 || NKV <= 0 || head_dim <= 0 || cur_len <= 0 || NQ % NKV) return 0;
+    const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);
+    if (!p.fast) return 0;
+    return static_cast<size_t>(NQ) * p.nsplit * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                    uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim,
+                                    int64_t cur_len, float scale, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    const char* what = "soi_decode_attention";
+    SOI_REQUIRE(NQ >= 1 && NKV >= 1 && NQ % NKV == 0, "%s: num_q_heads must be a positive multiple of num_kv_heads",
+                what);
+    SOI_REQUIRE(head_dim >= 1 && head_dim <= 1024, "%s: head_dim must be in [1, 1024]", what);
+    SOI_REQUIRE(max_seq >= 1 && cur_len >= 1 && cur_len <= max_seq, "%s: cur_len out of range for max_seq_len", what);
+    SOI_REQUIRE(NQ <= 65535 && max_seq <= (int64_t(1) << 30), "%s: size out of range", what);
+    SOI_REQUIRE(q && k_cache && v_cache && out, "%s: null pointer", what);
+    hipStream_t st = as_stream(stream);
+    const float scale_log2 = scale * kLog2e;
+    const int rep = static_cast<int>(NQ / NKV);
+    const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);
+    const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
+    if (!p.fast || !aligned) {
+        hipLaunchKernelGGL(attn_simple_kernel, dim3(static_cast<unsigned>(NQ)), dim3(64), 0, st, q, k_cache, v_cache,
+                           out, rep, static_cast<int>(max_seq), static_cast<int>(head_dim),
+                           static_cast<int>(cur_len), scale_log2);
+        return launch_status(what);
+    }
+    const size_t need = static_cast<size_t>(NQ) * p.nsplit * (head_dim + 2) * sizeof(float);
+    if (!workspace || workspace_bytes < need) {
+        set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+        return SOI_ERR_WORKSPACE;
+    }
+    float* part = static_cast<float*>(workspace);
+    const dim3 grid(static_cast<unsigned>(NKV), static_cast<unsigned>(p.nsplit));
+    const int S = static_cast<int>(max_seq), L = static_cast<int>(cur_len);
+#define SOI_A(LL, RR)                                                                                              \
+    hipLaunchKernelGGL((attn_split_kernel<LL, RR>), grid, dim3(kAttnThreads), 0, st, q, k_cache, v_cache, part, rep, \
+                       S, L, p.tps, p.nsplit, scale_log2)
+#define SOI_AR(LL)                       \
+    switch (p.rep_t) {                   \
+        case 1: SOI_A(LL, 1); break;     \
+        case 2: SOI_A(LL, 2); break;     \
+        case 4: SOI_A(LL, 4); break;     \
+        default: SOI_A(LL, 8); break;    \
+    }
+    switch (p.lpr) {
+        case 1: SOI_AR(1); break;
+        case 2: SOI_AR(2); break;
+        case 4: SOI_AR(4); break;
+        case 8: SOI_AR(8); break;
+        case 16: SOI_AR(16); break;
+        case 32: SOI_AR(32); break;
+        default: SOI_AR(64); break;
+    }
+#undef SOI_AR
+#undef SOI_A
+    int s = launch_status(what);
+    if (s) return s;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(NQ)), dim3(128), 0, st, part, out,
+                       static_cast<int>(head_dim), p.nsplit);
+    return launch_status(what);
+}

@@ -1,0 +1,110 @@
+// Hot-channel cache descriptors and the device-resident row gather.
+//
+// build_dip_descriptors restates csrc/kernels/gemv_dip_fused.cu:17-42: for
+// each selected channel, its cache slot (top bit 0) or its position in the
+// miss list (top bit 1). The reference numbers misses with atomicAdd, so the
+// staging layout changes from run to run; here misses are numbered in
+// ascending j with an ordered ballot prefix scan in one workgroup, so the
+// staging layout is a pure function of the selection.
+#include "soi_device.h"
+#include "soi_host.h"
+
+namespace soi {
+
+constexpr int kDescThreads = 1024;
+constexpr int kDescWaves = kDescThreads / kWave;
+
+__global__ __launch_bounds__(kDescThreads) void build_dip_descriptors_kernel(
+    const int32_t* __restrict__ sel, int k, const int32_t* __restrict__ slot_of, int num_channels,
+    int32_t* __restrict__ desc, int32_t* __restrict__ miss_channels, int32_t* __restrict__ miss_count) {
+    __shared__ uint32_t s_cnt[2][kDescWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    uint32_t running = 0;
+    int parity = 0;
+    for (int b = 0; b < k; b += kDescThreads, parity ^= 1) {
+        const int j = b + tid;
+        int32_t ch = 0, slot = -1;
+        if (j < k) {
+            ch = sel[j];
+            slot = (ch >= 0 && ch < num_channels) ? slot_of[ch] : -1;
+        }
+        const bool miss = (j < k) && slot < 0;
+        const uint64_t m = ballot(miss);
+        if (lane == 0) s_cnt[parity][wave] = static_cast<uint32_t>(__builtin_popcountll(m));
+        __syncthreads();
+        uint32_t before = 0, blk = 0;
+#pragma unroll
+        for (int w = 0; w < kDescWaves; ++w) {
+            const uint32_t c = s_cnt[parity][w];
+            before += (w < wave) ? c : 0u;
+            blk += c;
+        }
+        if (j < k) {
+            if (miss) {
+                const uint32_t pos = running + before + mask_prefix(m);
+                miss_channels[pos] = ch;
+                desc[j] = static_cast<int32_t>(pos | 0x80000000u);
+            } else {
+                desc[j] = slot;
+            }
+        }
+        running += blk;
+    }
+    if (tid == 0) *miss_count = static_cast<int32_t>(running);
+}
+
+// dst[j,:] = src[idx[j],:]; 16-byte vector copies when rows allow it.
+template <bool VEC>
+__global__ __launch_bounds__(256) void gather_rows_device_kernel(const uint8_t* __restrict__ src, int64_t num_rows,
+                                                                  int64_t row_nbytes, const int32_t* __restrict__ idx,
+                                                                  int64_t k, uint8_t* __restrict__ dst) {
+    const int64_t j = blockIdx.x;
+    const int32_t r = idx[j];
+    const bool ok = r >= 0 && r < num_rows;
+    uint8_t* d = dst + j * row_nbytes;
+    const uint8_t* s = src + (ok ? static_cast<int64_t>(r) : 0) * row_nbytes;
+    if (VEC) {
+        const int64_t n16 = row_nbytes / 16;
+        for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) {
+            u32x4 v = ok ? reinterpret_cast<const u32x4*>(s)[i] : u32x4{0u, 0u, 0u, 0u};
+            reinterpret_cast<u32x4*>(d)[i] = v;
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < row_nbytes; i += blockDim.x) d[i] = ok ? s[i] : 0;
+    }
+}
+
+}  // namespace soi
+
+using namespace soi;
+
+extern "C" int soi_build_dip_descriptors(const int32_t* sel, int64_t k, const int32_t* slot_of, int64_t num_channels,
+                                         int32_t* desc, int32_t* miss_channels, int32_t* miss_count, void* stream) {
+    const char* what = "soi_build_dip_descriptors";
+    SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 30), "%s: k out of range", what);
+    SOI_REQUIRE(num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1, "%s: num_channels out of range", what);
+    SOI_REQUIRE(miss_count, "%s: null miss_count", what);
+    SOI_REQUIRE(k == 0 || (sel && desc && miss_channels), "%s: null pointer", what);
+    SOI_REQUIRE(num_channels == 0 || slot_of, "%s: null slot_of", what);
+    hipLaunchKernelGGL(build_dip_descriptors_kernel, dim3(1), dim3(kDescThreads), 0, as_stream(stream), sel,
+                       static_cast<int>(k), slot_of, static_cast<int>(num_channels), desc, miss_channels, miss_count);
+    return launch_status(what);
+}
+
+extern "C" int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
+                                      int64_t k, uint8_t* dst, void* stream) {
+    const char* what = "soi_gather_rows_device";
+    SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 31) - 1 && num_rows >= 0 && row_nbytes >= 0, "%s: size out of range",
+                what);
+    if (k == 0 || row_nbytes == 0) return SOI_OK;
+    SOI_REQUIRE(src && indices && dst, "%s: null pointer", what);
+    const bool vec = (row_nbytes % 16 == 0) && aligned16(src) && aligned16(dst);
+    hipStream_t st = as_stream(stream);
+    if (vec)
+        hipLaunchKernelGGL(gather_rows_device_kernel<true>, dim3(static_cast<unsigned>(k)), dim3(256), 0, st, src,
+                           num_rows, row_nbytes, indices, k, dst);
+    else
+        hipLaunchKernelGGL(gather_rows_device_kernel<false>, dim3(static_cast<unsigned>(k)), dim3(256), 0, st, src,
+                           num_rows, row_nbytes, indices, k, dst);
+    return launch_status(what);
+}

@@ -1,0 +1,151 @@
+// Device-side primitives shared by every soinfer HIP kernel (gfx950, wave64).
+//
+// Numeric conventions used throughout the library:
+//   * weights are symmetric integers (INT4 in [-8,7], INT8 in [-128,127]) with
+//     fp32 per-group scales; activations are IEEE binary16;
+//   * dequantisation produces EXACT small integers in binary16 (no rounding),
+//     products of two binary16 values are exact in binary32, and every sum is
+//     accumulated in binary32 in a fixed order, so every kernel is
+//     deterministic run to run;
+//   * the order of a reduction is part of a kernel's contract: kernels that
+//     must agree bit-for-bit (dense vs. descriptor-driven) share the same
+//     accumulation templates below.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace soi {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// ---------------------------------------------------------------------------
+// INT4 (AWQ nibble order) -> binary16, two methods with identical results.
+//
+// Word layout: nibble i (bits 4i..4i+3) of a little-endian uint32 holds
+// logical element AWQ[i] with AWQ = [0,2,4,6,1,3,5,7]; each nibble is a
+// two's-complement signed 4-bit value. Both methods return the four pairs
+// (v0,v1), (v2,v3), (v4,v5), (v6,v7) as packed binary16, i.e. consecutive
+// k elements, matching a contiguous load of x.
+// ---------------------------------------------------------------------------
+
+// Method "bitfield": IEEE-754 binary16 exponent-bias construction. A value u
+// in [0,15] placed in the low mantissa bits of 0x6400 (= 1024.0, where the
+// binary16 spacing is exactly 1) encodes 1024+u; placed in mantissa bits 4..7
+// it encodes 1024+16u. XOR 0x8 on each nibble maps a signed nibble n to
+// u = n+8 (offset binary). Then
+//   (1024+u)       - 1032       = n   (one packed add)
+//   (1024+16u)/16  - 72         = n   (one packed fma; /16 is exact)
+// All intermediate values are integers below 2048, hence exact in binary16.
+// The mask/xor/or step is one three-input bitwise op (v_bitop3_b32) per pair.
+__device__ __forceinline__ void dequant_int4x8_bitfield(uint32_t w, f16x2 out[4]) {
+    const uint32_t t = w ^ 0x88888888u;
+    const uint32_t t8 = t >> 8;
+    const uint32_t p0 = (t & 0x000f000fu) | 0x64006400u;   // nibbles 0,4 -> v0, v1
+    const uint32_t p1 = (t & 0x00f000f0u) | 0x64006400u;   // nibbles 1,5 -> v2, v3 (x16)
+    const uint32_t p2 = (t8 & 0x000f000fu) | 0x64006400u;  // nibbles 2,6 -> v4, v5
+    const uint32_t p3 = (t8 & 0x00f000f0u) | 0x64006400u;  // nibbles 3,7 -> v6, v7 (x16)
+    const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 bias16 = {(f16)-72.0f, (f16)-72.0f};
+    out[0] = as_f16x2(p0) + bias;
+    out[1] = __builtin_elementwise_fma(as_f16x2(p1), sixteenth, bias16);
+    out[2] = as_f16x2(p2) + bias;
+    out[3] = __builtin_elementwise_fma(as_f16x2(p3), sixteenth, bias16);
+}
+
+// Method "scalar": per-nibble signed bitfield extract and integer -> binary16
+// conversion (v_bfe_i32 + v_cvt_f16_i16). Slower; kept as the independent
+// second derivation of the same exact values.
+__device__ __forceinline__ void dequant_int4x8_scalar(uint32_t w, f16x2 out[4]) {
+    // nibble index holding logical element j
+    constexpr int nib[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int a = __builtin_amdgcn_sbfe(static_cast<int>(w), 4 * nib[2 * p], 4);
+        const int b = __builtin_amdgcn_sbfe(static_cast<int>(w), 4 * nib[2 * p + 1], 4);
+        out[p] = f16x2{static_cast<f16>(static_cast<int16_t>(a)), static_cast<f16>(static_cast<int16_t>(b))};
+    }
+}
+
+// INT8 -> binary16: four signed bytes b0..b3 of a word become (b0,b1),(b2,b3).
+// XOR 0x80 maps b to u = b+128; 0x6400|u encodes 1024+u exactly; subtracting
+// 1152 returns b exactly.
+__device__ __forceinline__ void dequant_int8x4(uint32_t w, f16x2 out[2]) {
+    const uint32_t t = w ^ 0x80808080u;
+    const uint32_t p0 = (t & 0xffu) | ((t & 0xff00u) << 8) | 0x64006400u;
+    const uint32_t p1 = ((t >> 16) & 0xffu) | ((t >> 8) & 0xff0000u) | 0x64006400u;
+    const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+    out[0] = as_f16x2(p0) + bias;
+    out[1] = as_f16x2(p1) + bias;
+}
+
+// a.x*b.x + a.y*b.y + c, products exact in binary32 (v_dot2c_f32_f16).
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions with DPP. Fixed order: within quads, then 8 lanes, then
+// 16-lane rows, then rows (1+0), (3+2), then (3+2)+(1+0). Result valid in
+// lane 63; wave_sum_bcast returns it to every lane.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf,
+                                                                 false));
+}
+
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp_f<0xb1>(v);        // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e>(v);        // quad_perm [2,3,0,1]
+    v += dpp_f<0x124>(v);       // row_ror:4
+    v += dpp_f<0x128>(v);       // row_ror:8  -> every lane holds its 16-lane row sum
+    v += dpp_f<0x142, 0xa>(v);  // row_bcast:15 into rows 1,3
+    v += dpp_f<0x143, 0xc>(v);  // row_bcast:31 into rows 2,3
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_lane63(v)), 63));
+}
+
+__device__ __forceinline__ float wave_max_bcast(float v) {
+    v = fmaxf(v, dpp_f<0xb1>(v));
+    v = fmaxf(v, dpp_f<0x4e>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    // cross-row: rows 1,3 take max with lane 15/47, then rows 2,3 with lane 31
+    {
+        float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                                        __builtin_bit_cast(int, v), 0x142, 0xa, 0xf,
+                                                                        false));
+        v = fmaxf(v, o);
+        o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                                  __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+        v = fmaxf(v, o);
+    }
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// number of set bits of a 64-bit wave mask strictly below this lane
+__device__ __forceinline__ uint32_t mask_prefix(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<f16>(v));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return static_cast<float>(__builtin_bit_cast(f16, b)); }
+
+}  // namespace soi

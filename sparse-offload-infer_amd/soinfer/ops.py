@@ -1,0 +1,113 @@
+"""Typed wrappers over soinfer._C, the MI355X hot-path operators.
+
+Names, arguments and return values follow the reference's python/soinfer/ops.py
+(gemv_w8a16 :92-96, gemv_w4a16_group{,_lop3} :99-109, topk_threshold_select
+:151-158, gather_rows_{staged,naive} :161-176, gemv_w4a16_sparse_accumulate
+:179-188, build_dip_descriptors :191-199, gemv_dip_fused_{up,down} :202-219,
+decode_attention :253-260). Validation errors surface as RuntimeError, as in
+the reference. Three operators have no reference counterpart: the
+index-driven sparse GEMVs over HBM-resident weights and the device row
+gather, which the resident DIP path uses instead of host gathers.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _C
+
+
+def gemv_w8a16(Wq: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, group_size: int) -> torch.Tensor:
+    """y = dequant(Wq, scale) @ x. Wq: [N, K] int8; scale: [N, num_groups] or [1, num_groups] fp32 (per-tensor
+    broadcast); x: [K] fp16. group_size: K for per-tensor/per-channel, else the quant group size."""
+    return _C.gemv_w8a16(Wq, scale, x, group_size)
+
+
+def gemv_w4a16_group(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, K: int,
+                     group_size: int) -> torch.Tensor:
+    """y = dequant(Wq_packed, scale) @ x. Wq_packed: [N, ceil(K/8)*4] uint8 AWQ-order INT4 (soinfer.quant.pack);
+    scale: [N, ceil(K/group_size)] fp32; group_size a positive multiple of 8. Per-nibble scalar dequant."""
+    return _C.gemv_w4a16_group(Wq_packed, scale, x, K, group_size)
+
+
+def gemv_w4a16_group_lop3(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, K: int,
+                          group_size: int) -> torch.Tensor:
+    """Same contract and bit-identical result as gemv_w4a16_group; dequantizes with three-input bitwise
+    binary16 construction (v_bitop3) instead of per-nibble conversion."""
+    return _C.gemv_w4a16_group_lop3(Wq_packed, scale, x, K, group_size)
+
+
+def topk_threshold_select(abs_g: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices (int32 [k], ascending) selected by the reference's threshold rule over abs_g (1-D fp32,
+    non-negative): tau from 24 fp32 bisection steps, then the first k indices with abs_g >= tau.
+    Deterministic: repeated calls return identical tensors."""
+    indices, _count = _C.topk_threshold_select(abs_g, k)
+    return indices
+
+
+def gather_rows_staged(matrix: torch.Tensor, indices: torch.Tensor, staging: torch.Tensor,
+                       gpu_dst: torch.Tensor) -> None:
+    """Copy the selected rows of `matrix` (pinned CPU uint8 [num_rows, row_nbytes]) into pinned `staging`
+    (>= k*row_nbytes) with host memcpy, then one async H2D copy into `gpu_dst` on the current stream.
+    indices: 1-D int64 CPU tensor (range-checked). Synchronize before reading gpu_dst."""
+    _C.gather_rows_staged(matrix, indices, staging, gpu_dst)
+
+
+def gather_rows_naive(matrix: torch.Tensor, indices: torch.Tensor, gpu_dst: torch.Tensor) -> None:
+    """One async H2D copy per selected row; same arguments and semantics as gather_rows_staged."""
+    _C.gather_rows_naive(matrix, indices, gpu_dst)
+
+
+def gemv_w4a16_sparse_accumulate(Wq_selected: torch.Tensor, scale_selected: torch.Tensor,
+                                 h_selected: torch.Tensor, H: int, group_size: int) -> torch.Tensor:
+    """y[H] = sum_i h_selected[i] * dequant(Wq_selected[i, :]) over k already-gathered rows of down_proj stored
+    transposed ([intermediate, hidden]). Deterministic split over rows with a fixed-order combine."""
+    return _C.gemv_w4a16_sparse_accumulate(Wq_selected, scale_selected, h_selected, H, group_size)
+
+
+def build_dip_descriptors(selected_indices: torch.Tensor, slot_of: torch.Tensor):
+    """(descriptors, miss_channels, miss_count) for the hot-channel cache: descriptor = cache slot, or miss
+    position | 1<<31. Misses are numbered in ascending selection order; only miss_channels[:miss_count] is
+    valid."""
+    return _C.build_dip_descriptors(selected_indices, slot_of)
+
+
+def gemv_dip_fused_up(cache_Wq: torch.Tensor, cache_scale: torch.Tensor, staging_Wq: torch.Tensor,
+                      staging_scale: torch.Tensor, descriptors: torch.Tensor, x: torch.Tensor, K: int,
+                      group_size: int) -> torch.Tensor:
+    """y[k] = selected rows @ x, each row read from the resident cache or the staging buffer per its
+    descriptor. Bit-identical to gemv_w4a16_group_lop3 on the same logical rows."""
+    return _C.gemv_dip_fused_up(cache_Wq, cache_scale, staging_Wq, staging_scale, descriptors, x, K, group_size)
+
+
+def gemv_dip_fused_down(cache_Wq: torch.Tensor, cache_scale: torch.Tensor, staging_Wq: torch.Tensor,
+                        staging_scale: torch.Tensor, descriptors: torch.Tensor, h_selected: torch.Tensor, H: int,
+                        group_size: int) -> torch.Tensor:
+    """Descriptor-driven form of gemv_w4a16_sparse_accumulate; bit-identical to it on the same logical rows."""
+    return _C.gemv_dip_fused_down(cache_Wq, cache_scale, staging_Wq, staging_scale, descriptors, h_selected, H,
+                                  group_size)
+
+
+def gemv_w4a16_indexed(Wq_packed: torch.Tensor, scale: torch.Tensor, idx: torch.Tensor, x: torch.Tensor, K: int,
+                       group_size: int) -> torch.Tensor:
+    """y[j] = row idx[j] of the HBM-resident INT4 matrix @ x (no gather). Bit-identical to
+    gemv_w4a16_group_lop3(Wq_packed[idx], scale[idx], x, K, group_size)."""
+    return _C.gemv_w4a16_indexed(Wq_packed, scale, idx, x, K, group_size)
+
+
+def gemv_w4a16_indexed_accumulate(Wq_T: torch.Tensor, scale_T: torch.Tensor, idx: torch.Tensor,
+                                  h_selected: torch.Tensor, H: int, group_size: int) -> torch.Tensor:
+    """y[H] = sum_j h_selected[j] * row idx[j] of the HBM-resident down_proj^T (no gather). Bit-identical to
+    gemv_w4a16_sparse_accumulate(Wq_T[idx], scale_T[idx], h_selected, H, group_size)."""
+    return _C.gemv_w4a16_indexed_accumulate(Wq_T, scale_T, idx, h_selected, H, group_size)
+
+
+def gather_rows_device(src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor) -> None:
+    """dst[j, :] = src[idx[j], :] for device-resident rows (int32 indices; out-of-range -> zero row)."""
+    _C.gather_rows_device(src, idx, dst)
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cur_len: int) -> torch.Tensor:
+    """out = attention(q, k_cache[:, :cur_len], v_cache[:, :cur_len]) for one query token. q: [NQ, hd] fp16
+    (already RoPE'd / QK-normed); caches: [NKV, max_seq_len, hd] fp16; NQ % NKV == 0 (query head h reads KV
+    head h // (NQ // NKV)); scale 1/sqrt(hd)."""
+    return _C.decode_attention(q, k_cache, v_cache, cur_len)

@@ -1,0 +1,74 @@
+"""Decode attention parity on the GPU (counterpart of tests/test_m5_kernels.py:157-213 in the reference).
+
+HIP split-KV attention vs the oracle's binary64 softmax attention on the same
+fp16 q / K / V, within the tolerance rule of tests/helpers.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops(cuda):
+    import soinfer.ops as ops
+
+    return ops
+
+
+def _qkv(NQ, NKV, hd, S, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(NQ, hd, generator=g).half()
+    k = torch.randn(NKV, S, hd, generator=g).half()
+    v = torch.randn(NKV, S, hd, generator=g).half()
+    return q, k, v
+
+
+@pytest.mark.parametrize("L", [1, 2, 17, 63, 64, 65, 300, 1000, 2047, 2048])
+def test_qwen_shape_matches_oracle(ops, L):
+    q, k, v = _qkv(16, 8, 128, 2048, seed=L)
+    ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), L)
+    out = ops.decode_attention(q.cuda(), k.cuda(), v.cuda(), L)
+    assert_close(out, ref, f"attention L={L}")
+
+
+@pytest.mark.parametrize("NQ,NKV,hd,S,L", [(4, 2, 16, 8, 5), (8, 8, 64, 100, 77), (32, 4, 128, 512, 300),
+                                          (16, 16, 256, 64, 64), (6, 3, 24, 40, 33), (2, 1, 100, 20, 20),
+                                          (12, 1, 128, 256, 200)])
+def test_other_shapes_match_oracle(ops, NQ, NKV, hd, S, L):
+    q, k, v = _qkv(NQ, NKV, hd, S, seed=NQ + hd + L)
+    ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), L)
+    out = ops.decode_attention(q.cuda(), k.cuda(), v.cuda(), L)
+    assert_close(out, ref, f"attention {NQ}/{NKV}/{hd} L={L}")
+
+
+def test_large_scores_stable(ops):
+    q, k, v = _qkv(16, 8, 128, 256, seed=3)
+    q = (q.float() * 8).half()
+    ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), 256)
+    out = ops.decode_attention(q.cuda(), k.cuda(), v.cuda(), 256)
+    assert_close(out, ref, "attention large scores")
+
+
+def test_deterministic(ops):
+    q, k, v = _qkv(16, 8, 128, 2048, seed=4)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    first = ops.decode_attention(qd, kd, vd, 2048)
+    for _ in range(5):
+        assert torch.equal(first, ops.decode_attention(qd, kd, vd, 2048))
+
+
+def test_rejections(ops):
+    q = torch.randn(15, 128, device="cuda").half()
+    k = torch.randn(8, 64, 128, device="cuda").half()
+    with pytest.raises(RuntimeError):
+        ops.decode_attention(q, k, k, 1)  # 15 query heads over 8 KV heads
+    q16 = torch.randn(16, 128, device="cuda").half()
+    with pytest.raises(RuntimeError):
+        ops.decode_attention(q16, k, k, 0)
+    with pytest.raises(RuntimeError):
+        ops.decode_attention(q16, k, k, 65)

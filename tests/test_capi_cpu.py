@@ -1,0 +1,86 @@
+"""The C-ABI library (libsoinfer_hip.so) loads on a machine without a GPU and exports every
+function include/soinfer_amd.h declares; argument checks return SOI_ERR_INVALID_ARGUMENT before
+any HIP call (so they are safe to exercise here); status strings and workspace queries are pure host code.
+"""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "soinfer_amd.h"
+LIB = REPO / "sparse-offload-infer_amd" / "soinfer" / "libsoinfer_hip.so"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch  # noqa: F401  (same HIP runtime as the product process)
+
+    assert LIB.exists(), "libsoinfer_hip.so not built: run __graft_entry__.build()"
+    return C.CDLL(str(LIB))
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(soi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for required in ("soi_gemv_w4a16_group", "soi_gemv_w4a16_group_lop3", "soi_gemv_w8a16",
+                     "soi_topk_threshold_select", "soi_gather_rows_staged", "soi_gather_rows_naive",
+                     "soi_gemv_w4a16_sparse_accumulate", "soi_build_dip_descriptors", "soi_gemv_dip_fused_up",
+                     "soi_gemv_dip_fused_down", "soi_decode_attention"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_status_strings_and_version(lib):
+    lib.soi_status_string.restype = C.c_char_p
+    lib.soi_version.restype = C.c_char_p
+    assert lib.soi_status_string(0) == b"success"
+    assert lib.soi_status_string(1) == b"invalid argument"
+    assert b"gfx950" in lib.soi_version()
+
+
+def test_argument_checks_return_before_launch(lib):
+    lib.soi_last_error.restype = C.c_char_p
+    i64 = C.c_int64
+    f = lib.soi_gemv_w4a16_group_lop3
+    f.argtypes = [C.c_void_p] * 4 + [i64] * 4 + [C.c_void_p]
+    # group_size 7 is rejected
+    assert f(None, None, None, None, 16, 256, 7, 2, None) == 1
+    assert b"group_size" in lib.soi_last_error()
+    # num_groups must be ceil(K/gs)
+    assert f(None, None, None, None, 16, 256, 128, 3, None) == 1
+    t = lib.soi_topk_threshold_select
+    t.argtypes = [C.c_void_p, i64, i64, C.c_void_p, C.c_void_p, C.c_void_p]
+    assert t(None, 100, 0, None, None, None) == 1  # k < 1
+    assert t(None, 100, 101, None, None, None) == 1  # k > n
+    a = lib.soi_decode_attention
+    a.argtypes = [C.c_void_p] * 4 + [i64] * 5 + [C.c_float, C.c_void_p, C.c_size_t, C.c_void_p]
+    assert a(None, None, None, None, 15, 8, 64, 128, 1, C.c_float(0.1), None, 0, None) == 1  # 15 % 8 != 0
+    g = lib.soi_gather_rows_naive
+    g.argtypes = [C.c_void_p, i64, i64, C.c_void_p, i64, C.c_void_p, C.c_void_p]
+    idx = (C.c_int64 * 2)(0, 5)
+    buf = (C.c_uint8 * 64)()
+    assert g(buf, 4, 8, idx, 2, buf, None) == 1  # index 5 out of range [0, 4)
+    assert b"out of range" in lib.soi_last_error()
+
+
+def test_workspace_queries(lib):
+    lib.soi_sparse_accumulate_workspace_bytes.restype = C.c_size_t
+    lib.soi_sparse_accumulate_workspace_bytes.argtypes = [C.c_int64, C.c_int64]
+    w = lib.soi_sparse_accumulate_workspace_bytes(2048, 3072)
+    assert w > 0 and w % (2048 * 4) == 0
+    assert lib.soi_sparse_accumulate_workspace_bytes(2048, 0) == 0
+    lib.soi_decode_attention_workspace_bytes.restype = C.c_size_t
+    lib.soi_decode_attention_workspace_bytes.argtypes = [C.c_int64] * 4
+    a = lib.soi_decode_attention_workspace_bytes(16, 8, 128, 2048)
+    assert a > 0 and a % (16 * 130 * 4) == 0

@@ -1,0 +1,158 @@
+"""INT4 / INT8 dequant-GEMV parity on the GPU (counterpart of the reference's tests/test_m4_kernels.py).
+
+HIP kernels vs. the CPU oracle's binary64 GEMV on identical packed bytes:
+  * basis vectors x = e_k give the binary16 rounding of the binary32 dequantized column, bit-exact;
+  * seeded random problems within the tolerance rule of tests/helpers.py (1e-3);
+  * gemv_w4a16_group (scalar nibble dequant) == gemv_w4a16_group_lop3 (bitfield dequant), bit-exact;
+  * unaligned / ragged shapes take the dword path and agree bit-exactly with the 16-byte path;
+  * the reference's argument checks raise RuntimeError.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, int4_problem
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+W4_FNS = ["gemv_w4a16_group", "gemv_w4a16_group_lop3"]
+
+
+@pytest.fixture(scope="module")
+def ops(cuda):
+    import soinfer.ops as ops
+
+    return ops
+
+
+@pytest.mark.parametrize("fn", W4_FNS)
+@pytest.mark.parametrize("K", [256, 4096])
+def test_w4_basis_vectors_exact(ops, fn, K):
+    p = int4_problem(16, K, 128, seed=2, std=3.0)
+    Wd = O.dequant_int4(p["Wq"], p["s"], p["K"], 128)  # binary32 fl(q*s)
+    expect = torch.from_numpy(Wd.astype(np.float16))
+    eye = torch.eye(K, dtype=torch.float16, device="cuda")
+    for k in range(0, K, 41):
+        y = getattr(ops, fn)(p["Wq_d"], p["s_d"], eye[k].contiguous(), K, 128)
+        assert torch.equal(y.cpu(), expect[:, k]), f"{fn} K={K} column {k}"
+
+
+SHAPES = [
+    (512, 4096, 128), (512, 4099, 128),  # reference test shapes (4099 pads to 4224)
+    (6144, 2048, 128), (2048, 6144, 128), (2048, 2048, 128), (1024, 2048, 128),  # Qwen3-1.7B
+    (37, 512, 32), (64, 256, 64), (33, 200, 8), (17, 1000, 40),  # non-32-multiple groups
+    (1, 8, 8), (3, 100, 16),  # tiny / unaligned rows
+]
+
+
+@pytest.mark.parametrize("N,K,gs", SHAPES)
+def test_w4_matches_oracle(ops, N, K, gs):
+    p = int4_problem(N, K, gs, seed=N + K + gs)
+    ref = O.gemv_w4_f64(p["Wq"], p["s"], p["x"], p["K"], gs)
+    a = ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], gs)
+    b = ops.gemv_w4a16_group(p["Wq_d"], p["s_d"], p["x_d"], p["K"], gs)
+    assert_close(a, ref, f"int4 {N}x{K} gs{gs}")
+    assert torch.equal(a, b), "scalar and bitfield dequant must agree bit for bit"
+
+
+def test_w4_unaligned_path_bit_identical(ops):
+    p = int4_problem(96, 2048, 128, seed=5)
+    y_vec = ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], 128)
+    # same bytes at a 4-byte (not 16-byte) aligned address, x likewise misaligned
+    wbuf = torch.empty(p["Wq_d"].numel() + 4, dtype=torch.uint8, device="cuda")
+    wv = wbuf[4:].view(96, -1)
+    wv.copy_(p["Wq_d"])
+    xbuf = torch.empty(p["K"] + 2, dtype=torch.float16, device="cuda")
+    xv = xbuf[2:]
+    xv.copy_(p["x_d"])
+    y_dw = ops.gemv_w4a16_group_lop3(wv, p["s_d"], xv, p["K"], 128)
+    assert torch.equal(y_vec, y_dw)
+
+
+def test_w4_deterministic(ops):
+    p = int4_problem(6144, 2048, 128, seed=8)
+    first = ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], 128)
+    for _ in range(5):
+        assert torch.equal(first, ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], 128))
+
+
+@pytest.mark.parametrize("fn", W4_FNS)
+def test_w4_rejects_bad_arguments(ops, fn):
+    p = int4_problem(4, 64, 32, seed=1)
+    f = getattr(ops, fn)
+    with pytest.raises(RuntimeError):
+        f(p["Wq_d"], p["s_d"], p["x_d"], 64, 7)  # group_size not a multiple of 8
+    with pytest.raises(RuntimeError):
+        f(p["Wq_d"], p["s_d"][:, :1].contiguous(), p["x_d"], 64, 32)  # too few groups
+    with pytest.raises(RuntimeError):
+        f(p["Wq_d"], p["s_d"], p["x_d"][:-8].contiguous(), 56, 32)  # Wq width != ceil(K/8)*4
+    with pytest.raises(RuntimeError):
+        f(p["Wq_d"].cpu(), p["s_d"], p["x_d"], 64, 32)  # not a device tensor
+    q65 = int4_problem(4, 65, 32, seed=2)  # ragged: 65 -> 96 padded, 3 groups
+    with pytest.raises(RuntimeError):
+        f(q65["Wq_d"], q65["s_d"][:, :2].contiguous(), q65["x_d"], q65["K"], 32)
+
+
+# ---------------------------------------------------------------------------
+# INT8
+# ---------------------------------------------------------------------------
+
+def _int8_problem(N, K, gran, gs, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * std).numpy()
+    if gran == "group":
+        q, s = O.quantize_group(w, gs, bits=8)
+        q = q[:, :K].copy()  # K is a multiple of gs in these cases
+    else:
+        q, s = O.quantize_simple(w, gran, bits=8)
+    x = torch.randn(K, generator=g).half()
+    return q, s, x
+
+
+W8 = [("per_tensor", None), ("per_channel", None), ("group", 128)]
+
+
+@pytest.mark.parametrize("gran,gs", W8)
+def test_w8_basis_vectors_exact(ops, gran, gs):
+    K = 256
+    q, s, _ = _int8_problem(16, K, gran, gs or K, seed=0, std=3.0)
+    gsize = gs or K
+    srep = np.broadcast_to(np.repeat(s, gsize, axis=1)[:, :K], (16, K)) if s.shape[1] > 1 else np.broadcast_to(s, (16, K))
+    expect = (q.astype(np.float32) * srep.astype(np.float32)).astype(np.float16)
+    Wq, sd = torch.from_numpy(q).cuda(), torch.from_numpy(np.ascontiguousarray(s)).cuda()
+    eye = torch.eye(K, dtype=torch.float16, device="cuda")
+    for k in range(0, K, 37):
+        y = ops.gemv_w8a16(Wq, sd, eye[k].contiguous(), gsize)
+        assert torch.equal(y.cpu(), torch.from_numpy(expect[:, k].copy())), f"{gran} column {k}"
+
+
+@pytest.mark.parametrize("gran,gs", W8 + [("group", 32), ("group", 4), ("group", 12)])
+@pytest.mark.parametrize("N,K", [(512, 4096), (6144, 2048), (2048, 6144), (1024, 2048), (7, 96)])
+def test_w8_matches_oracle(ops, gran, gs, N, K):
+    if gs and K % gs:
+        pytest.skip("K not a multiple of the group size in this grid")
+    q, s, x = _int8_problem(N, K, gran, gs or K, seed=N + K)
+    ref = O.gemv_w8_f64(q, s, x.numpy(), gs or K)
+    y = ops.gemv_w8a16(torch.from_numpy(q).cuda(), torch.from_numpy(np.ascontiguousarray(s)).cuda(), x.cuda(), gs or K)
+    assert_close(y, ref, f"int8 {gran} {N}x{K}")
+
+
+def test_w8_ragged_k_path(ops):
+    q, s, x = _int8_problem(9, 101, "per_channel", 101, seed=3)
+    ref = O.gemv_w8_f64(q, s, x.numpy(), 101)
+    y = ops.gemv_w8a16(torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), x.cuda(), 101)
+    assert_close(y, ref, "int8 ragged")
+
+
+def test_w8_rejects_bad_arguments(ops):
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(4, 64, generator=g).numpy()
+    q, s = O.quantize_group(w, 16, bits=8)
+    Wq, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+    x = torch.randn(64, generator=g).half().cuda()
+    with pytest.raises(RuntimeError):
+        ops.gemv_w8a16(Wq, sd[:, :3].contiguous(), x, 16)  # too few groups
+    q3, s3 = O.quantize_group(w, 3, bits=8)  # num_groups > 1 with gs not a multiple of 4
+    with pytest.raises(RuntimeError):
+        ops.gemv_w8a16(torch.from_numpy(q3[:, :64].copy()).cuda(), torch.from_numpy(s3[:, :22].copy()).cuda(), x, 3)
