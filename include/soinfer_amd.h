@@ -61,6 +61,18 @@ int soi_gemv_w4a16_group(const uint8_t* Wq, const float* scale, const uint16_t* 
 int soi_gemv_w4a16_group_lop3(const uint8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N,
                               int64_t K, int64_t group_size, int64_t num_groups, void* stream);
 
+/* Batched form: P independent problems of one shape in ONE launch.
+ * Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs are DEVICE arrays of P device pointers
+ * (problem p: Wq [N, ceil(K/8)*4], scale [N, num_groups], x [K], y [N]).
+ * The pointer table is trusted (the caller validated the buffers); a problem
+ * whose pointers are null, or not 16-byte aligned when K % 32 == 0, is
+ * skipped. Each y is bit-identical to soi_gemv_w4a16_group_lop3 on that
+ * problem. No reference counterpart: amortises the ~2.6 us per-launch latency
+ * floor of MI355X over many GEMVs (the reference launches one per matrix). */
+int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
+                           const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t P, int64_t N, int64_t K,
+                           int64_t group_size, int64_t num_groups, void* stream);
+
 /* --------------------------------------------------------------------------
  * INT8 GEMV, y[N] = sum_k scale[n*scale_row_stride + k/group_size] * Wq[n,k] * x[k].
  * Wq: int8 [N, K]; scale: fp32 [N or 1, num_groups]; scale_row_stride is 0

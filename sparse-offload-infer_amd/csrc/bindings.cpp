@@ -140,6 +140,28 @@ torch::Tensor gemv_w4a16_group_lop3(torch::Tensor Wq_packed, torch::Tensor scale
                                  soi_gemv_w4a16_group_lop3);
 }
 
+// P same-shape INT4 GEMVs in one launch; pointer tables are int64 device tensors
+// of data pointers built (and validated) by soinfer.ops.GemvBatch.
+void gemv_w4a16_batched(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::Tensor x_ptrs, torch::Tensor y_ptrs,
+                        int64_t N, int64_t K, int64_t group_size) {
+    const char* name = "gemv_w4a16_batched";
+    for (const auto* t : {&Wq_ptrs, &scale_ptrs, &x_ptrs, &y_ptrs}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kInt64 && t->dim() == 1 && t->is_contiguous(), name,
+                    ": pointer tables must be contiguous 1D int64 CUDA tensors");
+        TORCH_CHECK(t->size(0) == Wq_ptrs.size(0), name, ": pointer tables must have the same length");
+        check_same_device(Wq_ptrs, *t, name);
+    }
+    TORCH_CHECK(group_size >= 1 && group_size % 8 == 0, name, ": group_size must be a positive multiple of 8");
+    const at::DeviceGuard guard(Wq_ptrs.device());
+    check_status(soi_gemv_w4a16_batched(reinterpret_cast<const uint8_t* const*>(Wq_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const float* const*>(scale_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const uint16_t* const*>(x_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<uint16_t* const*>(y_ptrs.data_ptr<int64_t>()),
+                                        Wq_ptrs.size(0), N, K, group_size, expected_num_groups(K, group_size),
+                                        cur_stream(Wq_ptrs)),
+                 name);
+}
+
 // ---------------------------------------------------------------------------
 // sparse down accumulate
 // ---------------------------------------------------------------------------
@@ -468,6 +490,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
     m.def("gemv_w4a16_group", &gemv_w4a16_group, "INT4 group GEMV (scalar nibble dequant)");
     m.def("gemv_w4a16_group_lop3", &gemv_w4a16_group_lop3, "INT4 group GEMV (bitfield dequant)");
+    m.def("gemv_w4a16_batched", &gemv_w4a16_batched, "P same-shape INT4 GEMVs in one launch");
     m.def("gemv_w4a16_sparse_accumulate", &gemv_w4a16_sparse_accumulate, "sparse down-proj accumulate");
     m.def("build_dip_descriptors", &build_dip_descriptors, "hot-cache descriptors");
     m.def("gemv_dip_fused_up", &gemv_dip_fused_up, "descriptor-driven up GEMV");

@@ -77,12 +77,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const uint16_t
 
     const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * S * HD;
     const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * S * HD;
-    for (int tb = t0 + wave * RPI; tb < t1; tb += kAttnWaves * RPI) {
-        const int t = tb + g;
-        const bool valid = t < t1;
-        const int tl = valid ? t : t1 - 1;
-        const u32x4 kk = reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(tl) * HD)[u];
-        const u32x4 vv = reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(tl) * HD)[u];
+    // Software pipeline: the next iteration's K/V rows are requested before the
+    // current ones are consumed. Rows past the range are clamped to the last
+    // valid row (always a legal address) and masked out of the softmax.
+    auto load_kv = [&](int tb_, u32x4& kk_, u32x4& vv_) {
+        const int t = tb_ + g;
+        const int tl = t < t1 ? t : t1 - 1;
+        kk_ = reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(tl) * HD)[u];
+        vv_ = reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(tl) * HD)[u];
+    };
+    u32x4 kk, vv;
+    int tb = t0 + wave * RPI;
+    load_kv(tb, kk, vv);
+    for (; tb < t1; tb += kAttnWaves * RPI) {
+        u32x4 kn, vn;
+        load_kv(tb + kAttnWaves * RPI, kn, vn);
+        const bool valid = tb + g < t1;
         const f16x2 k0 = as_f16x2(kk.x), k1 = as_f16x2(kk.y), k2 = as_f16x2(kk.z), k3 = as_f16x2(kk.w);
         const f16x2 v2[4] = {as_f16x2(vv.x), as_f16x2(vv.y), as_f16x2(vv.z), as_f16x2(vv.w)};
 #pragma unroll
@@ -105,6 +115,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const uint16_t
             }
             m[hh] = mn;
         }
+        kk = kn;
+        vv = vn;
     }
 
     // merge lane groups (same u, different timesteps) inside the wave

@@ -23,33 +23,33 @@
 
 namespace soi {
 
-template <bool VEC>
-__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int K, int k0, f16x2 xv[16]) {
-    if (VEC && k0 + 32 <= K) {
-        const u32x4* xp = reinterpret_cast<const u32x4*>(x + k0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 t = xp[i];
-            xv[4 * i + 0] = as_f16x2(t.x);
-            xv[4 * i + 1] = as_f16x2(t.y);
-            xv[4 * i + 2] = as_f16x2(t.z);
-            xv[4 * i + 3] = as_f16x2(t.w);
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int ka = k0 + 2 * e, kb = ka + 1;
-            const uint32_t lo = (ka < K) ? x[ka] : 0u;
-            const uint32_t hi = (kb < K) ? x[kb] : 0u;
-            xv[e] = as_f16x2(lo | (hi << 16));
-        }
-    }
+template <bool BITFIELD>
+__device__ __forceinline__ void nibble_pairs(uint32_t w, f16x2 lo[2], f16x2 hi[2]) {
+    if (BITFIELD)
+        int4x8_subnormal_bitfield(w, lo, hi);
+    else
+        int4x8_subnormal_scalar(w, lo, hi);
 }
 
-template <bool VEC>
-__device__ __forceinline__ void load_w_chunk(const uint8_t* __restrict__ row, int words, int c, uint32_t wv[4]) {
+// sum q*x of one word's 8 values from its subnormal pairs and sum(x) (see soi_device.h)
+constexpr float kTwo24 = 16777216.0f;
+constexpr float kTwo20 = 1048576.0f;
+
+// Loads are unconditional and go through the global address space. With FULL
+// (every row exists and every lane of every pass has a chunk: N % R == 0 and
+// chunks % 64 == 0, true for all Qwen3 shapes) there are no guards at all:
+// row pointers stay wave-uniform (SGPR base + lane offset). Otherwise a lane
+// or row with nothing to read loads from g_zero16 instead (address select, no
+// branch), contributing exact zeros.
+
+template <bool VEC, bool FULL>
+__device__ __forceinline__ void load_w_chunk(const uint8_t* __restrict__ row, bool ok, int words, int c,
+                                             uint32_t wv[4]) {
+    const uint32_t* z = g_zero16;
     if (VEC) {
-        const u32x4 t = reinterpret_cast<const u32x4*>(row)[c];
+        const u32x4* p = reinterpret_cast<const u32x4*>(row) + c;
+        if (!FULL) p = ok ? p : reinterpret_cast<const u32x4*>(z);
+        const u32x4 t = ldg(p);
         wv[0] = t.x;
         wv[1] = t.y;
         wv[2] = t.z;
@@ -59,134 +59,295 @@ __device__ __forceinline__ void load_w_chunk(const uint8_t* __restrict__ row, in
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int wi = 4 * c + i;
-            wv[i] = (wi < words) ? rw[wi] : 0u;
+            wv[i] = ldg((ok && wi < words) ? rw + wi : z);
         }
     }
 }
 
-template <bool BITFIELD>
-__device__ __forceinline__ void dequant8(uint32_t w, f16x2 q[4]) {
-    if (BITFIELD)
-        dequant_int4x8_bitfield(w, q);
-    else
-        dequant_int4x8_scalar(w, q);
+template <bool VEC, bool FULL>
+__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int K, int c, bool cv, f16x2 xv[16]) {
+    const int k0 = 32 * c;
+    if (VEC) {  // K % 32 == 0: a valid chunk is fully inside x
+        const u32x4* z = reinterpret_cast<const u32x4*>(g_zero16);
+        const u32x4* xp = reinterpret_cast<const u32x4*>(x + k0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 t = ldg(FULL ? xp + i : (cv ? xp + i : z));
+            xv[4 * i + 0] = as_f16x2(t.x);
+            xv[4 * i + 1] = as_f16x2(t.y);
+            xv[4 * i + 2] = as_f16x2(t.z);
+            xv[4 * i + 3] = as_f16x2(t.w);
+        }
+    } else {
+        const uint16_t* z = reinterpret_cast<const uint16_t*>(g_zero16);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int ka = k0 + 2 * e, kb = ka + 1;
+            const uint32_t lo = ldg((cv && ka < K) ? x + ka : z);
+            const uint32_t hi = ldg((cv && kb < K) ? x + kb : z);
+            xv[e] = as_f16x2(lo | (hi << 16));
+        }
+    }
 }
 
-template <int R, bool VEC, bool CHUNK_SCALE, bool BITFIELD, class Rows>
-__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x,
-                                                       uint16_t* __restrict__ y, int K, int gs) {
+// R rows per wave; PU passes (64 chunks each) loaded per batch, so a wave has
+// R*PU 1 KB row segments in flight before it does any arithmetic.
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows>
+__device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, const uint16_t* __restrict__ x,
+                                               uint16_t* __restrict__ y, int K, int gs, int64_t row0) {
+    constexpr int SC = CHUNK_SCALE ? 1 : 4;
     const int lane = threadIdx.x;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
     const int words = (K + 7) >> 3;
     const int chunks = (words + 3) >> 2;
 
     RowRef ref[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) ref[r] = (row0 + r < N) ? rows.get(row0 + r) : RowRef{nullptr, nullptr, false};
+    for (int r = 0; r < R; ++r) {
+        if (FULL) {
+            ref[r] = rows.get(row0 + r);
+        } else {
+            const bool in = row0 + r < N;
+            ref[r] = rows.get(in ? row0 + r : N - 1);
+            if (!in) ref[r].ok = false;
+        }
+    }
+    bool valid[R];  // row exists and resolved (else y untouched / NaN)
+#pragma unroll
+    for (int r = 0; r < R; ++r) valid[r] = ref[r].ok;
+    if (FULL) {
+        // an unresolvable row reads row 0 of the batch instead (wave-uniform select) and is written as NaN
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (!valid[r]) {
+                ref[r].w = ref[0].ok ? ref[0].w : reinterpret_cast<const uint8_t*>(x);
+                ref[r].s = ref[0].ok ? ref[0].s : reinterpret_cast<const float*>(x);
+            }
+        }
+    }
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int c0 = 0; c0 < chunks; c0 += kWave) {
-        const int c = c0 + lane;
-        if (c < chunks) {
-            uint32_t wv[R][4];
+    for (int c0 = 0; c0 < chunks; c0 += kWave * PU) {
+        uint32_t wv[PU][R][4];
+        float sc[PU][R][SC];
+        f16x2 xv[PU][16];
+        float xs[PU][SC];  // sum of x over the chunk (or over each word)
+#pragma unroll
+        for (int p = 0; p < PU; ++p) {
+            const int c = c0 + p * kWave + lane;
+            const bool cv = FULL || c < chunks;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (ref[r].ok) {
-                    load_w_chunk<VEC>(ref[r].w, words, c, wv[r]);
-                } else {
-                    wv[r][0] = wv[r][1] = wv[r][2] = wv[r][3] = 0u;
-                }
-            }
-            const int k0 = 32 * c;
-            float sc[R][CHUNK_SCALE ? 1 : 4];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
+                const bool ok = FULL || (valid[r] && cv);
+                load_w_chunk<VEC, FULL>(ref[r].w, ok, words, c, wv[p][r]);
+                const float* zf = reinterpret_cast<const float*>(g_zero16);
                 if (CHUNK_SCALE) {
-                    sc[r][0] = ref[r].ok ? ref[r].s[k0 / gs] : 0.0f;
+                    sc[p][r][0] = ldg(ok ? ref[r].s + (32 * c) / gs : zf);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < (CHUNK_SCALE ? 1 : 4); ++i) {
+                    for (int i = 0; i < SC; ++i) {
                         const int wi = 4 * c + i;
-                        sc[r][i] = (ref[r].ok && wi < words) ? ref[r].s[(8 * wi) / gs] : 0.0f;
+                        sc[p][r][i] = ldg((ok && wi < words) ? ref[r].s + (8 * wi) / gs : zf);
                     }
                 }
             }
-            f16x2 xv[16];
-            load_x_chunk<VEC>(x, K, k0, xv);
+            load_x_chunk<VEC, FULL>(x, K, c, cv, xv[p]);
+            const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+            for (int i = 0; i < SC; ++i) {
+                float t = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16 / SC; ++e) t = dot2(xv[p][(16 / SC) * i + e], ones, t);
+                xs[p][i] = t;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PU; ++p) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 if (CHUNK_SCALE) {
-                    float t = 0.0f;
+                    float ta = 0.0f, tb = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        f16x2 q[4];
-                        dequant8<BITFIELD>(wv[r][i], q);
-#pragma unroll
-                        for (int p = 0; p < 4; ++p) t = dot2(q[p], xv[4 * i + p], t);
+                        f16x2 lo[2], hi[2];
+                        nibble_pairs<BITFIELD>(wv[p][r][i], lo, hi);
+                        ta = dot2(lo[0], xv[p][4 * i + 0], ta);
+                        tb = dot2(hi[0], xv[p][4 * i + 1], tb);
+                        ta = dot2(lo[1], xv[p][4 * i + 2], ta);
+                        tb = dot2(hi[1], xv[p][4 * i + 3], tb);
                     }
-                    acc[r] = fmaf(sc[r][0], t, acc[r]);
+                    const float v = fmaf(ta, kTwo24, fmaf(tb, kTwo20, -8.0f * xs[p][0]));
+                    acc[r] = fmaf(sc[p][r][0], v, acc[r]);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < (CHUNK_SCALE ? 1 : 4); ++i) {
-                        f16x2 q[4];
-                        dequant8<BITFIELD>(wv[r][i], q);
-                        float t = 0.0f;
-#pragma unroll
-                        for (int p = 0; p < 4; ++p) t = dot2(q[p], xv[4 * i + p], t);
-                        acc[r] = fmaf(sc[r][i], t, acc[r]);
+                    for (int i = 0; i < SC; ++i) {
+                        f16x2 lo[2], hi[2];
+                        nibble_pairs<BITFIELD>(wv[p][r][i], lo, hi);
+                        float ta = dot2(lo[0], xv[p][4 * i + 0], 0.0f);
+                        float tb = dot2(hi[0], xv[p][4 * i + 1], 0.0f);
+                        ta = dot2(lo[1], xv[p][4 * i + 2], ta);
+                        tb = dot2(hi[1], xv[p][4 * i + 3], tb);
+                        const float v = fmaf(ta, kTwo24, fmaf(tb, kTwo20, -8.0f * xs[p][i]));
+                        acc[r] = fmaf(sc[p][r][i], v, acc[r]);
                     }
                 }
             }
         }
     }
 
+    const float total = reduce_rows<R>(acc);
+    const int r = reduce_rows_row<R>(static_cast<uint32_t>(lane));
+    bool vr = valid[0];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float total = wave_sum_lane63(acc[r]);
-        if (lane == 63 && row0 + r < N) y[row0 + r] = ref[r].ok ? f32_to_f16_bits(total) : uint16_t(0x7e00u);
-    }
+    for (int i = 1; i < R; ++i) vr = (r == i) ? valid[i] : vr;
+    if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N))
+        stg(y + row0 + r, vr ? f32_to_f16_bits(total) : uint16_t(0x7e00u));
+}
+
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows>
+__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x,
+                                                       uint16_t* __restrict__ y, int K, int gs) {
+    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, x, y, K, gs,
+                                                           static_cast<int64_t>(blockIdx.x) * R);
+}
+
+// Batched form: P independent problems of one shape [N, K]; workgroup b takes
+// row tile b % tiles of problem b / tiles. Pointer tables live in device
+// memory; a problem whose pointers are not 16-byte aligned (when the vector
+// path is compiled in) or null writes nothing.
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* const* __restrict__ Wp,
+                                                               const float* const* __restrict__ Sp,
+                                                               const uint16_t* const* __restrict__ Xp,
+                                                               uint16_t* const* __restrict__ Yp, int64_t N, int K,
+                                                               int gs, int G, int tiles) {
+    const int p = blockIdx.x / tiles;
+    const int tile = blockIdx.x - p * tiles;
+    const uint8_t* W = ldg(Wp + p);
+    const float* S = ldg(Sp + p);
+    const uint16_t* x = ldg(Xp + p);
+    uint16_t* y = ldg(Yp + p);
+    const uintptr_t bad = reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x);
+    if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
+    const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
+    DenseRows rows{W, S, row_bytes, G};
+    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, x, y, K, gs, static_cast<int64_t>(tile) * R);
 }
 
 // ---------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------
 
-// Rows per wave: keep >= ~1024 waves in flight (4 per CU on 256 CUs) while
-// giving each wave as many independent 1 KB row loads as that allows.
-static int pick_rows_per_wave(int64_t N) {
-    if (N >= 8 * 1024) return 8;
-    if (N >= 4 * 1024) return 4;
-    if (N >= 2 * 1024) return 2;
-    return 1;
+struct Int4Plan {
+    int R, PU;
+};
+
+// PU: passes per batch (all of them up to 4); R: rows per wave, so that a
+// wave has R*PU <= 8 row segments in flight and the grid keeps >= ~1024 waves.
+static Int4Plan plan_int4(int64_t N, int64_t K, bool vec) {
+    const int64_t chunks = ceil_div64(ceil_div64(K, 8), 4);
+    const int64_t passes = ceil_div64(chunks, kWave);
+    Int4Plan p{1, 1};
+    p.PU = vec ? static_cast<int>(passes < 4 ? passes : 4) : 1;
+    if (p.PU == 3 && passes > 3) p.PU = 4;
+    int R = N >= 8 * 1024 ? 8 : N >= 4 * 1024 ? 4 : N >= 2 * 1024 ? 2 : 1;
+    while (R * p.PU > 8) R >>= 1;
+    p.R = R < 1 ? 1 : R;
+    return p;
 }
 
 template <bool BITFIELD, class Rows>
 static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, uint16_t* y, int64_t K, int64_t gs, bool vec,
                        hipStream_t st, const char* what) {
     if (N == 0) return SOI_OK;
-    const int R = pick_rows_per_wave(N);
-    const bool chunk_scale = (gs % 32) == 0;
-    const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
+    const Int4Plan pl = plan_int4(N, K, vec);
+    const bool cs = (gs % 32) == 0;
+    const bool full = vec && cs && (N % pl.R == 0) && ((K / 32) % (64 * pl.PU) == 0);
+    const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
     const int Ki = static_cast<int>(K), gi = static_cast<int>(gs);
-#define SOI_L(RR, V, CS) \
-    hipLaunchKernelGGL((gemv_int4_kernel<RR, V, CS, BITFIELD, Rows>), grid, dim3(64), 0, st, rows, N, x, y, Ki, gi)
-#define SOI_LR(V, CS)          \
-    switch (R) {               \
-        case 8: SOI_L(8, V, CS); break; \
-        case 4: SOI_L(4, V, CS); break; \
-        case 2: SOI_L(2, V, CS); break; \
-        default: SOI_L(1, V, CS); break; \
-    }
+#define SOI_L(RR, PP, V, CS, FL) \
+    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows>), grid, dim3(64), 0, st, rows, N, x, y, Ki, gi)
+#define SOI_CS(RR, PP, V)                    \
+    if (V && full) SOI_L(RR, PP, V, true, true); \
+    else if (cs) SOI_L(RR, PP, V, true, false);  \
+    else SOI_L(RR, PP, V, false, false)
+    const int key = pl.R * 10 + pl.PU;
     if (vec) {
-        if (chunk_scale) { SOI_LR(true, true) } else { SOI_LR(true, false) }
+        switch (key) {
+            case 81: SOI_CS(8, 1, true); break;
+            case 41: SOI_CS(4, 1, true); break;
+            case 21: SOI_CS(2, 1, true); break;
+            case 11: SOI_CS(1, 1, true); break;
+            case 42: SOI_CS(4, 2, true); break;
+            case 22: SOI_CS(2, 2, true); break;
+            case 12: SOI_CS(1, 2, true); break;
+            case 23: SOI_CS(2, 3, true); break;
+            case 13: SOI_CS(1, 3, true); break;
+            case 24: SOI_CS(2, 4, true); break;
+            default: SOI_CS(1, 4, true); break;
+        }
     } else {
-        if (chunk_scale) { SOI_LR(false, true) } else { SOI_LR(false, false) }
+        switch (pl.R) {
+            case 8: SOI_CS(8, 1, false); break;
+            case 4: SOI_CS(4, 1, false); break;
+            case 2: SOI_CS(2, 1, false); break;
+            default: SOI_CS(1, 1, false); break;
+        }
     }
-#undef SOI_LR
+#undef SOI_CS
 #undef SOI_L
+    return launch_status(what);
+}
+
+static int launch_int4_batched(const uint8_t* const* Wp, const float* const* Sp, const uint16_t* const* Xp,
+                               uint16_t* const* Yp, int64_t P, int64_t N, int64_t K, int64_t gs, int64_t G,
+                               hipStream_t st, const char* what) {
+    const bool vec = (K % 32) == 0;
+    Int4Plan pl = plan_int4(N * P, K, vec);  // rows per wave chosen on the total row count
+    if (P > 1) {  // throughput regime: one pass per batch, 8 rows per wave (measured best when streaming)
+        pl.PU = 1;
+        pl.R = (N * P >= 8 * 1024) ? 8 : pl.R;
+    }
+    const int64_t tiles = ceil_div64(N, pl.R);
+    SOI_REQUIRE(tiles * P <= (int64_t(1) << 31) - 1, "%s: too many row tiles", what);
+    const bool cs = (gs % 32) == 0;
+    const bool full = vec && cs && (N % pl.R == 0) && ((K / 32) % (64 * pl.PU) == 0);
+    const dim3 grid(static_cast<unsigned>(tiles * P));
+    const int Ki = static_cast<int>(K), gi = static_cast<int>(gs), Gi = static_cast<int>(G), ti = static_cast<int>(tiles);
+#define SOI_B(RR, PP, V, CS, FL)                                                                             \
+    hipLaunchKernelGGL((gemv_int4_batched_kernel<RR, PP, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, N, Ki, \
+                       gi, Gi, ti)
+#define SOI_BCS(RR, PP, V)                        \
+    if (V && full) SOI_B(RR, PP, V, true, true);  \
+    else if (cs) SOI_B(RR, PP, V, true, false);   \
+    else SOI_B(RR, PP, V, false, false)
+    const int key = pl.R * 10 + pl.PU;
+    if (vec) {
+        switch (key) {
+            case 81: SOI_BCS(8, 1, true); break;
+            case 41: SOI_BCS(4, 1, true); break;
+            case 21: SOI_BCS(2, 1, true); break;
+            case 11: SOI_BCS(1, 1, true); break;
+            case 42: SOI_BCS(4, 2, true); break;
+            case 22: SOI_BCS(2, 2, true); break;
+            case 12: SOI_BCS(1, 2, true); break;
+            case 23: SOI_BCS(2, 3, true); break;
+            case 13: SOI_BCS(1, 3, true); break;
+            case 24: SOI_BCS(2, 4, true); break;
+            default: SOI_BCS(1, 4, true); break;
+        }
+    } else {
+        switch (pl.R) {
+            case 8: SOI_BCS(8, 1, false); break;
+            case 4: SOI_BCS(4, 1, false); break;
+            case 2: SOI_BCS(2, 1, false); break;
+            default: SOI_BCS(1, 1, false); break;
+        }
+    }
+#undef SOI_BCS
+#undef SOI_B
     return launch_status(what);
 }
 
@@ -208,7 +369,7 @@ static int dense_int4(const uint8_t* Wq, const float* scale, const uint16_t* x, 
     if (N == 0) return SOI_OK;
     SOI_REQUIRE(Wq && scale && x && y, "%s: null pointer", what);
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
-    const bool vec = (row_bytes % 16 == 0) && aligned16(Wq) && aligned16(x);
+    const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
     DenseRows rows{Wq, scale, row_bytes, G};
     return launch_int4<BITFIELD>(rows, N, x, y, K, gs, vec, as_stream(stream), what);
 }
@@ -239,7 +400,7 @@ extern "C" int soi_gemv_dip_fused_up(const uint8_t* cache_Wq, const float* cache
     if (k == 0) return SOI_OK;
     SOI_REQUIRE(desc && x && y, "%s: null pointer", what);
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
-    const bool vec = (row_bytes % 16 == 0) && aligned16(x) && (cache_rows == 0 || aligned16(cache_Wq)) &&
+    const bool vec = (K % 32 == 0) && aligned16(x) && (cache_rows == 0 || aligned16(cache_Wq)) &&
                      (staging_rows == 0 || aligned16(staging_Wq));
     DescRows rows{cache_Wq, cache_scale, cache_rows, staging_Wq, staging_scale, staging_rows, desc, row_bytes,
                   num_groups};
@@ -256,7 +417,20 @@ extern "C" int soi_gemv_w4a16_indexed(const uint8_t* Wq, const float* scale, int
     if (k == 0) return SOI_OK;
     SOI_REQUIRE(Wq && scale && idx && x && y, "%s: null pointer", what);
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
-    const bool vec = (row_bytes % 16 == 0) && aligned16(Wq) && aligned16(x);
+    const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
     IndexRows rows{Wq, scale, num_rows, idx, row_bytes, num_groups};
     return launch_int4<true>(rows, k, x, y, K, group_size, vec, as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
+                                      const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t P, int64_t N,
+                                      int64_t K, int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_w4a16_batched";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(P >= 0 && N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: P or N out of range", what);
+    if (P == 0 || N == 0) return SOI_OK;
+    SOI_REQUIRE(Wq_ptrs && scale_ptrs && x_ptrs && y_ptrs, "%s: null pointer table", what);
+    return launch_int4_batched(Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs, P, N, K, group_size, num_groups,
+                               as_stream(stream), what);
 }

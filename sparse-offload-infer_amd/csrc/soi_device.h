@@ -23,6 +23,32 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// 16 zero bytes: the load target of lanes / rows that have nothing to read,
+// so loads can be issued unconditionally (no branch, no serialising wait)
+// and contribute exact zeros.
+// (Never written; one private copy per code object.)
+__device__ uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
+
+// Loads through the global address space (global_load_*, not flat_load_*):
+// pointers read from memory or chosen by a select lose the address-space
+// information the compiler needs, so the kernels cast explicitly.
+template <class T>
+__device__ __forceinline__ T ldg(const T* p) {
+    typedef const __attribute__((address_space(1))) T gT;
+    return *(gT*)(p);
+}
+template <class T>
+__device__ __forceinline__ void stg(T* p, T v) {
+    typedef __attribute__((address_space(1))) T gT;
+    *(gT*)(p) = v;
+}
+// Same, marked non-temporal (streamed once: weights).
+template <class T>
+__device__ __forceinline__ T ldg_stream(const T* p) {
+    typedef const __attribute__((address_space(1))) T gT;
+    return __builtin_nontemporal_load((gT*)(p));
+}
+
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
@@ -45,13 +71,19 @@ __device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(
 //   (1024+16u)/16  - 72         = n   (one packed fma; /16 is exact)
 // All intermediate values are integers below 2048, hence exact in binary16.
 // The mask/xor/or step is one three-input bitwise op (v_bitop3_b32) per pair.
+// Since the mask bits and the 0x6400 bits are disjoint,
+// ((w ^ 0x8..) & m) | 0x6400.. == (w & m) ^ (0x6400.. | 0x8 at the nibble),
+// a single v_bitop3_b32 with truth table 0x6A = (a & b) ^ c.
+__device__ __forceinline__ uint32_t and_xor(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x6A);
+}
+
 __device__ __forceinline__ void dequant_int4x8_bitfield(uint32_t w, f16x2 out[4]) {
-    const uint32_t t = w ^ 0x88888888u;
-    const uint32_t t8 = t >> 8;
-    const uint32_t p0 = (t & 0x000f000fu) | 0x64006400u;   // nibbles 0,4 -> v0, v1
-    const uint32_t p1 = (t & 0x00f000f0u) | 0x64006400u;   // nibbles 1,5 -> v2, v3 (x16)
-    const uint32_t p2 = (t8 & 0x000f000fu) | 0x64006400u;  // nibbles 2,6 -> v4, v5
-    const uint32_t p3 = (t8 & 0x00f000f0u) | 0x64006400u;  // nibbles 3,7 -> v6, v7 (x16)
+    const uint32_t w8 = w >> 8;
+    const uint32_t p0 = and_xor(w, 0x000f000fu, 0x64086408u);   // nibbles 0,4 -> v0, v1
+    const uint32_t p1 = and_xor(w, 0x00f000f0u, 0x64806480u);   // nibbles 1,5 -> v2, v3 (x16)
+    const uint32_t p2 = and_xor(w8, 0x000f000fu, 0x64086408u);  // nibbles 2,6 -> v4, v5
+    const uint32_t p3 = and_xor(w8, 0x00f000f0u, 0x64806480u);  // nibbles 3,7 -> v6, v7 (x16)
     const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
     const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
     const f16x2 bias16 = {(f16)-72.0f, (f16)-72.0f};
@@ -59,6 +91,38 @@ __device__ __forceinline__ void dequant_int4x8_bitfield(uint32_t w, f16x2 out[4]
     out[1] = __builtin_elementwise_fma(as_f16x2(p1), sixteenth, bias16);
     out[2] = as_f16x2(p2) + bias;
     out[3] = __builtin_elementwise_fma(as_f16x2(p3), sixteenth, bias16);
+}
+
+// Method used by the dot-product kernels: offset-binary nibbles as binary16
+// SUBNORMALS. With u = n + 8 in [0,15], the half with bit pattern u encodes
+// exactly u * 2^-24 and the pattern u<<4 encodes 16u * 2^-24, so no bias
+// subtraction is needed per value: one v_bitop3 ((w & mask) ^ 0x8..) per pair.
+//   lo[0] = (u0, u1) * 2^-24     hi[0] = (u2, u3) * 2^-20
+//   lo[1] = (u4, u5) * 2^-24     hi[1] = (u6, u7) * 2^-20
+// A dot product then recovers sum q*x = 2^24 * sum(lo.x) + 2^20 * sum(hi.x)
+// - 8 * sum(x): the products u * 2^-24 * x are exact in binary32 (binary16
+// denormals are preserved by the dot instructions), the power-of-two
+// rescales are exact, and sum(x) is shared by every row of a tile.
+__device__ __forceinline__ void int4x8_subnormal_bitfield(uint32_t w, f16x2 lo[2], f16x2 hi[2]) {
+    const uint32_t w8 = w >> 8;
+    lo[0] = as_f16x2(and_xor(w, 0x000f000fu, 0x00080008u));
+    hi[0] = as_f16x2(and_xor(w, 0x00f000f0u, 0x00800080u));
+    lo[1] = as_f16x2(and_xor(w8, 0x000f000fu, 0x00080008u));
+    hi[1] = as_f16x2(and_xor(w8, 0x00f000f0u, 0x00800080u));
+}
+
+// Same bit patterns built nibble by nibble (bitfield extract, xor, shift, or):
+// the independent second derivation, bit-identical to the above.
+__device__ __forceinline__ void int4x8_subnormal_scalar(uint32_t w, f16x2 lo[2], f16x2 hi[2]) {
+    // nibble index holding logical element j (AWQ order)
+    constexpr int nib[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    uint32_t u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u[j] = __builtin_amdgcn_ubfe(w, 4 * nib[j], 4) ^ 8u;
+    lo[0] = as_f16x2(u[0] | (u[1] << 16));
+    hi[0] = as_f16x2((u[2] << 4) | (u[3] << 20));
+    lo[1] = as_f16x2(u[4] | (u[5] << 16));
+    hi[1] = as_f16x2((u[6] << 4) | (u[7] << 20));
 }
 
 // Method "scalar": per-nibble signed bitfield extract and integer -> binary16
@@ -131,6 +195,98 @@ __device__ __forceinline__ float wave_max_bcast(float v) {
         v = fmaxf(v, o);
     }
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// ---------------------------------------------------------------------------
+// Transposed reduction of R per-lane partials (R rows) across the wave, R in
+// {1,2,4,8}: each exchange step halves the number of live values per lane
+// (v_permlane32_swap / v_permlane16_swap / DPP row_ror:8 move the halves a
+// lane gives away), then an 8-lane DPP sum finishes. Every lane ends with the
+// full sum of row reduce_rows_row<R>(lane); the order of additions is fixed.
+// kSwapUpperToVdst: v_permlane{32,16}_swap exchange the upper half of VDST
+// with the lower half of VSRC0 (measured on gfx950).
+// ---------------------------------------------------------------------------
+constexpr bool kSwapUpperToVdst = true;
+
+// The swaps are written as inline asm with both registers as read-write
+// operands: through the two-result builtins the compiler was observed to read
+// the second result from the first register.
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// sum over the 8 lanes of each aligned 8-lane group, result in every lane
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror: lane i <- 7-i within each 8 lanes
+    return v;
+}
+
+template <int R>
+__device__ __forceinline__ float reduce_rows(float a[R]) {
+    const uint32_t lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    if (R == 8) {
+        float b[4], c[2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float hi = a[j + 4], lo = a[j];
+            swap32(hi, lo);
+            b[j] = hi + lo;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float hi = b[j + 2], lo = b[j];
+            swap16(hi, lo);
+            c[j] = hi + lo;
+        }
+        const bool e = lane & 8u;
+        const float keep = e ? c[0] : c[1];
+        const float send = e ? c[1] : c[0];
+        return sum8(keep + dpp_f<0x128>(send));  // row_ror:8 = lane ^ 8 within 16
+    } else if (R == 4) {
+        float b[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float hi = a[j + 2], lo = a[j];
+            swap32(hi, lo);
+            b[j] = hi + lo;
+        }
+        float hi = b[1], lo = b[0];
+        swap16(hi, lo);
+        const float c = hi + lo;
+        return sum8(c + dpp_f<0x128>(c));
+    } else if (R == 2) {
+        // Never swap a value with itself: the compiler folds swap(x, x) as if
+        // both results were equal. Swapping against zero instead leaves the
+        // row totals in the lower 16 lanes of each 32-lane half.
+        float hi = a[1], lo = a[0];
+        swap32(hi, lo);
+        float b = hi + lo, z = 0.0f;
+        swap16(b, z);
+        const float c = b + z;
+        return sum8(c + dpp_f<0x128>(c));
+    } else {
+        float v = a[0], z = 0.0f;
+        swap32(v, z);
+        float b = v + z, z2 = 0.0f;
+        swap16(b, z2);
+        const float c = b + z2;
+        return sum8(c + dpp_f<0x128>(c));
+    }
+}
+
+// which row's total reduce_rows<R> leaves in `lane`
+template <int R>
+__device__ __forceinline__ int reduce_rows_row(uint32_t lane) {
+    const int g = static_cast<int>(lane >> 3);  // 8-lane group 0..7
+    if (R == 8) return kSwapUpperToVdst ? 7 - g : g;
+    if (R == 4) return kSwapUpperToVdst ? 3 - (g >> 1) : (g >> 1);
+    if (R == 2) return kSwapUpperToVdst ? 1 - (g >> 2) : (g >> 2);
+    return 0;
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

@@ -27,10 +27,13 @@ constexpr int kDownThreads = kDownWaves * kWave;
 constexpr int kSlabCols = kWave * 32;  // columns covered by one wave-wide row load
 constexpr int kRedPad = kWave + 1;      // LDS row pitch (floats) for the wave-sum transpose
 
-template <bool VEC, bool CHUNK_SCALE, class Rows>
+// U rows per wave per batch, all loads of a batch issued before arithmetic
+// (a lane with no chunk or a row past the range reads g_zero16 instead).
+template <int U, bool VEC, bool CHUNK_SCALE, class Rows>
 __global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows rows, const uint16_t* __restrict__ h,
                                                                             float* __restrict__ partial, int64_t k,
                                                                             int H, int gs, int rows_per_wg) {
+    constexpr int SC = CHUNK_SCALE ? 1 : 4;
     __shared__ float red[kDownWaves * 32 * kRedPad];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int words = (H + 7) >> 3;
@@ -39,48 +42,56 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows 
     const bool cvalid = c < chunks;
     const int64_t j0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
     const int64_t j1 = (j0 + rows_per_wg < k) ? j0 + rows_per_wg : k;
+    const uint32_t* z = g_zero16;
+    const float* zf = reinterpret_cast<const float*>(g_zero16);
 
     float acc[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] = 0.0f;
 
-    for (int64_t j = j0 + wave; j < j1; j += kDownWaves) {
-        const RowRef ref = rows.get(j);
-        const float hj = f16_bits_to_f32(h[j]);
-        if (!ref.ok) {
+    for (int64_t jb = j0 + static_cast<int64_t>(wave) * U; jb < j1; jb += static_cast<int64_t>(kDownWaves) * U) {
+        uint32_t wv[U][4];
+        float coef[U][SC];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) acc[i] = __builtin_nanf("");
-            continue;
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = jb + u;
+            const bool in = j < j1;
+            const RowRef ref = rows.get(in ? j : j0);
+            const bool ok = in && ref.ok && cvalid;
+            const float hj = in ? f16_bits_to_f32(h[in ? j : j0]) : 0.0f;
+            if (VEC) {
+                const u32x4 t = __builtin_nontemporal_load(ok ? reinterpret_cast<const u32x4*>(ref.w) + c
+                                                              : reinterpret_cast<const u32x4*>(z));
+                wv[u][0] = t.x;
+                wv[u][1] = t.y;
+                wv[u][2] = t.z;
+                wv[u][3] = t.w;
+            } else {
+                const uint32_t* rw = reinterpret_cast<const uint32_t*>(ref.w);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[u][i] = *((ok && 4 * c + i < words) ? rw + 4 * c + i : z);
+            }
+            const float bad = (in && !ref.ok) ? __builtin_nanf("") : 1.0f;  // unresolvable row -> NaN
+#pragma unroll
+            for (int i = 0; i < SC; ++i) {
+                const int wi = 4 * c + i;
+                const float sv = CHUNK_SCALE ? *(ok ? ref.s + (32 * c) / gs : zf)
+                                             : *((ok && wi < words) ? ref.s + (8 * wi) / gs : zf);
+                coef[u][i] = (hj * sv) * bad;
+            }
         }
-        if (!cvalid) continue;
-        uint32_t wv[4];
-        if (VEC) {
-            const u32x4 t = reinterpret_cast<const u32x4*>(ref.w)[c];
-            wv[0] = t.x;
-            wv[1] = t.y;
-            wv[2] = t.z;
-            wv[3] = t.w;
-        } else {
-            const uint32_t* rw = reinterpret_cast<const uint32_t*>(ref.w);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wv[i] = (4 * c + i < words) ? rw[4 * c + i] : 0u;
-        }
-        float coef[4];
-        if (CHUNK_SCALE) {
-            coef[0] = hj * ref.s[(32 * c) / gs];
-        } else {
+        for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) coef[i] = (4 * c + i < words) ? hj * ref.s[(8 * (4 * c + i)) / gs] : 0.0f;
-        }
+            for (int i = 0; i < 4; ++i) {
+                f16x2 q[4];
+                dequant_int4x8_bitfield(wv[u][i], q);
+                const float cf = coef[u][CHUNK_SCALE ? 0 : i];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f16x2 q[4];
-            dequant_int4x8_bitfield(wv[i], q);
-            const float cf = CHUNK_SCALE ? coef[0] : coef[i];
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                acc[8 * i + 2 * p] = fmaf(cf, static_cast<float>(q[p].x), acc[8 * i + 2 * p]);
-                acc[8 * i + 2 * p + 1] = fmaf(cf, static_cast<float>(q[p].y), acc[8 * i + 2 * p + 1]);
+                for (int p = 0; p < 4; ++p) {
+                    acc[8 * i + 2 * p] = fmaf(cf, static_cast<float>(q[p].x), acc[8 * i + 2 * p]);
+                    acc[8 * i + 2 * p + 1] = fmaf(cf, static_cast<float>(q[p].y), acc[8 * i + 2 * p + 1]);
+                }
             }
         }
     }
@@ -114,10 +125,13 @@ __global__ __launch_bounds__(256) void sparse_down_reduce_kernel(const float* __
 // Rows per workgroup: a multiple of the wave count, large enough to amortise
 // the partial-row write (8 KB per 2048 columns), small enough to spread k rows
 // over ~128 workgroups.
+constexpr int kDownU = 4;  // rows per wave per batch
+
 static int64_t pick_rows_per_wg(int64_t k) {
-    int64_t r = ceil_div64(k, 128);
-    if (r < 16) r = 16;
-    return ceil_div64(r, kDownWaves) * kDownWaves;
+    const int64_t step = static_cast<int64_t>(kDownWaves) * kDownU;
+    int64_t r = ceil_div64(k, 64);
+    if (r < step) r = step;
+    return ceil_div64(r, step) * step;
 }
 
 static int64_t num_splits(int64_t k) { return k == 0 ? 0 : ceil_div64(k, pick_rows_per_wg(k)); }
@@ -138,7 +152,7 @@ static int launch_sparse_down(const Rows& rows, int64_t k, const uint16_t* h, ui
         const bool cs = (gs % 32) == 0;
         const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(rpw);
 #define SOI_D(V, CS)                                                                                             \
-    hipLaunchKernelGGL((sparse_down_partial_kernel<V, CS, Rows>), grid, dim3(kDownThreads), 0, st, rows, h, partial, \
+    hipLaunchKernelGGL((sparse_down_partial_kernel<kDownU, V, CS, Rows>), grid, dim3(kDownThreads), 0, st, rows, h, partial, \
                        k, Hi, gi, ri)
         if (vec) {
             if (cs) SOI_D(true, true); else SOI_D(true, false);

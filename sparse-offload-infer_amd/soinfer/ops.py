@@ -36,6 +36,52 @@ def gemv_w4a16_group_lop3(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch
     return _C.gemv_w4a16_group_lop3(Wq_packed, scale, x, K, group_size)
 
 
+class GemvBatch:
+    """P independent INT4 GEMVs of one shape [N, K] executed in ONE kernel launch.
+
+    Validates every tensor once and keeps device pointer tables, so run() is a
+    single launch (and can be captured in a HIP graph). y[p] is bit-identical to
+    gemv_w4a16_group_lop3(Wqs[p], scales[p], xs[p], K, group_size)."""
+
+    def __init__(self, Wqs, scales, xs, K: int, group_size: int, ys=None):
+        P = len(Wqs)
+        if not (len(scales) == len(xs) == P and P > 0):
+            raise ValueError("GemvBatch: Wqs, scales and xs must be non-empty lists of equal length")
+        N = Wqs[0].shape[0]
+        G = -(-K // group_size)
+        dev = Wqs[0].device
+        if ys is None:
+            ys = [torch.empty(N, dtype=torch.float16, device=dev) for _ in range(P)]
+        for W, s, x, y in zip(Wqs, scales, xs, ys):
+            if not (W.dtype == torch.uint8 and W.is_contiguous() and tuple(W.shape) == (N, -(-K // 8) * 4)):
+                raise RuntimeError("GemvBatch: every Wq must be a contiguous uint8 [N, ceil(K/8)*4] tensor")
+            if not (s.dtype == torch.float32 and s.is_contiguous() and tuple(s.shape) == (N, G)):
+                raise RuntimeError("GemvBatch: every scale must be a contiguous float32 [N, ceil(K/gs)] tensor")
+            if not (x.dtype == torch.float16 and x.is_contiguous() and tuple(x.shape) == (K,)):
+                raise RuntimeError("GemvBatch: every x must be a contiguous float16 [K] tensor")
+            if not (y.dtype == torch.float16 and y.is_contiguous() and tuple(y.shape) == (N,)):
+                raise RuntimeError("GemvBatch: every y must be a contiguous float16 [N] tensor")
+            if not all(t.device == dev for t in (W, s, x, y)):
+                raise RuntimeError("GemvBatch: all tensors must be on one device")
+        self._keep = (list(Wqs), list(scales), list(xs), list(ys))
+        self.ys = self._keep[3]
+        self.N, self.K, self.group_size = N, K, group_size
+
+        def table(ts):
+            return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+
+        self._tables = tuple(table(ts) for ts in self._keep)
+
+    def run(self):
+        _C.gemv_w4a16_batched(*self._tables, self.N, self.K, self.group_size)
+        return self.ys
+
+
+def gemv_w4a16_batched(Wqs, scales, xs, K: int, group_size: int):
+    """Convenience one-shot form of GemvBatch: returns the list of outputs."""
+    return GemvBatch(Wqs, scales, xs, K, group_size).run()
+
+
 def topk_threshold_select(abs_g: torch.Tensor, k: int) -> torch.Tensor:
     """Indices (int32 [k], ascending) selected by the reference's threshold rule over abs_g (1-D fp32,
     non-negative): tau from 24 fp32 bisection steps, then the first k indices with abs_g >= tau.

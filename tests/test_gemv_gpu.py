@@ -156,3 +156,25 @@ def test_w8_rejects_bad_arguments(ops):
     q3, s3 = O.quantize_group(w, 3, bits=8)  # num_groups > 1 with gs not a multiple of 4
     with pytest.raises(RuntimeError):
         ops.gemv_w8a16(torch.from_numpy(q3[:, :64].copy()).cuda(), torch.from_numpy(s3[:, :22].copy()).cuda(), x, 3)
+
+
+# ---------------------------------------------------------------------------
+# batched (one launch, many problems)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K,P", [(6144, 2048, 5), (1024, 2048, 9), (2048, 6144, 3), (33, 96, 4), (7, 200, 3)])
+def test_batched_bit_identical_to_single(ops, N, K, P):
+    probs = [int4_problem(N, K, 8 if K % 32 else 32 if K == 96 else 128, seed=100 + i) for i in range(P)]
+    gs = probs[0]["gs"]
+    ys = ops.gemv_w4a16_batched([p["Wq_d"] for p in probs], [p["s_d"] for p in probs], [p["x_d"] for p in probs],
+                                probs[0]["K"], gs)
+    for p, y in zip(probs, ys):
+        assert torch.equal(y, ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], gs))
+    assert_close(ys[0], O.gemv_w4_f64(probs[0]["Wq"], probs[0]["s"], probs[0]["x"], probs[0]["K"], gs), "batched")
+
+
+def test_batched_rejects_mismatched_shapes(ops):
+    a = int4_problem(64, 256, 128, seed=1)
+    b = int4_problem(32, 256, 128, seed=2)
+    with pytest.raises(RuntimeError):
+        ops.gemv_w4a16_batched([a["Wq_d"], b["Wq_d"]], [a["s_d"], b["s_d"]], [a["x_d"], b["x_d"]], 256, 128)
