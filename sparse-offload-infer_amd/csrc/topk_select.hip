@@ -9,15 +9,14 @@
 // Counts are integers, so the decisions (and hence tau = lo) do not depend on
 // how the counting is parallelised.
 //
-// gfx950 design: ONE workgroup of 16 waves holds all values in registers
-// (element i = j*1024 + tid). Each bisection step is one compare per element,
-// a 64-lane ballot + popcount per wave, and one LDS exchange of 16 per-wave
-// counts behind a single barrier (double-buffered by step parity, so no second
-// barrier is needed). Every thread replays lo/hi/mid redundantly in fp32 in
-// the same order as the reference's thread 0. The final compaction is an
-// ordered ballot prefix scan: position = (elements before this block) +
-// (earlier waves in this block) + (earlier lanes in this wave), so the
-// output order is ascending index order by construction.
+// gfx950 design: ONE workgroup of 16 waves holds all values in registers.
+// The 24 bisection steps are replayed 8 at a time from one LDS histogram of
+// the values against the exact node values of the next 8 levels (three
+// rounds, two barriers each, instead of one barrier round per step); see
+// topk_rule_a_regs_kernel. The final compaction is an ordered ballot prefix
+// scan: position = (elements of earlier waves) + (earlier rows of this wave)
+// + (earlier lanes in this row), so the output is in ascending index order
+// by construction and identical on every call.
 #include "soi_device.h"
 #include "soi_host.h"
 
@@ -40,21 +39,72 @@ __device__ __forceinline__ float block_max_from(float local, float* s_max, int w
     return m;
 }
 
-// E values per thread held in registers: n <= 1024*E.
+// Value of bisection node `i` (in-order index 1..255 of the next 8 levels)
+// reached from state (lo, hi) by the reference recurrence: at each level
+// mid = fl(0.5f * fl(lo + hi)), going right sets lo = mid, left sets hi = mid.
+__device__ __forceinline__ float bisection_node(float lo, float hi, int i) {
+    int c = 128, step = 64;
+    float m = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        m = 0.5f * (lo + hi);
+        if (i == c) break;
+        if (i > c) {
+            lo = m;
+            c += step;
+        } else {
+            hi = m;
+            c -= step;
+        }
+        step >>= 1;
+    }
+    return m;
+}
+
+// Inclusive prefix sum over the 64 lanes (DPP, fixed order).
+__device__ __forceinline__ uint32_t wave_prefix_u32(uint32_t x) {
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, false));  // row_shr:1
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xf, 0xf, false));  // row_shr:2
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xf, false));  // row_shr:4
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x118, 0xf, 0xf, false));  // row_shr:8
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x142, 0xa, 0xf, false));  // row_bcast:15
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return x;
+}
+
+// E values per thread held in registers: n <= 1024*E. Wave w owns elements
+// [w*64E, (w+1)*64E), element (j, lane) = w*64E + 64j + lane, so each load is
+// 64 contiguous floats and the ascending-index order is (wave, j, lane).
+//
+// The 24 bisection steps are replayed 8 at a time. For the current (lo, hi)
+// the 255 node values T_1 <= ... <= T_255 of the next 8 levels are computed
+// with the reference's fp32 recurrence (thread t computes T_{t+1}). With
+// pos(v) = #{i : T_i <= v}, count(v >= T_c) = S(c) = #{pos >= c} + #{v >= hi},
+// non-increasing in c, so the 8 sequential decisions "S(mid) >= k" of a
+// binary search over the nodes end exactly at c* = #{c : S(c) >= k}: the
+// new state is lo = T_{c*} (unchanged if c* = 0), hi = T_{c*+1} (unchanged if
+// c* = 255). One histogram of pos over the candidates lo <= v < hi gives all
+// S(c); pos is estimated from the even node spacing and verified against the
+// exact node values (an exact search runs only when the estimate is off).
+// Node and histogram buffers are double-buffered by round: two barriers per
+// round, three rounds.
 template <int E>
 __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const float* __restrict__ v, int n, int k,
                                                                          int32_t* __restrict__ out_idx,
                                                                          int32_t* __restrict__ out_count) {
     __shared__ float s_max[kTopkWaves];
-    __shared__ uint32_t s_cnt[2][kTopkWaves];
-    __shared__ uint32_t s_blk[E][kTopkWaves];
+    __shared__ float s_T[2][256];     // s_T[b][i] = T_i, i in 1..255
+    __shared__ uint32_t s_hist[2][256];  // pos histogram of candidates
+    __shared__ uint32_t s_above[2];      // count of v >= hi
+    __shared__ __attribute__((aligned(16))) uint32_t s_tot[kTopkWaves];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int base_i = wave * kWave * E + lane;
 
     float val[E];
     float local_max = 0.0f;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const int i = j * kTopkThreads + tid;
+        const int i = base_i + j * kWave;
         val[j] = (i < n) ? v[i] : -__builtin_inff();
         local_max = fmaxf(local_max, val[j]);
     }
@@ -63,46 +113,91 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const fl
     float lo = 0.0f;
     float hi = total_max + 1e-3f;
 #pragma unroll 1
-    for (int it = 0; it < kBisectionSteps; ++it) {
-        const float mid = 0.5f * (lo + hi);
-        uint32_t cnt = 0;
-#pragma unroll
-        for (int j = 0; j < E; ++j) cnt += popc64(ballot(val[j] >= mid));
-        if (lane == 0) s_cnt[it & 1][wave] = cnt;
+    for (int round = 0; round < 3; ++round) {
+        const int b = round & 1;
+        if (tid < 255) s_T[b][tid + 1] = bisection_node(lo, hi, tid + 1);
+        if (tid < 256) s_hist[b][tid] = 0u;
+        if (tid == 0) s_above[b] = 0u;
         __syncthreads();
-        uint32_t total = 0;
+
+        const float est = 256.0f / (hi - lo);
+        uint32_t above = 0;
+        int p[E];
+        float ta[E], tb[E];
 #pragma unroll
-        for (int w = 0; w < kTopkWaves; ++w) total += s_cnt[it & 1][w];
-        if (total >= static_cast<uint32_t>(k))
-            lo = mid;
-        else
-            hi = mid;
+        for (int j = 0; j < E; ++j) {
+            const float x = val[j];
+            above += popc64(ballot(x >= hi));
+            int q = static_cast<int>((x - lo) * est);
+            q = q < 0 ? 0 : (q > 255 ? 255 : q);
+            p[j] = q;
+            ta[j] = s_T[b][q > 0 ? q : 1];
+            tb[j] = s_T[b][q < 255 ? q + 1 : 255];
+        }
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const float x = val[j];
+            if (x >= lo && x < hi) {
+                int q = p[j];
+                const bool ok = (q == 0 || x >= ta[j]) && (q == 255 || x < tb[j]);
+                if (!ok) {  // exact search from the estimate (rare)
+                    while (q < 255 && x >= s_T[b][q + 1]) ++q;
+                    while (q > 0 && x < s_T[b][q]) --q;
+                }
+                atomicAdd(&s_hist[b][q], 1u);
+            }
+        }
+        if (lane == 0 && above) atomicAdd(&s_above[b], above);
+        __syncthreads();
+
+        // lane l holds buckets c = 255-4l-jj (jj = 0..3): a lane prefix in that order is a suffix over c
+        uint32_t a[4];
+        uint32_t run = 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            run += s_hist[b][255 - 4 * lane - jj];
+            a[jj] = run;
+        }
+        const uint32_t excl = wave_prefix_u32(run) - run + s_above[b];
+        uint32_t cstar = 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int c = 255 - 4 * lane - jj;
+            cstar += popc64(ballot(c >= 1 && excl + a[jj] >= static_cast<uint32_t>(k)));
+        }
+        const float new_lo = cstar >= 1 ? s_T[b][cstar >= 1 ? cstar : 1] : lo;
+        const float new_hi = cstar <= 254 ? s_T[b][cstar <= 254 ? cstar + 1 : 255] : hi;
+        lo = new_lo;
+        hi = new_hi;
     }
     const float tau = lo;
 
     uint64_t m[E];
+    uint32_t cnt[E];
+    uint32_t wave_total = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         m[j] = ballot(val[j] >= tau);
-        if (lane == 0) s_blk[j][wave] = popc64(m[j]);
+        cnt[j] = popc64(m[j]);
+        wave_total += cnt[j];
     }
+    if (lane == 0) s_tot[wave] = wave_total;
     __syncthreads();
-    uint32_t running = 0;
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kTopkWaves; ++w) {
+        const uint32_t c = s_tot[w];
+        before += (w < wave) ? c : 0u;
+        total += c;
+    }
+    uint32_t running = before;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        uint32_t before = 0, blk = 0;
-#pragma unroll
-        for (int w = 0; w < kTopkWaves; ++w) {
-            const uint32_t c = s_blk[j][w];
-            before += (w < wave) ? c : 0u;
-            blk += c;
-        }
-        const bool flag = val[j] >= tau;
-        const uint32_t pos = running + before + mask_prefix(m[j]);
-        if (flag && pos < static_cast<uint32_t>(k)) out_idx[pos] = j * kTopkThreads + tid;
-        running += blk;
+        const uint32_t pos = running + mask_prefix(m[j]);
+        if (val[j] >= tau && pos < static_cast<uint32_t>(k)) out_idx[pos] = base_i + j * kWave;
+        running += cnt[j];
     }
-    if (tid == 0) *out_count = static_cast<int32_t>(running < static_cast<uint32_t>(k) ? running : k);
+    if (tid == 0) *out_count = static_cast<int32_t>(total < static_cast<uint32_t>(k) ? total : k);
 }
 
 // Any n: values streamed from global memory (L2-resident after the first
