@@ -8,13 +8,22 @@ weight of a 28-layer Qwen3-1.7B-shaped decoder -- per layer q [2048x2048],
 k/v [1024x2048], o [2048x2048], gate/up [6144x2048], down [2048x6144] --
 196 GEMVs, 750,862,336 algorithmic bytes (packed weights + fp32 scales +
 fp16 x + fp16 y), each weight resident in HBM and touched once per step
-(751 MB > the 256 MB Infinity Cache, so reads come from HBM). The 196 launches
-are captured once in a HIP graph and replayed, so the figure is GPU time, not
-Python launch overhead. value = algorithmic bytes / step time.
+(751 MB > the 256 MB Infinity Cache, so reads come from HBM). Independent
+GEMVs of one shape class run as one batched launch (4 launches per step).
+value = algorithmic bytes / step time, timed over --steps steps between two
+device synchronisations.
 
-Also reported: per-shape kernel time and GB/s on rotating cold copies
-(> 512 MB per shape) for INT4 and INT8, the dominant kernel's roofline, the
-top-k latency at I=6144, and the CPU oracle timed on a bounded sample.
+Also reported:
+  roofline        the dominant launch (56 x gate/up 6144x2048), timed per launch
+                  with HIP events on the launching stream; `traffic` is the
+                  HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter
+                  summary committed under profiles/ (null when absent);
+  copy_reference  a plain device-to-device copy of 512 MiB (the calibration
+                  kernel of the counter runs, and the box's streaming rate);
+  decode_chain    the 112 dependent launches of one decode step, graph-replayed;
+  per_shape_cold  per-shape INT4 / INT8 single-launch times on cold copies;
+  topk_us_I6144   top-k latency at I=6144;
+  cpu_baseline    the CPU oracle on a bounded sample (one thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -39,6 +48,11 @@ H, I, NQ, NKV, HD, GS = 2048, 6144, 16, 8, 128, 128
 LAYER_SHAPES = [("q", NQ * HD, H), ("k", NKV * HD, H), ("v", NKV * HD, H), ("o", H, NQ * HD),
                 ("gate", I, H), ("up", I, H), ("down", H, I)]
 METRIC = "INT4 GEMV HBM GB/s (% of peak); DIP decode tok/s, Qwen3-1.7B shape, bs=1"
+
+
+def log(msg: str) -> None:
+    """Progress line on stderr (stdout carries only the JSON result)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def int4_bytes(N: int, K: int, gs: int = GS) -> int:
@@ -111,6 +125,33 @@ def time_graph_per_launch(fn, args_list, reps: int = 5):
     return {"mean_us": us, "p90_us": us}
 
 
+TRAFFIC_FILE = REPO / "profiles" / "gemv_int4_batched_gate_up_qwen3_1p7b_traffic.md"
+
+
+def read_traffic(path: Path = TRAFFIC_FILE):
+    """HBM bytes per dominant launch from the committed counter summary (line `traffic_bytes_per_launch: N`)."""
+    import re
+
+    try:
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", path.read_text(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def copy_reference(nbytes: int = 512 << 20, reps: int = 10):
+    """A plain device-to-device copy of `nbytes` (torch's copy kernel): read + write bytes / kernel time."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 256)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    t = time_per_launch(lambda: dst.copy_(src), [()], reps=reps)
+    del src, dst
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(t["mean_us"], 2),
+            "GBps": round(2 * nbytes / (t["mean_us"] * 1e-6) / 1e9, 1)}
+
+
 def cold_copies(nbytes: int, target: int = 600 << 20) -> int:
     return max(8, -(-target // nbytes))
 
@@ -162,101 +203,9 @@ def bench_topk(ops, dev, gen):
     return res
 
 
-def cpu_baseline(layer_mats_cpu, budget_s: float = 12.0):
-    """The CPU oracle (scalar C, one thread) on layer 0's seven GEMVs, repeated to ~budget_s."""
-    import numpy as np
-
-    from oracle import oracle as O
-
-    t0 = time.perf_counter()
-    done_bytes = 0
-    reps = 0
-    while True:
-        for Wq, s, x, K in layer_mats_cpu:
-            O.gemv_w4_f64(Wq, s, x, K, GS)
-            done_bytes += int4_bytes(Wq.shape[0], K)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/soi_oracle.c soi_ref_gemv_w4_f64 (binary64 accumulation, one thread) over layer 0's "
-                      f"7 INT4 GEMVs (26.8 MB), {reps} passes in {el:.1f} s on {os.cpu_count()} visible host cores"}
-
-
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip per-shape / top-k tables")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU (the hot path is single-GPU; --gpus {args.gpus} is not "
-              "supported). Run with --gpus 1.", file=sys.stderr)
-        return 2
-
-    import numpy as np
+def bench_decode_chain(ops, layers, step_bytes):
+    """One decode step as 112 dependent launches (qkv and gate|up rows concatenated), replayed as a HIP graph."""
     import torch
-
-    import soinfer.ops as ops
-
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev).manual_seed(0)
-
-    # ---- the 28-layer weight set, resident in HBM ----
-    layers = []
-    step_bytes = 0
-    for layer in range(LAYERS):
-        mats = {}
-        for name, N, K in LAYER_SHAPES:
-            Wq, s = make_int4(N, K, gen, dev)
-            x = torch.randn(K, generator=gen, device=dev).half()
-            mats[name] = (Wq, s, x, N, K)
-            step_bytes += int4_bytes(N, K)
-        layers.append(mats)
-    torch.cuda.synchronize()
-
-    # One step = every GEMV of the weight set. Independent GEMVs of one shape
-    # class run as one batched launch (4 launches per step).
-    classes = [("gate", "up"), ("q", "o"), ("k", "v"), ("down",)]
-    batches = []
-    for names in classes:
-        group = [layers[l][n] for l in range(LAYERS) for n in names]
-        N, K = group[0][3], group[0][4]
-        batches.append(ops.GemvBatch([g[0] for g in group], [g[1] for g in group], [g[2] for g in group], K, GS))
-
-    def step():
-        for b in batches:
-            b.run()
-
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed / args.steps * 1e3
-    value = step_bytes / (elapsed / args.steps) / 1e9  # GB/s
-
-    # the batched outputs equal single launches (spot check, bit-exact)
-    g0 = layers[0]["gate"]
-    assert torch.equal(batches[0].ys[0], ops.gemv_w4a16_group_lop3(g0[0], g0[1], g0[2], g0[4], GS))
-
-    # ---- dominant kernel: the batched gate/up launch (56 x 6144x2048), HIP events per launch ----
-    dom_bytes = 2 * LAYERS * int4_bytes(I, H)
-    tdom = time_per_launch(lambda b: b.run(), [(batches[0],)], reps=30)
-    achieved = dom_bytes / (tdom["mean_us"] * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
-                "kernel": "soi::gemv_int4_batched_kernel<8,1,true,true> (56 x gate/up 6144x2048)",
-                "bytes_per_launch": dom_bytes, "avg_launch_us": round(tdom["mean_us"], 3)}
 
     # ---- decode chain: per layer qkv (concatenated rows), o, gate|up (concatenated), down; dependent order ----
     chain = []
@@ -293,6 +242,111 @@ def main() -> int:
                     "note": "one launch per dependent GEMV of a decode step (qkv and gate|up rows concatenated), "
                             "HIP-graph replay"}
     del chain, graph
+    return decode_chain
+
+
+def cpu_baseline(layer_mats_cpu, budget_s: float = 12.0):
+    """The CPU oracle (scalar C, one thread) on layer 0's seven GEMVs, repeated to ~budget_s."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    t0 = time.perf_counter()
+    done_bytes = 0
+    reps = 0
+    while True:
+        for Wq, s, x, K in layer_mats_cpu:
+            O.gemv_w4_f64(Wq, s, x, K, GS)
+            done_bytes += int4_bytes(Wq.shape[0], K)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/soi_oracle.c soi_ref_gemv_w4_f64 (binary64 accumulation, one thread) over layer 0's "
+                      f"7 INT4 GEMVs (26.8 MB), {reps} passes in {el:.1f} s on {os.cpu_count()} visible host cores"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the decode-chain, per-shape and top-k tables")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU (the hot path is single-GPU; --gpus {args.gpus} is not "
+              "supported). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import soinfer.ops as ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    # ---- the 28-layer weight set, resident in HBM ----
+    layers = []
+    step_bytes = 0
+    for layer in range(LAYERS):
+        mats = {}
+        for name, N, K in LAYER_SHAPES:
+            Wq, s = make_int4(N, K, gen, dev)
+            x = torch.randn(K, generator=gen, device=dev).half()
+            mats[name] = (Wq, s, x, N, K)
+            step_bytes += int4_bytes(N, K)
+        layers.append(mats)
+    torch.cuda.synchronize()
+    log(f"weight set ready: {LAYERS} layers, {step_bytes} bytes per step")
+
+    # One step = every GEMV of the weight set. Independent GEMVs of one shape
+    # class run as one batched launch (4 launches per step).
+    classes = [("gate", "up"), ("q", "o"), ("k", "v"), ("down",)]
+    batches = []
+    for names in classes:
+        group = [layers[l][n] for l in range(LAYERS) for n in names]
+        N, K = group[0][3], group[0][4]
+        batches.append(ops.GemvBatch([g[0] for g in group], [g[1] for g in group], [g[2] for g in group], K, GS))
+
+    def step():
+        for b in batches:
+            b.run()
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    log(f"{args.steps} timed steps: {elapsed / args.steps * 1e3:.4f} ms/step")
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_bytes / (elapsed / args.steps) / 1e9  # GB/s
+
+    # the batched outputs equal single launches (spot check, bit-exact)
+    g0 = layers[0]["gate"]
+    assert torch.equal(batches[0].ys[0], ops.gemv_w4a16_group_lop3(g0[0], g0[1], g0[2], g0[4], GS))
+
+    # ---- dominant kernel: the batched gate/up launch (56 x 6144x2048), HIP events per launch ----
+    dom_bytes = 2 * LAYERS * int4_bytes(I, H)
+    tdom = time_per_launch(lambda b: b.run(), [(batches[0],)], reps=30)
+    achieved = dom_bytes / (tdom["mean_us"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(),
+                "kernel": "soi::gemv_int4_batched_kernel<8,1,true,true,true> (56 x gate/up 6144x2048, "
+                          "43008 workgroups of 64)",
+                "bytes_per_launch": dom_bytes, "avg_launch_us": round(tdom["mean_us"], 3)}
+    log(f"dominant launch: {tdom['mean_us']:.3f} us")
+    copy_ref = copy_reference()
+    log(f"copy reference: {copy_ref['us']} us")
+
 
     result = {
         "metric": METRIC,
@@ -314,13 +368,17 @@ def main() -> int:
                    "group_size": GS},
         "frac_of_hbm_peak": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": roofline,
-        "decode_chain": decode_chain,
+        "copy_reference": copy_ref,
     }
     if not args.no_extras:
+        result["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
+        log("decode chain done")
         del layers, batches
         torch.cuda.empty_cache()
         result["per_shape_cold"] = bench_shapes(ops, dev, gen)
+        log("per-shape table done")
         result["topk_us_I6144"] = bench_topk(ops, dev, gen)
+        log("top-k done")
     if not args.no_cpu_baseline:
         g = torch.Generator().manual_seed(1)
         layer0 = []
@@ -330,6 +388,7 @@ def main() -> int:
             q, s = O.quantize_group((torch.randn(N, K, generator=g) * 0.02).numpy(), GS)
             layer0.append((O.pack_int4(q), s, torch.randn(K, generator=g).half().numpy(), K))
         result["cpu_baseline"] = cpu_baseline(layer0)
+        log("cpu baseline done")
     print(json.dumps(result))
     return 0
 
