@@ -8,16 +8,17 @@ weight of a 28-layer Qwen3-1.7B-shaped decoder -- per layer q [2048x2048],
 k/v [1024x2048], o [2048x2048], gate/up [6144x2048], down [2048x6144] --
 196 GEMVs, 750,862,336 algorithmic bytes (packed weights + fp32 scales +
 fp16 x + fp16 y), each weight resident in HBM and touched once per step
-(751 MB > the 256 MB Infinity Cache, so reads come from HBM). Independent
-GEMVs of one shape class run as one batched launch (4 launches per step).
+(751 MB > the 256 MB Infinity Cache, so reads come from HBM). The 196
+independent GEMVs run as ONE grouped launch per step (4 shape classes).
 value = algorithmic bytes / step time, timed over --steps steps between two
 device synchronisations.
 
 Also reported:
-  roofline        the dominant launch (56 x gate/up 6144x2048), timed per launch
-                  with HIP events on the launching stream; `traffic` is the
+  roofline        the dominant (and only) launch of a step, timed with HIP events
+                  around back-to-back launches on the launching stream; `traffic` is the
                   HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter
                   summary committed under profiles/ (null when absent);
+  batched_per_class  the same GEMVs as one launch per shape class, per class;
   copy_reference  a plain device-to-device copy of 512 MiB (the calibration
                   kernel of the counter runs, and the box's streaming rate);
   decode_chain    the 112 dependent launches of one decode step, graph-replayed;
@@ -85,23 +86,19 @@ def make_int8(N, K, gen, device):
     return qt.qweight.contiguous(), qt.scale.contiguous()
 
 
-def time_per_launch(fn, args_list, reps: int = 3):
-    """Average kernel time from HIP events recorded around each launch on the launching stream."""
+def time_back_to_back(fn, launches: int = 30):
+    """Average duration of `launches` back-to-back launches: two HIP events on the launching (current) stream."""
     import torch
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(len(args_list) * reps)]
+    fn()
     torch.cuda.synchronize()
-    i = 0
-    for _ in range(reps):
-        for a in args_list:
-            ev[i][0].record()
-            fn(*a)
-            ev[i][1].record()
-            i += 1
-    torch.cuda.synchronize()
-    ts = sorted(s.elapsed_time(e) * 1e3 for s, e in ev)  # microseconds
-    return {"mean_us": sum(ts) / len(ts), "median_us": ts[len(ts) // 2], "p90_us": ts[int(len(ts) * 0.9)]}
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(launches):
+        fn()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) * 1e3 / launches  # microseconds
 
 
 def time_graph_per_launch(fn, args_list, reps: int = 5):
@@ -125,7 +122,7 @@ def time_graph_per_launch(fn, args_list, reps: int = 5):
     return {"mean_us": us, "p90_us": us}
 
 
-TRAFFIC_FILE = REPO / "profiles" / "gemv_int4_batched_gate_up_qwen3_1p7b_traffic.md"
+TRAFFIC_FILE = REPO / "profiles" / "gemv_int4_grouped_qwen3_1p7b_step_traffic.md"
 
 
 def read_traffic(path: Path = TRAFFIC_FILE):
@@ -146,10 +143,10 @@ def copy_reference(nbytes: int = 512 << 20, reps: int = 10):
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 256)
     dst = torch.empty_like(src)
     dst.copy_(src)
-    t = time_per_launch(lambda: dst.copy_(src), [()], reps=reps)
+    us = time_back_to_back(lambda: dst.copy_(src), launches=reps)
     del src, dst
-    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(t["mean_us"], 2),
-            "GBps": round(2 * nbytes / (t["mean_us"] * 1e-6) / 1e9, 1)}
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
+            "GBps": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
 
 
 def cold_copies(nbytes: int, target: int = 600 << 20) -> int:
@@ -302,18 +299,13 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"weight set ready: {LAYERS} layers, {step_bytes} bytes per step")
 
-    # One step = every GEMV of the weight set. Independent GEMVs of one shape
-    # class run as one batched launch (4 launches per step).
-    classes = [("gate", "up"), ("q", "o"), ("k", "v"), ("down",)]
-    batches = []
-    for names in classes:
-        group = [layers[l][n] for l in range(LAYERS) for n in names]
-        N, K = group[0][3], group[0][4]
-        batches.append(ops.GemvBatch([g[0] for g in group], [g[1] for g in group], [g[2] for g in group], K, GS))
+    # One step = every GEMV of the weight set, all 196 in ONE grouped launch
+    # (4 shape classes; the long-row down class is laid out first).
+    order = [(l, n) for l in range(LAYERS) for n, _, _ in LAYER_SHAPES]
+    group = ops.GemvGroup([(layers[l][n][0], layers[l][n][1], layers[l][n][2], layers[l][n][4]) for l, n in order], GS)
 
     def step():
-        for b in batches:
-            b.run()
+        group.run()
 
     for _ in range(3):
         step()
@@ -330,20 +322,37 @@ def main() -> int:
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9  # GB/s
 
-    # the batched outputs equal single launches (spot check, bit-exact)
-    g0 = layers[0]["gate"]
-    assert torch.equal(batches[0].ys[0], ops.gemv_w4a16_group_lop3(g0[0], g0[1], g0[2], g0[4], GS))
+    # the grouped outputs equal single launches (spot checks, bit-exact)
+    for i in (0, 4, 6, len(order) - 1):
+        l, n = order[i]
+        m = layers[l][n]
+        assert torch.equal(group.ys[i], ops.gemv_w4a16_group_lop3(m[0], m[1], m[2], m[4], GS)), f"grouped {l}.{n}"
 
-    # ---- dominant kernel: the batched gate/up launch (56 x 6144x2048), HIP events per launch ----
-    dom_bytes = 2 * LAYERS * int4_bytes(I, H)
-    tdom = time_per_launch(lambda b: b.run(), [(batches[0],)], reps=30)
-    achieved = dom_bytes / (tdom["mean_us"] * 1e-6) / 1e9
+    # ---- dominant kernel: the grouped launch (the whole step), HIP events around back-to-back launches ----
+    dom_us = time_back_to_back(group.run, launches=30)
+    achieved = step_bytes / (dom_us * 1e-6) / 1e9
+    n_wg = sum(c * (nn // 8) for c, nn in zip(group.class_count, group.class_N))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(),
-                "kernel": "soi::gemv_int4_batched_kernel<8,1,true,true,true> (56 x gate/up 6144x2048, "
-                          "43008 workgroups of 64)",
-                "bytes_per_launch": dom_bytes, "avg_launch_us": round(tdom["mean_us"], 3)}
-    log(f"dominant launch: {tdom['mean_us']:.3f} us")
+                "kernel": f"soi::gemv_int4_grouped_kernel<8,true,true,true> (196 GEMVs in 4 shape classes, "
+                          f"{n_wg} workgroups of 64)",
+                "bytes_per_launch": step_bytes, "avg_launch_us": round(dom_us, 3),
+                "timing": "HIP events around 30 back-to-back launches on the launching stream"}
+    log(f"dominant launch: {dom_us:.3f} us")
+
+    # ---- the same work as one batched launch per shape class (4 launches), per class ----
+    per_class = {}
+    for names in (("down",), ("gate", "up"), ("q", "o"), ("k", "v")):
+        mats = [layers[l][n] for l in range(LAYERS) for n in names]
+        N, K = mats[0][3], mats[0][4]
+        bt = ops.GemvBatch([m[0] for m in mats], [m[1] for m in mats], [m[2] for m in mats], K, GS)
+        us = time_back_to_back(bt.run, launches=20)
+        nbytes = len(mats) * int4_bytes(N, K)
+        per_class["/".join(names)] = {"problems": len(mats), "N": N, "K": K, "bytes": nbytes, "us": round(us, 3),
+                                      "GBps": round(nbytes / us / 1e3, 1),
+                                      "frac_of_hbm": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+        del bt
+    log("per-class batched launches done")
     copy_ref = copy_reference()
     log(f"copy reference: {copy_ref['us']} us")
 
@@ -363,17 +372,18 @@ def main() -> int:
         "data": "synthetic: W ~ N(0,0.02) quantized INT4 g128 (fp32 scales), x ~ N(0,1) fp16, seeded",
         "config": {"workload": "INT4 g128 GEMV sweep at batch 1 over all 196 linear weights of a 28-layer "
                                "Qwen3-1.7B-shaped decoder (q,k,v,o,gate,up,down; each GEMV its own x), HBM-resident; "
-                               "independent same-shape GEMVs batched into one launch (4 launches per step)",
+                               "all 196 GEMVs in one grouped launch per step",
                    "bytes_per_step": step_bytes, "layers": LAYERS, "hidden": H, "intermediate": I,
                    "group_size": GS},
         "frac_of_hbm_peak": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": roofline,
         "copy_reference": copy_ref,
+        "batched_per_class": per_class,
     }
     if not args.no_extras:
         result["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
         log("decode chain done")
-        del layers, batches
+        del layers, group
         torch.cuda.empty_cache()
         result["per_shape_cold"] = bench_shapes(ops, dev, gen)
         log("per-shape table done")

@@ -73,6 +73,20 @@ int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* sc
                            const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t P, int64_t N, int64_t K,
                            int64_t group_size, int64_t num_groups, void* stream);
 
+/* Grouped form: independent problems of up to 8 shape classes in ONE launch.
+ * The pointer tables (device arrays, as for the batched form) list the
+ * problems class by class: class c has class_count[c] problems of shape
+ * [class_N[c], class_K[c]] with ceil(class_K[c]/group_size) scale columns.
+ * class_count, class_N, class_K are HOST arrays of num_classes (<= 8)
+ * entries. Workgroups are laid out class by class in the given order (put
+ * the longest rows first to keep the tail short). Each y is bit-identical to
+ * soi_gemv_w4a16_group_lop3 on that problem. No reference counterpart: one
+ * launch for a whole decoder's independent GEMVs. */
+int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
+                           const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t num_classes,
+                           const int64_t* class_count, const int64_t* class_N, const int64_t* class_K,
+                           int64_t group_size, void* stream);
+
 /* --------------------------------------------------------------------------
  * INT8 GEMV, y[N] = sum_k scale[n*scale_row_stride + k/group_size] * Wq[n,k] * x[k].
  * Wq: int8 [N, K]; scale: fp32 [N or 1, num_groups]; scale_row_stride is 0

@@ -17,6 +17,7 @@
 
 #include <cmath>
 #include <tuple>
+#include <vector>
 
 #include "../../include/soinfer_amd.h"
 
@@ -159,6 +160,31 @@ void gemv_w4a16_batched(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::
                                         reinterpret_cast<uint16_t* const*>(y_ptrs.data_ptr<int64_t>()),
                                         Wq_ptrs.size(0), N, K, group_size, expected_num_groups(K, group_size),
                                         cur_stream(Wq_ptrs)),
+                 name);
+}
+
+void gemv_w4a16_grouped(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::Tensor x_ptrs, torch::Tensor y_ptrs,
+                        std::vector<int64_t> class_count, std::vector<int64_t> class_N, std::vector<int64_t> class_K,
+                        int64_t group_size) {
+    const char* name = "gemv_w4a16_grouped";
+    for (const auto* t : {&Wq_ptrs, &scale_ptrs, &x_ptrs, &y_ptrs}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kInt64 && t->dim() == 1 && t->is_contiguous(), name,
+                    ": pointer tables must be contiguous 1D int64 CUDA tensors");
+        TORCH_CHECK(t->size(0) == Wq_ptrs.size(0), name, ": pointer tables must have the same length");
+        check_same_device(Wq_ptrs, *t, name);
+    }
+    TORCH_CHECK(class_count.size() == class_N.size() && class_count.size() == class_K.size(), name,
+                ": class arrays must have the same length");
+    int64_t total = 0;
+    for (int64_t c : class_count) total += c;
+    TORCH_CHECK(total == Wq_ptrs.size(0), name, ": class counts must add up to the pointer table length");
+    const at::DeviceGuard guard(Wq_ptrs.device());
+    check_status(soi_gemv_w4a16_grouped(reinterpret_cast<const uint8_t* const*>(Wq_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const float* const*>(scale_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const uint16_t* const*>(x_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<uint16_t* const*>(y_ptrs.data_ptr<int64_t>()),
+                                        static_cast<int64_t>(class_count.size()), class_count.data(), class_N.data(),
+                                        class_K.data(), group_size, cur_stream(Wq_ptrs)),
                  name);
 }
 
@@ -491,6 +517,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_w4a16_group", &gemv_w4a16_group, "INT4 group GEMV (scalar nibble dequant)");
     m.def("gemv_w4a16_group_lop3", &gemv_w4a16_group_lop3, "INT4 group GEMV (bitfield dequant)");
     m.def("gemv_w4a16_batched", &gemv_w4a16_batched, "P same-shape INT4 GEMVs in one launch");
+    m.def("gemv_w4a16_grouped", &gemv_w4a16_grouped, "INT4 GEMVs of up to 8 shapes in one launch");
     m.def("gemv_w4a16_sparse_accumulate", &gemv_w4a16_sparse_accumulate, "sparse down-proj accumulate");
     m.def("build_dip_descriptors", &build_dip_descriptors, "hot-cache descriptors");
     m.def("gemv_dip_fused_up", &gemv_dip_fused_up, "descriptor-driven up GEMV");

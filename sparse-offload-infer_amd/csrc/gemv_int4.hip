@@ -236,6 +236,58 @@ __global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* co
     gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, x, y, K, gs, static_cast<int64_t>(tile) * R);
 }
 
+// Grouped form: problems of up to kMaxClasses shapes in one launch. Class c
+// owns workgroups [first_wg[c], first_wg[c+1]) and problems
+// [first_problem[c], first_problem[c] + count[c]) of the pointer tables; the
+// class of a workgroup is found by comparisons against kernel arguments
+// (constant indices only, so the table stays in SGPRs).
+constexpr int kMaxClasses = 8;
+
+struct GroupClasses {
+    int n;
+    int first_wg[kMaxClasses];
+    int tiles[kMaxClasses];
+    int first_problem[kMaxClasses];
+    int N[kMaxClasses];
+    int K[kMaxClasses];
+    int G[kMaxClasses];
+};
+
+template <int R, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int4_grouped_kernel(const uint8_t* const* __restrict__ Wp,
+                                                               const float* const* __restrict__ Sp,
+                                                               const uint16_t* const* __restrict__ Xp,
+                                                               uint16_t* const* __restrict__ Yp, GroupClasses cl,
+                                                               int gs) {
+    const int b = blockIdx.x;
+    int first = cl.first_wg[0], tiles = cl.tiles[0], p0 = cl.first_problem[0];
+    int N = cl.N[0], K = cl.K[0], G = cl.G[0];
+#pragma unroll
+    for (int i = 1; i < kMaxClasses; ++i) {
+        if (i < cl.n && b >= cl.first_wg[i]) {
+            first = cl.first_wg[i];
+            tiles = cl.tiles[i];
+            p0 = cl.first_problem[i];
+            N = cl.N[i];
+            K = cl.K[i];
+            G = cl.G[i];
+        }
+    }
+    const int local = b - first;
+    const int pi = local / tiles;
+    const int tile = local - pi * tiles;
+    const int p = p0 + pi;
+    const uint8_t* W = ldg(Wp + p);
+    const float* S = ldg(Sp + p);
+    const uint16_t* x = ldg(Xp + p);
+    uint16_t* y = ldg(Yp + p);
+    const uintptr_t bad = reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x);
+    if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
+    const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
+    DenseRows rows{W, S, row_bytes, G};
+    gemv_int4_tile<R, 1, VEC, CHUNK_SCALE, true, FULL>(rows, N, x, y, K, gs, static_cast<int64_t>(tile) * R);
+}
+
 // ---------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------
@@ -420,6 +472,65 @@ extern "C" int soi_gemv_w4a16_indexed(const uint8_t* Wq, const float* scale, int
     const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
     IndexRows rows{Wq, scale, num_rows, idx, row_bytes, num_groups};
     return launch_int4<true>(rows, k, x, y, K, group_size, vec, as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
+                                      const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t num_classes,
+                                      const int64_t* class_count, const int64_t* class_N, const int64_t* class_K,
+                                      int64_t group_size, void* stream) {
+    const char* what = "soi_gemv_w4a16_grouped";
+    SOI_REQUIRE(num_classes >= 0 && num_classes <= kMaxClasses, "%s: num_classes must be in [0, %d], got %lld", what,
+                kMaxClasses, (long long)num_classes);
+    if (num_classes == 0) return SOI_OK;
+    SOI_REQUIRE(class_count && class_N && class_K, "%s: null class array", what);
+    SOI_REQUIRE(group_size >= 1 && group_size % 8 == 0, "%s: group_size must be a positive multiple of 8", what);
+    constexpr int R = 8;
+    GroupClasses cl{};
+    int64_t wg = 0, problems = 0;
+    bool vec = true, full = (group_size % 32) == 0;
+    int n = 0;
+    for (int64_t c = 0; c < num_classes; ++c) {
+        const int64_t P = class_count[c], N = class_N[c], K = class_K[c];
+        SOI_REQUIRE(P >= 0 && N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: class %lld count or N out of range", what,
+                    (long long)c);
+        SOI_REQUIRE(K >= 1 && K <= (int64_t(1) << 30), "%s: class %lld K must be in [1, 2^30]", what, (long long)c);
+        if (P == 0 || N == 0) {
+            problems += P;
+            continue;
+        }
+        const int64_t tiles = ceil_div64(N, R);
+        cl.first_wg[n] = static_cast<int>(wg);
+        cl.tiles[n] = static_cast<int>(tiles);
+        cl.first_problem[n] = static_cast<int>(problems);
+        cl.N[n] = static_cast<int>(N);
+        cl.K[n] = static_cast<int>(K);
+        cl.G[n] = static_cast<int>(ceil_div64(K, group_size));
+        vec = vec && (K % 32) == 0;
+        full = full && (N % R) == 0 && ((K / 32) % 64) == 0;
+        wg += tiles * P;
+        problems += P;
+        ++n;
+        SOI_REQUIRE(wg <= (int64_t(1) << 31) - 1 && problems <= (int64_t(1) << 31) - 1, "%s: too many row tiles",
+                    what);
+    }
+    if (n == 0) return SOI_OK;
+    SOI_REQUIRE(Wq_ptrs && scale_ptrs && x_ptrs && y_ptrs, "%s: null pointer table", what);
+    cl.n = n;
+    full = full && vec;
+    const dim3 grid(static_cast<unsigned>(wg));
+    const int gi = static_cast<int>(group_size);
+    const bool cs = (group_size % 32) == 0;
+    hipStream_t st = as_stream(stream);
+#define SOI_G(V, CS, FL) \
+    hipLaunchKernelGGL((gemv_int4_grouped_kernel<R, V, CS, FL>), grid, dim3(64), 0, st, Wq_ptrs, scale_ptrs, x_ptrs, \
+                       y_ptrs, cl, gi)
+    if (full) SOI_G(true, true, true);
+    else if (vec && cs) SOI_G(true, true, false);
+    else if (vec) SOI_G(true, false, false);
+    else if (cs) SOI_G(false, true, false);
+    else SOI_G(false, false, false);
+#undef SOI_G
+    return launch_status(what);
 }
 
 extern "C" int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,

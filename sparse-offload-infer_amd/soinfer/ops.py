@@ -77,6 +77,57 @@ class GemvBatch:
         return self.ys
 
 
+class GemvGroup:
+    """Independent INT4 GEMVs of up to 8 different shapes executed in ONE kernel launch.
+
+    problems: list of (Wq, scale, x, K). Problems are grouped by shape; classes are
+    laid out longest-row first. run() is a single launch; ys[i] (same order as
+    problems) is bit-identical to gemv_w4a16_group_lop3 on problem i."""
+
+    def __init__(self, problems, group_size: int, ys=None):
+        if not problems:
+            raise ValueError("GemvGroup: no problems")
+        dev = problems[0][0].device
+        shapes = []
+        for W, s, x, K in problems:
+            N = W.shape[0]
+            G = -(-K // group_size)
+            if not (W.dtype == torch.uint8 and W.is_contiguous() and tuple(W.shape) == (N, -(-K // 8) * 4)):
+                raise RuntimeError("GemvGroup: every Wq must be a contiguous uint8 [N, ceil(K/8)*4] tensor")
+            if not (s.dtype == torch.float32 and s.is_contiguous() and tuple(s.shape) == (N, G)):
+                raise RuntimeError("GemvGroup: every scale must be a contiguous float32 [N, ceil(K/gs)] tensor")
+            if not (x.dtype == torch.float16 and x.is_contiguous() and tuple(x.shape) == (K,)):
+                raise RuntimeError("GemvGroup: every x must be a contiguous float16 [K] tensor")
+            if not all(t.device == dev for t in (W, s, x)):
+                raise RuntimeError("GemvGroup: all tensors must be on one device")
+            shapes.append((N, K))
+        classes = sorted(set(shapes), key=lambda nk: (-nk[1], -nk[0]))
+        if len(classes) > 8:
+            raise RuntimeError("GemvGroup: at most 8 distinct shapes per launch")
+        if ys is None:
+            ys = [torch.empty(N, dtype=torch.float16, device=dev) for N, _ in shapes]
+        for y, (N, _) in zip(ys, shapes):
+            if not (y.dtype == torch.float16 and y.is_contiguous() and tuple(y.shape) == (N,) and y.device == dev):
+                raise RuntimeError("GemvGroup: every y must be a contiguous float16 [N] tensor on the device")
+        order = [i for c in classes for i, sh in enumerate(shapes) if sh == c]
+        self._keep = ([problems[i][0] for i in order], [problems[i][1] for i in order],
+                      [problems[i][2] for i in order], [ys[i] for i in order])
+        self.ys = list(ys)
+        self.class_count = [shapes.count(c) for c in classes]
+        self.class_N = [c[0] for c in classes]
+        self.class_K = [c[1] for c in classes]
+        self.group_size = group_size
+
+        def table(ts):
+            return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+
+        self._tables = tuple(table(ts) for ts in self._keep)
+
+    def run(self):
+        _C.gemv_w4a16_grouped(*self._tables, self.class_count, self.class_N, self.class_K, self.group_size)
+        return self.ys
+
+
 def gemv_w4a16_batched(Wqs, scales, xs, K: int, group_size: int):
     """Convenience one-shot form of GemvBatch: returns the list of outputs."""
     return GemvBatch(Wqs, scales, xs, K, group_size).run()

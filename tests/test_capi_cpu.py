@@ -72,6 +72,13 @@ def test_argument_checks_return_before_launch(lib):
     buf = (C.c_uint8 * 64)()
     assert g(buf, 4, 8, idx, 2, buf, None) == 1  # index 5 out of range [0, 4)
     assert b"out of range" in lib.soi_last_error()
+    gr = lib.soi_gemv_w4a16_grouped
+    gr.argtypes = [C.c_void_p] * 4 + [i64, C.c_void_p, C.c_void_p, C.c_void_p, i64, C.c_void_p]
+    cnt, n, k = (C.c_int64 * 9)(*[1] * 9), (C.c_int64 * 9)(*[8] * 9), (C.c_int64 * 9)(*[256] * 9)
+    assert gr(None, None, None, None, 9, cnt, n, k, 128, None) == 1  # more than 8 classes
+    assert b"num_classes" in lib.soi_last_error()
+    assert gr(None, None, None, None, 1, cnt, n, k, 12, None) == 1  # group_size not a multiple of 8
+    assert gr(None, None, None, None, 0, None, None, None, 128, None) == 0  # nothing to do
 
 
 def test_workspace_queries(lib):

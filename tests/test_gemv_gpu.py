@@ -178,3 +178,38 @@ def test_batched_rejects_mismatched_shapes(ops):
     b = int4_problem(32, 256, 128, seed=2)
     with pytest.raises(RuntimeError):
         ops.gemv_w4a16_batched([a["Wq_d"], b["Wq_d"]], [a["s_d"], b["s_d"]], [a["x_d"], b["x_d"]], 256, 128)
+
+
+# ---------------------------------------------------------------------------
+# grouped (one launch, several shapes)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("gs,shapes", [
+    (128, [(6144, 2048, 2), (2048, 6144, 2), (2048, 2048, 3), (1024, 2048, 3)]),  # Qwen3-1.7B classes (FULL path)
+    (32, [(37, 512, 2), (64, 256, 3), (7, 96, 2)]),  # ragged N, short rows
+    (8, [(33, 200, 2), (5, 8, 1), (17, 1000, 2)]),  # K not a multiple of 32 (dword path)
+])
+def test_grouped_bit_identical_to_single(ops, gs, shapes):
+    probs = []
+    for i, (N, K, P) in enumerate(shapes):
+        for j in range(P):
+            probs.append(int4_problem(N, K, gs, seed=1000 + 17 * i + j))
+    # interleave shapes so the grouping has to reorder
+    probs = probs[::2] + probs[1::2]
+    grp = ops.GemvGroup([(p["Wq_d"], p["s_d"], p["x_d"], p["K"]) for p in probs], gs)
+    ys = grp.run()
+    for p, y in zip(probs, ys):
+        assert torch.equal(y, ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], gs))
+    assert_close(ys[0], O.gemv_w4_f64(probs[0]["Wq"], probs[0]["s"], probs[0]["x"], probs[0]["K"], gs), "grouped")
+    again = [y.clone() for y in ys]
+    grp.run()
+    assert all(torch.equal(a, b) for a, b in zip(again, grp.ys))
+
+
+def test_grouped_rejects_bad_arguments(ops):
+    a = int4_problem(64, 256, 128, seed=1)
+    with pytest.raises(RuntimeError):
+        ops.GemvGroup([(a["Wq_d"], a["s_d"], a["x_d"], 512)], 128)  # K does not match the packed width
+    many = [int4_problem(8 * (i + 1), 64, 32, seed=i) for i in range(9)]
+    with pytest.raises(RuntimeError):
+        ops.GemvGroup([(p["Wq_d"], p["s_d"], p["x_d"], 64) for p in many], 32)  # 9 distinct shapes
