@@ -110,6 +110,13 @@ int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16_t* x, uint
 int soi_topk_threshold_select(const float* abs_g, int64_t n, int64_t k, int32_t* out_indices, int32_t* out_count,
                               void* stream);
 
+/* Same selection over |gate| of binary16 gate values: identical output to
+ * soi_topk_threshold_select on gate.float().abs() (the conversion and the
+ * absolute value are exact). Fuses the glue of generate.py:276-277 into the
+ * load; no separate reference entry point. */
+int soi_topk_threshold_select_f16abs(const uint16_t* gate, int64_t n, int64_t k, int32_t* out_indices,
+                                     int32_t* out_count, void* stream);
+
 /* --------------------------------------------------------------------------
  * Row gather from pinned host memory into device memory.
  * matrix: pinned host bytes [num_rows, row_nbytes]; indices: host int64 [k],
@@ -133,6 +140,15 @@ int soi_gather_rows_naive(const uint8_t* matrix, int64_t num_rows, int64_t row_n
  * No reference counterpart: on MI355X the weights stay resident in HBM. */
 int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
                            int64_t k, uint8_t* dst, void* stream);
+
+/* Same with the row count read from device memory: rows j < count[0] (<= max_k)
+ * are copied. src may be a device mapping of pinned host memory
+ * (hipHostGetDevicePointer), so the hot-cache miss rows can be fetched inside
+ * a captured graph with no host round trip. No reference counterpart: the
+ * reference copies misses with host-side gathers after a device-to-host sync
+ * (generate.py:367-404). */
+int soi_gather_rows_device_counted(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
+                                   const int32_t* count, int64_t max_k, uint8_t* dst, void* stream);
 
 /* --------------------------------------------------------------------------
  * Sparse down projection over k gathered rows of down_proj^T:
@@ -211,6 +227,72 @@ size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t hea
 int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
                          int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, int64_t cur_len, float scale,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device-position form of soi_decode_attention: cur_len = pos[0] + 1 read on
+ * the device (clamped to [1, max_seq]), so one captured graph serves every
+ * position. The split plan is the one for cur_len = max_seq; splits past the
+ * current length contribute nothing. Workspace: soi_decode_attention_workspace_bytes
+ * (NQ, NKV, head_dim, max_seq). Used by the decode engine. */
+int soi_decode_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                            int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, const int32_t* pos,
+                            float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Decoder-step glue (binary16 in/out, fp32 math).
+ *
+ * soi_rmsnorm: out[r,:] = x[r,:] * rsqrt(mean(x[r,:]^2) + eps) * weight, one
+ *   row of `hidden` per r. Replaces launch_rmsnorm (csrc/kernels/rmsnorm.cu:
+ *   46-50; binding csrc/bindings.cpp:141-150); qk_norm is the same op with
+ *   rows = heads, hidden = head_dim (python/soinfer/ops.py qk_norm).
+ * soi_residual_rmsnorm: x[r,:] <- x[r,:] + delta[r,:] (binary16 add, in place),
+ *   then out = rmsnorm(x). Fuses `h2 = residual + o` and the next rmsnorm of
+ *   generate.py:171-175; identical to the two separate ops.
+ * soi_rope_apply: RoPE in place on x [num_heads, head_dim], rotate-half
+ *   convention, cos/sin fp32 [head_dim/2]. Replaces launch_rope_apply
+ *   (rope.cu:21-25; bindings.cpp:490-505).
+ * soi_kv_cache_append: k/v_new [NKV, hd] into k/v_cache [NKV, max_seq, hd] at
+ *   pos. Replaces launch_kv_cache_append (kv_cache.cu:22-27; bindings.cpp:450-466).
+ * soi_gemv_f16: y[N] = W[N,K] x[K] with fp16 W (the LM head). Replaces
+ *   launch_gemv_fp16_v3 (gemv_fp16.cu:89-93; bindings.cpp:201-208).
+ * soi_argmax_f16: index of the largest of n binary16 values (NaN above every
+ *   number, ties to the lowest index: torch.argmax, generate.py:446). Writes
+ *   out_index[0]; if log/log_len are given, also log[log_len[0]] = index and
+ *   log_len[0] += 1 while log_len[0] < log_cap. Workspace:
+ *   soi_argmax_workspace_bytes(n).
+ * soi_silu_mul: out = fp16(silu(fp32 gate) * fp32 up), silu(t) = t/(1+exp(-t))
+ *   (generate.py:178). soi_silu_mul_indexed: out[j] = fp16(silu(gate[idx[j]]) *
+ *   u_sel[j]) (generate.py:304-305); an index outside [0, n_gate) gives NaN.
+ * soi_embed_lookup: out = table[token[0], :] with the token read on the device
+ *   (a token outside [0, rows) gives zeros) (generate.py:440).
+ * soi_qk_norm_rope_append: the engine form of q/k norm + RoPE + KV append of
+ *   one layer (generate.py:160-168) for the fused projection qkv
+ *   [q (NQ*hd) | k (NKV*hd) | v (NKV*hd)], at position pos[0] read on the
+ *   device, with RoPE tables cos/sin fp32 [max_seq, hd/2]. Writes q_out
+ *   [NQ, hd] and the caches; a position outside [0, max_seq) writes nothing.
+ * soi_advance_position: pos[0] += delta on the device.
+ * ------------------------------------------------------------------------ */
+int soi_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* out, int64_t rows, int64_t hidden, float eps,
+                void* stream);
+int soi_residual_rmsnorm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out, int64_t rows,
+                         int64_t hidden, float eps, void* stream);
+int soi_rope_apply(uint16_t* x, const float* cos_vals, const float* sin_vals, int64_t num_heads, int64_t head_dim,
+                   void* stream);
+int soi_kv_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
+                        int64_t num_kv_heads, int64_t max_seq, int64_t head_dim, int64_t pos, void* stream);
+int soi_gemv_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N, int64_t K, void* stream);
+size_t soi_argmax_workspace_bytes(int64_t n);
+int soi_argmax_f16(const uint16_t* x, int64_t n, int32_t* out_index, int32_t* log, int32_t* log_len, int64_t log_cap,
+                   void* workspace, size_t workspace_bytes, void* stream);
+int soi_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, void* stream);
+int soi_silu_mul_indexed(const uint16_t* gate, int64_t n_gate, const int32_t* idx, const uint16_t* u_sel,
+                         uint16_t* out, int64_t k, void* stream);
+int soi_embed_lookup(const uint16_t* table, int64_t rows, int64_t hidden, const int32_t* token, uint16_t* out,
+                     void* stream);
+int soi_qk_norm_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                            const float* cos_table, const float* sin_table, const int32_t* pos, uint16_t* q_out,
+                            uint16_t* k_cache, uint16_t* v_cache, int64_t num_q_heads, int64_t num_kv_heads,
+                            int64_t max_seq, int64_t head_dim, float eps, void* stream);
+int soi_advance_position(int32_t* pos, int32_t delta, void* stream);
 
 #ifdef __cplusplus
 }

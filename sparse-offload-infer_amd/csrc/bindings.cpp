@@ -511,6 +511,414 @@ void gather_rows_naive(torch::Tensor matrix, torch::Tensor indices, torch::Tenso
                  "gather_rows_naive");
 }
 
+// ---------------------------------------------------------------------------
+// decoder-step glue (reference names: rmsnorm 141-150, gemv_fp16_v3 201-208,
+// kv_cache_append 450-466, rope_apply 490-505)
+// ---------------------------------------------------------------------------
+
+torch::Tensor rmsnorm(torch::Tensor x, torch::Tensor weight, double eps) {
+    check_f16_cuda_contiguous(x, "rmsnorm(x)");
+    check_f16_cuda_contiguous(weight, "rmsnorm(weight)");
+    TORCH_CHECK(x.dim() == 2, "rmsnorm: x must be 2D [rows, hidden]");
+    TORCH_CHECK(weight.dim() == 1 && weight.size(0) == x.size(1), "rmsnorm: weight shape must match x's hidden dim");
+    TORCH_CHECK(x.size(1) % 2 == 0, "rmsnorm: hidden dim must be even (half2 vectorization)");
+    check_same_device(x, weight, "rmsnorm");
+    const at::DeviceGuard guard(x.device());
+    auto out = torch::empty_like(x);
+    check_status(soi_rmsnorm(h16(x), h16(weight), h16m(out), x.size(0), x.size(1), static_cast<float>(eps),
+                             cur_stream(x)),
+                 "rmsnorm");
+    return out;
+}
+
+torch::Tensor gemv_fp16_v3(torch::Tensor W, torch::Tensor x) {
+    check_f16_cuda_contiguous(W, "gemv_fp16_v3(W)");
+    check_f16_cuda_contiguous(x, "gemv_fp16_v3(x)");
+    TORCH_CHECK(W.dim() == 2, "gemv_fp16_v3: W must be 2D [N, K]");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == W.size(1), "gemv_fp16_v3: x must be 1D [K] matching W's K");
+    TORCH_CHECK(W.size(1) % 8 == 0, "gemv_fp16_v3: K must be a multiple of 8 (float4-vectorized loads)");
+    check_same_device(W, x, "gemv_fp16_v3");
+    const at::DeviceGuard guard(x.device());
+    auto y = torch::empty({W.size(0)}, x.options());
+    check_status(soi_gemv_f16(h16(W), h16(x), h16m(y), W.size(0), W.size(1), cur_stream(x)), "gemv_fp16_v3");
+    return y;
+}
+
+void kv_cache_append(torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor k_new, torch::Tensor v_new,
+                     int64_t pos) {
+    check_f16_cuda_contiguous(k_cache, "kv_cache_append(k_cache)");
+    check_f16_cuda_contiguous(v_cache, "kv_cache_append(v_cache)");
+    check_f16_cuda_contiguous(k_new, "kv_cache_append(k_new)");
+    check_f16_cuda_contiguous(v_new, "kv_cache_append(v_new)");
+    TORCH_CHECK(k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes(),
+                "kv_cache_append: k_cache/v_cache must be 3D [num_kv_heads, max_seq_len, head_dim] and same shape");
+    TORCH_CHECK(k_new.sizes() == v_new.sizes(), "kv_cache_append: k_new/v_new must have the same shape");
+    TORCH_CHECK(k_new.dim() == 2 && k_new.size(0) == k_cache.size(0) && k_new.size(1) == k_cache.size(2),
+                "kv_cache_append: k_new/v_new must be 2D [num_kv_heads, head_dim] matching the cache");
+    TORCH_CHECK(pos >= 0 && pos < k_cache.size(1), "kv_cache_append: pos out of range for max_seq_len");
+    for (const auto* t : {&v_cache, &k_new, &v_new}) check_same_device(k_cache, *t, "kv_cache_append");
+    const at::DeviceGuard guard(k_cache.device());
+    check_status(soi_kv_cache_append(h16(k_new), h16(v_new), h16m(k_cache), h16m(v_cache), k_cache.size(0),
+                                     k_cache.size(1), k_cache.size(2), pos, cur_stream(k_cache)),
+                 "kv_cache_append");
+}
+
+void rope_apply(torch::Tensor x, torch::Tensor cos_vals, torch::Tensor sin_vals) {
+    check_f16_cuda_contiguous(x, "rope_apply(x)");
+    TORCH_CHECK(x.dim() == 2, "rope_apply: x must be 2D [num_heads, head_dim]");
+    TORCH_CHECK(x.size(1) % 2 == 0, "rope_apply: head_dim must be even");
+    TORCH_CHECK(cos_vals.is_cuda() && cos_vals.scalar_type() == torch::kFloat32 && cos_vals.is_contiguous(),
+                "rope_apply: cos_vals must be a contiguous float32 CUDA tensor");
+    TORCH_CHECK(sin_vals.is_cuda() && sin_vals.scalar_type() == torch::kFloat32 && sin_vals.is_contiguous() &&
+                    sin_vals.sizes() == cos_vals.sizes(),
+                "rope_apply: sin_vals must match cos_vals (contiguous float32 CUDA, same shape)");
+    TORCH_CHECK(cos_vals.dim() == 1 && cos_vals.size(0) == x.size(1) / 2,
+                "rope_apply: cos_vals/sin_vals must be 1D [head_dim / 2]");
+    check_same_device(x, cos_vals, "rope_apply");
+    check_same_device(x, sin_vals, "rope_apply");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_rope_apply(h16m(x), cos_vals.data_ptr<float>(), sin_vals.data_ptr<float>(), x.size(0), x.size(1),
+                                cur_stream(x)),
+                 "rope_apply");
+}
+
+// ---------------------------------------------------------------------------
+// decode-engine forms: write into caller buffers, allocate nothing (so a
+// captured HIP graph replays them); position / token / counts are device int32
+// ---------------------------------------------------------------------------
+
+namespace {
+
+void need(const torch::Tensor& t, torch::ScalarType dt, const torch::Tensor& dev, const char* name, const char* arg) {
+    TORCH_CHECK(t.is_cuda() && t.scalar_type() == dt && t.is_contiguous(), name, "(", arg, "): must be a contiguous ",
+                c10::toString(dt), " CUDA tensor");
+    TORCH_CHECK(t.device() == dev.device(), name, "(", arg, "): all tensors must be on one device");
+}
+
+void need_numel(const torch::Tensor& t, int64_t n, const char* name, const char* arg) {
+    TORCH_CHECK(t.numel() >= n, name, "(", arg, "): needs at least ", n, " elements, has ", t.numel());
+}
+
+}  // namespace
+
+void rmsnorm_into(torch::Tensor x, torch::Tensor weight, torch::Tensor out, double eps) {
+    const char* n = "rmsnorm_into";
+    need(x, torch::kFloat16, x, n, "x");
+    need(weight, torch::kFloat16, x, n, "weight");
+    need(out, torch::kFloat16, x, n, "out");
+    const int64_t hidden = weight.numel();
+    TORCH_CHECK(hidden >= 1 && x.numel() % hidden == 0 && out.numel() == x.numel(), n, ": shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_rmsnorm(h16(x), h16(weight), h16m(out), x.numel() / hidden, hidden, static_cast<float>(eps),
+                             cur_stream(x)),
+                 n);
+}
+
+void residual_rmsnorm_(torch::Tensor x, torch::Tensor delta, torch::Tensor weight, torch::Tensor out, double eps) {
+    const char* n = "residual_rmsnorm_";
+    need(x, torch::kFloat16, x, n, "x");
+    need(delta, torch::kFloat16, x, n, "delta");
+    need(weight, torch::kFloat16, x, n, "weight");
+    need(out, torch::kFloat16, x, n, "out");
+    const int64_t hidden = weight.numel();
+    TORCH_CHECK(hidden >= 1 && x.numel() % hidden == 0 && delta.numel() == x.numel() && out.numel() == x.numel(), n,
+                ": shape mismatch");
+    TORCH_CHECK(out.data_ptr() != x.data_ptr() && out.data_ptr() != delta.data_ptr(), n,
+                ": out must not alias x or delta");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_residual_rmsnorm(h16m(x), h16(delta), h16(weight), h16m(out), x.numel() / hidden, hidden,
+                                      static_cast<float>(eps), cur_stream(x)),
+                 n);
+}
+
+void qk_norm_rope_append(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm, torch::Tensor cos_table,
+                         torch::Tensor sin_table, torch::Tensor pos, torch::Tensor q_out, torch::Tensor k_cache,
+                         torch::Tensor v_cache, double eps) {
+    const char* n = "qk_norm_rope_append";
+    need(qkv, torch::kFloat16, qkv, n, "qkv");
+    need(q_norm, torch::kFloat16, qkv, n, "q_norm");
+    need(k_norm, torch::kFloat16, qkv, n, "k_norm");
+    need(cos_table, torch::kFloat32, qkv, n, "cos_table");
+    need(sin_table, torch::kFloat32, qkv, n, "sin_table");
+    need(pos, torch::kInt32, qkv, n, "pos");
+    need(q_out, torch::kFloat16, qkv, n, "q_out");
+    need(k_cache, torch::kFloat16, qkv, n, "k_cache");
+    need(v_cache, torch::kFloat16, qkv, n, "v_cache");
+    TORCH_CHECK(k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes(), n,
+                ": caches must be 3D [num_kv_heads, max_seq_len, head_dim] of one shape");
+    TORCH_CHECK(q_out.dim() == 2 && q_out.size(1) == k_cache.size(2), n, ": q_out must be 2D [num_q_heads, head_dim]");
+    const int64_t NQ = q_out.size(0), NKV = k_cache.size(0), S = k_cache.size(1), hd = k_cache.size(2);
+    TORCH_CHECK(qkv.numel() == (NQ + 2 * NKV) * hd, n, ": qkv must hold (NQ + 2*NKV) * head_dim values");
+    TORCH_CHECK(q_norm.numel() == hd && k_norm.numel() == hd, n, ": norm weights must be [head_dim]");
+    TORCH_CHECK(cos_table.numel() == S * (hd / 2) && sin_table.numel() == S * (hd / 2), n,
+                ": RoPE tables must be [max_seq_len, head_dim/2]");
+    need_numel(pos, 1, n, "pos");
+    const at::DeviceGuard guard(qkv.device());
+    check_status(soi_qk_norm_rope_append(h16(qkv), h16(q_norm), h16(k_norm), cos_table.data_ptr<float>(),
+                                         sin_table.data_ptr<float>(), pos.data_ptr<int32_t>(), h16m(q_out),
+                                         h16m(k_cache), h16m(v_cache), NQ, NKV, S, hd, static_cast<float>(eps),
+                                         cur_stream(qkv)),
+                 n);
+}
+
+int64_t decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len) {
+    return static_cast<int64_t>(soi_decode_attention_workspace_bytes(NQ, NKV, head_dim, cur_len));
+}
+
+void decode_attention_at(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor pos,
+                         torch::Tensor out, torch::Tensor workspace_buf) {
+    const char* n = "decode_attention_at";
+    need(q, torch::kFloat16, q, n, "q");
+    need(k_cache, torch::kFloat16, q, n, "k_cache");
+    need(v_cache, torch::kFloat16, q, n, "v_cache");
+    need(pos, torch::kInt32, q, n, "pos");
+    need(out, torch::kFloat16, q, n, "out");
+    need(workspace_buf, torch::kUInt8, q, n, "workspace");
+    TORCH_CHECK(q.dim() == 2 && k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes() &&
+                    q.size(1) == k_cache.size(2) && out.numel() == q.numel(),
+                n, ": shape mismatch");
+    need_numel(pos, 1, n, "pos");
+    const int64_t NQ = q.size(0), NKV = k_cache.size(0), S = k_cache.size(1), hd = k_cache.size(2);
+    const at::DeviceGuard guard(q.device());
+    check_status(soi_decode_attention_at(h16(q), h16(k_cache), h16(v_cache), h16m(out), NQ, NKV, S, hd,
+                                         pos.data_ptr<int32_t>(), 1.0f / std::sqrt(static_cast<float>(hd)),
+                                         workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(q)),
+                 n);
+}
+
+void gemv_w4a16_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x, torch::Tensor y, int64_t K,
+                     int64_t group_size) {
+    const char* n = "gemv_w4a16_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(x, torch::kFloat16, x, n, "x");
+    need(y, torch::kFloat16, x, n, "y");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K, n, ": Wq / x shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0) && y.numel() == Wq.size(0), n,
+                ": scale / y shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_group_lop3(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), h16m(y),
+                                           Wq.size(0), K, group_size, scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void gemv_w4a16_indexed_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
+                             torch::Tensor y, int64_t K, int64_t group_size) {
+    const char* n = "gemv_w4a16_indexed_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(idx, torch::kInt32, x, n, "idx");
+    need(x, torch::kFloat16, x, n, "x");
+    need(y, torch::kFloat16, x, n, "y");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K, n, ": Wq / x shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0) && y.numel() == idx.numel(), n,
+                ": scale / y shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_indexed(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), Wq.size(0),
+                                        idx.data_ptr<int32_t>(), idx.numel(), h16(x), h16m(y), K, group_size,
+                                        scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void gemv_w4a16_indexed_accumulate_into(torch::Tensor Wq_T, torch::Tensor scale_T, torch::Tensor idx,
+                                        torch::Tensor h_sel, torch::Tensor y, int64_t H, int64_t group_size,
+                                        torch::Tensor workspace_buf) {
+    const char* n = "gemv_w4a16_indexed_accumulate_into";
+    need(Wq_T, torch::kUInt8, h_sel, n, "Wq_T");
+    need(scale_T, torch::kFloat32, h_sel, n, "scale_T");
+    need(idx, torch::kInt32, h_sel, n, "idx");
+    need(h_sel, torch::kFloat16, h_sel, n, "h_sel");
+    need(y, torch::kFloat16, h_sel, n, "y");
+    need(workspace_buf, torch::kUInt8, h_sel, n, "workspace");
+    TORCH_CHECK(Wq_T.dim() == 2 && Wq_T.size(1) == ((H + 7) / 8) * 4 && y.numel() == H, n, ": Wq_T / y mismatch");
+    TORCH_CHECK(scale_T.dim() == 2 && scale_T.size(0) == Wq_T.size(0) && h_sel.numel() == idx.numel(), n,
+                ": scale_T / h_sel shape mismatch");
+    const at::DeviceGuard guard(h_sel.device());
+    check_status(soi_gemv_w4a16_indexed_accumulate(Wq_T.data_ptr<uint8_t>(), scale_T.data_ptr<float>(), Wq_T.size(0),
+                                                   idx.data_ptr<int32_t>(), idx.numel(), h16(h_sel), h16m(y), H,
+                                                   group_size, scale_T.size(1), workspace_buf.data_ptr<uint8_t>(),
+                                                   workspace_buf.numel(), cur_stream(h_sel)),
+                 n);
+}
+
+int64_t sparse_accumulate_workspace_bytes(int64_t H, int64_t k) {
+    return static_cast<int64_t>(soi_sparse_accumulate_workspace_bytes(H, k));
+}
+
+void build_dip_descriptors_into(torch::Tensor sel, torch::Tensor slot_of, torch::Tensor desc,
+                                torch::Tensor miss_channels, torch::Tensor miss_count) {
+    const char* n = "build_dip_descriptors_into";
+    for (auto* t : {&sel, &slot_of, &desc, &miss_channels, &miss_count}) need(*t, torch::kInt32, sel, n, "int32 arg");
+    TORCH_CHECK(desc.numel() >= sel.numel() && miss_channels.numel() >= sel.numel() && miss_count.numel() >= 1, n,
+                ": output buffers too small");
+    const at::DeviceGuard guard(sel.device());
+    check_status(soi_build_dip_descriptors(sel.data_ptr<int32_t>(), sel.numel(), slot_of.data_ptr<int32_t>(),
+                                           slot_of.numel(), desc.data_ptr<int32_t>(),
+                                           miss_channels.data_ptr<int32_t>(), miss_count.data_ptr<int32_t>(),
+                                           cur_stream(sel)),
+                 n);
+}
+
+void gemv_dip_fused_up_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor staging_Wq,
+                            torch::Tensor staging_scale, torch::Tensor desc, torch::Tensor x, torch::Tensor y,
+                            int64_t K, int64_t group_size) {
+    const char* n = "gemv_dip_fused_up_into";
+    check_dip_fused_common(cache_Wq, cache_scale, staging_Wq, staging_scale, desc, K, n);
+    need(x, torch::kFloat16, desc, n, "x");
+    need(y, torch::kFloat16, desc, n, "y");
+    TORCH_CHECK(x.numel() == K && y.numel() == desc.numel(), n, ": x / y shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_dip_fused_up(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(),
+                                       std::min(cache_Wq.size(0), cache_scale.size(0)), staging_Wq.data_ptr<uint8_t>(),
+                                       staging_scale.data_ptr<float>(),
+                                       std::min(staging_Wq.size(0), staging_scale.size(0)), desc.data_ptr<int32_t>(),
+                                       desc.numel(), h16(x), h16m(y), K, group_size, cache_scale.size(1),
+                                       cur_stream(x)),
+                 n);
+}
+
+void gemv_dip_fused_down_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor staging_Wq,
+                              torch::Tensor staging_scale, torch::Tensor desc, torch::Tensor h_sel, torch::Tensor y,
+                              int64_t H, int64_t group_size, torch::Tensor workspace_buf) {
+    const char* n = "gemv_dip_fused_down_into";
+    check_dip_fused_common(cache_Wq, cache_scale, staging_Wq, staging_scale, desc, H, n);
+    need(h_sel, torch::kFloat16, desc, n, "h_sel");
+    need(y, torch::kFloat16, desc, n, "y");
+    need(workspace_buf, torch::kUInt8, desc, n, "workspace");
+    TORCH_CHECK(h_sel.numel() == desc.numel() && y.numel() == H, n, ": h_sel / y shape mismatch");
+    const at::DeviceGuard guard(h_sel.device());
+    check_status(soi_gemv_dip_fused_down(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(),
+                                         std::min(cache_Wq.size(0), cache_scale.size(0)),
+                                         staging_Wq.data_ptr<uint8_t>(), staging_scale.data_ptr<float>(),
+                                         std::min(staging_Wq.size(0), staging_scale.size(0)),
+                                         desc.data_ptr<int32_t>(), desc.numel(), h16(h_sel), h16m(y), H, group_size,
+                                         cache_scale.size(1), workspace_buf.data_ptr<uint8_t>(),
+                                         workspace_buf.numel(), cur_stream(h_sel)),
+                 n);
+}
+
+void gemv_f16_into(torch::Tensor W, torch::Tensor x, torch::Tensor y) {
+    const char* n = "gemv_f16_into";
+    need(W, torch::kFloat16, x, n, "W");
+    need(x, torch::kFloat16, x, n, "x");
+    need(y, torch::kFloat16, x, n, "y");
+    TORCH_CHECK(W.dim() == 2 && W.size(1) == x.numel() && y.numel() == W.size(0), n, ": shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_f16(h16(W), h16(x), h16m(y), W.size(0), W.size(1), cur_stream(x)), n);
+}
+
+int64_t argmax_workspace_bytes(int64_t n) { return static_cast<int64_t>(soi_argmax_workspace_bytes(n)); }
+
+void argmax_f16_into(torch::Tensor x, torch::Tensor out_index, c10::optional<torch::Tensor> log,
+                     c10::optional<torch::Tensor> log_len, torch::Tensor workspace_buf) {
+    const char* n = "argmax_f16_into";
+    need(x, torch::kFloat16, x, n, "x");
+    need(out_index, torch::kInt32, x, n, "out_index");
+    need(workspace_buf, torch::kUInt8, x, n, "workspace");
+    need_numel(out_index, 1, n, "out_index");
+    TORCH_CHECK(log.has_value() == log_len.has_value(), n, ": log and log_len go together");
+    int32_t* lp = nullptr;
+    int32_t* llp = nullptr;
+    int64_t cap = 0;
+    if (log.has_value()) {
+        need(*log, torch::kInt32, x, n, "log");
+        need(*log_len, torch::kInt32, x, n, "log_len");
+        need_numel(*log_len, 1, n, "log_len");
+        lp = log->data_ptr<int32_t>();
+        llp = log_len->data_ptr<int32_t>();
+        cap = log->numel();
+    }
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_argmax_f16(h16(x), x.numel(), out_index.data_ptr<int32_t>(), lp, llp, cap,
+                                workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(x)),
+                 n);
+}
+
+void silu_mul_into(torch::Tensor gate, torch::Tensor up, torch::Tensor out) {
+    const char* n = "silu_mul_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(up, torch::kFloat16, gate, n, "up");
+    need(out, torch::kFloat16, gate, n, "out");
+    TORCH_CHECK(up.numel() == gate.numel() && out.numel() == gate.numel(), n, ": shape mismatch");
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_silu_mul(h16(gate), h16(up), h16m(out), gate.numel(), cur_stream(gate)), n);
+}
+
+void silu_mul_indexed_into(torch::Tensor gate, torch::Tensor idx, torch::Tensor u_sel, torch::Tensor out) {
+    const char* n = "silu_mul_indexed_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(idx, torch::kInt32, gate, n, "idx");
+    need(u_sel, torch::kFloat16, gate, n, "u_sel");
+    need(out, torch::kFloat16, gate, n, "out");
+    TORCH_CHECK(u_sel.numel() == idx.numel() && out.numel() == idx.numel(), n, ": shape mismatch");
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_silu_mul_indexed(h16(gate), gate.numel(), idx.data_ptr<int32_t>(), h16(u_sel), h16m(out),
+                                      idx.numel(), cur_stream(gate)),
+                 n);
+}
+
+void embed_lookup_into(torch::Tensor table, torch::Tensor token, torch::Tensor out) {
+    const char* n = "embed_lookup_into";
+    need(table, torch::kFloat16, table, n, "table");
+    need(token, torch::kInt32, table, n, "token");
+    need(out, torch::kFloat16, table, n, "out");
+    TORCH_CHECK(table.dim() == 2 && out.numel() == table.size(1), n, ": out must be [hidden]");
+    need_numel(token, 1, n, "token");
+    const at::DeviceGuard guard(table.device());
+    check_status(soi_embed_lookup(h16(table), table.size(0), table.size(1), token.data_ptr<int32_t>(), h16m(out),
+                                  cur_stream(table)),
+                 n);
+}
+
+void advance_position(torch::Tensor pos, int64_t delta) {
+    const char* n = "advance_position";
+    need(pos, torch::kInt32, pos, n, "pos");
+    need_numel(pos, 1, n, "pos");
+    const at::DeviceGuard guard(pos.device());
+    check_status(soi_advance_position(pos.data_ptr<int32_t>(), static_cast<int32_t>(delta), cur_stream(pos)), n);
+}
+
+void topk_threshold_select_f16abs_into(torch::Tensor gate, int64_t k, torch::Tensor idx_out, torch::Tensor count_out) {
+    const char* n = "topk_threshold_select_f16abs_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(idx_out, torch::kInt32, gate, n, "idx_out");
+    need(count_out, torch::kInt32, gate, n, "count_out");
+    TORCH_CHECK(k >= 1 && k <= gate.numel(), n, ": k must be in [1, n]");
+    need_numel(idx_out, k, n, "idx_out");
+    need_numel(count_out, 1, n, "count_out");
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_topk_threshold_select_f16abs(h16(gate), gate.numel(), k, idx_out.data_ptr<int32_t>(),
+                                                  count_out.data_ptr<int32_t>(), cur_stream(gate)),
+                 n);
+}
+
+// Device address of pinned host memory (hipHostGetDevicePointer), for the
+// zero-copy miss gather. Raises if the memory is not device-mapped.
+int64_t host_device_pointer(torch::Tensor t) {
+    TORCH_CHECK(t.is_cpu() && t.is_pinned(), "host_device_pointer: tensor must be pinned host memory");
+    void* dp = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dp, t.data_ptr(), 0);
+    TORCH_CHECK(e == hipSuccess && dp != nullptr, "host_device_pointer: hipHostGetDevicePointer failed: ",
+                hipGetErrorString(e));
+    return reinterpret_cast<int64_t>(dp);
+}
+
+void gather_rows_device_counted(int64_t src_addr, int64_t num_rows, int64_t row_nbytes, torch::Tensor idx,
+                                torch::Tensor count, torch::Tensor dst) {
+    const char* n = "gather_rows_device_counted";
+    need(idx, torch::kInt32, idx, n, "idx");
+    need(count, torch::kInt32, idx, n, "count");
+    need(dst, torch::kUInt8, idx, n, "dst");
+    need_numel(count, 1, n, "count");
+    TORCH_CHECK(src_addr != 0 && num_rows >= 0 && row_nbytes >= 0, n, ": bad source");
+    TORCH_CHECK(dst.numel() >= idx.numel() * row_nbytes, n, "(dst): too small for max_k * row_nbytes bytes");
+    const at::DeviceGuard guard(idx.device());
+    check_status(soi_gather_rows_device_counted(reinterpret_cast<const uint8_t*>(src_addr), num_rows, row_nbytes,
+                                                idx.data_ptr<int32_t>(), count.data_ptr<int32_t>(), idx.numel(),
+                                                dst.data_ptr<uint8_t>(), cur_stream(idx)),
+                 n);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "soinfer MI355X (gfx950) quantized decode hot path";
     m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
@@ -530,5 +938,33 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("topk_threshold_select", &topk_threshold_select, "deterministic threshold top-k");
     m.def("gather_rows_staged", &gather_rows_staged, "pinned-host row gather, staged");
     m.def("gather_rows_naive", &gather_rows_naive, "pinned-host row gather, per row");
+    m.def("rmsnorm", &rmsnorm, "RMSNorm over the last dim (reference rmsnorm)");
+    m.def("gemv_fp16_v3", &gemv_fp16_v3, "fp16 GEMV (LM head)");
+    m.def("kv_cache_append", &kv_cache_append, "KV cache append at pos");
+    m.def("rope_apply", &rope_apply, "RoPE in place (rotate-half)");
+    m.def("rmsnorm_into", &rmsnorm_into, "RMSNorm into a caller buffer");
+    m.def("residual_rmsnorm_", &residual_rmsnorm_, "x += delta (fp16), out = rmsnorm(x)");
+    m.def("qk_norm_rope_append", &qk_norm_rope_append, "q/k norm + RoPE + KV append at a device position");
+    m.def("decode_attention_workspace_bytes", &decode_attention_workspace_bytes, "attention workspace size");
+    m.def("decode_attention_at", &decode_attention_at, "decode attention over pos[0]+1 timesteps");
+    m.def("gemv_w4a16_into", &gemv_w4a16_into, "INT4 GEMV into a caller buffer");
+    m.def("gemv_w4a16_indexed_into", &gemv_w4a16_indexed_into, "index-driven INT4 GEMV into a caller buffer");
+    m.def("gemv_w4a16_indexed_accumulate_into", &gemv_w4a16_indexed_accumulate_into,
+          "index-driven sparse down accumulate into a caller buffer");
+    m.def("sparse_accumulate_workspace_bytes", &sparse_accumulate_workspace_bytes, "sparse down workspace size");
+    m.def("build_dip_descriptors_into", &build_dip_descriptors_into, "hot-cache descriptors into caller buffers");
+    m.def("gemv_dip_fused_up_into", &gemv_dip_fused_up_into, "descriptor-driven up GEMV into a caller buffer");
+    m.def("gemv_dip_fused_down_into", &gemv_dip_fused_down_into, "descriptor-driven down into a caller buffer");
+    m.def("gemv_f16_into", &gemv_f16_into, "fp16 GEMV into a caller buffer");
+    m.def("argmax_workspace_bytes", &argmax_workspace_bytes, "argmax workspace size");
+    m.def("argmax_f16_into", &argmax_f16_into, "argmax of fp16 values (torch.argmax order)");
+    m.def("silu_mul_into", &silu_mul_into, "fp16(silu(gate) * up)");
+    m.def("silu_mul_indexed_into", &silu_mul_indexed_into, "fp16(silu(gate[idx]) * u_sel)");
+    m.def("embed_lookup_into", &embed_lookup_into, "embedding row of a device token");
+    m.def("advance_position", &advance_position, "pos[0] += delta on the device");
+    m.def("topk_threshold_select_f16abs_into", &topk_threshold_select_f16abs_into,
+          "threshold top-k over |fp16 gate| into caller buffers");
+    m.def("host_device_pointer", &host_device_pointer, "device address of pinned host memory");
+    m.def("gather_rows_device_counted", &gather_rows_device_counted, "device gather of count[0] rows");
     m.def("version", []() { return std::string(soi_version()); });
 }

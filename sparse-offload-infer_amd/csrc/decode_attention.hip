@@ -33,6 +33,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Context length: the host value, or (device form) pos[0] + 1 clamped to [1, S].
+// A split that starts at or past L writes the neutral state (m = -1e30, l = 0).
+__device__ __forceinline__ int cur_len_of(int L_arg, const int32_t* pos, int S) {
+    if (!pos) return L_arg;
+    const int p = ldg(pos);
+    return p < 0 ? 1 : (p >= S ? S : p + 1);
+}
+
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
@@ -45,14 +53,16 @@ template <int LPR, int REP>
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const uint16_t* __restrict__ q,
                                                                    const uint16_t* __restrict__ kc,
                                                                    const uint16_t* __restrict__ vc,
-                                                                   float* __restrict__ part, int rep, int S, int L,
-                                                                   int tps, int nsplit, float scale_log2) {
+                                                                   float* __restrict__ part, int rep, int S, int L_arg,
+                                                                   const int32_t* __restrict__ pos, int tps, int nsplit,
+                                                                   float scale_log2) {
     constexpr int HD = LPR * 8;
     constexpr int RPI = kWave / LPR;  // timesteps per wave instruction
     __shared__ float s_state[kAttnWaves][REP][HD + 2];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int g = lane / LPR, u = lane % LPR;
     const int kvh = blockIdx.x, split = blockIdx.y;
+    const int L = cur_len_of(L_arg, pos, S);
     const int t0 = split * tps;
     const int t1 = min(L, t0 + tps);
 
@@ -189,8 +199,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // General shapes: one wave per query head, lanes over dims, online softmax.
 __global__ __launch_bounds__(64) void attn_simple_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
-                                                          int rep, int S, int hd, int L, float scale_log2) {
+                                                          int rep, int S, int hd, int L_arg,
+                                                          const int32_t* __restrict__ pos, float scale_log2) {
     const int h = blockIdx.x, lane = threadIdx.x;
+    const int L = cur_len_of(L_arg, pos, S);
     const int kvh = h / rep;
     const uint16_t* kb = kc + static_cast<int64_t>(kvh) * S * hd;
     const uint16_t* vb = vc + static_cast<int64_t>(kvh) * S * hd;
@@ -255,37 +267,18 @@ static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
     return p;
 }
 
-}  // namespace soi
-
-using namespace soi;
-
-extern "C" size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len) {
-    if (NQ <= 0 || NKV <= 0 || head_dim <= 0 || cur_len <= 0 || NQ % NKV) return 0;
-    const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);
-    if (!p.fast) return 0;
-    return static_cast<size_t>(NQ) * p.nsplit * (head_dim + 2) * sizeof(float);
-}
-
-extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                    uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim,
-                                    int64_t cur_len, float scale, void* workspace, size_t workspace_bytes,
-                                    void* stream) {
-    const char* what = "soi_decode_attention";
-    SOI_REQUIRE(NQ >= 1 && NKV >= 1 && NQ % NKV == 0, "%s: num_q_heads must be a positive multiple of num_kv_heads",
-                what);
-    SOI_REQUIRE(head_dim >= 1 && head_dim <= 1024, "%s: head_dim must be in [1, 1024]", what);
-    SOI_REQUIRE(max_seq >= 1 && cur_len >= 1 && cur_len <= max_seq, "%s: cur_len out of range for max_seq_len", what);
-    SOI_REQUIRE(NQ <= 65535 && max_seq <= (int64_t(1) << 30), "%s: size out of range", what);
-    SOI_REQUIRE(q && k_cache && v_cache && out, "%s: null pointer", what);
-    hipStream_t st = as_stream(stream);
+static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                            int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, int64_t plan_len,
+                            int64_t cur_len, const int32_t* pos, float scale, void* workspace, size_t workspace_bytes,
+                            hipStream_t st, const char* what) {
     const float scale_log2 = scale * kLog2e;
     const int rep = static_cast<int>(NQ / NKV);
-    const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);
+    const AttnPlan p = plan_attention(NQ, NKV, head_dim, plan_len);
     const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
     if (!p.fast || !aligned) {
         hipLaunchKernelGGL(attn_simple_kernel, dim3(static_cast<unsigned>(NQ)), dim3(64), 0, st, q, k_cache, v_cache,
                            out, rep, static_cast<int>(max_seq), static_cast<int>(head_dim),
-                           static_cast<int>(cur_len), scale_log2);
+                           static_cast<int>(cur_len), pos, scale_log2);
         return launch_status(what);
     }
     const size_t need = static_cast<size_t>(NQ) * p.nsplit * (head_dim + 2) * sizeof(float);
@@ -298,7 +291,7 @@ extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, 
     const int S = static_cast<int>(max_seq), L = static_cast<int>(cur_len);
 #define SOI_A(LL, RR)                                                                                              \
     hipLaunchKernelGGL((attn_split_kernel<LL, RR>), grid, dim3(kAttnThreads), 0, st, q, k_cache, v_cache, part, rep, \
-                       S, L, p.tps, p.nsplit, scale_log2)
+                       S, L, pos, p.tps, p.nsplit, scale_log2)
 #define SOI_AR(LL)                       \
     switch (p.rep_t) {                   \
         case 1: SOI_A(LL, 1); break;     \
@@ -322,4 +315,50 @@ extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, 
     hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(NQ)), dim3(128), 0, st, part, out,
                        static_cast<int>(head_dim), p.nsplit);
     return launch_status(what);
+}
+
+static int check_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                           int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, const char* what) {
+    SOI_REQUIRE(NQ >= 1 && NKV >= 1 && NQ % NKV == 0, "%s: num_q_heads must be a positive multiple of num_kv_heads",
+                what);
+    SOI_REQUIRE(head_dim >= 1 && head_dim <= 1024, "%s: head_dim must be in [1, 1024]", what);
+    SOI_REQUIRE(max_seq >= 1 && max_seq <= (int64_t(1) << 30), "%s: max_seq_len out of range", what);
+    SOI_REQUIRE(NQ <= 65535, "%s: too many heads", what);
+    SOI_REQUIRE(q && k_cache && v_cache && out, "%s: null pointer", what);
+    return SOI_OK;
+}
+
+}  // namespace soi
+
+using namespace soi;
+
+extern "C" size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len) {
+    if (NQ <= 0 || NKV <= 0 || head_dim <= 0 || cur_len <= 0 || NQ % NKV) return 0;
+    const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);
+    if (!p.fast) return 0;
+    return static_cast<size_t>(NQ) * p.nsplit * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                    uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim,
+                                    int64_t cur_len, float scale, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    const char* what = "soi_decode_attention";
+    int st = check_attention(q, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, what);
+    if (st) return st;
+    SOI_REQUIRE(cur_len >= 1 && cur_len <= max_seq, "%s: cur_len out of range for max_seq_len", what);
+    return launch_attention(q, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, cur_len, cur_len, nullptr, scale,
+                            workspace, workspace_bytes, as_stream(stream), what);
+}
+
+extern "C" int soi_decode_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                       uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim,
+                                       const int32_t* pos, float scale, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    const char* what = "soi_decode_attention_at";
+    int st = check_attention(q, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, what);
+    if (st) return st;
+    SOI_REQUIRE(pos, "%s: null position pointer", what);
+    return launch_attention(q, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, max_seq, max_seq, pos, scale,
+                            workspace, workspace_bytes, as_stream(stream), what);
 }

@@ -53,12 +53,16 @@ __global__ __launch_bounds__(kDescThreads) void build_dip_descriptors_kernel(
     if (tid == 0) *miss_count = static_cast<int32_t>(running);
 }
 
-// dst[j,:] = src[idx[j],:]; 16-byte vector copies when rows allow it.
+// dst[j,:] = src[idx[j],:]; 16-byte vector copies when rows allow it. With
+// `count` (device), only rows j < count[0] are copied (the grid covers the
+// maximum). src may be device memory or a device mapping of pinned host memory.
 template <bool VEC>
 __global__ __launch_bounds__(256) void gather_rows_device_kernel(const uint8_t* __restrict__ src, int64_t num_rows,
                                                                   int64_t row_nbytes, const int32_t* __restrict__ idx,
-                                                                  int64_t k, uint8_t* __restrict__ dst) {
+                                                                  const int32_t* __restrict__ count,
+                                                                  uint8_t* __restrict__ dst) {
     const int64_t j = blockIdx.x;
+    if (count && j >= ldg(count)) return;
     const int32_t r = idx[j];
     const bool ok = r >= 0 && r < num_rows;
     uint8_t* d = dst + j * row_nbytes;
@@ -91,9 +95,8 @@ extern "C" int soi_build_dip_descriptors(const int32_t* sel, int64_t k, const in
     return launch_status(what);
 }
 
-extern "C" int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
-                                      int64_t k, uint8_t* dst, void* stream) {
-    const char* what = "soi_gather_rows_device";
+static int launch_gather(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
+                         const int32_t* count, int64_t k, uint8_t* dst, void* stream, const char* what) {
     SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 31) - 1 && num_rows >= 0 && row_nbytes >= 0, "%s: size out of range",
                 what);
     if (k == 0 || row_nbytes == 0) return SOI_OK;
@@ -102,9 +105,22 @@ extern "C" int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int6
     hipStream_t st = as_stream(stream);
     if (vec)
         hipLaunchKernelGGL(gather_rows_device_kernel<true>, dim3(static_cast<unsigned>(k)), dim3(256), 0, st, src,
-                           num_rows, row_nbytes, indices, k, dst);
+                           num_rows, row_nbytes, indices, count, dst);
     else
         hipLaunchKernelGGL(gather_rows_device_kernel<false>, dim3(static_cast<unsigned>(k)), dim3(256), 0, st, src,
-                           num_rows, row_nbytes, indices, k, dst);
+                           num_rows, row_nbytes, indices, count, dst);
     return launch_status(what);
+}
+
+extern "C" int soi_gather_rows_device(const uint8_t* src, int64_t num_rows, int64_t row_nbytes, const int32_t* indices,
+                                      int64_t k, uint8_t* dst, void* stream) {
+    return launch_gather(src, num_rows, row_nbytes, indices, nullptr, k, dst, stream, "soi_gather_rows_device");
+}
+
+extern "C" int soi_gather_rows_device_counted(const uint8_t* src, int64_t num_rows, int64_t row_nbytes,
+                                              const int32_t* indices, const int32_t* count, int64_t max_k,
+                                              uint8_t* dst, void* stream) {
+    const char* what = "soi_gather_rows_device_counted";
+    SOI_REQUIRE(count, "%s: null count", what);
+    return launch_gather(src, num_rows, row_nbytes, indices, count, max_k, dst, stream, what);
 }

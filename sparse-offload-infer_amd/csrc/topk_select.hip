@@ -88,8 +88,20 @@ __device__ __forceinline__ uint32_t wave_prefix_u32(uint32_t x) {
 // exact node values (an exact search runs only when the estimate is off).
 // Node and histogram buffers are double-buffered by round: two barriers per
 // round, three rounds.
-template <int E>
-__global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const float* __restrict__ v, int n, int k,
+// Value sources: fp32 values as given, or |x| of binary16 values (the fp32
+// conversion and the absolute value are exact, so selecting over F16Abs(g)
+// equals selecting over g.float().abs()).
+struct F32Values {
+    const float* p;
+    __device__ __forceinline__ float operator[](int i) const { return ldg(p + i); }
+};
+struct F16AbsValues {
+    const uint16_t* p;
+    __device__ __forceinline__ float operator[](int i) const { return fabsf(f16_bits_to_f32(ldg(p + i))); }
+};
+
+template <int E, class Values>
+__global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const Values v, int n, int k,
                                                                          int32_t* __restrict__ out_idx,
                                                                          int32_t* __restrict__ out_count) {
     __shared__ float s_max[kTopkWaves];
@@ -202,7 +214,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const fl
 
 // Any n: values streamed from global memory (L2-resident after the first
 // pass) in blocks of 1024, same arithmetic and same output order.
-__global__ __launch_bounds__(kTopkThreads) void topk_rule_a_stream_kernel(const float* __restrict__ v, int n, int k,
+template <class Values>
+__global__ __launch_bounds__(kTopkThreads) void topk_rule_a_stream_kernel(const Values v, int n, int k,
                                                                            int32_t* __restrict__ out_idx,
                                                                            int32_t* __restrict__ out_count) {
     __shared__ float s_max[kTopkWaves];
@@ -253,22 +266,18 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_stream_kernel(const 
     if (tid == 0) *out_count = static_cast<int32_t>(running < static_cast<uint32_t>(k) ? running : k);
 }
 
-}  // namespace soi
-
-using namespace soi;
-
-extern "C" int soi_topk_threshold_select(const float* abs_g, int64_t n, int64_t k, int32_t* out_indices,
-                                         int32_t* out_count, void* stream) {
-    const char* what = "soi_topk_threshold_select";
+template <class Values>
+static int launch_topk(const Values v, int64_t n, int64_t k, int32_t* out_indices, int32_t* out_count, void* stream,
+                       const char* what) {
     SOI_REQUIRE(n >= 1 && n <= (int64_t(1) << 30), "%s: n must be in [1, 2^30]", what);
     SOI_REQUIRE(k >= 1 && k <= n, "%s: k must be in [1, n]", what);
-    SOI_REQUIRE(abs_g && out_indices && out_count, "%s: null pointer", what);
+    SOI_REQUIRE(v.p && out_indices && out_count, "%s: null pointer", what);
     hipStream_t st = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
     const int64_t e = ceil_div64(n, kTopkThreads);
-#define SOI_T(EE)                                                                                                   \
-    hipLaunchKernelGGL((topk_rule_a_regs_kernel<EE>), dim3(1), dim3(kTopkThreads), 0, st, abs_g, ni, ki, out_indices, \
-                       out_count)
+#define SOI_T(EE)                                                                                               \
+    hipLaunchKernelGGL((topk_rule_a_regs_kernel<EE, Values>), dim3(1), dim3(kTopkThreads), 0, st, v, ni, ki, \
+                       out_indices, out_count)
     if (e <= 1) SOI_T(1);
     else if (e <= 2) SOI_T(2);
     else if (e <= 4) SOI_T(4);
@@ -279,8 +288,22 @@ extern "C" int soi_topk_threshold_select(const float* abs_g, int64_t n, int64_t 
     else if (e <= 24) SOI_T(24);
     else if (e <= 32) SOI_T(32);
     else
-        hipLaunchKernelGGL(topk_rule_a_stream_kernel, dim3(1), dim3(kTopkThreads), 0, st, abs_g, ni, ki, out_indices,
-                           out_count);
+        hipLaunchKernelGGL((topk_rule_a_stream_kernel<Values>), dim3(1), dim3(kTopkThreads), 0, st, v, ni, ki,
+                           out_indices, out_count);
 #undef SOI_T
     return launch_status(what);
+}
+
+}  // namespace soi
+
+using namespace soi;
+
+extern "C" int soi_topk_threshold_select(const float* abs_g, int64_t n, int64_t k, int32_t* out_indices,
+                                         int32_t* out_count, void* stream) {
+    return launch_topk(F32Values{abs_g}, n, k, out_indices, out_count, stream, "soi_topk_threshold_select");
+}
+
+extern "C" int soi_topk_threshold_select_f16abs(const uint16_t* gate, int64_t n, int64_t k, int32_t* out_indices,
+                                                int32_t* out_count, void* stream) {
+    return launch_topk(F16AbsValues{gate}, n, k, out_indices, out_count, stream, "soi_topk_threshold_select_f16abs");
 }

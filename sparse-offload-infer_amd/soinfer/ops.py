@@ -4,10 +4,13 @@ Names, arguments and return values follow the reference's python/soinfer/ops.py
 (gemv_w8a16 :92-96, gemv_w4a16_group{,_lop3} :99-109, topk_threshold_select
 :151-158, gather_rows_{staged,naive} :161-176, gemv_w4a16_sparse_accumulate
 :179-188, build_dip_descriptors :191-199, gemv_dip_fused_{up,down} :202-219,
-decode_attention :253-260). Validation errors surface as RuntimeError, as in
-the reference. Three operators have no reference counterpart: the
-index-driven sparse GEMVs over HBM-resident weights and the device row
-gather, which the resident DIP path uses instead of host gathers.
+decode_attention :253-260) and, for the decode step around the hot path,
+rmsnorm :57-59, gemv_fp16_v3 :82-84, precompute_rope_cos_sin / apply_rope /
+qk_norm / kv_cache_append :222-250. Validation errors surface as
+RuntimeError, as in the reference. Operators with no reference counterpart:
+the batched / grouped GEMVs, the index-driven sparse GEMVs over HBM-resident
+weights and the device row gather (the resident DIP path uses them instead of
+host gathers); the decode engine's no-allocation forms live in soinfer._C.
 """
 from __future__ import annotations
 
@@ -208,3 +211,52 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     (already RoPE'd / QK-normed); caches: [NKV, max_seq_len, hd] fp16; NQ % NKV == 0 (query head h reads KV
     head h // (NQ // NKV)); scale 1/sqrt(hd)."""
     return _C.decode_attention(q, k_cache, v_cache, cur_len)
+
+
+# ---------------------------------------------------------------------------
+# decode-step glue (reference python/soinfer/ops.py:57-59, 82-84, 222-250)
+# ---------------------------------------------------------------------------
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm over the last dim: x * rsqrt(mean(x^2) + eps) * weight. x: [rows, hidden] fp16, weight: [hidden]
+    fp16, hidden even; fp32 math, fp16 out."""
+    return _C.rmsnorm(x, weight, eps)
+
+
+def gemv_fp16_v3(W: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """y = W @ x for fp16 W [N, K] and x [K] (K % 8 == 0), fp32 accumulation, fp16 out (the LM head)."""
+    return _C.gemv_fp16_v3(W, x)
+
+
+def precompute_rope_cos_sin(head_dim: int, theta: float, pos: int, device, dtype=torch.float32):
+    """cos/sin [head_dim/2] at absolute position pos: inv_freq[i] = 1 / theta^(2i/head_dim),
+    angle_i = pos * inv_freq[i], computed in fp32 (the Qwen3 / HF rotary convention)."""
+    cos_t, sin_t = rope_tables(head_dim, theta, pos + 1, device)
+    return cos_t[pos].to(dtype).contiguous(), sin_t[pos].to(dtype).contiguous()
+
+
+def rope_tables(head_dim: int, theta: float, max_seq: int, device):
+    """cos/sin tables [max_seq, head_dim/2] fp32, row p = the angles at position p (same fp32 operations as
+    precompute_rope_cos_sin, one row per position)."""
+    exponent = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim
+    inv_freq = 1.0 / (theta ** exponent)
+    angles = torch.arange(max_seq, dtype=torch.float32, device=device)[:, None] * inv_freq[None, :]
+    return angles.cos().contiguous(), angles.sin().contiguous()
+
+
+def apply_rope(x: torch.Tensor, cos_vals: torch.Tensor, sin_vals: torch.Tensor) -> torch.Tensor:
+    """RoPE in place on x [num_heads, head_dim] fp16 (rotate-half convention); cos/sin fp32 [head_dim/2].
+    Returns x."""
+    _C.rope_apply(x, cos_vals, sin_vals)
+    return x
+
+
+def qk_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Qwen3 per-head QK-norm: RMSNorm over head_dim for each head of x [num_heads, head_dim]."""
+    return rmsnorm(x, weight, eps)
+
+
+def kv_cache_append(k_cache: torch.Tensor, v_cache: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                    pos: int) -> None:
+    """Write k_new / v_new [NKV, hd] into the caches [NKV, max_seq, hd] at position pos, in place."""
+    _C.kv_cache_append(k_cache, v_cache, k_new, v_new, pos)

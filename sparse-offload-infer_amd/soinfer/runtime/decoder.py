@@ -1,0 +1,370 @@
+"""Batch-1 greedy decoding of a Qwen3-shaped INT4 decoder on one MI355X.
+
+Follows the reference's decode step (python/soinfer/runtime/generate.py):
+per layer (run_decoder_layer_streaming :141-182, run_decoder_layer_dip
+:215-310, run_decoder_layer_cached_dip :313-404)
+
+    h    = rmsnorm(x, input_layernorm)
+    q,k,v= INT4 GEMV(h)                            (one fused [q|k|v] GEMV here)
+    q,k  = rope(qk_norm(q)), rope(qk_norm(k));  append k, v at pos
+    a    = decode_attention(q, caches, pos + 1)
+    x    = x + INT4 GEMV(W_o, a)
+    h3   = rmsnorm(x, post_attention_layernorm)
+    MLP  dense: down(fp16(silu(gate) * up))     DIP: top-k of |gate|, sparse up/down
+    x    = x + MLP(h3)
+
+and the loop of generate_streaming / generate_dip / generate_cached_dip
+(:429-520): prompt tokens one at a time, then rmsnorm(final_norm) -> fp16
+LM head GEMV -> argmax per new token.
+
+MI355X design: every weight is resident in HBM (the whole 1.7B INT4 model,
+its fp16 embedding and LM head take ~2.2 GB of 288 GB); the token, the
+position and the generated-token log live in device memory, every op writes
+into preallocated buffers, and one decode step (LM head + argmax + 28 layers)
+is captured once as a HIP graph and replayed, so generation needs no host
+round trip until the end. The residual add is fused into the following
+RMSNorm and q/k-norm + RoPE + KV append into one launch; both give the same
+binary16 values as the separate ops. The cache-aware DIP mode keeps the
+up / down^T rows of non-hot channels in pinned host memory and fetches the
+misses inside the graph with a device gather from the host mapping, so its
+output is bit-identical to DIP with everything resident.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from .. import _C
+from .. import ops
+from ..offload.hot_cache import HotCache
+from ..quant import formats, pack
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    hidden: int = 2048
+    layers: int = 28
+    q_heads: int = 16
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 6144
+    vocab: int = 151936
+    group_size: int = 128
+    rms_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    max_seq: int = 2048
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.q_heads + 2 * self.kv_heads) * self.head_dim
+
+
+QWEN3_1P7B = DecoderConfig()
+
+
+@dataclass
+class LayerWeights:
+    in_norm: torch.Tensor  # [H] fp16
+    post_norm: torch.Tensor  # [H]
+    q_norm: torch.Tensor  # [hd]
+    k_norm: torch.Tensor  # [hd]
+    qkv_Wq: torch.Tensor  # [(NQ+2NKV)*hd, H/2] uint8, rows q | k | v
+    qkv_scale: torch.Tensor  # [(NQ+2NKV)*hd, H/gs] fp32
+    o_Wq: torch.Tensor  # [H, NQ*hd/2]
+    o_scale: torch.Tensor
+    gu_Wq: torch.Tensor  # [2I, H/2], rows gate | up
+    gu_scale: torch.Tensor
+    down_Wq: torch.Tensor  # [H, I/2] (dense path)
+    down_scale: torch.Tensor
+    down_T_Wq: torch.Tensor  # [I, H/2] (DIP path: a channel is a row)
+    down_T_scale: torch.Tensor
+
+    def gate(self, I: int):
+        return self.gu_Wq[:I], self.gu_scale[:I]
+
+    def up(self, I: int):
+        return self.gu_Wq[I:], self.gu_scale[I:]
+
+
+@dataclass
+class DecoderWeights:
+    config: DecoderConfig
+    embed: torch.Tensor  # [V, H] fp16
+    lm_head: torch.Tensor  # [V, H] fp16
+    final_norm: torch.Tensor  # [H] fp16
+    layers: list = field(default_factory=list)
+
+
+def _quant_int4(w: torch.Tensor, gs: int):
+    qt = formats.quantize(w, formats.QuantConfig(bits=4, granularity="group", group_size=gs))
+    Wq, _ = pack.pack_int4(qt.qweight)
+    return Wq.contiguous(), qt.scale.contiguous()
+
+
+def random_decoder(config: DecoderConfig = QWEN3_1P7B, seed: int = 0, device="cuda", linear_std: float = 0.02,
+                   norm_jitter: float = 0.0) -> DecoderWeights:
+    """Random-init weights of the given shape: linears N(0, linear_std) quantized to INT4 (group
+    config.group_size, fp32 scales), embedding N(0, 1) and LM head N(0, linear_std) in fp16, norms 1
+    (+ N(0, norm_jitter) when given). down_proj is quantized twice, as [H, I] for the dense path and as
+    its transpose [I, H] for DIP (the reference registers both, load_hf_checkpoint.py:90-111)."""
+    c = config
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def randn(*shape, std=1.0):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std
+
+    def norm(n):
+        v = torch.ones(n, device=device)
+        if norm_jitter:
+            v = v + randn(n, std=norm_jitter)
+        return v.half().contiguous()
+
+    H, I, hd, gs = c.hidden, c.intermediate, c.head_dim, c.group_size
+    layers = []
+    for _ in range(c.layers):
+        wq = randn(c.qkv_rows, H, std=linear_std)
+        wo = randn(H, c.q_heads * hd, std=linear_std)
+        wgu = randn(2 * I, H, std=linear_std)
+        wd = randn(H, I, std=linear_std)
+        qkv_Wq, qkv_s = _quant_int4(wq, gs)
+        o_Wq, o_s = _quant_int4(wo, gs)
+        gu_Wq, gu_s = _quant_int4(wgu, gs)
+        d_Wq, d_s = _quant_int4(wd, gs)
+        dT_Wq, dT_s = _quant_int4(wd.t().contiguous(), gs)
+        del wq, wo, wgu, wd
+        layers.append(LayerWeights(norm(H), norm(H), norm(hd), norm(hd), qkv_Wq, qkv_s, o_Wq, o_s, gu_Wq, gu_s,
+                                   d_Wq, d_s, dT_Wq, dT_s))
+    embed = randn(c.vocab, H).half().contiguous()
+    lm_head = randn(c.vocab, H, std=linear_std).half().contiguous()
+    return DecoderWeights(c, embed, lm_head, norm(H), layers)
+
+
+class DecodeEngine:
+    """Greedy decoder over DecoderWeights. mode: "dense", "dip" (top dip_k channels per layer, weights
+    resident) or "cached_dip" (hot channels resident, the rest fetched from pinned host memory).
+
+    All buffers are allocated here; decode steps launch only this package's kernels on the current stream
+    and are captured into HIP graphs by capture()."""
+
+    def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
+                 hot_channels: Optional[list] = None, max_new_tokens: int = 256):
+        if mode not in ("dense", "dip", "cached_dip"):
+            raise ValueError(f"unknown mode {mode!r}")
+        c = w.config
+        self.w, self.c, self.mode = w, c, mode
+        dev = w.embed.device
+        self.device = dev
+        H, I, hd = c.hidden, c.intermediate, c.head_dim
+        f16, i32 = torch.float16, torch.int32
+
+        def buf(n, dtype=f16):
+            return torch.zeros(n, dtype=dtype, device=dev)
+
+        self.token = buf(1, i32)
+        self.pos = buf(1, i32)
+        self.log = buf(max_new_tokens, i32)
+        self.log_len = buf(1, i32)
+        self.x, self.h, self.hn = buf(H), buf(H), buf(H)
+        self.qkv = buf(c.qkv_rows)
+        self.q = torch.zeros(c.q_heads, hd, dtype=f16, device=dev)
+        self.attn = buf(c.q_heads * hd)
+        self.o, self.down = buf(H), buf(H)
+        self.gu = buf(2 * I)
+        self.mlp_h = buf(I)
+        self.logits = buf(c.vocab)
+        self.k_cache = [torch.zeros(c.kv_heads, c.max_seq, hd, dtype=f16, device=dev) for _ in range(c.layers)]
+        self.v_cache = [torch.zeros(c.kv_heads, c.max_seq, hd, dtype=f16, device=dev) for _ in range(c.layers)]
+        self.cos_t, self.sin_t = ops.rope_tables(hd, c.rope_theta, c.max_seq, dev)
+        self.attn_ws = buf(max(1, _C.decode_attention_workspace_bytes(c.q_heads, c.kv_heads, hd, c.max_seq)),
+                           torch.uint8)
+        self.argmax_ws = buf(_C.argmax_workspace_bytes(c.vocab), torch.uint8)
+        self.counts = None  # optional per-layer channel selection counts (eager calibration only)
+
+        if mode != "dense":
+            if dip_k is None or not 1 <= dip_k <= I:
+                raise ValueError("dip_k must be in [1, intermediate]")
+            self.k = dip_k
+            self.idx, self.cnt = buf(dip_k, i32), buf(1, i32)
+            self.u_sel, self.h_sel = buf(dip_k), buf(dip_k)
+            self.sd_ws = buf(max(1, _C.sparse_accumulate_workspace_bytes(H, dip_k)), torch.uint8)
+        if mode == "cached_dip":
+            if hot_channels is None or len(hot_channels) != c.layers:
+                raise ValueError("cached_dip needs one hot-channel list per layer")
+            self._setup_cache(hot_channels)
+        self._graph_layers = None
+        self._graph_gen = None
+
+    # ---- cache-aware DIP: hot rows in HBM, the rest in pinned host memory ----
+    def _setup_cache(self, hot_channels):
+        c, dev, k = self.c, self.device, self.k
+        I = c.intermediate
+        self.caches, self.host_up, self.host_down, self.host_up_ptr, self.host_down_ptr = [], [], [], [], []
+        for L, hot in zip(self.w.layers, hot_channels):
+            up_Wq, up_s = L.up(I)
+            self.caches.append(HotCache.build(up_Wq, up_s, L.down_T_Wq, L.down_T_scale, hot))
+            hu = torch.empty(up_Wq.shape, dtype=torch.uint8, pin_memory=True)
+            hd_ = torch.empty(L.down_T_Wq.shape, dtype=torch.uint8, pin_memory=True)
+            hu.copy_(up_Wq)
+            hd_.copy_(L.down_T_Wq)
+            self.host_up.append(hu)
+            self.host_down.append(hd_)
+            self.host_up_ptr.append(_C.host_device_pointer(hu))
+            self.host_down_ptr.append(_C.host_device_pointer(hd_))
+        row_up = self.w.layers[0].gu_Wq.shape[1]
+        row_dn = self.w.layers[0].down_T_Wq.shape[1]
+        G = self.w.layers[0].gu_scale.shape[1]
+        u8, f32, i32 = torch.uint8, torch.float32, torch.int32
+        self.desc = torch.zeros(k, dtype=i32, device=dev)
+        self.miss_ch = torch.zeros(k, dtype=i32, device=dev)
+        self.miss_cnt = torch.zeros(1, dtype=i32, device=dev)
+        self.st_up = torch.zeros(k, row_up, dtype=u8, device=dev)
+        self.st_dn = torch.zeros(k, row_dn, dtype=u8, device=dev)
+        self.st_up_s = torch.zeros(k, G, dtype=f32, device=dev)
+        self.st_dn_s = torch.zeros(k, G, dtype=f32, device=dev)
+
+    # ---- one layer ----
+    def _mlp(self, l: int, L: LayerWeights):
+        c = self.c
+        H, I, gs = c.hidden, c.intermediate, c.group_size
+        if self.mode == "dense":
+            _C.gemv_w4a16_into(L.gu_Wq, L.gu_scale, self.h, self.gu, H, gs)
+            _C.silu_mul_into(self.gu[:I], self.gu[I:], self.mlp_h)
+            _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
+            return
+        gate = self.gu[:I]
+        gW, gS = L.gate(I)
+        _C.gemv_w4a16_into(gW, gS, self.h, gate, H, gs)
+        _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
+        if self.counts is not None:
+            self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
+                                                                     device=self.device))
+        if self.mode == "dip":
+            uW, uS = L.up(I)
+            _C.gemv_w4a16_indexed_into(uW, uS, self.idx, self.h, self.u_sel, H, gs)
+            _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
+            _C.gemv_w4a16_indexed_accumulate_into(L.down_T_Wq, L.down_T_scale, self.idx, self.h_sel, self.down, H,
+                                                  gs, self.sd_ws)
+            return
+        cache = self.caches[l]
+        _, uS = L.up(I)
+        _C.build_dip_descriptors_into(self.idx, cache.slot_of, self.desc, self.miss_ch, self.miss_cnt)
+        _C.gather_rows_device_counted(self.host_up_ptr[l], I, self.st_up.shape[1], self.miss_ch, self.miss_cnt,
+                                      self.st_up)
+        _C.gather_rows_device_counted(self.host_down_ptr[l], I, self.st_dn.shape[1], self.miss_ch, self.miss_cnt,
+                                      self.st_dn)
+        _C.gather_rows_device_counted(uS.data_ptr(), I, uS.shape[1] * 4, self.miss_ch, self.miss_cnt,
+                                      self.st_up_s.view(torch.uint8))
+        _C.gather_rows_device_counted(L.down_T_scale.data_ptr(), I, L.down_T_scale.shape[1] * 4, self.miss_ch,
+                                      self.miss_cnt, self.st_dn_s.view(torch.uint8))
+        _C.gemv_dip_fused_up_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc, self.h,
+                                  self.u_sel, H, gs)
+        _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
+        _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
+                                    self.h_sel, self.down, H, gs, self.sd_ws)
+
+    def _layers(self):
+        """Embedding of the device token, all layers at the device position, final norm; pos += 1."""
+        c, eps = self.c, self.c.rms_eps
+        H, gs = c.hidden, c.group_size
+        _C.embed_lookup_into(self.w.embed, self.token, self.x)
+        for l, L in enumerate(self.w.layers):
+            if l == 0:
+                _C.rmsnorm_into(self.x, L.in_norm, self.h, eps)
+            else:
+                _C.residual_rmsnorm_(self.x, self.down, L.in_norm, self.h, eps)
+            _C.gemv_w4a16_into(L.qkv_Wq, L.qkv_scale, self.h, self.qkv, H, gs)
+            _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
+                                   self.k_cache[l], self.v_cache[l], eps)
+            _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
+            _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
+            _C.residual_rmsnorm_(self.x, self.o, L.post_norm, self.h, eps)
+            self._mlp(l, L)
+        _C.residual_rmsnorm_(self.x, self.down, self.w.final_norm, self.hn, eps)
+        _C.advance_position(self.pos, 1)
+
+    def _head(self):
+        """LM head on the final-normed hidden state and argmax into the device token (and the log)."""
+        _C.gemv_f16_into(self.w.lm_head, self.hn, self.logits)
+        _C.argmax_f16_into(self.logits, self.token, self.log, self.log_len, self.argmax_ws)
+
+    # ---- graphs ----
+    def capture(self):
+        """Capture the prompt step (layers) and the generation step (head + layers) as HIP graphs."""
+        saved = (self.pos.clone(), self.log_len.clone(), self.token.clone())
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):  # warm up outside capture (first-launch costs)
+            self._layers()
+            self._head()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        self._graph_layers = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._graph_layers):
+            self._layers()
+        self._graph_gen = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._graph_gen):
+            self._head()
+            self._layers()
+        self.pos.copy_(saved[0])
+        self.log_len.copy_(saved[1])
+        self.token.copy_(saved[2])
+        torch.cuda.synchronize(self.device)
+
+    def reset(self):
+        self.pos.zero_()
+        self.log_len.zero_()
+
+    def prefill(self, prompt_ids, use_graph: bool = True):
+        prompt = torch.as_tensor(list(prompt_ids), dtype=torch.int32, device=self.device)
+        if prompt.numel() + 1 > self.c.max_seq:
+            raise ValueError("prompt longer than the KV cache")
+        for i in range(prompt.numel()):
+            self.token.copy_(prompt[i:i + 1])
+            if use_graph:
+                self._graph_layers.replay()
+            else:
+                self._layers()
+
+    def decode(self, n_new: int, use_graph: bool = True):
+        if n_new > self.log.numel():
+            raise ValueError("n_new exceeds max_new_tokens")
+        for _ in range(n_new):
+            if use_graph:
+                self._graph_gen.replay()
+            else:
+                self._head()
+                self._layers()
+
+    def generate(self, prompt_ids, n_new: int, use_graph: bool = True, eos_token_id: Optional[int] = None):
+        """Greedy decoding: returns prompt_ids + the n_new generated tokens (cut after eos_token_id, as the
+        reference's early stop; the device loop runs all n_new steps and the host truncates)."""
+        if len(prompt_ids) + n_new > self.c.max_seq:
+            raise ValueError("prompt + new tokens exceed the KV cache length")
+        if use_graph and self._graph_gen is None:
+            self.capture()
+        self.reset()
+        self.prefill(prompt_ids, use_graph)
+        self.decode(n_new, use_graph)
+        out = self.log[:n_new].tolist()
+        if eos_token_id is not None and eos_token_id in out:
+            out = out[:out.index(eos_token_id) + 1]
+        return list(prompt_ids) + out
+
+
+def calibrate_hot_channels(w: DecoderWeights, dip_k: int, calib_tokens, cache_fraction: float = 0.2):
+    """Hot set per layer: the cache_fraction * I most frequently selected channels (ties to the lower index)
+    while decoding calib_tokens with the DIP engine (reference generate.py:579-609 counts selections the same
+    way; StaticFrequencyPolicy orders them)."""
+    from ..offload.hot_cache import StaticFrequencyPolicy
+
+    c = w.config
+    eng = DecodeEngine(w, "dip", dip_k=dip_k, max_new_tokens=1)
+    eng.counts = [torch.zeros(c.intermediate, dtype=torch.int64, device=eng.device) for _ in range(c.layers)]
+    eng.reset()
+    eng.prefill(calib_tokens, use_graph=False)
+    C = int(round(cache_fraction * c.intermediate))
+    hot = [StaticFrequencyPolicy(cnt.cpu(), C).hot_indices.tolist() for cnt in eng.counts]
+    del eng
+    return hot

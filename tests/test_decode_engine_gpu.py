@@ -1,0 +1,127 @@
+"""Decode engine (soinfer.runtime.decoder) on the GPU: greedy decoding of a Qwen3-shaped INT4 decoder
+against the CPU oracle decoder (oracle/decoder.py), and the engine's own invariants.
+
+* dense and DIP decoding, step by step: the GPU's logits vs the oracle's on the same token history
+  (normalized max error <= 5e-3 of max|logit| for dense, 2e-2 for DIP, whose top-k boundary may select a
+  different channel when two |gate| values are within the fp32-vs-fp64 difference), and the GPU's token is
+  the oracle's argmax unless the oracle's top-2 margin is inside that bound;
+* HIP-graph replay == eager launches, bit for bit (same kernels, same order);
+* cache-aware DIP == DIP bit for bit (generated tokens and the final hidden state) for hot caches of
+  0%, 20% (calibrated) and 100% of the channels, with misses fetched from pinned host memory;
+* the full Qwen3-1.7B shape (28 layers, vocab 151936) against the oracle for the first generated tokens.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import decoder as OD
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dec(cuda):
+    from soinfer.runtime import decoder
+
+    return decoder
+
+
+TINY = dict(hidden=256, layers=2, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=1000,
+            group_size=128, max_seq=64)
+
+
+@pytest.fixture(scope="module")
+def tiny(dec):
+    cfg = dec.DecoderConfig(**TINY)
+    return dec.random_decoder(cfg, seed=3, linear_std=0.05, norm_jitter=0.1)
+
+
+def prompt_ids(n, vocab, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (n,), generator=g).tolist()
+
+
+def run_against_oracle(dec, w, mode, dip_k, n_prompt, n_new, tol):
+    eng = dec.DecodeEngine(w, mode, dip_k=dip_k, max_new_tokens=n_new)
+    emb, lm, fn, layers = OD.from_device(w)
+    ora = OD.OracleDecoder(w.config, emb, lm, fn, layers, mode="dip" if mode != "dense" else "dense", dip_k=dip_k)
+    eng.reset()
+    prompt = prompt_ids(n_prompt, w.config.vocab)
+    eng.prefill(prompt, use_graph=False)
+    for t in prompt:
+        ora.step(t)
+    tokens = []
+    for i in range(n_new):
+        eng._head()
+        logits = eng.logits.float().cpu().numpy().astype(np.float64)
+        ref = ora.logits().astype(np.float64)
+        scale = np.abs(ref).max()
+        err = np.abs(logits - ref).max()
+        assert err <= tol * scale, f"{mode} step {i}: logits error {err / scale:.2e} > {tol}"
+        tok = int(eng.token.item())
+        srt = np.sort(ref)
+        if srt[-1] - srt[-2] > 2 * tol * scale:
+            assert tok == OD.argmax_first(ref), f"{mode} step {i}: token {tok} != oracle {OD.argmax_first(ref)}"
+        tokens.append(tok)
+        eng._layers()
+        ora.step(tok)
+    return tokens
+
+
+def test_dense_decode_matches_oracle(dec, tiny):
+    run_against_oracle(dec, tiny, "dense", None, n_prompt=6, n_new=6, tol=5e-3)
+
+
+def test_dip_decode_matches_oracle(dec, tiny):
+    run_against_oracle(dec, tiny, "dip", 256, n_prompt=6, n_new=6, tol=2e-2)
+
+
+@pytest.mark.parametrize("mode,k", [("dense", None), ("dip", 128)])
+def test_graph_replay_equals_eager(dec, tiny, mode, k):
+    prompt = prompt_ids(5, tiny.config.vocab, seed=11)
+    a = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8)
+    eager = a.generate(prompt, 8, use_graph=False)
+    x_eager = a.x.clone()
+    b = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8)
+    for rep in range(3):  # replays after the first must agree too
+        graph = b.generate(prompt, 8, use_graph=True)
+        assert graph == eager, f"replay {rep}"
+        assert torch.equal(b.x, x_eager)
+        torch.cuda.synchronize()
+        _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+
+
+def test_cached_dip_bit_identical_to_dip(dec, tiny):
+    cfg = tiny.config
+    k = cfg.intermediate // 2
+    prompt = prompt_ids(6, cfg.vocab, seed=5)
+    plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6)
+    want = plain.generate(prompt, 6, use_graph=True)
+    calib = prompt_ids(16, cfg.vocab, seed=1000)
+    hot20 = dec.calibrate_hot_channels(tiny, k, calib, cache_fraction=0.2)
+    assert all(len(h) == round(0.2 * cfg.intermediate) for h in hot20)
+    for name, hot in (("0%", [[] for _ in range(cfg.layers)]), ("20%", hot20),
+                      ("100%", [list(range(cfg.intermediate)) for _ in range(cfg.layers)])):
+        eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6)
+        for use_graph in (False, True):
+            got = eng.generate(prompt, 6, use_graph=use_graph)
+            assert got == want, f"cache {name} graph={use_graph}"
+            assert torch.equal(eng.x, plain.x), f"cache {name} graph={use_graph}: final hidden state differs"
+
+
+def test_engine_rejects_bad_arguments(dec, tiny):
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "sparse")
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dip", dip_k=0)
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "cached_dip", dip_k=8, hot_channels=[[]])  # one list per layer
+    eng = dec.DecodeEngine(tiny, "dense", max_new_tokens=4)
+    with pytest.raises(ValueError):
+        eng.generate(prompt_ids(10, tiny.config.vocab), 60)  # longer than max_seq
+
+
+def test_full_qwen3_shape_first_tokens_match_oracle(dec):
+    """28 layers, hidden 2048, 16/8 heads, I=6144, vocab 151936: dense, 2 prompt tokens, 2 new tokens."""
+    w = dec.random_decoder(dec.QWEN3_1P7B, seed=0)
+    run_against_oracle(dec, w, "dense", None, n_prompt=2, n_new=2, tol=5e-3)

@@ -1,0 +1,248 @@
+"""Decode-step glue on the GPU against the CPU oracle (oracle/decoder.py), op by op on identical inputs
+(counterpart of the reference's tests/test_m2_kernels.py and test_m5_kernels.py for rmsnorm, gemv_fp16,
+rope, kv_cache_append).
+
+Tolerance for floating-point outputs: the rule of tests/helpers.py (1e-3 relative). Integer / byte outputs
+(argmax index, KV rows, embedding rows) are compared exactly. Engine forms (device position / token,
+fused residual add, fused q/k norm + RoPE + append) are checked against the separate reference-named ops,
+bit for bit where they share the arithmetic.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close
+from oracle import decoder as OD
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops(cuda):
+    import soinfer.ops as ops
+
+    return ops
+
+
+@pytest.fixture(scope="module")
+def C(cuda):
+    from soinfer import _C
+
+    return _C
+
+
+def rnd(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).half()
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 2048), (16, 128), (8, 128), (3, 1000), (1, 6)])
+def test_rmsnorm_matches_oracle(ops, rows, hidden):
+    x, w = rnd((rows, hidden), 1, 3.0), rnd((hidden,), 2) + 1
+    y = ops.rmsnorm(x.cuda(), w.half().cuda(), 1e-6)
+    ref = OD.rmsnorm(x.numpy(), w.numpy(), 1e-6)
+    assert_close(y, ref.astype(np.float64), f"rmsnorm {rows}x{hidden}")
+
+
+def test_rmsnorm_rejects_bad_arguments(ops):
+    with pytest.raises(RuntimeError):
+        ops.rmsnorm(rnd((2, 7), 0).cuda(), rnd((7,), 1).cuda())  # odd hidden (reference requires even)
+    with pytest.raises(RuntimeError):
+        ops.rmsnorm(rnd((2, 8), 0).cuda(), rnd((6,), 1).cuda())  # weight shape
+
+
+@pytest.mark.parametrize("hidden", [2048, 1000])
+def test_residual_rmsnorm_equals_add_then_rmsnorm(C, ops, hidden):
+    x, d, w = rnd((hidden,), 3), rnd((hidden,), 4), rnd((hidden,), 5) + 1
+    xd, dd, wd = x.cuda(), d.cuda(), w.half().cuda()
+    out = torch.empty_like(xd)
+    C.residual_rmsnorm_(xd, dd, wd, out, 1e-6)
+    s = (x.float() + d.float()).half()  # binary16 add, rounded once
+    assert torch.equal(xd.cpu(), s), "x must hold the binary16 sum"
+    assert torch.equal(out, ops.rmsnorm(s.cuda().view(1, -1), wd, 1e-6).view(-1))
+    assert np.array_equal(s.numpy(), OD.residual_add(x.numpy(), d.numpy()))
+
+
+@pytest.mark.parametrize("heads,hd,pos", [(16, 128, 0), (16, 128, 1), (8, 128, 2047), (4, 64, 77)])
+def test_rope_matches_oracle(ops, heads, hd, pos):
+    x = rnd((heads, hd), 6 + pos, 2.0)
+    cos_v, sin_v = ops.precompute_rope_cos_sin(hd, 1e6, pos, "cuda")
+    y = ops.apply_rope(x.cuda(), cos_v, sin_v)
+    ref = OD.rope(x.numpy(), hd, 1e6, pos)
+    assert_close(y, ref.astype(np.float64), f"rope pos {pos}")
+    if pos == 0:
+        assert torch.equal(y.cpu(), x), "angle 0 is the identity"
+
+
+def test_rope_tables_match_single_position(ops):
+    cos_t, sin_t = ops.rope_tables(128, 1e6, 300, "cuda")
+    for p in (0, 1, 17, 299):
+        c, s = ops.precompute_rope_cos_sin(128, 1e6, p, "cuda")
+        assert torch.equal(cos_t[p], c) and torch.equal(sin_t[p], s)
+
+
+def test_kv_cache_append_exact(ops):
+    kc = torch.zeros(8, 64, 128, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    k, v = rnd((8, 128), 10).cuda(), rnd((8, 128), 11).cuda()
+    ops.kv_cache_append(kc, vc, k, v, 37)
+    assert torch.equal(kc[:, 37], k) and torch.equal(vc[:, 37], v)
+    assert kc[:, :37].abs().sum() == 0 and kc[:, 38:].abs().sum() == 0
+    with pytest.raises(RuntimeError):
+        ops.kv_cache_append(kc, vc, k, v, 64)  # pos == max_seq
+
+
+@pytest.mark.parametrize("N,K", [(151936 // 16, 2048), (1000, 256), (37, 2048), (5, 24), (7, 100)])
+def test_gemv_fp16_matches_oracle(ops, C, N, K):
+    W, x = rnd((N, K), 12, 0.05), rnd((K,), 13)
+    ref = OD.gemv_f16(W.numpy(), x.numpy())
+    if K % 8 == 0:
+        y = ops.gemv_fp16_v3(W.cuda(), x.cuda())
+    else:
+        y = torch.empty(N, dtype=torch.float16, device="cuda")
+        C.gemv_f16_into(W.cuda(), x.cuda(), y)
+    assert_close(y, ref.astype(np.float64), f"gemv_f16 {N}x{K}")
+
+
+def test_gemv_fp16_v3_requires_k_multiple_of_8(ops):
+    with pytest.raises(RuntimeError):
+        ops.gemv_fp16_v3(rnd((4, 12), 0).cuda(), rnd((12,), 1).cuda())
+
+
+def argmax_dev(C, x):
+    ws = torch.empty(C.argmax_workspace_bytes(x.numel()), dtype=torch.uint8, device="cuda")
+    out = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    C.argmax_f16_into(x, out, None, None, ws)
+    return int(out.item())
+
+
+def test_argmax_first_maximum(C):
+    x = rnd((151936,), 14)
+    assert argmax_dev(C, x.cuda()) == OD.argmax_first(x.numpy()) == int(torch.argmax(x.float()))
+    t = torch.zeros(10000, dtype=torch.float16)
+    t[[17, 4099, 9000]] = 3.0  # ties in different workgroups -> lowest index
+    assert argmax_dev(C, t.cuda()) == 17
+    t[5000] = float("nan")
+    assert argmax_dev(C, t.cuda()) == 5000 == OD.argmax_first(t.numpy())
+    assert argmax_dev(C, torch.full((1,), -2.0, dtype=torch.float16).cuda()) == 0
+
+
+def test_argmax_log(C):
+    x = rnd((3000,), 15).cuda()
+    ws = torch.empty(C.argmax_workspace_bytes(3000), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    log = torch.full((2,), -1, dtype=torch.int32, device="cuda")
+    n = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for _ in range(3):  # the third call finds the log full and leaves it unchanged
+        C.argmax_f16_into(x, out, log, n, ws)
+    want = int(torch.argmax(x.float()))
+    assert log.tolist() == [want, want] and n.item() == 2 and out.item() == want
+
+
+def test_silu_mul_matches_oracle(C):
+    g, u = rnd((6144,), 16, 3.0), rnd((6144,), 17)
+    out = torch.empty(6144, dtype=torch.float16, device="cuda")
+    C.silu_mul_into(g.cuda(), u.cuda(), out)
+    assert_close(out, OD.silu_mul(g.numpy(), u.numpy()).astype(np.float64), "silu_mul")
+    ref_torch = (torch.nn.functional.silu(g.float()) * u.float()).half()
+    diff = (out.cpu().float() - ref_torch.float()).abs()
+    assert (diff <= 1e-3 * ref_torch.float().abs() + 1e-6).all(), "torch F.silu glue agrees to the fp16 rounding"
+
+
+def test_silu_mul_indexed(C):
+    g, u = rnd((512,), 18, 2.0), rnd((5,), 19)
+    idx = torch.tensor([3, 0, 511, 100, 512], dtype=torch.int32)  # 512 is out of range -> NaN
+    out = torch.empty(5, dtype=torch.float16, device="cuda")
+    C.silu_mul_indexed_into(g.cuda(), idx.cuda(), u.cuda(), out)
+    ref = OD.silu_mul(g.numpy()[idx[:4].numpy()], u.numpy()[:4])
+    assert_close(out[:4], ref.astype(np.float64), "silu_mul_indexed")
+    assert torch.isnan(out[4])
+
+
+def test_embed_lookup(C):
+    table = rnd((1000, 256), 20).cuda()
+    out = torch.empty(256, dtype=torch.float16, device="cuda")
+    for t in (0, 999, 417):
+        C.embed_lookup_into(table, torch.tensor([t], dtype=torch.int32, device="cuda"), out)
+        assert torch.equal(out, table[t])
+    C.embed_lookup_into(table, torch.tensor([1000], dtype=torch.int32, device="cuda"), out)
+    assert out.abs().sum() == 0, "an out-of-range token gives zeros"
+
+
+@pytest.mark.parametrize("NQ,NKV,hd,S,pos", [(16, 8, 128, 2048, 0), (16, 8, 128, 2048, 1500), (4, 2, 64, 64, 63)])
+def test_qk_norm_rope_append_equals_separate_ops(C, ops, NQ, NKV, hd, S, pos):
+    qkv = rnd(((NQ + 2 * NKV) * hd,), 21 + pos, 2.0).cuda()
+    qn, kn = (rnd((hd,), 22) * 0.1 + 1).half().cuda(), (rnd((hd,), 23) * 0.1 + 1).half().cuda()
+    cos_t, sin_t = ops.rope_tables(hd, 1e6, S, "cuda")
+    kc = torch.zeros(NKV, S, hd, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+    C.qk_norm_rope_append(qkv, qn, kn, cos_t, sin_t, torch.tensor([pos], dtype=torch.int32, device="cuda"), q_out,
+                          kc, vc, 1e-6)
+    q = qkv[:NQ * hd].view(NQ, hd).contiguous()
+    k = qkv[NQ * hd:(NQ + NKV) * hd].view(NKV, hd).contiguous()
+    v = qkv[(NQ + NKV) * hd:].view(NKV, hd)
+    c, s = ops.precompute_rope_cos_sin(hd, 1e6, pos, "cuda")
+    q_ref = ops.apply_rope(ops.qk_norm(q, qn), c, s)
+    k_ref = ops.apply_rope(ops.qk_norm(k, kn), c, s)
+    # same binary16 rounding points; only the fp32 sum order of the norm differs
+    # Two binary16 rounding points (norm, then RoPE). One ulp of the normalised value (fp32 rsqrt here,
+    # binary64 in the oracle) moves a RoPE output by up to ~1e-3 of the row scale, which can be large relative
+    # to an output that cancels to near zero, so the bound is normalised by the row scale.
+    ref_q = OD.rope(OD.rmsnorm(q.cpu().numpy(), qn.cpu().numpy(), 1e-6), hd, 1e6, pos).astype(np.float64)
+    err = np.abs(q_out.float().cpu().numpy() - ref_q)
+    assert err.max() <= 2e-3 * np.abs(ref_q).max(), f"q: normalized error {err.max() / np.abs(ref_q).max():.2e}"
+    assert (q_out.float() - q_ref.float()).abs().max() <= 2e-3 * q_ref.float().abs().max()
+    assert (kc[:, pos].float() - k_ref.float()).abs().max() <= 2e-3 * k_ref.float().abs().max()
+    assert torch.equal(vc[:, pos], v)
+    C.qk_norm_rope_append(qkv, qn, kn, cos_t, sin_t, torch.tensor([S], dtype=torch.int32, device="cuda"), q_out,
+                          kc, vc, 1e-6)  # position past the cache: nothing written, no fault
+
+
+@pytest.mark.parametrize("NQ,NKV,hd,S,L", [(16, 8, 128, 2048, 1), (16, 8, 128, 2048, 192), (16, 8, 128, 2048, 2048),
+                                           (4, 2, 64, 64, 40)])
+def test_decode_attention_at_matches_oracle(C, NQ, NKV, hd, S, L):
+    q = rnd((NQ, hd), 30).cuda()
+    kc, vc = rnd((NKV, S, hd), 31).cuda(), rnd((NKV, S, hd), 32).cuda()
+    ws = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+    C.decode_attention_at(q, kc, vc, torch.tensor([L - 1], dtype=torch.int32, device="cuda"), out, ws)
+    ref = O.decode_attention_f64(q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy(), L)
+    assert_close(out, ref, f"attention at len {L}")
+
+
+def test_topk_f16abs_equals_fp32_abs(C, ops):
+    g = rnd((6144,), 40, 0.9)
+    g[::97] = 0.0
+    g[1::89] = -g[2::89][: g[1::89].numel()]  # +/- pairs: equal |g|
+    gd = g.cuda()
+    for k in (768, 1536, 3072, 6144, 1):
+        idx = torch.empty(k, dtype=torch.int32, device="cuda")
+        cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+        C.topk_threshold_select_f16abs_into(gd, k, idx, cnt)
+        ref = ops.topk_threshold_select(gd.float().abs().contiguous(), k)
+        assert torch.equal(idx, ref) and cnt.item() == k
+        assert np.array_equal(idx.cpu().numpy(), O.topk_rule_a(np.abs(g.float().numpy()), k))
+
+
+def test_counted_device_gather(C):
+    src = torch.randint(0, 256, (300, 64), dtype=torch.uint8, device="cuda")
+    idx = torch.tensor([5, 299, 0, 7, 8], dtype=torch.int32, device="cuda")
+    dst = torch.full((5, 64), 0xAB, dtype=torch.uint8, device="cuda")
+    C.gather_rows_device_counted(src.data_ptr(), 300, 64, idx, torch.tensor([3], dtype=torch.int32, device="cuda"),
+                                 dst)
+    assert torch.equal(dst[:3], src[idx[:3].long()])
+    assert (dst[3:] == 0xAB).all(), "rows at or past count are not written"
+
+
+def test_counted_gather_from_pinned_host(C):
+    host = torch.randint(0, 256, (256, 1024), dtype=torch.uint8).pin_memory()
+    ptr = C.host_device_pointer(host)
+    idx = torch.tensor([255, 3, 128, 0], dtype=torch.int32, device="cuda")
+    dst = torch.zeros(4, 1024, dtype=torch.uint8, device="cuda")
+    C.gather_rows_device_counted(ptr, 256, 1024, idx, torch.tensor([4], dtype=torch.int32, device="cuda"), dst)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), host[idx.cpu().long()])
+    with pytest.raises(RuntimeError):
+        C.host_device_pointer(torch.zeros(16, dtype=torch.uint8))  # not pinned

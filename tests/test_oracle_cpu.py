@@ -301,3 +301,65 @@ def test_decode_attention_f64_matches_numpy(NQ, NKV, hd, S, L):
     p /= p.sum(axis=1, keepdims=True)
     ref = np.einsum("ht,htd->hd", p, Vr)
     assert np.allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# decode-step oracle (oracle/decoder.py): closed forms and invariants
+# ---------------------------------------------------------------------------
+
+def test_decoder_oracle_rmsnorm_closed_form():
+    from oracle import decoder as OD
+
+    for a in (0.5, 3.0, -7.25):
+        x = np.full(64, a, np.float16)
+        w = np.linspace(0.5, 1.5, 64).astype(np.float16)
+        want = (a / np.sqrt(a * a + 1e-6)) * w.astype(np.float64)
+        assert np.array_equal(OD.rmsnorm(x, w, 1e-6), OD.f16(want))
+    x = (np.random.default_rng(0).standard_normal((3, 256)) * 4).astype(np.float16)
+    w = np.ones(256, np.float16)
+    # mean (not sum) of squares, per row: eps = 0 makes the result scale-free, exactly for a power of two
+    assert np.array_equal(OD.rmsnorm(x, w, 0.0), OD.rmsnorm((x.astype(np.float64) * 2).astype(np.float16), w, 0.0))
+    r = OD.rmsnorm(x, w, 0.0).astype(np.float64)
+    assert np.allclose(np.mean(r * r, axis=1), 1.0, rtol=2e-3)
+
+
+def test_decoder_oracle_rope_closed_form():
+    from oracle import decoder as OD
+
+    x = np.array([[1.0, 0.0]], np.float16)  # head_dim 2: one pair, inv_freq 1, angle = pos radians
+    for pos in (0, 1, 2, 5):
+        out = OD.rope(x, 2, 10000.0, pos).astype(np.float64)
+        assert np.array_equal(out, OD.f16([[np.cos(pos), np.sin(pos)]]).astype(np.float64))
+    y = (np.random.default_rng(1).standard_normal((4, 128))).astype(np.float16)
+    assert np.array_equal(OD.rope(y, 128, 1e6, 0), y), "position 0 is the identity"
+    r = OD.rope(y, 128, 1e6, 1234).astype(np.float64)
+    n0 = y[:, :64].astype(np.float64) ** 2 + y[:, 64:].astype(np.float64) ** 2
+    n1 = r[:, :64] ** 2 + r[:, 64:] ** 2
+    assert np.allclose(n0, n1, rtol=3e-3, atol=1e-6), "each (i, i + hd/2) pair is rotated"
+    ang = OD.rope_angles(128, 1e6, 77)
+    assert ang[0] == np.float32(77.0) and ang.dtype == np.float32
+
+
+def test_decoder_oracle_silu_argmax_add():
+    from oracle import decoder as OD
+
+    t = np.linspace(-8, 8, 101)
+    assert np.allclose(OD.silu(t) - OD.silu(-t), t, atol=1e-12)
+    assert OD.silu(np.array([0.0]))[0] == 0.0
+    assert OD.argmax_first(np.array([1, 3, 3, 2], np.float16)) == 1
+    assert OD.argmax_first(np.array([1, np.nan, 5, np.nan], np.float16)) == 1
+    a = np.random.default_rng(2).standard_normal(1000).astype(np.float16)
+    b = np.random.default_rng(3).standard_normal(1000).astype(np.float16)
+    assert np.array_equal(OD.residual_add(a, b), (a.astype(np.float32) + b.astype(np.float32)).astype(np.float16))
+
+
+def test_decoder_oracle_gemv_f16():
+    from oracle import decoder as OD
+
+    W = (np.random.default_rng(4).standard_normal((64, 96)) * 0.1).astype(np.float16)
+    e = np.zeros(96, np.float16)
+    e[17] = 1.0
+    assert np.array_equal(OD.gemv_f16(W, e), W[:, 17])
+    x = np.random.default_rng(5).standard_normal(96).astype(np.float16)
+    ref = W.astype(np.float64) @ x.astype(np.float64)
+    assert np.allclose(OD.gemv_f16(W, x).astype(np.float64), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
