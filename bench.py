@@ -24,6 +24,10 @@ Also reported:
   decode_chain    the 112 dependent launches of one decode step, graph-replayed;
   per_shape_cold  per-shape INT4 / INT8 single-launch times on cold copies;
   topk_us_I6144   top-k latency at I=6144;
+  dip_mlp_layer   BASELINE configs 3-4: one layer's dense / DIP (k/I 0.125, 0.25, 0.5) / cache-aware
+                  DIP MLP, graph-replayed over 28 distinct layers;
+  decode          BASELINE config 5: greedy decode tok/s of the random-init 28-layer Qwen3-1.7B
+                  shape, dense vs DIP vs cache-aware DIP at k/I = 0.5 (64-token prompt, 128 tokens);
   cpu_baseline    the CPU oracle on a bounded sample (one thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -241,6 +245,129 @@ def bench_decode_chain(ops, layers, step_bytes):
     del chain, graph
     return decode_chain
 
+def mlp_bytes(L, I: int, H: int, k=None) -> int:
+    """Algorithmic bytes of one layer's MLP: dense reads gate|up and down; DIP reads gate, k rows of up and
+    k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes."""
+    row = L.gu_Wq.shape[1] + 4 * L.gu_scale.shape[1]
+    if k is None:
+        return 2 * I * row + L.down_Wq.numel() + 4 * L.down_scale.numel() + 2 * (H + 3 * I + H)
+    row_t = L.down_T_Wq.shape[1] + 4 * L.down_T_scale.shape[1]
+    return I * row + k * (row + row_t) + 2 * (H + I + 2 * k + H) + 4 * (I + k)
+
+
+def graph_time_us(fn, reps: int = 10) -> float:
+    """Average time of fn's launches captured once in a HIP graph and replayed `reps` times (two HIP events
+    on the current stream around the replays)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def bench_dip_mlp(D, w, hot, dev):
+    """BASELINE configs 3 and 4: one layer's DIP MLP (gate GEMV, top-k of |gate|, sparse up, SiLU gating, sparse
+    down) at k/I in {0.125, 0.25, 0.5}, the dense MLP, and the cache-aware form at k/I = 0.5 with a 20% hot
+    cache whose misses come from pinned host memory. Each figure is the time of the 28 layers' MLPs replayed
+    from one graph, divided by 28 (28 distinct weight sets, 540 MB, so weights come from HBM)."""
+    import torch
+
+    c = w.config
+    I, H = c.intermediate, c.hidden
+    x = (torch.randn(H, generator=torch.Generator().manual_seed(1)).half()).to(dev)
+    res = {}
+
+    def run(eng):
+        eng.h.copy_(x)
+        torch.cuda.synchronize()
+        return graph_time_us(lambda: [eng._mlp(l, L) for l, L in enumerate(w.layers)]) / c.layers
+
+    eng = D.DecodeEngine(w, "dense", max_new_tokens=1)
+    us = run(eng)
+    nb = mlp_bytes(w.layers[0], I, H)
+    res["dense"] = {"us": round(us, 2), "bytes": nb, "GBps": round(nb / us / 1e3, 1)}
+    del eng
+    for frac in (0.125, 0.25, 0.5):
+        k = int(I * frac)
+        eng = D.DecodeEngine(w, "dip", dip_k=k, max_new_tokens=1)
+        us = run(eng)
+        nb = mlp_bytes(w.layers[0], I, H, k)
+        res[f"dip_k{k}"] = {"k_over_I": frac, "us": round(us, 2), "bytes": nb, "GBps": round(nb / us / 1e3, 1)}
+        if frac == 0.5:
+            y_dip = eng.down.clone()
+        del eng
+    k = I // 2
+    eng = D.DecodeEngine(w, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=1)
+    us = run(eng)
+    assert torch.equal(eng.down, y_dip), "cache-aware DIP must equal DIP bit for bit"
+    misses = int(eng.miss_cnt.item())
+    nb = mlp_bytes(w.layers[0], I, H, k)
+    res[f"cached_dip_k{k}"] = {"k_over_I": 0.5, "hot_fraction": 0.2, "us": round(us, 2),
+                               "misses_last_layer": misses, "bit_identical_to_dip": True,
+                               "host_bytes_last_layer": misses * (w.layers[0].gu_Wq.shape[1] +
+                                                                  w.layers[0].down_T_Wq.shape[1]),
+                               "note": "misses read from pinned host memory by an in-graph device gather"}
+    del eng
+    return res
+
+
+def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
+    """greedy decoding of the random-init 28-layer Qwen3-1.7B-shaped INT4 decoder from a
+    seeded 64-token prompt, 128 new tokens, dense vs DIP vs cache-aware DIP at k/I = 0.5 (20% hot cache,
+    misses from pinned host memory). One HIP graph per token; decode_tok_s = new tokens / decode time,
+    end_to_end_tok_s = new tokens / (prefill + decode) time (the reference's tokens/sec, bench_m7_pareto.py:87-90)."""
+    import torch
+
+    c = w.config
+    I = c.intermediate
+    prompt = torch.randint(0, c.vocab, (n_prompt,), generator=torch.Generator().manual_seed(7)).tolist()
+    k = I // 2
+    out, toks = {}, {}
+    L0 = w.layers[0]
+    attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
+    for mode in ("dense", "dip", "cached_dip"):
+        eng = D.DecodeEngine(w, mode, dip_k=None if mode == "dense" else k,
+                             hot_channels=hot if mode == "cached_dip" else None, max_new_tokens=n_new)
+        eng.capture()
+        eng.generate(prompt[:8], 8)  # warm up the graphs
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.reset()
+        eng.prefill(prompt)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        eng.decode(n_new)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        toks[mode] = eng.log[:n_new].tolist()
+        mlp = mlp_bytes(L0, I, c.hidden, None if mode == "dense" else k)
+        per_tok = c.layers * (attn_w + mlp) + w.lm_head.numel() * 2
+        out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
+                     "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
+                     "weight_bytes_per_token": per_tok,
+                     "weight_GBps": round(per_tok * n_new / (t2 - t1) / 1e9, 1)}
+        del eng
+        torch.cuda.empty_cache()
+        log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
+    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"]
+    assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
+    out["config"] = {"prompt_tokens": n_prompt, "new_tokens": n_new, "dip_k": k, "hot_fraction": 0.2,
+                     "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed and LM head",
+                     "kv": "fp16, max_seq 2048"}
+    return out
+
+
 
 def cpu_baseline(layer_mats_cpu, budget_s: float = 12.0):
     """The CPU oracle (scalar C, one thread) on layer 0's seven GEMVs, repeated to ~budget_s."""
@@ -271,6 +398,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the decode-chain, per-shape and top-k tables")
+    ap.add_argument("--no-decode", action="store_true", help="skip the DIP MLP and decode tok/s sections")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU (the hot path is single-GPU; --gpus {args.gpus} is not "
@@ -389,6 +517,23 @@ def main() -> int:
         log("per-shape table done")
         result["topk_us_I6144"] = bench_topk(ops, dev, gen)
         log("top-k done")
+    if not args.no_decode:
+        from soinfer.runtime import decoder as D
+
+        try:
+            del layers, group
+        except NameError:
+            pass
+        torch.cuda.empty_cache()
+        w = D.random_decoder(D.QWEN3_1P7B, seed=0)
+        calib = torch.randint(0, D.QWEN3_1P7B.vocab, (64,), generator=torch.Generator().manual_seed(1000)).tolist()
+        hot = D.calibrate_hot_channels(w, D.QWEN3_1P7B.intermediate // 2, calib, cache_fraction=0.2)
+        log("decoder weights and hot sets ready")
+        result["dip_mlp_layer"] = bench_dip_mlp(D, w, hot, dev)
+        log("DIP MLP done")
+        result["decode"] = bench_decode(D, w, hot, dev)
+        del w
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         g = torch.Generator().manual_seed(1)
         layer0 = []
