@@ -294,6 +294,38 @@ int soi_qk_norm_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const u
                             int64_t max_seq, int64_t head_dim, float eps, void* stream);
 int soi_advance_position(int32_t* pos, int32_t delta, void* stream);
 
+/* --------------------------------------------------------------------------
+ * Fused decode-step GEMVs (no reference entry points: each fuses glue of
+ * generate.py into the INT4 GEMV so a decoder layer needs fewer launches;
+ * every rounding point of the separate ops is kept).
+ *
+ * soi_gemv_w4a16_rmsnorm: y = W . rmsnorm(x + delta, norm_weight) with the
+ *   residual add (binary16) and RMSNorm done while loading x. delta may be
+ *   NULL (no add). When given, x_out receives x + delta and h_out the
+ *   normalised vector (both fp16 [K], must not alias x or delta). K % 32 == 0;
+ *   Wq, x, delta, norm_weight, x_out, h_out 16-byte aligned. With swiglu != 0
+ *   the rows of W are interleaved by 8-row tiles (gate rows 4t..4t+3, then up
+ *   rows 4t..4t+3) and y[i] = fp16(silu(fp16(gate_i)) * fp16(up_i)) for
+ *   i < N/2 (N % 8 == 0): the dense SwiGLU of generate.py:176-178 in one pass.
+ * soi_gemv_w4a16_indexed_silu: h_sel[j] = fp16(silu(gate[idx[j]]) *
+ *   fp16(sum_k W[idx[j],k] x[k])): the DIP up projection with the SiLU gating
+ *   of generate.py:301-305 in its epilogue (NaN for an index outside
+ *   [0, min(num_rows, n_gate))).
+ * soi_gemv_dip_fused_up_silu: the same epilogue on soi_gemv_dip_fused_up
+ *   (descriptor rows; sel = the selected channel indices).
+ * ------------------------------------------------------------------------ */
+int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
+                           const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out, uint16_t* y,
+                           int64_t N, int64_t K, int64_t group_size, int64_t num_groups, int swiglu, void* stream);
+int soi_gemv_w4a16_indexed_silu(const uint8_t* Wq, const float* scale, int64_t num_rows, const int32_t* idx,
+                                int64_t k, const uint16_t* x, const uint16_t* gate, int64_t n_gate, uint16_t* h_sel,
+                                int64_t K, int64_t group_size, int64_t num_groups, void* stream);
+int soi_gemv_dip_fused_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                               const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
+                               const int32_t* desc, const int32_t* sel, int64_t k, const uint16_t* x,
+                               const uint16_t* gate, int64_t n_gate, uint16_t* h_sel, int64_t K, int64_t group_size,
+                               int64_t num_groups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -919,6 +919,85 @@ void gather_rows_device_counted(int64_t src_addr, int64_t num_rows, int64_t row_
                  n);
 }
 
+void gemv_w4a16_rmsnorm_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x, c10::optional<torch::Tensor> delta,
+                             torch::Tensor norm_weight, double eps, c10::optional<torch::Tensor> x_out,
+                             c10::optional<torch::Tensor> h_out, torch::Tensor y, int64_t K, int64_t group_size,
+                             bool swiglu) {
+    const char* n = "gemv_w4a16_rmsnorm_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(x, torch::kFloat16, x, n, "x");
+    need(norm_weight, torch::kFloat16, x, n, "norm_weight");
+    need(y, torch::kFloat16, x, n, "y");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K && norm_weight.numel() == K, n,
+                ": Wq / x / norm_weight shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0), n, ": scale must be [N, num_groups]");
+    TORCH_CHECK(y.numel() == (swiglu ? Wq.size(0) / 2 : Wq.size(0)), n, ": y must have N (or N/2 with swiglu) values");
+    const uint16_t* dp = nullptr;
+    uint16_t* xo = nullptr;
+    uint16_t* ho = nullptr;
+    if (delta.has_value()) {
+        need(*delta, torch::kFloat16, x, n, "delta");
+        TORCH_CHECK(delta->numel() == K, n, ": delta must be [K]");
+        dp = h16(*delta);
+    }
+    if (x_out.has_value()) {
+        need(*x_out, torch::kFloat16, x, n, "x_out");
+        TORCH_CHECK(x_out->numel() == K, n, ": x_out must be [K]");
+        xo = h16m(*x_out);
+    }
+    if (h_out.has_value()) {
+        need(*h_out, torch::kFloat16, x, n, "h_out");
+        TORCH_CHECK(h_out->numel() == K, n, ": h_out must be [K]");
+        ho = h16m(*h_out);
+    }
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_rmsnorm(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), dp, h16(norm_weight),
+                                        static_cast<float>(eps), xo, ho, h16m(y), Wq.size(0), K, group_size,
+                                        scale.size(1), swiglu ? 1 : 0, cur_stream(x)),
+                 n);
+}
+
+void gemv_w4a16_indexed_silu_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
+                                  torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
+    const char* n = "gemv_w4a16_indexed_silu_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(idx, torch::kInt32, x, n, "idx");
+    need(x, torch::kFloat16, x, n, "x");
+    need(gate, torch::kFloat16, x, n, "gate");
+    need(h_sel, torch::kFloat16, x, n, "h_sel");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K, n, ": Wq / x shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0) && h_sel.numel() == idx.numel(), n,
+                ": scale / h_sel shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_indexed_silu(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), Wq.size(0),
+                                             idx.data_ptr<int32_t>(), idx.numel(), h16(x), h16(gate), gate.numel(),
+                                             h16m(h_sel), K, group_size, scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void gemv_dip_fused_up_silu_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor staging_Wq,
+                                 torch::Tensor staging_scale, torch::Tensor desc, torch::Tensor sel, torch::Tensor x,
+                                 torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
+    const char* n = "gemv_dip_fused_up_silu_into";
+    check_dip_fused_common(cache_Wq, cache_scale, staging_Wq, staging_scale, desc, K, n);
+    need(sel, torch::kInt32, desc, n, "sel");
+    need(x, torch::kFloat16, desc, n, "x");
+    need(gate, torch::kFloat16, desc, n, "gate");
+    need(h_sel, torch::kFloat16, desc, n, "h_sel");
+    TORCH_CHECK(x.numel() == K && h_sel.numel() == desc.numel() && sel.numel() >= desc.numel(), n, ": shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_dip_fused_up_silu(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(),
+                                            std::min(cache_Wq.size(0), cache_scale.size(0)),
+                                            staging_Wq.data_ptr<uint8_t>(), staging_scale.data_ptr<float>(),
+                                            std::min(staging_Wq.size(0), staging_scale.size(0)),
+                                            desc.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), desc.numel(), h16(x),
+                                            h16(gate), gate.numel(), h16m(h_sel), K, group_size, cache_scale.size(1),
+                                            cur_stream(x)),
+                 n);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "soinfer MI355X (gfx950) quantized decode hot path";
     m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
@@ -966,5 +1045,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "threshold top-k over |fp16 gate| into caller buffers");
     m.def("host_device_pointer", &host_device_pointer, "device address of pinned host memory");
     m.def("gather_rows_device_counted", &gather_rows_device_counted, "device gather of count[0] rows");
+    m.def("gemv_w4a16_rmsnorm_into", &gemv_w4a16_rmsnorm_into,
+          "INT4 GEMV of rmsnorm(x + delta) (optionally with the interleaved SwiGLU epilogue)");
+    m.def("gemv_w4a16_indexed_silu_into", &gemv_w4a16_indexed_silu_into, "DIP up GEMV with SiLU gating");
+    m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");
     m.def("version", []() { return std::string(soi_version()); });
 }

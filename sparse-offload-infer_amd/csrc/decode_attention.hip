@@ -180,19 +180,65 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const uint16_t
     }
 }
 
-// out[h,d] = (sum_s acc_s[d] 2^(m_s-M)) / (sum_s l_s 2^(m_s-M)), s ascending
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, uint16_t* __restrict__ out,
-                                                            int hd, int nsplit) {
-    const int h = blockIdx.x;
-    const float* ph = part + static_cast<int64_t>(h) * nsplit * (hd + 2);
-    float M = kNegBig;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ph[s * (hd + 2)]);
-    float Lsum = 0.0f;
-    for (int s = 0; s < nsplit; ++s) Lsum += ph[s * (hd + 2) + 1] * fast_exp2(ph[s * (hd + 2)] - M);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+// out[h,d] = (sum_s acc_s[d] 2^(m_s-M)) / (sum_s l_s 2^(m_s-M)) over the active
+// splits (all of them, or, in the device-position form, those that start
+// below the current length: the others hold the neutral state and add exact
+// zeros). M and the denominator are block reductions over the splits; each
+// thread then sums its dimension over the splits in ascending order with the
+// loads issued 8 at a time. Fixed order: deterministic.
+constexpr int kCombineThreads = 128;
+constexpr int kCombineMaxSplits = 256;  // nsplit <= 256 by construction of the plan
+
+__device__ __forceinline__ float block_reduce_128(float v, float* s_red, bool is_max) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    v = is_max ? wave_max_bcast(v) : wave_sum_bcast(v);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    return is_max ? fmaxf(s_red[0], s_red[1]) : s_red[0] + s_red[1];
+}
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,
+                                                                        uint16_t* __restrict__ out, int hd,
+                                                                        int nsplit, int tps,
+                                                                        const int32_t* __restrict__ pos, int S) {
+    __shared__ float s_w[kCombineMaxSplits];
+    __shared__ float s_red[kCombineThreads / kWave];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int stride = hd + 2;
+    const float* ph = part + static_cast<int64_t>(h) * nsplit * stride;
+    int ns = nsplit;
+    if (pos) {
+        const int L = cur_len_of(0, pos, S);
+        const int act = (L + tps - 1) / tps;
+        ns = act < nsplit ? act : nsplit;
+    }
+    float m = kNegBig;
+    for (int sp = tid; sp < ns; sp += kCombineThreads) m = fmaxf(m, ldg(ph + sp * stride));
+    const float M = block_reduce_128(m, s_red, true);
+    float lp = 0.0f;
+    for (int sp = tid; sp < ns; sp += kCombineThreads) {
+        const float w = fast_exp2(ldg(ph + sp * stride) - M);
+        if (sp < kCombineMaxSplits) s_w[sp] = w;
+        lp = fmaf(ldg(ph + sp * stride + 1), w, lp);
+    }
+    const float Lsum = block_reduce_128(lp, s_red, false);
+    __syncthreads();  // s_w complete
+    for (int d = tid; d < hd; d += kCombineThreads) {
         float a = 0.0f;
-        for (int s = 0; s < nsplit; ++s) a += ph[s * (hd + 2) + 2 + d] * fast_exp2(ph[s * (hd + 2)] - M);
-        out[static_cast<int64_t>(h) * hd + d] = f32_to_f16_bits(a / Lsum);
+        int sp = 0;
+        for (; sp + 8 <= ns && sp + 8 <= kCombineMaxSplits; sp += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ldg(ph + (sp + u) * stride + 2 + d);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a = fmaf(v[u], s_w[sp + u], a);
+        }
+        for (; sp < ns; ++sp) {
+            const float w = sp < kCombineMaxSplits ? s_w[sp] : fast_exp2(ldg(ph + sp * stride) - M);
+            a = fmaf(ldg(ph + sp * stride + 2 + d), w, a);
+        }
+        stg(out + static_cast<int64_t>(h) * hd + d, f32_to_f16_bits(a / Lsum));
     }
 }
 
@@ -312,8 +358,8 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
 #undef SOI_A
     int s = launch_status(what);
     if (s) return s;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(NQ)), dim3(128), 0, st, part, out,
-                       static_cast<int>(head_dim), p.nsplit);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(NQ)), dim3(kCombineThreads), 0, st, part, out,
+                       static_cast<int>(head_dim), p.nsplit, p.tps, pos, S);
     return launch_status(what);
 }
 

@@ -34,29 +34,6 @@ __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
     return t;
 }
 
-__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
-}
-
-// binary16 add of packed pairs: fp32 sum rounded once to binary16
-__device__ __forceinline__ uint32_t add_f16x2(uint32_t a, uint32_t b) {
-    const f16x2 x = as_f16x2(a), y = as_f16x2(b);
-    return pack_f16x2(static_cast<float>(x.x) + static_cast<float>(y.x),
-                      static_cast<float>(x.y) + static_cast<float>(y.y));
-}
-
-__device__ __forceinline__ float sumsq_f16x2(uint32_t a) {
-    const f16x2 x = as_f16x2(a);
-    const float u = static_cast<float>(x.x), v = static_cast<float>(x.y);
-    return fmaf(v, v, u * u);
-}
-
-__device__ __forceinline__ uint32_t norm_f16x2(uint32_t a, uint32_t w, float inv) {
-    const f16x2 x = as_f16x2(a), g = as_f16x2(w);
-    return pack_f16x2(static_cast<float>(x.x) * inv * static_cast<float>(g.x),
-                      static_cast<float>(x.y) * inv * static_cast<float>(g.y));
-}
-
 // One workgroup per row. ADD: the row is v = x + delta (binary16), x is
 // replaced by v, and the normalised row is computed from v. Both passes read
 // the original x and delta (the update is written in the second pass), so no
@@ -363,9 +340,6 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const floa
         }
     }
 }
-
-// h = fp16(silu(fp32(g)) * fp32(u)), silu(t) = t / (1 + exp(-t)).
-__device__ __forceinline__ float silu_f32(float t) { return t / (1.0f + expf(-t)); }
 
 // dense: gate = gu[0, n), up = gu[up_offset, up_offset + n) of one buffer or two
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,

@@ -90,11 +90,92 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int
     }
 }
 
+// x sources. PlainX: x as given. NormX: x = rmsnorm(a (+ d), w) computed on
+// load, with inv = 1/sqrt(mean((a+d)^2) + eps) precomputed by the workgroup:
+// element h = fp16(fp16(a + d) * inv * w), the rounding points of the separate
+// residual add and RMSNorm (VEC only: K % 32 == 0, 16-byte aligned vectors).
+// base(): a K-element fp16 vector (2K bytes), a legal read target for a row
+// that cannot be resolved (its K/2 packed bytes and K/gs scales fit in it).
+struct PlainX {
+    const uint16_t* x;
+    __device__ __forceinline__ const uint16_t* base() const { return x; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int K, int c, bool cv, f16x2 xv[16]) const {
+        load_x_chunk<VEC, FULL>(x, K, c, cv, xv);
+    }
+};
+
+struct NormX {
+    const uint16_t* a;
+    const uint16_t* d;  // may be null
+    const uint16_t* w;
+    float inv;
+    __device__ __forceinline__ const uint16_t* base() const { return a; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int, int c, bool cv, f16x2 xv[16]) const {
+        const u32x4* z = reinterpret_cast<const u32x4*>(g_zero16);
+        const u32x4* a4 = reinterpret_cast<const u32x4*>(a) + 4 * c;
+        const u32x4* d4 = reinterpret_cast<const u32x4*>(d) + 4 * c;
+        const u32x4* w4 = reinterpret_cast<const u32x4*>(w) + 4 * c;
+        const bool ok = FULL || cv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u32x4 t = ldg(ok ? a4 + i : z);
+            if (d) {
+                const u32x4 e = ldg(ok ? d4 + i : z);
+                t.x = add_f16x2(t.x, e.x);
+                t.y = add_f16x2(t.y, e.y);
+                t.z = add_f16x2(t.z, e.z);
+                t.w = add_f16x2(t.w, e.w);
+            }
+            const u32x4 g = ldg(ok ? w4 + i : z);
+            xv[4 * i + 0] = as_f16x2(norm_f16x2(t.x, g.x, inv));
+            xv[4 * i + 1] = as_f16x2(norm_f16x2(t.y, g.y, inv));
+            xv[4 * i + 2] = as_f16x2(norm_f16x2(t.z, g.z, inv));
+            xv[4 * i + 3] = as_f16x2(norm_f16x2(t.w, g.w, inv));
+        }
+    }
+};
+
+// Epilogues: row r of the tile has its fp32 total in the lanes reduce_rows_row
+// assigns to it. StoreY: y[row] = fp16(total) (NaN for an unresolvable row).
+// SiluIdxY: y[row] = fp16(silu(gate[idx[row]]) * fp16(total)), the SwiGLU gating
+// of the selected channels (generate.py:304-305). SwigluY (R = 8 only, rows
+// interleaved by 8-row tiles as 4 gate rows then the 4 matching up rows):
+// y[4*tile + i] = fp16(silu(fp16(gate_i)) * fp16(up_i)) (generate.py:178).
+struct StoreY {
+    static constexpr bool kSwiglu = false;
+    uint16_t* y;
+    __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
+        stg(y + row, valid ? f32_to_f16_bits(total) : uint16_t(0x7e00u));
+    }
+};
+
+struct SiluIdxY {
+    static constexpr bool kSwiglu = false;
+    uint16_t* y;
+    const uint16_t* gate;
+    const int32_t* idx;
+    int n_gate;
+    __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
+        const int c = ldg(idx + row);
+        const bool ok = valid && c >= 0 && c < n_gate;
+        const float u = f16_bits_to_f32(f32_to_f16_bits(total));
+        const float g = ok ? f16_bits_to_f32(ldg(gate + c)) : 0.0f;
+        stg(y + row, ok ? f32_to_f16_bits(silu_f32(g) * u) : uint16_t(0x7e00u));
+    }
+};
+
+struct SwigluY {
+    static constexpr bool kSwiglu = true;
+    uint16_t* y;
+};
+
 // R rows per wave; PU passes (64 chunks each) loaded per batch, so a wave has
 // R*PU 1 KB row segments in flight before it does any arithmetic.
-template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows>
-__device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, const uint16_t* __restrict__ x,
-                                               uint16_t* __restrict__ y, int K, int gs, int64_t row0) {
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class XS, class EP>
+__device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, const XS& xsrc, const EP& ep, int K,
+                                               int gs, int64_t row0) {
     constexpr int SC = CHUNK_SCALE ? 1 : 4;
     const int lane = threadIdx.x;
     const int words = (K + 7) >> 3;
@@ -119,8 +200,8 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (!valid[r]) {
-                ref[r].w = ref[0].ok ? ref[0].w : reinterpret_cast<const uint8_t*>(x);
-                ref[r].s = ref[0].ok ? ref[0].s : reinterpret_cast<const float*>(x);
+                ref[r].w = ref[0].ok ? ref[0].w : reinterpret_cast<const uint8_t*>(xsrc.base());
+                ref[r].s = ref[0].ok ? ref[0].s : reinterpret_cast<const float*>(xsrc.base());
             }
         }
     }
@@ -153,7 +234,7 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
                     }
                 }
             }
-            load_x_chunk<VEC, FULL>(x, K, c, cv, xv[p]);
+            xsrc.template load<VEC, FULL>(K, c, cv, xv[p]);
             const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 #pragma unroll
             for (int i = 0; i < SC; ++i) {
@@ -202,14 +283,25 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
     bool vr = valid[0];
 #pragma unroll
     for (int i = 1; i < R; ++i) vr = (r == i) ? valid[i] : vr;
-    if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N))
-        stg(y + row0 + r, vr ? f32_to_f16_bits(total) : uint16_t(0x7e00u));
+    if constexpr (EP::kSwiglu) {
+        static_assert(R == 8, "the SwiGLU epilogue pairs rows i and i+4 of an 8-row tile");
+        // lanes 0-31 hold rows 7..4 (up), lanes 32-63 rows 3..0 (gate): row r and r-4 are 32 lanes apart
+        const float other = __shfl_xor(total, 32, kWave);
+        const bool vo = __shfl_xor(vr ? 1 : 0, 32, kWave) != 0;
+        if ((lane & 7) == 0 && r >= 4) {
+            const float g = f16_bits_to_f32(f32_to_f16_bits(other));
+            const float u = f16_bits_to_f32(f32_to_f16_bits(total));
+            stg(ep.y + (row0 >> 1) + (r - 4), (vr && vo) ? f32_to_f16_bits(silu_f32(g) * u) : uint16_t(0x7e00u));
+        }
+    } else {
+        if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) ep.store(row0 + r, total, vr);
+    }
 }
 
-template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows>
-__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x,
-                                                       uint16_t* __restrict__ y, int K, int gs) {
-    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, x, y, K, gs,
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY>
+__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x, EP ep,
+                                                       int K, int gs) {
+    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, PlainX{x}, ep, K, gs,
                                                            static_cast<int64_t>(blockIdx.x) * R);
 }
 
@@ -233,7 +325,64 @@ __global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* co
     if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
     const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
     DenseRows rows{W, S, row_bytes, G};
-    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, x, y, K, gs, static_cast<int64_t>(tile) * R);
+    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,
+                                                       static_cast<int64_t>(tile) * R);
+}
+
+// Decode-step form: y = W . rmsnorm(a + d, w) with the residual add and the
+// RMSNorm done on load. Every workgroup computes inv = 1/sqrt(mean((a+d)^2) +
+// eps) with the same wave reduction (so all agree bit for bit); workgroup 0
+// also writes x_out = a + d and h_out = rmsnorm(a + d, w) when given. a, d,
+// w, x_out, h_out: fp16 [K], K % 32 == 0, 16-byte aligned; x_out and h_out
+// must not alias a or d (other workgroups are still reading them).
+template <int R, bool CHUNK_SCALE, bool FULL, class EP>
+__global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int64_t N, const uint16_t* __restrict__ a,
+                                                            const uint16_t* __restrict__ d,
+                                                            const uint16_t* __restrict__ w, float eps,
+                                                            uint16_t* __restrict__ x_out, uint16_t* __restrict__ h_out,
+                                                            EP ep, int K, int gs) {
+    const int lane = threadIdx.x;
+    const u32x4* a4 = reinterpret_cast<const u32x4*>(a);
+    const u32x4* d4 = reinterpret_cast<const u32x4*>(d);
+    const int n8 = K >> 3;
+    float ss = 0.0f;
+    for (int c = lane; c < n8; c += kWave) {
+        u32x4 t = ldg(a4 + c);
+        if (d) {
+            const u32x4 e = ldg(d4 + c);
+            t.x = add_f16x2(t.x, e.x);
+            t.y = add_f16x2(t.y, e.y);
+            t.z = add_f16x2(t.z, e.z);
+            t.w = add_f16x2(t.w, e.w);
+        }
+        ss += sumsq_f16x2(t.x) + sumsq_f16x2(t.y) + sumsq_f16x2(t.z) + sumsq_f16x2(t.w);
+    }
+    const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(K) + eps);
+    if (blockIdx.x == 0 && (x_out || h_out)) {
+        const u32x4* w4 = reinterpret_cast<const u32x4*>(w);
+        for (int c = lane; c < n8; c += kWave) {
+            u32x4 t = ldg(a4 + c);
+            if (d) {
+                const u32x4 e = ldg(d4 + c);
+                t.x = add_f16x2(t.x, e.x);
+                t.y = add_f16x2(t.y, e.y);
+                t.z = add_f16x2(t.z, e.z);
+                t.w = add_f16x2(t.w, e.w);
+            }
+            if (x_out) stg(reinterpret_cast<u32x4*>(x_out) + c, t);
+            if (h_out) {
+                const u32x4 g = ldg(w4 + c);
+                u32x4 r;
+                r.x = norm_f16x2(t.x, g.x, inv);
+                r.y = norm_f16x2(t.y, g.y, inv);
+                r.z = norm_f16x2(t.z, g.z, inv);
+                r.w = norm_f16x2(t.w, g.w, inv);
+                stg(reinterpret_cast<u32x4*>(h_out) + c, r);
+            }
+        }
+    }
+    gemv_int4_tile<R, 1, true, CHUNK_SCALE, true, FULL>(rows, N, NormX{a, d, w, inv}, ep, K, gs,
+                                                       static_cast<int64_t>(blockIdx.x) * R);
 }
 
 // Grouped form: problems of up to kMaxClasses shapes in one launch. Class c
@@ -285,7 +434,8 @@ __global__ __launch_bounds__(64) void gemv_int4_grouped_kernel(const uint8_t* co
     if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
     const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
     DenseRows rows{W, S, row_bytes, G};
-    gemv_int4_tile<R, 1, VEC, CHUNK_SCALE, true, FULL>(rows, N, x, y, K, gs, static_cast<int64_t>(tile) * R);
+    gemv_int4_tile<R, 1, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,
+                                                      static_cast<int64_t>(tile) * R);
 }
 
 // ---------------------------------------------------------------------------
@@ -310,8 +460,8 @@ static Int4Plan plan_int4(int64_t N, int64_t K, bool vec) {
     return p;
 }
 
-template <bool BITFIELD, class Rows>
-static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, uint16_t* y, int64_t K, int64_t gs, bool vec,
+template <bool BITFIELD, class Rows, class EP = StoreY>
+static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP& ep, int64_t K, int64_t gs, bool vec,
                        hipStream_t st, const char* what) {
     if (N == 0) return SOI_OK;
     const Int4Plan pl = plan_int4(N, K, vec);
@@ -319,8 +469,9 @@ static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, uint16_t*
     const bool full = vec && cs && (N % pl.R == 0) && ((K / 32) % (64 * pl.PU) == 0);
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
     const int Ki = static_cast<int>(K), gi = static_cast<int>(gs);
-#define SOI_L(RR, PP, V, CS, FL) \
-    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows>), grid, dim3(64), 0, st, rows, N, x, y, Ki, gi)
+#define SOI_L(RR, PP, V, CS, FL)                                                                                \
+    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows, EP>), grid, dim3(64), 0, st, rows, N, x, ep, \
+                       Ki, gi)
 #define SOI_CS(RR, PP, V)                    \
     if (V && full) SOI_L(RR, PP, V, true, true); \
     else if (cs) SOI_L(RR, PP, V, true, false);  \
@@ -423,7 +574,7 @@ static int dense_int4(const uint8_t* Wq, const float* scale, const uint16_t* x, 
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
     const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
     DenseRows rows{Wq, scale, row_bytes, G};
-    return launch_int4<BITFIELD>(rows, N, x, y, K, gs, vec, as_stream(stream), what);
+    return launch_int4<BITFIELD>(rows, N, x, StoreY{y}, K, gs, vec, as_stream(stream), what);
 }
 
 }  // namespace soi
@@ -456,7 +607,7 @@ extern "C" int soi_gemv_dip_fused_up(const uint8_t* cache_Wq, const float* cache
                      (staging_rows == 0 || aligned16(staging_Wq));
     DescRows rows{cache_Wq, cache_scale, cache_rows, staging_Wq, staging_scale, staging_rows, desc, row_bytes,
                   num_groups};
-    return launch_int4<true>(rows, k, x, y, K, group_size, vec, as_stream(stream), what);
+    return launch_int4<true>(rows, k, x, StoreY{y}, K, group_size, vec, as_stream(stream), what);
 }
 
 extern "C" int soi_gemv_w4a16_indexed(const uint8_t* Wq, const float* scale, int64_t num_rows, const int32_t* idx,
@@ -471,7 +622,7 @@ extern "C" int soi_gemv_w4a16_indexed(const uint8_t* Wq, const float* scale, int
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
     const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
     IndexRows rows{Wq, scale, num_rows, idx, row_bytes, num_groups};
-    return launch_int4<true>(rows, k, x, y, K, group_size, vec, as_stream(stream), what);
+    return launch_int4<true>(rows, k, x, StoreY{y}, K, group_size, vec, as_stream(stream), what);
 }
 
 extern "C" int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
@@ -544,4 +695,105 @@ extern "C" int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float
     SOI_REQUIRE(Wq_ptrs && scale_ptrs && x_ptrs && y_ptrs, "%s: null pointer table", what);
     return launch_int4_batched(Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs, P, N, K, group_size, num_groups,
                                as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
+                                      const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out,
+                                      uint16_t* y, int64_t N, int64_t K, int64_t group_size, int64_t num_groups,
+                                      int swiglu, void* stream) {
+    const char* what = "soi_gemv_w4a16_rmsnorm";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: N out of range", what);
+    SOI_REQUIRE(K % 32 == 0, "%s: K must be a multiple of 32", what);
+    SOI_REQUIRE(Wq && scale && x && norm_weight && y, "%s: null pointer", what);
+    SOI_REQUIRE(aligned16(Wq) && aligned16(x) && aligned16(norm_weight) && (!delta || aligned16(delta)) &&
+                    (!x_out || aligned16(x_out)) && (!h_out || aligned16(h_out)),
+                "%s: vectors and weights must be 16-byte aligned", what);
+    const void* ins[2] = {x, delta};
+    for (const void* o : {static_cast<const void*>(x_out), static_cast<const void*>(h_out)})
+        for (const void* i : ins) SOI_REQUIRE(!o || o != i, "%s: x_out / h_out must not alias x or delta", what);
+    SOI_REQUIRE(!swiglu || N % 8 == 0, "%s: the SwiGLU form needs N %% 8 == 0 (8-row gate/up tiles)", what);
+    if (N == 0) return SOI_OK;
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    DenseRows rows{Wq, scale, row_bytes, num_groups};
+    hipStream_t s = as_stream(stream);
+    const bool cs = (group_size % 32) == 0;
+    const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size);
+    const bool full_k = (K / 32) % 64 == 0;
+    if (swiglu) {
+        const dim3 grid(static_cast<unsigned>(N / 8));
+        const SwigluY ep{y};
+#define SOI_N(CS, FL)                                                                                                  \
+    hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, SwigluY>), grid, dim3(64), 0, s, rows, N, x, delta, norm_weight, \
+                       eps, x_out, h_out, ep, Ki, gi)
+        if (cs && full_k) SOI_N(true, true);
+        else if (cs) SOI_N(true, false);
+        else SOI_N(false, false);
+#undef SOI_N
+        return launch_status(what);
+    }
+    const int R = N >= 8 * 1024 ? 8 : N >= 4 * 1024 ? 4 : N >= 2 * 1024 ? 2 : 1;
+    const bool full = cs && full_k && N % R == 0;
+    const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
+    const StoreY ep{y};
+#define SOI_N(RR, CS, FL)                                                                                              \
+    hipLaunchKernelGGL((gemv_int4_norm_kernel<RR, CS, FL, StoreY>), grid, dim3(64), 0, s, rows, N, x, delta,           \
+                       norm_weight, eps, x_out, h_out, ep, Ki, gi)
+#define SOI_NR(RR)                         \
+    if (full) SOI_N(RR, true, true);       \
+    else if (cs) SOI_N(RR, true, false);   \
+    else SOI_N(RR, false, false)
+    switch (R) {
+        case 8: SOI_NR(8); break;
+        case 4: SOI_NR(4); break;
+        case 2: SOI_NR(2); break;
+        default: SOI_NR(1); break;
+    }
+#undef SOI_NR
+#undef SOI_N
+    return launch_status(what);
+}
+
+extern "C" int soi_gemv_w4a16_indexed_silu(const uint8_t* Wq, const float* scale, int64_t num_rows, const int32_t* idx,
+                                           int64_t k, const uint16_t* x, const uint16_t* gate, int64_t n_gate,
+                                           uint16_t* h_sel, int64_t K, int64_t group_size, int64_t num_groups,
+                                           void* stream) {
+    const char* what = "soi_gemv_w4a16_indexed_silu";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 31) - 1 && num_rows >= 0 && n_gate >= 0 &&
+                    n_gate <= (int64_t(1) << 31) - 1,
+                "%s: size out of range", what);
+    if (k == 0) return SOI_OK;
+    SOI_REQUIRE(Wq && scale && idx && x && gate && h_sel, "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
+    IndexRows rows{Wq, scale, num_rows, idx, row_bytes, num_groups};
+    return launch_int4<true>(rows, k, x, SiluIdxY{h_sel, gate, idx, static_cast<int>(n_gate)}, K, group_size, vec,
+                             as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_dip_fused_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                                          const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
+                                          const int32_t* desc, const int32_t* sel, int64_t k, const uint16_t* x,
+                                          const uint16_t* gate, int64_t n_gate, uint16_t* h_sel, int64_t K,
+                                          int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_dip_fused_up_silu";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 31) - 1 && n_gate >= 0 && n_gate <= (int64_t(1) << 31) - 1,
+                "%s: size out of range", what);
+    SOI_REQUIRE(cache_rows >= 0 && staging_rows >= 0, "%s: negative row count", what);
+    if (k == 0) return SOI_OK;
+    SOI_REQUIRE(desc && sel && x && gate && h_sel, "%s: null pointer", what);
+    SOI_REQUIRE((cache_rows == 0 || (cache_Wq && cache_scale)) && (staging_rows == 0 || (staging_Wq && staging_scale)),
+                "%s: null row source", what);
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    const bool vec = (K % 32 == 0) && (cache_rows == 0 || aligned16(cache_Wq)) &&
+                     (staging_rows == 0 || aligned16(staging_Wq)) && aligned16(x);
+    DescRows rows{cache_Wq, cache_scale, cache_rows, staging_Wq, staging_scale, staging_rows, desc, row_bytes,
+                  num_groups};
+    return launch_int4<true>(rows, k, x, SiluIdxY{h_sel, gate, sel, static_cast<int>(n_gate)}, K, group_size, vec,
+                             as_stream(stream), what);
 }

@@ -20,6 +20,7 @@ namespace soi {
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
@@ -303,5 +304,35 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<f16>(v));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return static_cast<float>(__builtin_bit_cast(f16, b)); }
+
+
+// ---------------------------------------------------------------------------
+// binary16 element helpers shared by the decode-step kernels
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
+}
+
+// binary16 add of packed pairs: fp32 sum rounded once to binary16
+__device__ __forceinline__ uint32_t add_f16x2(uint32_t a, uint32_t b) {
+    const f16x2 x = as_f16x2(a), y = as_f16x2(b);
+    return pack_f16x2(static_cast<float>(x.x) + static_cast<float>(y.x),
+                      static_cast<float>(x.y) + static_cast<float>(y.y));
+}
+
+__device__ __forceinline__ float sumsq_f16x2(uint32_t a) {
+    const f16x2 x = as_f16x2(a);
+    const float u = static_cast<float>(x.x), v = static_cast<float>(x.y);
+    return fmaf(v, v, u * u);
+}
+
+__device__ __forceinline__ uint32_t norm_f16x2(uint32_t a, uint32_t w, float inv) {
+    const f16x2 x = as_f16x2(a), g = as_f16x2(w);
+    return pack_f16x2(static_cast<float>(x.x) * inv * static_cast<float>(g.x),
+                      static_cast<float>(x.y) * inv * static_cast<float>(g.y));
+}
+
+// silu(t) = t / (1 + exp(-t)) in fp32 (SwiGLU gating, generate.py:178)
+__device__ __forceinline__ float silu_f32(float t) { return t / (1.0f + expf(-t)); }
 
 }  // namespace soi

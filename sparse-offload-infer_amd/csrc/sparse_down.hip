@@ -5,14 +5,17 @@
 //   y[c] = sum_{j<k} (h_j * s[j, c/gs]) * q[j, c],  fp32 accumulation, fp16 out.
 // The reference runs one thread per output column over all k rows, which
 // touches 4 bytes per row per thread and uses a handful of CUs. Here:
-//   pass 1 (partial): workgroup g owns rows [g*R, (g+1)*R); its 8 waves take
-//     rows round-robin; lane l owns a 16-byte chunk (32 consecutive columns)
-//     of a 2048-column slab, so each row is read as one coalesced 1 KB wave
-//     load. Each lane keeps 32 fp32 sums; per row: coef = fl(h_j*s),
+//   pass 1 (partial): workgroup g owns rows [g*R, (g+1)*R) (R chosen so that
+//     k rows spread over ~256 workgroups); its 4 waves take blocks of U = 4
+//     rows in turn; lane l owns a 16-byte chunk (32 consecutive columns) of a
+//     2048-column slab, so each row is read as one coalesced 1 KB wave load.
+//     Each lane keeps 32 fp32 sums; per row: coef = fl(h_j*s),
 //     acc_c = fma(coef, q_c, acc_c) with q_c an exact binary16 integer
-//     (v_fma_mix_f32). The 8 waves are summed in LDS in wave order and the
+//     (v_fma_mix_f32). The waves are summed in LDS in wave order and the
 //     workgroup's partial row is written to the workspace.
-//   pass 2 (reduce): y[c] = fp16(sum over g in ascending order of partial[g,c]).
+//   pass 2 (reduce): y[c] = fp16(sum over g of partial[g,c]): 8 interleaved
+//     groups of g per column, each summed in ascending g with its loads
+//     issued 8 at a time, then the 8 group sums in a fixed order.
 // Fixed partition and fixed order: deterministic, and every row source
 // (gathered rows, hot cache + staging descriptors, resident index list) gives
 // bit-identical results for the same logical rows.
@@ -22,7 +25,7 @@
 
 namespace soi {
 
-constexpr int kDownWaves = 8;
+constexpr int kDownWaves = 4;
 constexpr int kDownThreads = kDownWaves * kWave;
 constexpr int kSlabCols = kWave * 32;  // columns covered by one wave-wide row load
 constexpr int kRedPad = kWave + 1;      // LDS row pitch (floats) for the wave-sum transpose
@@ -113,23 +116,75 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows 
     }
 }
 
+// Thread (c4, t): columns 4*c4..4*c4+3, partial rows g = t, t+8, t+16, ...;
+// the 8 group sums are then added in t order through LDS. A fixed order for a
+// given G: deterministic. G == 0 writes zeros (the empty sum).
+constexpr int kRedGroups = 8;
+constexpr int kRedCols = 128;  // columns per workgroup (32 threads x 4)
+
 __global__ __launch_bounds__(256) void sparse_down_reduce_kernel(const float* __restrict__ partial, int G, int H,
-                                                                  uint16_t* __restrict__ y) {
-    const int col = blockIdx.x * 256 + threadIdx.x;
-    if (col >= H) return;
-    float s = 0.0f;
-    for (int g = 0; g < G; ++g) s += partial[static_cast<int64_t>(g) * H + col];
-    y[col] = f32_to_f16_bits(s);
+                                                                  uint16_t* __restrict__ y, int vec_ok) {
+    __shared__ f32x4 s_part[kRedGroups][kRedCols / 4];
+    const int c4 = threadIdx.x & 31, t = threadIdx.x >> 5;
+    const int col = blockIdx.x * kRedCols + 4 * c4;
+    const bool vec = vec_ok != 0;  // H % 4 == 0 and a 16-byte aligned workspace
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (col < H) {
+        int g = t;
+        for (; g + 7 * kRedGroups < G; g += 8 * kRedGroups) {
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float* p = partial + static_cast<int64_t>(g + u * kRedGroups) * H + col;
+                v[u] = vec ? ldg(reinterpret_cast<const f32x4*>(p))
+                           : f32x4{ldg(p), col + 1 < H ? ldg(p + 1) : 0.0f, col + 2 < H ? ldg(p + 2) : 0.0f,
+                                    col + 3 < H ? ldg(p + 3) : 0.0f};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc.x += v[u].x;
+                acc.y += v[u].y;
+                acc.z += v[u].z;
+                acc.w += v[u].w;
+            }
+        }
+        for (; g < G; g += kRedGroups) {
+            const float* p = partial + static_cast<int64_t>(g) * H + col;
+            const f32x4 v = vec ? ldg(reinterpret_cast<const f32x4*>(p))
+                                 : f32x4{ldg(p), col + 1 < H ? ldg(p + 1) : 0.0f, col + 2 < H ? ldg(p + 2) : 0.0f,
+                                          col + 3 < H ? ldg(p + 3) : 0.0f};
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+    }
+    s_part[t][c4] = acc;
+    __syncthreads();
+    if (t == 0 && col < H) {
+        f32x4 s = s_part[0][c4];
+#pragma unroll
+        for (int u = 1; u < kRedGroups; ++u) {
+            const f32x4 o = s_part[u][c4];
+            s.x += o.x;
+            s.y += o.y;
+            s.z += o.z;
+            s.w += o.w;
+        }
+        const float r[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (col + e < H) stg(y + col + e, f32_to_f16_bits(r[e]));
+    }
 }
 
-// Rows per workgroup: a multiple of the wave count, large enough to amortise
-// the partial-row write (8 KB per 2048 columns), small enough to spread k rows
-// over ~128 workgroups.
+// Rows per workgroup: a multiple of waves x U (one batch per wave at least),
+// chosen to spread k rows over ~256 workgroups (one per CU).
 constexpr int kDownU = 4;  // rows per wave per batch
 
 static int64_t pick_rows_per_wg(int64_t k) {
     const int64_t step = static_cast<int64_t>(kDownWaves) * kDownU;
-    int64_t r = ceil_div64(k, 64);
+    int64_t r = ceil_div64(k, 256);
     if (r < step) r = step;
     return ceil_div64(r, step) * step;
 }
@@ -162,14 +217,14 @@ static int launch_sparse_down(const Rows& rows, int64_t k, const uint16_t* h, ui
 #undef SOI_D
         int s = launch_status(what);
         if (s) return s;
-        hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, 256))), dim3(256), 0, st,
-                           partial, static_cast<int>(G), Hi, y);
+        hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, kRedCols))), dim3(256), 0,
+                           st, partial, static_cast<int>(G), Hi, y, (H % 4 == 0 && aligned16(partial)) ? 1 : 0);
         return launch_status(what);
     }
     // k == 0: y = 0 (empty sum), as the reference's loop yields; a fill kernel
     // rather than a memset so the call stays capturable in a HIP graph.
-    hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, 256))), dim3(256), 0, st,
-                       static_cast<const float*>(nullptr), 0, static_cast<int>(H), y);
+    hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, kRedCols))), dim3(256), 0, st,
+                       static_cast<const float*>(nullptr), 0, static_cast<int>(H), y, 0);
     return launch_status(what);
 }
 

@@ -149,11 +149,11 @@ class DecodeEngine:
     and are captured into HIP graphs by capture()."""
 
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
-                 hot_channels: Optional[list] = None, max_new_tokens: int = 256):
+                 hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         c = w.config
-        self.w, self.c, self.mode = w, c, mode
+        self.w, self.c, self.mode, self.fused = w, c, mode, fused
         dev = w.embed.device
         self.device = dev
         H, I, hd = c.hidden, c.intermediate, c.head_dim
@@ -167,6 +167,7 @@ class DecodeEngine:
         self.log = buf(max_new_tokens, i32)
         self.log_len = buf(1, i32)
         self.x, self.h, self.hn = buf(H), buf(H), buf(H)
+        self.x2 = buf(H)  # second residual buffer (the fused GEMVs write x + delta to the other buffer)
         self.qkv = buf(c.qkv_rows)
         self.q = torch.zeros(c.q_heads, hd, dtype=f16, device=dev)
         self.attn = buf(c.q_heads * hd)
@@ -193,6 +194,13 @@ class DecodeEngine:
             if hot_channels is None or len(hot_channels) != c.layers:
                 raise ValueError("cached_dip needs one hot-channel list per layer")
             self._setup_cache(hot_channels)
+        if fused and mode == "dense":
+            # gate|up rows interleaved by 8-row tiles (gate 4t..4t+3, up 4t..4t+3) for the SwiGLU epilogue
+            t = torch.arange(I // 4, device=dev)
+            perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
+            self.gu_il = [(L.gu_Wq.index_select(0, perm).contiguous(), L.gu_scale.index_select(0, perm).contiguous())
+                          for L in w.layers]
+        self._x_final = self.x
         self._graph_layers = None
         self._graph_gen = None
 
@@ -249,6 +257,18 @@ class DecodeEngine:
             return
         cache = self.caches[l]
         _, uS = L.up(I)
+        self._fetch_misses(l, L, uS)
+        _C.gemv_dip_fused_up_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc, self.h,
+                                  self.u_sel, H, gs)
+        _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
+        _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
+                                    self.h_sel, self.down, H, gs, self.sd_ws)
+
+    def _fetch_misses(self, l: int, L: LayerWeights, uS: torch.Tensor):
+        """Descriptors for this layer's selection, then the miss rows into staging: packed rows from pinned
+        host memory (device gather through the host mapping), scale rows from HBM."""
+        I = self.c.intermediate
+        cache = self.caches[l]
         _C.build_dip_descriptors_into(self.idx, cache.slot_of, self.desc, self.miss_ch, self.miss_cnt)
         _C.gather_rows_device_counted(self.host_up_ptr[l], I, self.st_up.shape[1], self.miss_ch, self.miss_cnt,
                                       self.st_up)
@@ -258,14 +278,12 @@ class DecodeEngine:
                                       self.st_up_s.view(torch.uint8))
         _C.gather_rows_device_counted(L.down_T_scale.data_ptr(), I, L.down_T_scale.shape[1] * 4, self.miss_ch,
                                       self.miss_cnt, self.st_dn_s.view(torch.uint8))
-        _C.gemv_dip_fused_up_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc, self.h,
-                                  self.u_sel, H, gs)
-        _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
-        _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
-                                    self.h_sel, self.down, H, gs, self.sd_ws)
 
     def _layers(self):
         """Embedding of the device token, all layers at the device position, final norm; pos += 1."""
+        if self.fused:
+            self._layers_fused()
+            return
         c, eps = self.c, self.c.rms_eps
         H, gs = c.hidden, c.group_size
         _C.embed_lookup_into(self.w.embed, self.token, self.x)
@@ -282,7 +300,63 @@ class DecodeEngine:
             _C.residual_rmsnorm_(self.x, self.o, L.post_norm, self.h, eps)
             self._mlp(l, L)
         _C.residual_rmsnorm_(self.x, self.down, self.w.final_norm, self.hn, eps)
+        self._x_final = self.x
         _C.advance_position(self.pos, 1)
+
+    def _layers_fused(self):
+        """Same computation with the residual add + RMSNorm done inside the following GEMV (the residual
+        stream alternates between two buffers) and the SiLU gating in the up / gate|up GEMV epilogue."""
+        c, eps = self.c, self.c.rms_eps
+        H, I, gs = c.hidden, c.intermediate, c.group_size
+        cur, other = self.x, self.x2
+        _C.embed_lookup_into(self.w.embed, self.token, cur)
+        for l, L in enumerate(self.w.layers):
+            if l == 0:
+                _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, None, L.in_norm, eps, None, None, self.qkv,
+                                           H, gs, False)
+            else:
+                _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, self.down, L.in_norm, eps, other, None,
+                                           self.qkv, H, gs, False)
+                cur, other = other, cur
+            _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
+                                   self.k_cache[l], self.v_cache[l], eps)
+            _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
+            _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
+            if self.mode == "dense":
+                gW, gS = self.gu_il[l]
+                _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, None, self.mlp_h, H, gs,
+                                           True)
+                cur, other = other, cur
+                _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
+                continue
+            gate = self.gu[:I]
+            gW, gS = L.gate(I)
+            _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
+            cur, other = other, cur
+            _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
+            if self.counts is not None:
+                self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
+                                                                         device=self.device))
+            uW, uS = L.up(I)
+            if self.mode == "dip":
+                _C.gemv_w4a16_indexed_silu_into(uW, uS, self.idx, self.h, gate, self.h_sel, H, gs)
+                _C.gemv_w4a16_indexed_accumulate_into(L.down_T_Wq, L.down_T_scale, self.idx, self.h_sel, self.down,
+                                                      H, gs, self.sd_ws)
+                continue
+            cache = self.caches[l]
+            self._fetch_misses(l, L, uS)
+            _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc,
+                                           self.idx, self.h, gate, self.h_sel, H, gs)
+            _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
+                                        self.h_sel, self.down, H, gs, self.sd_ws)
+        _C.residual_rmsnorm_(cur, self.down, self.w.final_norm, self.hn, eps)
+        self._x_final = cur
+        _C.advance_position(self.pos, 1)
+
+    @property
+    def x_final(self) -> torch.Tensor:
+        """The residual stream after the last layer of the latest step."""
+        return self._x_final
 
     def _head(self):
         """LM head on the final-normed hidden state and argmax into the device token (and the log)."""

@@ -41,8 +41,8 @@ def prompt_ids(n, vocab, seed=7):
     return torch.randint(0, vocab, (n,), generator=g).tolist()
 
 
-def run_against_oracle(dec, w, mode, dip_k, n_prompt, n_new, tol):
-    eng = dec.DecodeEngine(w, mode, dip_k=dip_k, max_new_tokens=n_new)
+def run_against_oracle(dec, w, mode, dip_k, n_prompt, n_new, tol, fused=True):
+    eng = dec.DecodeEngine(w, mode, dip_k=dip_k, max_new_tokens=n_new, fused=fused)
     emb, lm, fn, layers = OD.from_device(w)
     ora = OD.OracleDecoder(w.config, emb, lm, fn, layers, mode="dip" if mode != "dense" else "dense", dip_k=dip_k)
     eng.reset()
@@ -68,45 +68,49 @@ def run_against_oracle(dec, w, mode, dip_k, n_prompt, n_new, tol):
     return tokens
 
 
-def test_dense_decode_matches_oracle(dec, tiny):
-    run_against_oracle(dec, tiny, "dense", None, n_prompt=6, n_new=6, tol=5e-3)
+@pytest.mark.parametrize("fused", [True, False])
+def test_dense_decode_matches_oracle(dec, tiny, fused):
+    run_against_oracle(dec, tiny, "dense", None, n_prompt=6, n_new=6, tol=5e-3, fused=fused)
 
 
-def test_dip_decode_matches_oracle(dec, tiny):
-    run_against_oracle(dec, tiny, "dip", 256, n_prompt=6, n_new=6, tol=2e-2)
+@pytest.mark.parametrize("fused", [True, False])
+def test_dip_decode_matches_oracle(dec, tiny, fused):
+    run_against_oracle(dec, tiny, "dip", 256, n_prompt=6, n_new=6, tol=2e-2, fused=fused)
 
 
-@pytest.mark.parametrize("mode,k", [("dense", None), ("dip", 128)])
-def test_graph_replay_equals_eager(dec, tiny, mode, k):
+@pytest.mark.parametrize("mode,k,fused", [("dense", None, True), ("dip", 128, True), ("dense", None, False),
+                                          ("dip", 128, False)])
+def test_graph_replay_equals_eager(dec, tiny, mode, k, fused):
     prompt = prompt_ids(5, tiny.config.vocab, seed=11)
-    a = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8)
+    a = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8, fused=fused)
     eager = a.generate(prompt, 8, use_graph=False)
-    x_eager = a.x.clone()
-    b = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8)
+    x_eager = a.x_final.clone()
+    b = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=8, fused=fused)
     for rep in range(3):  # replays after the first must agree too
         graph = b.generate(prompt, 8, use_graph=True)
         assert graph == eager, f"replay {rep}"
-        assert torch.equal(b.x, x_eager)
+        assert torch.equal(b.x_final, x_eager)
         torch.cuda.synchronize()
         _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
 
 
-def test_cached_dip_bit_identical_to_dip(dec, tiny):
+@pytest.mark.parametrize("fused", [True, False])
+def test_cached_dip_bit_identical_to_dip(dec, tiny, fused):
     cfg = tiny.config
     k = cfg.intermediate // 2
     prompt = prompt_ids(6, cfg.vocab, seed=5)
-    plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6)
+    plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
     want = plain.generate(prompt, 6, use_graph=True)
     calib = prompt_ids(16, cfg.vocab, seed=1000)
     hot20 = dec.calibrate_hot_channels(tiny, k, calib, cache_fraction=0.2)
     assert all(len(h) == round(0.2 * cfg.intermediate) for h in hot20)
     for name, hot in (("0%", [[] for _ in range(cfg.layers)]), ("20%", hot20),
                       ("100%", [list(range(cfg.intermediate)) for _ in range(cfg.layers)])):
-        eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6)
+        eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6, fused=fused)
         for use_graph in (False, True):
             got = eng.generate(prompt, 6, use_graph=use_graph)
             assert got == want, f"cache {name} graph={use_graph}"
-            assert torch.equal(eng.x, plain.x), f"cache {name} graph={use_graph}: final hidden state differs"
+            assert torch.equal(eng.x_final, plain.x_final), f"cache {name} graph={use_graph}: hidden state differs"
 
 
 def test_engine_rejects_bad_arguments(dec, tiny):

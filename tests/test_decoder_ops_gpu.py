@@ -246,3 +246,93 @@ def test_counted_gather_from_pinned_host(C):
     assert torch.equal(dst.cpu(), host[idx.cpu().long()])
     with pytest.raises(RuntimeError):
         C.host_device_pointer(torch.zeros(16, dtype=torch.uint8))  # not pinned
+
+
+# ---------------------------------------------------------------------------
+# fused decode-step GEMVs: each equals the separate ops on the same values
+# ---------------------------------------------------------------------------
+
+def int4_mat(N, K, seed, gs=128):
+    from helpers import int4_problem
+
+    return int4_problem(N, K, gs, seed=seed)
+
+
+@pytest.mark.parametrize("N,with_delta", [(4096, True), (6144, False), (1000, True), (37, True)])
+def test_gemv_rmsnorm_equals_norm_then_gemv(C, ops, N, with_delta):
+    K = 2048
+    p = int4_mat(N, K, 50 + N)
+    x, d, w = rnd((K,), 51, 2.0).cuda(), rnd((K,), 52).cuda(), (rnd((K,), 53) * 0.2 + 1).half().cuda()
+    x_out, h_out = torch.empty_like(x), torch.empty_like(x)
+    y = torch.empty(N, dtype=torch.float16, device="cuda")
+    C.gemv_w4a16_rmsnorm_into(p["Wq_d"], p["s_d"], x, d if with_delta else None, w, 1e-6, x_out, h_out, y, K, 128,
+                              False)
+    s = (x.float() + d.float()).half() if with_delta else x
+    assert torch.equal(x_out, s), "x_out = x + delta in binary16"
+    # h_out is rmsnorm(s) up to the fp32 sum order of the mean square: within one binary16 rounding
+    h_ref = ops.rmsnorm(s.view(1, -1), w, 1e-6).view(-1)
+    assert (h_out.float() - h_ref.float()).abs().max() <= 1e-3 * h_ref.float().abs().max()
+    # the GEMV consumed exactly h_out
+    assert torch.equal(y, ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], h_out, K, 128))
+
+
+def test_gemv_rmsnorm_swiglu_equals_gemv_then_silu_mul(C, ops):
+    K, I = 2048, 1024
+    g, u = int4_mat(I, K, 60), int4_mat(I, K, 61)
+    t = torch.arange(I // 4, device="cuda")
+    perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
+    W = torch.cat([g["Wq_d"], u["Wq_d"]]).index_select(0, perm).contiguous()
+    S = torch.cat([g["s_d"], u["s_d"]]).index_select(0, perm).contiguous()
+    x, d, w = rnd((K,), 62).cuda(), rnd((K,), 63).cuda(), (rnd((K,), 64) * 0.2 + 1).half().cuda()
+    h_out = torch.empty_like(x)
+    y = torch.empty(I, dtype=torch.float16, device="cuda")
+    C.gemv_w4a16_rmsnorm_into(W, S, x, d, w, 1e-6, None, h_out, y, K, 128, True)
+    gate = ops.gemv_w4a16_group_lop3(g["Wq_d"], g["s_d"], h_out, K, 128)
+    up = ops.gemv_w4a16_group_lop3(u["Wq_d"], u["s_d"], h_out, K, 128)
+    want = torch.empty_like(y)
+    C.silu_mul_into(gate, up, want)
+    assert torch.equal(y, want)
+
+
+def test_gemv_rmsnorm_rejects_aliasing(C):
+    K = 256
+    p = int4_mat(64, K, 70)
+    x, w = rnd((K,), 71).cuda(), rnd((K,), 72).cuda()
+    y = torch.empty(64, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError):
+        C.gemv_w4a16_rmsnorm_into(p["Wq_d"], p["s_d"], x, None, w, 1e-6, x, None, y, K, 128, False)
+    with pytest.raises(RuntimeError):  # SwiGLU needs N % 8 == 0
+        q = int4_mat(12, K, 73)
+        C.gemv_w4a16_rmsnorm_into(q["Wq_d"], q["s_d"], x, None, w, 1e-6, None, None, y[:6], K, 128, True)
+
+
+def test_indexed_silu_equals_indexed_then_silu(C, ops):
+    K, I = 2048, 6144
+    u = int4_mat(I, K, 80)
+    x, gate = rnd((K,), 81).cuda(), rnd((I,), 82, 2.0).cuda()
+    idx = torch.sort(torch.randperm(I, generator=torch.Generator().manual_seed(83))[:3072]).values.int().cuda()
+    h = torch.empty(3072, dtype=torch.float16, device="cuda")
+    C.gemv_w4a16_indexed_silu_into(u["Wq_d"], u["s_d"], idx, x, gate, h, K, 128)
+    u_sel = ops.gemv_w4a16_indexed(u["Wq_d"], u["s_d"], idx, x, K, 128)
+    want = torch.empty_like(h)
+    C.silu_mul_indexed_into(gate, idx, u_sel, want)
+    assert torch.equal(h, want)
+
+
+def test_fused_up_silu_equals_fused_up_then_silu(C, ops):
+    K, I = 2048, 512
+    u = int4_mat(I, K, 90)
+    x, gate = rnd((K,), 91).cuda(), rnd((I,), 92, 2.0).cuda()
+    sel = torch.arange(0, I, 2, dtype=torch.int32, device="cuda")
+    hot = torch.arange(0, I, 3, device="cuda")
+    slot_of = torch.full((I,), -1, dtype=torch.int32, device="cuda")
+    slot_of[hot] = torch.arange(hot.numel(), dtype=torch.int32, device="cuda")
+    desc, miss, mc = ops.build_dip_descriptors(sel, slot_of)
+    m = int(mc.item())
+    cW, cS = u["Wq_d"][hot].contiguous(), u["s_d"][hot].contiguous()
+    sW, sS = u["Wq_d"][miss[:m].long()].contiguous(), u["s_d"][miss[:m].long()].contiguous()
+    h = torch.empty(sel.numel(), dtype=torch.float16, device="cuda")
+    C.gemv_dip_fused_up_silu_into(cW, cS, sW, sS, desc, sel, x, gate, h, K, 128)
+    want = torch.empty_like(h)
+    C.silu_mul_indexed_into(gate, sel, ops.gemv_dip_fused_up(cW, cS, sW, sS, desc, x, K, 128), want)
+    assert torch.equal(h, want)
