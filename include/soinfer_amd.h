@@ -275,6 +275,11 @@ int soi_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* out, int64_
                 void* stream);
 int soi_residual_rmsnorm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out, int64_t rows,
                          int64_t hidden, float eps, void* stream);
+/* Engine form of the last op of a decode step: soi_residual_rmsnorm of one row
+ * (x += delta, out = rmsnorm(x), the final norm of generate.py:444) that also
+ * advances the device position: pos[0] += 1. */
+int soi_final_norm_advance(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out, int64_t hidden,
+                           float eps, int32_t* pos, void* stream);
 int soi_rope_apply(uint16_t* x, const float* cos_vals, const float* sin_vals, int64_t num_heads, int64_t head_dim,
                    void* stream);
 int soi_kv_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,

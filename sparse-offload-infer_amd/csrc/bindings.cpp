@@ -631,6 +631,25 @@ void residual_rmsnorm_(torch::Tensor x, torch::Tensor delta, torch::Tensor weigh
                  n);
 }
 
+void final_norm_advance(torch::Tensor x, torch::Tensor delta, torch::Tensor weight, torch::Tensor out, double eps,
+                        torch::Tensor pos) {
+    const char* n = "final_norm_advance";
+    need(x, torch::kFloat16, x, n, "x");
+    need(delta, torch::kFloat16, x, n, "delta");
+    need(weight, torch::kFloat16, x, n, "weight");
+    need(out, torch::kFloat16, x, n, "out");
+    need(pos, torch::kInt32, x, n, "pos");
+    need_numel(pos, 1, n, "pos");
+    TORCH_CHECK(x.numel() == weight.numel() && delta.numel() == x.numel() && out.numel() == x.numel(), n,
+                ": shape mismatch");
+    TORCH_CHECK(out.data_ptr() != x.data_ptr() && out.data_ptr() != delta.data_ptr(), n,
+                ": out must not alias x or delta");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_final_norm_advance(h16m(x), h16(delta), h16(weight), h16m(out), x.numel(), static_cast<float>(eps),
+                                        pos.data_ptr<int32_t>(), cur_stream(x)),
+                 n);
+}
+
 void qk_norm_rope_append(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm, torch::Tensor cos_table,
                          torch::Tensor sin_table, torch::Tensor pos, torch::Tensor q_out, torch::Tensor k_cache,
                          torch::Tensor v_cache, double eps) {
@@ -1023,6 +1042,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("rope_apply", &rope_apply, "RoPE in place (rotate-half)");
     m.def("rmsnorm_into", &rmsnorm_into, "RMSNorm into a caller buffer");
     m.def("residual_rmsnorm_", &residual_rmsnorm_, "x += delta (fp16), out = rmsnorm(x)");
+    m.def("final_norm_advance", &final_norm_advance, "x += delta, out = rmsnorm(x), pos[0] += 1");
     m.def("qk_norm_rope_append", &qk_norm_rope_append, "q/k norm + RoPE + KV append at a device position");
     m.def("decode_attention_workspace_bytes", &decode_attention_workspace_bytes, "attention workspace size");
     m.def("decode_attention_at", &decode_attention_at, "decode attention over pos[0]+1 timesteps");

@@ -43,7 +43,11 @@ template <bool ADD, bool VEC>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ delta,
                                                                const uint16_t* __restrict__ w,
-                                                               uint16_t* __restrict__ out, int hidden, float eps) {
+                                                               uint16_t* __restrict__ out, int hidden, float eps,
+                                                               int32_t* __restrict__ advance_pos) {
+    // engine form: the last op of a decode step also moves the device position (no kernel of this
+    // launch reads it; every earlier launch on the stream has completed)
+    if (advance_pos && blockIdx.x == 0 && threadIdx.x == 0) stg(advance_pos, ldg(advance_pos) + 1);
     __shared__ float s_red[kNormWaves];
     const int64_t base = static_cast<int64_t>(blockIdx.x) * hidden;
     uint16_t* xr = x + base;
@@ -264,7 +268,7 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 }
 
 constexpr int kArgmaxThreads = 256;
-constexpr int kArgmaxPerBlock = 4096;
+constexpr int kArgmaxPerBlock = 2048;  // one 16-byte load (8 values) per thread
 
 __device__ __forceinline__ void block_argmax(float& v, int& i, float* s_v, int* s_i) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -284,7 +288,9 @@ __device__ __forceinline__ void block_argmax(float& v, int& i, float* s_v, int* 
         }
 }
 
-// Stage 1: workgroup b reduces [b*4096, (b+1)*4096) to one (value, index).
+// Stage 1: workgroup b reduces [b*2048, (b+1)*2048) to one (value, index);
+// VEC (n % 8 == 0, 16-byte aligned x): one 16-byte load per thread.
+template <bool VEC>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const uint16_t* __restrict__ x, int n,
                                                                         float* __restrict__ pv,
                                                                         int* __restrict__ pi) {
@@ -294,11 +300,32 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const ui
     const int b1 = min(n, b0 + kArgmaxPerBlock);
     float v = -__builtin_inff();
     int i = 0x7fffffff;
-    for (int j = b0 + threadIdx.x; j < b1; j += kArgmaxThreads) {
-        const float t = f16_bits_to_f32(ldg(x + j));
-        if (arg_better(t, j, v, i)) {
-            v = t;
-            i = j;
+    if (VEC) {
+        const int j0 = b0 + 8 * threadIdx.x;
+        if (j0 < b1) {
+            const u32x4 t = ldg(reinterpret_cast<const u32x4*>(x + j0));
+            const uint32_t wds[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 h = as_f16x2(wds[e]);
+                const float lo = static_cast<float>(h.x), hi = static_cast<float>(h.y);
+                if (arg_better(lo, j0 + 2 * e, v, i)) {
+                    v = lo;
+                    i = j0 + 2 * e;
+                }
+                if (arg_better(hi, j0 + 2 * e + 1, v, i)) {
+                    v = hi;
+                    i = j0 + 2 * e + 1;
+                }
+            }
+        }
+    } else {
+        for (int j = b0 + threadIdx.x; j < b1; j += kArgmaxThreads) {
+            const float t = f16_bits_to_f32(ldg(x + j));
+            if (arg_better(t, j, v, i)) {
+                v = t;
+                i = j;
+            }
         }
     }
     block_argmax(v, i, s_v, s_i);
@@ -400,16 +427,15 @@ extern "C" int soi_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* 
     const int h = static_cast<int>(hidden);
     if (vec_ok(hidden, {x, weight, out}))
         hipLaunchKernelGGL((rmsnorm_kernel<false, true>), dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, st,
-                           xm, nullptr, weight, out, h, eps);
+                           xm, nullptr, weight, out, h, eps, nullptr);
     else
         hipLaunchKernelGGL((rmsnorm_kernel<false, false>), dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
-                           st, xm, nullptr, weight, out, h, eps);
+                           st, xm, nullptr, weight, out, h, eps, nullptr);
     return launch_status(what);
 }
 
-extern "C" int soi_residual_rmsnorm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out,
-                                    int64_t rows, int64_t hidden, float eps, void* stream) {
-    const char* what = "soi_residual_rmsnorm";
+static int residual_rmsnorm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out, int64_t rows,
+                            int64_t hidden, float eps, int32_t* advance_pos, void* stream, const char* what) {
     SOI_REQUIRE(rows >= 0 && rows <= (int64_t(1) << 31) - 1, "%s: rows out of range", what);
     SOI_REQUIRE(hidden >= 1 && hidden <= (int64_t(1) << 24), "%s: hidden must be in [1, 2^24]", what);
     if (rows == 0) return SOI_OK;
@@ -418,11 +444,23 @@ extern "C" int soi_residual_rmsnorm(uint16_t* x, const uint16_t* delta, const ui
     const int h = static_cast<int>(hidden);
     if (vec_ok(hidden, {x, delta, weight, out}))
         hipLaunchKernelGGL((rmsnorm_kernel<true, true>), dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, st,
-                           x, delta, weight, out, h, eps);
+                           x, delta, weight, out, h, eps, advance_pos);
     else
         hipLaunchKernelGGL((rmsnorm_kernel<true, false>), dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, st,
-                           x, delta, weight, out, h, eps);
+                           x, delta, weight, out, h, eps, advance_pos);
     return launch_status(what);
+}
+
+extern "C" int soi_residual_rmsnorm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out,
+                                    int64_t rows, int64_t hidden, float eps, void* stream) {
+    return residual_rmsnorm(x, delta, weight, out, rows, hidden, eps, nullptr, stream, "soi_residual_rmsnorm");
+}
+
+extern "C" int soi_final_norm_advance(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* out,
+                                      int64_t hidden, float eps, int32_t* pos, void* stream) {
+    const char* what = "soi_final_norm_advance";
+    SOI_REQUIRE(pos, "%s: null position pointer", what);
+    return residual_rmsnorm(x, delta, weight, out, 1, hidden, eps, pos, stream, what);
 }
 
 extern "C" int soi_rope_apply(uint16_t* x, const float* cos_vals, const float* sin_vals, int64_t num_heads,
@@ -519,8 +557,12 @@ extern "C" int soi_argmax_f16(const uint16_t* x, int64_t n, int32_t* out_index, 
     float* pv = static_cast<float*>(workspace);
     int* pi = reinterpret_cast<int*>(pv + nb);
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(static_cast<unsigned>(nb)), dim3(kArgmaxThreads), 0, st, x,
-                       static_cast<int>(n), pv, pi);
+    if (n % 8 == 0 && aligned16(x))
+        hipLaunchKernelGGL(argmax_partial_kernel<true>, dim3(static_cast<unsigned>(nb)), dim3(kArgmaxThreads), 0, st, x,
+                           static_cast<int>(n), pv, pi);
+    else
+        hipLaunchKernelGGL(argmax_partial_kernel<false>, dim3(static_cast<unsigned>(nb)), dim3(kArgmaxThreads), 0, st,
+                           x, static_cast<int>(n), pv, pi);
     int s = launch_status(what);
     if (s) return s;
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, st, pv, pi, static_cast<int>(nb),

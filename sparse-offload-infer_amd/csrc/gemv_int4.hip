@@ -137,6 +137,19 @@ struct NormX {
     }
 };
 
+// RegX: the lane's x chunk already in registers (single-pass shapes: K == 2048,
+// lane l owns chunk l), computed by the caller.
+struct RegX {
+    const f16x2* v;     // 16 pairs held by this lane
+    const uint16_t* b;  // a K-element vector for unresolvable rows
+    __device__ __forceinline__ const uint16_t* base() const { return b; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int, int, bool, f16x2 xv[16]) const {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xv[e] = v[e];
+    }
+};
+
 // Epilogues: row r of the tile has its fp32 total in the lanes reduce_rows_row
 // assigns to it. StoreY: y[row] = fp16(total) (NaN for an unresolvable row).
 // SiluIdxY: y[row] = fp16(silu(gate[idx[row]]) * fp16(total)), the SwiGLU gating
@@ -335,7 +348,7 @@ __global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* co
 // also writes x_out = a + d and h_out = rmsnorm(a + d, w) when given. a, d,
 // w, x_out, h_out: fp16 [K], K % 32 == 0, 16-byte aligned; x_out and h_out
 // must not alias a or d (other workgroups are still reading them).
-template <int R, bool CHUNK_SCALE, bool FULL, class EP>
+template <int R, bool CHUNK_SCALE, bool FULL, bool ONEPASS, class EP>
 __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int64_t N, const uint16_t* __restrict__ a,
                                                             const uint16_t* __restrict__ d,
                                                             const uint16_t* __restrict__ w, float eps,
@@ -344,6 +357,51 @@ __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int6
     const int lane = threadIdx.x;
     const u32x4* a4 = reinterpret_cast<const u32x4*>(a);
     const u32x4* d4 = reinterpret_cast<const u32x4*>(d);
+    const u32x4* w4 = reinterpret_cast<const u32x4*>(w);
+    if (ONEPASS) {
+        // K == 2048: lane l's 32 elements are exactly its GEMV chunk; keep them in registers
+        u32x4 t[4], g[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            t[i] = ldg(a4 + 4 * lane + i);
+            g[i] = ldg(w4 + 4 * lane + i);
+        }
+        if (d) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 e = ldg(d4 + 4 * lane + i);
+                t[i].x = add_f16x2(t[i].x, e.x);
+                t[i].y = add_f16x2(t[i].y, e.y);
+                t[i].z = add_f16x2(t[i].z, e.z);
+                t[i].w = add_f16x2(t[i].w, e.w);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ss += sumsq_f16x2(t[i].x) + sumsq_f16x2(t[i].y) + sumsq_f16x2(t[i].z) + sumsq_f16x2(t[i].w);
+        const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(K) + eps);
+        f16x2 hv[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u32x4 r;
+            r.x = norm_f16x2(t[i].x, g[i].x, inv);
+            r.y = norm_f16x2(t[i].y, g[i].y, inv);
+            r.z = norm_f16x2(t[i].z, g[i].z, inv);
+            r.w = norm_f16x2(t[i].w, g[i].w, inv);
+            hv[4 * i + 0] = as_f16x2(r.x);
+            hv[4 * i + 1] = as_f16x2(r.y);
+            hv[4 * i + 2] = as_f16x2(r.z);
+            hv[4 * i + 3] = as_f16x2(r.w);
+            if (blockIdx.x == 0) {
+                if (x_out) stg(reinterpret_cast<u32x4*>(x_out) + 4 * lane + i, t[i]);
+                if (h_out) stg(reinterpret_cast<u32x4*>(h_out) + 4 * lane + i, r);
+            }
+        }
+        gemv_int4_tile<R, 1, true, CHUNK_SCALE, true, FULL>(rows, N, RegX{hv, a}, ep, K, gs,
+                                                           static_cast<int64_t>(blockIdx.x) * R);
+        return;
+    }
     const int n8 = K >> 3;
     float ss = 0.0f;
     for (int c = lane; c < n8; c += kWave) {
@@ -359,7 +417,6 @@ __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int6
     }
     const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(K) + eps);
     if (blockIdx.x == 0 && (x_out || h_out)) {
-        const u32x4* w4 = reinterpret_cast<const u32x4*>(w);
         for (int c = lane; c < n8; c += kWave) {
             u32x4 t = ldg(a4 + c);
             if (d) {
@@ -721,15 +778,17 @@ extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, con
     const bool cs = (group_size % 32) == 0;
     const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size);
     const bool full_k = (K / 32) % 64 == 0;
+    const bool one = cs && K == 2048;  // one 64-chunk pass: the lane's x chunk stays in registers
     if (swiglu) {
         const dim3 grid(static_cast<unsigned>(N / 8));
         const SwigluY ep{y};
-#define SOI_N(CS, FL)                                                                                                  \
-    hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, SwigluY>), grid, dim3(64), 0, s, rows, N, x, delta, norm_weight, \
-                       eps, x_out, h_out, ep, Ki, gi)
-        if (cs && full_k) SOI_N(true, true);
-        else if (cs) SOI_N(true, false);
-        else SOI_N(false, false);
+#define SOI_N(CS, FL, OP)                                                                                          \
+    hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, OP, SwigluY>), grid, dim3(64), 0, s, rows, N, x, delta,    \
+                       norm_weight, eps, x_out, h_out, ep, Ki, gi)
+        if (one) SOI_N(true, true, true);
+        else if (cs && full_k) SOI_N(true, true, false);
+        else if (cs) SOI_N(true, false, false);
+        else SOI_N(false, false, false);
 #undef SOI_N
         return launch_status(what);
     }
@@ -737,13 +796,14 @@ extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, con
     const bool full = cs && full_k && N % R == 0;
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
     const StoreY ep{y};
-#define SOI_N(RR, CS, FL)                                                                                              \
-    hipLaunchKernelGGL((gemv_int4_norm_kernel<RR, CS, FL, StoreY>), grid, dim3(64), 0, s, rows, N, x, delta,           \
+#define SOI_N(RR, CS, FL, OP)                                                                                      \
+    hipLaunchKernelGGL((gemv_int4_norm_kernel<RR, CS, FL, OP, StoreY>), grid, dim3(64), 0, s, rows, N, x, delta,   \
                        norm_weight, eps, x_out, h_out, ep, Ki, gi)
-#define SOI_NR(RR)                         \
-    if (full) SOI_N(RR, true, true);       \
-    else if (cs) SOI_N(RR, true, false);   \
-    else SOI_N(RR, false, false)
+#define SOI_NR(RR)                                \
+    if (full && one) SOI_N(RR, true, true, true); \
+    else if (full) SOI_N(RR, true, true, false);  \
+    else if (cs) SOI_N(RR, true, false, false);   \
+    else SOI_N(RR, false, false, false)
     switch (R) {
         case 8: SOI_NR(8); break;
         case 4: SOI_NR(4); break;

@@ -349,9 +349,8 @@ class DecodeEngine:
                                            self.idx, self.h, gate, self.h_sel, H, gs)
             _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
                                         self.h_sel, self.down, H, gs, self.sd_ws)
-        _C.residual_rmsnorm_(cur, self.down, self.w.final_norm, self.hn, eps)
+        _C.final_norm_advance(cur, self.down, self.w.final_norm, self.hn, eps, self.pos)
         self._x_final = cur
-        _C.advance_position(self.pos, 1)
 
     @property
     def x_final(self) -> torch.Tensor:

@@ -126,6 +126,9 @@ def test_argmax_first_maximum(C):
     t[5000] = float("nan")
     assert argmax_dev(C, t.cuda()) == 5000 == OD.argmax_first(t.numpy())
     assert argmax_dev(C, torch.full((1,), -2.0, dtype=torch.float16).cuda()) == 0
+    odd = rnd((9999,), 24)  # not a multiple of 8: element-wise path
+    odd[[3, 9998]] = 9.0
+    assert argmax_dev(C, odd.cuda()) == 3
 
 
 def test_argmax_log(C):
