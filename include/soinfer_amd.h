@@ -237,6 +237,25 @@ int soi_decode_attention_at(const uint16_t* q, const uint16_t* k_cache, const ui
                             int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, const int32_t* pos,
                             float scale, void* workspace, size_t workspace_bytes, void* stream);
 
+/* One launch per decoder layer for the attention block of the decode engine
+ * (no reference entry point; fuses generate.py:160-169): for the fused
+ * projection qkv [q (NQ*hd) | k (NKV*hd) | v (NKV*hd)] at position p = pos[0],
+ * q/k RMSNorm (q_norm / k_norm) + RoPE (tables cos/sin [max_seq, hd/2]), the
+ * KV append of k, v at p, and attention of the NQ query heads over p + 1
+ * timesteps into out [NQ, hd]. Same binary16 rounding points as
+ * soi_qk_norm_rope_append followed by soi_decode_attention_at. The workspace
+ * (soi_decode_attention_step_workspace_bytes, 16-byte aligned) ends in a
+ * 256-byte block of counters that must be zero before the first call; every
+ * call leaves it zero, so a workspace is reused across calls and graph
+ * replays (calls that overlap on one workspace race). Returns
+ * SOI_ERR_UNSUPPORTED for head sizes outside the fast path. */
+size_t soi_decode_attention_step_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t max_seq);
+int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                              const float* cos_table, const float* sin_table, const int32_t* pos, uint16_t* k_cache,
+                              uint16_t* v_cache, uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq,
+                              int64_t head_dim, float eps, float scale, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* --------------------------------------------------------------------------
  * Decoder-step glue (binary16 in/out, fp32 math).
  *

@@ -680,6 +680,42 @@ void qk_norm_rope_append(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor 
                  n);
 }
 
+int64_t decode_attention_step_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t max_seq) {
+    return static_cast<int64_t>(soi_decode_attention_step_workspace_bytes(NQ, NKV, head_dim, max_seq));
+}
+
+void decode_attention_step(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm, torch::Tensor cos_table,
+                           torch::Tensor sin_table, torch::Tensor pos, torch::Tensor k_cache, torch::Tensor v_cache,
+                           torch::Tensor out, double eps, torch::Tensor workspace_buf) {
+    const char* n = "decode_attention_step";
+    need(qkv, torch::kFloat16, qkv, n, "qkv");
+    need(q_norm, torch::kFloat16, qkv, n, "q_norm");
+    need(k_norm, torch::kFloat16, qkv, n, "k_norm");
+    need(cos_table, torch::kFloat32, qkv, n, "cos_table");
+    need(sin_table, torch::kFloat32, qkv, n, "sin_table");
+    need(pos, torch::kInt32, qkv, n, "pos");
+    need(k_cache, torch::kFloat16, qkv, n, "k_cache");
+    need(v_cache, torch::kFloat16, qkv, n, "v_cache");
+    need(out, torch::kFloat16, qkv, n, "out");
+    need(workspace_buf, torch::kUInt8, qkv, n, "workspace");
+    TORCH_CHECK(k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes(), n,
+                ": caches must be 3D [num_kv_heads, max_seq_len, head_dim] of one shape");
+    TORCH_CHECK(out.dim() == 2 && out.size(1) == k_cache.size(2), n, ": out must be 2D [num_q_heads, head_dim]");
+    const int64_t NQ = out.size(0), NKV = k_cache.size(0), S = k_cache.size(1), hd = k_cache.size(2);
+    TORCH_CHECK(qkv.numel() == (NQ + 2 * NKV) * hd, n, ": qkv must hold (NQ + 2*NKV) * head_dim values");
+    TORCH_CHECK(q_norm.numel() == hd && k_norm.numel() == hd, n, ": norm weights must be [head_dim]");
+    TORCH_CHECK(cos_table.numel() == S * (hd / 2) && sin_table.numel() == S * (hd / 2), n,
+                ": RoPE tables must be [max_seq_len, head_dim/2]");
+    need_numel(pos, 1, n, "pos");
+    const at::DeviceGuard guard(qkv.device());
+    check_status(soi_decode_attention_step(h16(qkv), h16(q_norm), h16(k_norm), cos_table.data_ptr<float>(),
+                                           sin_table.data_ptr<float>(), pos.data_ptr<int32_t>(), h16m(k_cache),
+                                           h16m(v_cache), h16m(out), NQ, NKV, S, hd, static_cast<float>(eps),
+                                           1.0f / std::sqrt(static_cast<float>(hd)), workspace_buf.data_ptr<uint8_t>(),
+                                           workspace_buf.numel(), cur_stream(qkv)),
+                 n);
+}
+
 int64_t decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len) {
     return static_cast<int64_t>(soi_decode_attention_workspace_bytes(NQ, NKV, head_dim, cur_len));
 }
@@ -1046,6 +1082,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("qk_norm_rope_append", &qk_norm_rope_append, "q/k norm + RoPE + KV append at a device position");
     m.def("decode_attention_workspace_bytes", &decode_attention_workspace_bytes, "attention workspace size");
     m.def("decode_attention_at", &decode_attention_at, "decode attention over pos[0]+1 timesteps");
+    m.def("decode_attention_step_workspace_bytes", &decode_attention_step_workspace_bytes,
+          "workspace of decode_attention_step");
+    m.def("decode_attention_step", &decode_attention_step,
+          "q/k norm + RoPE + KV append + attention in one launch (device position)");
     m.def("gemv_w4a16_into", &gemv_w4a16_into, "INT4 GEMV into a caller buffer");
     m.def("gemv_w4a16_indexed_into", &gemv_w4a16_indexed_into, "index-driven INT4 GEMV into a caller buffer");
     m.def("gemv_w4a16_indexed_accumulate_into", &gemv_w4a16_indexed_accumulate_into,

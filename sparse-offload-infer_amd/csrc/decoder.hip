@@ -110,7 +110,8 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* __restr
 }
 
 // RoPE, rotate-half convention, in place: for i < hd/2,
-//   x[i] <- x[i] c_i - x[i+hd/2] s_i,  x[i+hd/2] <- x[i+hd/2] c_i + x[i] s_i.
+//   x[i] <- x[i] c_i - x[i+hd/2] s_i,  x[i+hd/2] <- x[i+hd/2] c_i + x[i] s_i
+// (rounded as fma(x[i], c, -(x[i+hd/2] s)) and fma(x[i+hd/2], c, x[i] s)).
 // One workgroup per head, one thread per pair.
 __global__ void rope_kernel(uint16_t* __restrict__ x, const float* __restrict__ cs, const float* __restrict__ sn,
                             int head_dim) {
@@ -120,8 +121,10 @@ __global__ void rope_kernel(uint16_t* __restrict__ x, const float* __restrict__ 
     uint16_t* row = x + static_cast<int64_t>(blockIdx.x) * head_dim;
     const float c = ldg(cs + i), s = ldg(sn + i);
     const float x1 = f16_bits_to_f32(ldg(row + i)), x2 = f16_bits_to_f32(ldg(row + i + half));
-    stg(row + i, f32_to_f16_bits(x1 * c - x2 * s));
-    stg(row + i + half, f32_to_f16_bits(x2 * c + x1 * s));
+    float o1, o2;
+    rope_pair(x1, x2, c, s, o1, o2);
+    stg(row + i, f32_to_f16_bits(o1));
+    stg(row + i + half, f32_to_f16_bits(o2));
 }
 
 // KV append at a host position (pos >= 0) or at pos_ptr[0] (device form).
@@ -152,7 +155,6 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_append_kernel(
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int32_t* __restrict__ pos_ptr,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int NQ, int NKV,
     int max_seq, int head_dim, float eps) {
-    __shared__ float s_red[kNormWaves];
     const int pos = ldg(pos_ptr);
     if (pos < 0 || pos >= max_seq) return;  // uniform over the workgroup
     const int h = blockIdx.x;
@@ -165,12 +167,15 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_append_kernel(
         return;
     }
     const uint16_t* wn = h < NQ ? q_norm : k_norm;
+    // every wave computes the same mean square (lanes stride 64 over the head), the reduction order of
+    // the one-launch attention step, so the two forms give identical values
+    const int lane = threadIdx.x & 63;
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < head_dim; i += kNormThreads) {
+    for (int i = lane; i < head_dim; i += kWave) {
         const float v = f16_bits_to_f32(ldg(src + i));
         ss = fmaf(v, v, ss);
     }
-    const float inv = rsqrtf(block_sum_256(ss, s_red) / static_cast<float>(head_dim) + eps);
+    const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(head_dim) + eps);
     uint16_t* dst = h < NQ ? q_out + static_cast<int64_t>(h) * head_dim
                            : kc + (static_cast<int64_t>(h - NQ) * max_seq + pos) * head_dim;
     const float* cr = cos_t + static_cast<int64_t>(pos) * half;
@@ -181,8 +186,10 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_append_kernel(
         const float b = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(ldg(src + i + half)) * inv *
                                                         f16_bits_to_f32(ldg(wn + i + half))));
         const float c = ldg(cr + i), s = ldg(sr + i);
-        stg(dst + i, f32_to_f16_bits(a * c - b * s));
-        stg(dst + i + half, f32_to_f16_bits(b * c + a * s));
+        float o1, o2;
+        rope_pair(a, b, c, s, o1, o2);
+        stg(dst + i, f32_to_f16_bits(o1));
+        stg(dst + i + half, f32_to_f16_bits(o2));
     }
 }
 

@@ -332,6 +332,14 @@ __device__ __forceinline__ uint32_t norm_f16x2(uint32_t a, uint32_t w, float inv
                       static_cast<float>(x.y) * inv * static_cast<float>(g.y));
 }
 
+// RoPE rotation of one (x_i, x_{i+hd/2}) pair with fixed rounding: explicit
+// fma so that every kernel applying it rounds identically (free contraction of
+// a*c - b*s could fuse either product).
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& o1, float& o2) {
+    o1 = fmaf(a, c, -(b * s));
+    o2 = fmaf(b, c, a * s);
+}
+
 // silu(t) = t / (1 + exp(-t)) in fp32 (SwiGLU gating, generate.py:178)
 __device__ __forceinline__ float silu_f32(float t) { return t / (1.0f + expf(-t)); }
 

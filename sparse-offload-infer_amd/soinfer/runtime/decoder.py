@@ -181,6 +181,9 @@ class DecodeEngine:
         self.attn_ws = buf(max(1, _C.decode_attention_workspace_bytes(c.q_heads, c.kv_heads, hd, c.max_seq)),
                            torch.uint8)
         self.argmax_ws = buf(_C.argmax_workspace_bytes(c.vocab), torch.uint8)
+        # one-launch attention (its workspace ends in counters that must start at zero: buf() zero-fills)
+        step_ws = _C.decode_attention_step_workspace_bytes(c.q_heads, c.kv_heads, hd, c.max_seq)
+        self.step_ws = buf(step_ws, torch.uint8) if (fused and step_ws > 0) else None
         self.counts = None  # optional per-layer channel selection counts (eager calibration only)
 
         if mode != "dense":
@@ -318,9 +321,14 @@ class DecodeEngine:
                 _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, self.down, L.in_norm, eps, other, None,
                                            self.qkv, H, gs, False)
                 cur, other = other, cur
-            _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
-                                   self.k_cache[l], self.v_cache[l], eps)
-            _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
+            if self.step_ws is not None:
+                _C.decode_attention_step(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos,
+                                         self.k_cache[l], self.v_cache[l], self.attn.view(c.q_heads, c.head_dim),
+                                         eps, self.step_ws)
+            else:
+                _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
+                                       self.k_cache[l], self.v_cache[l], eps)
+                _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
             if self.mode == "dense":
                 gW, gS = self.gu_il[l]

@@ -339,3 +339,42 @@ def test_fused_up_silu_equals_fused_up_then_silu(C, ops):
     want = torch.empty_like(h)
     C.silu_mul_indexed_into(gate, sel, ops.gemv_dip_fused_up(cW, cS, sW, sS, desc, x, K, 128), want)
     assert torch.equal(h, want)
+
+
+@pytest.mark.parametrize("NQ,NKV,hd,S,positions", [(16, 8, 128, 2048, [0, 1, 63, 64, 65, 700]),
+                                                   (4, 2, 64, 64, [0, 5, 63]), (8, 8, 128, 256, [0, 200])])
+def test_attention_step_equals_separate_ops(C, ops, NQ, NKV, hd, S, positions):
+    """One-launch attention == qk_norm_rope_append + decode_attention_at, bit for bit (outputs and both caches),
+    over a sequence of positions (the counters left zero by each call make the next one correct)."""
+    cos_t, sin_t = ops.rope_tables(hd, 1e6, S, "cuda")
+    qn, kn = (rnd((hd,), 22) * 0.1 + 1).half().cuda(), (rnd((hd,), 23) * 0.1 + 1).half().cuda()
+    kc_a = rnd((NKV, S, hd), 24).cuda()
+    vc_a = rnd((NKV, S, hd), 25).cuda()
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    ws_step = torch.zeros(C.decode_attention_step_workspace_bytes(NQ, NKV, hd, S), dtype=torch.uint8, device="cuda")
+    ws_at = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    q = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+    out_a = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+    out_b = torch.empty_like(out_a)
+    for i, p in enumerate(positions):
+        qkv = rnd(((NQ + 2 * NKV) * hd,), 100 + i, 2.0).cuda()
+        pos = torch.tensor([p], dtype=torch.int32, device="cuda")
+        C.decode_attention_step(qkv, qn, kn, cos_t, sin_t, pos, kc_a, vc_a, out_a, 1e-6, ws_step)
+        C.qk_norm_rope_append(qkv, qn, kn, cos_t, sin_t, pos, q, kc_b, vc_b, 1e-6)
+        C.decode_attention_at(q, kc_b, vc_b, pos, out_b, ws_at)
+        assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), f"caches at position {p}"
+        assert torch.equal(out_a, out_b), f"attention output at position {p}"
+    tail = ws_step[-256:]
+    assert tail.sum() == 0, "the counters are left at zero"
+
+
+@pytest.mark.parametrize("NQ,NKV,hd,S", [(16, 8, 128, 2048), (4, 2, 64, 64), (8, 1, 128, 1024)])
+def test_attention_device_position_equals_host_length(C, ops, NQ, NKV, hd, S):
+    """The device-position form plans its splits at run time with the host form's formula: identical outputs."""
+    q = rnd((NQ, hd), 40).cuda()
+    kc, vc = rnd((NKV, S, hd), 41).cuda(), rnd((NKV, S, hd), 42).cuda()
+    ws = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+    for L in sorted(L for L in {1, 2, 15, 16, 17, 100, S // 2, S - 1, S} if L <= S):
+        C.decode_attention_at(q, kc, vc, torch.tensor([L - 1], dtype=torch.int32, device="cuda"), out, ws)
+        assert torch.equal(out, ops.decode_attention(q, kc, vc, L)), f"length {L}"
