@@ -24,6 +24,8 @@ Also reported:
   decode_chain    the 112 dependent launches of one decode step, graph-replayed;
   per_shape_cold  per-shape INT4 / INT8 single-launch times on cold copies;
   topk_us_I6144   top-k latency at I=6144;
+  kernels         every other hot-path kernel at its BASELINE shape on cold copies:
+                  bytes, us per launch, GB/s, fraction of the HBM peak;
   dip_mlp_layer   BASELINE configs 3-4: one layer's dense / DIP (k/I 0.125, 0.25, 0.5) / cache-aware
                   DIP MLP, graph-replayed over 28 distinct layers;
   decode          BASELINE config 5: greedy decode tok/s of the random-init 28-layer Qwen3-1.7B
@@ -368,6 +370,138 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     return out
 
 
+def entry(nbytes: int, us: float, **extra) -> dict:
+    d = {"bytes": int(nbytes), "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+         "frac_of_hbm": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+    d.update(extra)
+    return d
+
+
+def bench_kernels(dev, gen):
+    """Every hot-path kernel at its BASELINE shape (Qwen3-1.7B: H 2048, I 6144, 16/8 heads, hd 128),
+    back-to-back launches replayed from a HIP graph over rotating copies of the large operands (>= 512 MB,
+    past the 256 MB Infinity Cache). bytes = the algorithmic bytes each launch must move."""
+    import torch
+
+    from soinfer import _C, ops
+
+    res = {}
+    H, I, G = 2048, 6144, 2048 // GS
+    row = H // 2
+    f16, i32 = torch.float16, torch.int32
+
+    # --- sparse down / indexed up / descriptors / fused GEMVs / device gather at k/I = 0.125 ... 0.5 ---
+    n_cp = cold_copies(I * (row + 4 * G))
+    Wt = [torch.randint(0, 256, (I, row), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n_cp)]
+    St = [(torch.rand(I, G, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n_cp)]
+    x = torch.randn(H, generator=gen, device=dev).half()
+    gate = torch.randn(I, generator=gen, device=dev).half()
+    for frac in (0.125, 0.25, 0.5):
+        k = int(I * frac)
+        idx = torch.sort(torch.randperm(I, device=dev, generator=gen)[:k]).values.to(i32)
+        h = torch.randn(k, generator=gen, device=dev).half()
+        y = torch.empty(H, dtype=f16, device=dev)
+        ws = torch.empty(max(1, _C.sparse_accumulate_workspace_bytes(H, k)), dtype=torch.uint8, device=dev)
+        t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_indexed_accumulate_into(W, S, idx, h, y, H, GS, ws),
+                                  list(zip(Wt, St)))
+        res[f"sparse_down_k{k}"] = entry(k * (row + 4 * G + 2) + 2 * H, t["mean_us"],
+                                         kernel="sparse_down_partial + reduce (2 launches)")
+        u = torch.empty(k, dtype=f16, device=dev)
+        t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_indexed_silu_into(W, S, idx, x, gate, u, H, GS),
+                                  list(zip(Wt, St)))
+        res[f"up_indexed_silu_k{k}"] = entry(k * (row + 4 * G + 4 + 2 + 2) + 2 * H, t["mean_us"],
+                                             kernel="gemv_int4 IndexRows + SiLU epilogue")
+        dst = torch.empty(k, row, dtype=torch.uint8, device=dev)
+        kcount = torch.full((1,), k, dtype=i32, device=dev)
+        t = time_graph_per_launch(lambda W: _C.gather_rows_device_counted(W.data_ptr(), I, row, idx, kcount, dst),
+                                  [(W,) for W in Wt])
+        res[f"gather_rows_device_k{k}"] = entry(2 * k * row + 4 * k, t["mean_us"], kernel="gather_rows_device")
+        if frac == 0.5:
+            hot = torch.sort(torch.randperm(I, device=dev, generator=gen)[: int(0.2 * I)]).values
+            slot_of = torch.full((I,), -1, dtype=i32, device=dev)
+            slot_of[hot] = torch.arange(hot.numel(), dtype=i32, device=dev)
+            desc, miss, mcount = torch.empty(k, dtype=i32, device=dev), torch.empty(k, dtype=i32, device=dev), \
+                torch.empty(1, dtype=i32, device=dev)
+            t = time_graph_per_launch(lambda: _C.build_dip_descriptors_into(idx, slot_of, desc, miss, mcount),
+                                      [()] * 64)
+            res[f"build_dip_descriptors_k{k}"] = entry(4 * k * 4 + 4, t["mean_us"], kernel="build_dip_descriptors")
+            _C.build_dip_descriptors_into(idx, slot_of, desc, miss, mcount)
+            mc = int(mcount.item())
+            caches = [(W.index_select(0, hot).contiguous(), S.index_select(0, hot).contiguous()) for W, S in
+                      zip(Wt, St)]
+            stag = [(W.index_select(0, miss[:mc].long()).contiguous(), S.index_select(0, miss[:mc].long()).contiguous())
+                    for W, S in zip(Wt, St)]
+            args = [(c[0], c[1], st[0], st[1]) for c, st in zip(caches, stag)]
+            t = time_graph_per_launch(lambda cW, cS, sW, sS: _C.gemv_dip_fused_up_into(cW, cS, sW, sS, desc, x, u, H,
+                                                                                        GS), args)
+            res[f"fused_up_k{k}"] = entry(k * (row + 4 * G + 4 + 2) + 2 * H, t["mean_us"], hot_fraction=0.2,
+                                          kernel="gemv_int4 DescRows")
+            t = time_graph_per_launch(lambda cW, cS, sW, sS: _C.gemv_dip_fused_down_into(cW, cS, sW, sS, desc, h, y,
+                                                                                          H, GS, ws), args)
+            res[f"fused_down_k{k}"] = entry(k * (row + 4 * G + 4 + 2) + 2 * H, t["mean_us"], hot_fraction=0.2,
+                                            kernel="sparse_down DescRows (2 launches)")
+            del caches, stag, args
+    del Wt, St
+    torch.cuda.empty_cache()
+
+    # --- decode attention (host length and the engine's one-launch form) ---
+    NQ, NKV, HD, S = 16, 8, 128, 2048
+    n_cp = cold_copies(2 * NKV * S * HD * 2)
+    KC = [torch.randn(NKV, S, HD, generator=gen, device=dev).half() for _ in range(n_cp)]
+    VC = [torch.randn(NKV, S, HD, generator=gen, device=dev).half() for _ in range(n_cp)]
+    q = torch.randn(NQ, HD, generator=gen, device=dev).half()
+    qkv = torch.randn((NQ + 2 * NKV) * HD, generator=gen, device=dev).half()
+    qn = torch.ones(HD, dtype=f16, device=dev)
+    cos_t, sin_t = ops.rope_tables(HD, 1e6, S, dev)
+    out = torch.empty(NQ, HD, dtype=f16, device=dev)
+    ws_at = torch.empty(_C.decode_attention_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
+    ws_step = torch.zeros(_C.decode_attention_step_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
+    for L in (192, 2048):
+        pos = torch.tensor([L - 1], dtype=i32, device=dev)
+        nb = 4096 * L + 8192
+        t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_at(q, kc, vc, pos, out, ws_at),
+                                  list(zip(KC, VC)))
+        res[f"attention_L{L}"] = entry(nb, t["mean_us"], kernel="attn_split + attn_combine (2 launches)")
+        t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_step(qkv, qn, qn, cos_t, sin_t, pos, kc, vc, out,
+                                                                          1e-6, ws_step), list(zip(KC, VC)))
+        res[f"attention_step_L{L}"] = entry(nb + 2 * (NQ + 2 * NKV) * HD, t["mean_us"],
+                                            kernel="attn_step (norm + RoPE + append + attention, 1 launch)")
+    del KC, VC
+    torch.cuda.empty_cache()
+
+    # --- LM head (fp16 151936 x 2048) and argmax ---
+    V = 151936
+    n_cp = max(2, cold_copies(V * H * 2))
+    LM = [torch.randn(V, H, generator=gen, device=dev).half() for _ in range(n_cp)]
+    logits = torch.empty(V, dtype=f16, device=dev)
+    t = time_graph_per_launch(lambda W: _C.gemv_f16_into(W, x, logits), [(W,) for W in LM])
+    res["lm_head_fp16_gemv"] = entry(V * H * 2 + 2 * H + 2 * V, t["mean_us"], kernel="gemv_f16")
+    del LM
+    tok = torch.empty(1, dtype=i32, device=dev)
+    aws = torch.empty(_C.argmax_workspace_bytes(V), dtype=torch.uint8, device=dev)
+    t = time_graph_per_launch(lambda: _C.argmax_f16_into(logits, tok, None, None, aws), [()] * 64)
+    res["argmax_vocab"] = entry(2 * V + 4, t["mean_us"], kernel="argmax partial + final (2 launches)")
+    torch.cuda.empty_cache()
+
+    # --- fused decode-step GEMVs (RMSNorm on load; SwiGLU epilogue) ---
+    for name, N, swiglu in (("qkv_rmsnorm_4096x2048", 4096, False), ("gate_up_swiglu_12288x2048", 12288, True)):
+        n_cp = cold_copies(N * (row + 4 * G))
+        Ws = [torch.randint(0, 256, (N, row), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n_cp)]
+        Ss = [(torch.rand(N, G, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n_cp)]
+        d = torch.randn(H, generator=gen, device=dev).half()
+        yy = torch.empty(N // 2 if swiglu else N, dtype=f16, device=dev)
+        xo = torch.empty(H, dtype=f16, device=dev)
+        nw = torch.ones(H, dtype=f16, device=dev)
+        t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_rmsnorm_into(W, S, x, d, nw, 1e-6, xo, None, yy, H, GS,
+                                                                          swiglu), list(zip(Ws, Ss)))
+        res[name] = entry(N * (row + 4 * G) + 3 * 2 * H + 2 * yy.numel(), t["mean_us"],
+                          kernel="gemv_int4_norm (residual add + RMSNorm on load" + (", SwiGLU epilogue)" if swiglu
+                                                                                      else ")"))
+        del Ws, Ss
+        torch.cuda.empty_cache()
+    return res
+
+
 
 def cpu_baseline(layer_mats_cpu, budget_s: float = 12.0):
     """The CPU oracle (scalar C, one thread) on layer 0's seven GEMVs, repeated to ~budget_s."""
@@ -517,6 +651,8 @@ def main() -> int:
         log("per-shape table done")
         result["topk_us_I6144"] = bench_topk(ops, dev, gen)
         log("top-k done")
+        result["kernels"] = bench_kernels(dev, gen)
+        log("kernel table done")
     if not args.no_decode:
         from soinfer.runtime import decoder as D
 
