@@ -401,11 +401,11 @@ def bench_kernels(dev, gen):
         idx = torch.sort(torch.randperm(I, device=dev, generator=gen)[:k]).values.to(i32)
         h = torch.randn(k, generator=gen, device=dev).half()
         y = torch.empty(H, dtype=f16, device=dev)
-        ws = torch.empty(max(1, _C.sparse_accumulate_workspace_bytes(H, k)), dtype=torch.uint8, device=dev)
+        ws = torch.zeros(max(1, _C.sparse_accumulate_workspace_bytes(H, k)), dtype=torch.uint8, device=dev)
         t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_indexed_accumulate_into(W, S, idx, h, y, H, GS, ws),
                                   list(zip(Wt, St)))
         res[f"sparse_down_k{k}"] = entry(k * (row + 4 * G + 2) + 2 * H, t["mean_us"],
-                                         kernel="sparse_down_partial + reduce (2 launches)")
+                                         kernel="sparse_down (1 launch, last workgroup per slice sums)")
         u = torch.empty(k, dtype=f16, device=dev)
         t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_indexed_silu_into(W, S, idx, x, gate, u, H, GS),
                                   list(zip(Wt, St)))
@@ -439,7 +439,7 @@ def bench_kernels(dev, gen):
             t = time_graph_per_launch(lambda cW, cS, sW, sS: _C.gemv_dip_fused_down_into(cW, cS, sW, sS, desc, h, y,
                                                                                           H, GS, ws), args)
             res[f"fused_down_k{k}"] = entry(k * (row + 4 * G + 4 + 2) + 2 * H, t["mean_us"], hot_fraction=0.2,
-                                            kernel="sparse_down DescRows (2 launches)")
+                                            kernel="sparse_down DescRows (1 launch)")
             del caches, stag, args
     del Wt, St
     torch.cuda.empty_cache()

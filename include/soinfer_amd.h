@@ -154,8 +154,15 @@ int soi_gather_rows_device_counted(const uint8_t* src, int64_t num_rows, int64_t
  * Sparse down projection over k gathered rows of down_proj^T:
  * y[H] = sum_{j<k} h_sel[j] * dequant(Wq_sel[j,:], scale_sel[j,:]).
  * Wq_sel: uint8 [k, ceil(H/8)*4]; scale_sel: fp32 [k, ceil(H/group_size)];
- * h_sel: fp16 [k]; y: fp16 [H]. Split over rows across workgroups, partial
- * sums combined in a fixed order (deterministic, no float atomics).
+ * h_sel: fp16 [k]; y: fp16 [H]. One launch: (256-column slice) x (row chunk)
+ * workgroups write fp32 partial rows; the last workgroup of each slice sums
+ * them in a fixed order (deterministic, no float atomics). The workspace
+ * (soi_sparse_accumulate_workspace_bytes) starts with per-slice arrival
+ * counters that must be zero before the first call (e.g. zero-filled once);
+ * every call leaves them zero, so one workspace serves repeated calls with
+ * the same H and any k it was sized for, including graph replays (calls that
+ * overlap on one workspace race). The same holds for the workspace of
+ * soi_gemv_dip_fused_down and soi_gemv_w4a16_indexed_accumulate.
  * Replaces launch_gemv_w4a16_sparse_accumulate
  * (csrc/kernels/gemv_sparse_accumulate.cu:40-47; binding csrc/bindings.cpp:311-339).
  * ------------------------------------------------------------------------ */

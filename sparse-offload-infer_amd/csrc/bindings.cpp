@@ -56,6 +56,11 @@ torch::Tensor workspace(const torch::Tensor& like, size_t bytes) {
     return torch::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(torch::kUInt8));
 }
 
+// a workspace whose arrival counters must start at zero (the sparse down projection)
+torch::Tensor zeroed_workspace(const torch::Tensor& like, size_t bytes) {
+    return torch::zeros({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(torch::kUInt8));
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -219,7 +224,7 @@ torch::Tensor gemv_w4a16_sparse_accumulate(torch::Tensor Wq_selected, torch::Ten
     const at::DeviceGuard guard(h_selected.device());
     auto y = torch::empty({H}, h_selected.options());
     const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
-    auto ws = workspace(h_selected, wsb);
+    auto ws = zeroed_workspace(h_selected, wsb);
     check_status(soi_gemv_w4a16_sparse_accumulate(Wq_selected.data_ptr<uint8_t>(), scale_selected.data_ptr<float>(),
                                                   h16(h_selected), h16m(y), H, k, group_size, num_groups,
                                                   ws.data_ptr<uint8_t>(), wsb, cur_stream(h_selected)),
@@ -334,7 +339,7 @@ torch::Tensor gemv_dip_fused_down(torch::Tensor cache_Wq, torch::Tensor cache_sc
     const at::DeviceGuard guard(h_selected.device());
     auto y = torch::empty({H}, h_selected.options());
     const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
-    auto ws = workspace(h_selected, wsb);
+    auto ws = zeroed_workspace(h_selected, wsb);
     const int64_t C = std::min(cache_Wq.size(0), cache_scale.size(0));
     const int64_t M = std::min(staging_Wq.size(0), staging_scale.size(0));
     check_status(soi_gemv_dip_fused_down(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), C,
@@ -400,7 +405,7 @@ torch::Tensor gemv_w4a16_indexed_accumulate(torch::Tensor Wq_T, torch::Tensor sc
     const int64_t k = idx.size(0);
     auto y = torch::empty({H}, h_selected.options());
     const size_t wsb = soi_sparse_accumulate_workspace_bytes(H, k);
-    auto ws = workspace(h_selected, wsb);
+    auto ws = zeroed_workspace(h_selected, wsb);
     check_status(soi_gemv_w4a16_indexed_accumulate(Wq_T.data_ptr<uint8_t>(), scale_T.data_ptr<float>(), Wq_T.size(0),
                                                    idx.data_ptr<int32_t>(), k, h16(h_selected), h16m(y), H, group_size,
                                                    scale_T.size(1), ws.data_ptr<uint8_t>(), wsb,

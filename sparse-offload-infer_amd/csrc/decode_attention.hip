@@ -417,10 +417,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(
                         reinterpret_cast<const u32x4*>(s_kv[0]), reinterpret_cast<const u32x4*>(s_kv[1]), s_state,
                         &k_first, &v_first);
 
-    // arrival: the last of the ns active splits of this KV head combines its query heads. Every thread
-    // releases its partial-state stores at device scope before thread 0 counts the workgroup in.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
+    // arrival: the last of the ns active splits of this KV head combines its query heads
+    arrive_release();
     if (threadIdx.x == 0) {
         const uint32_t prev = atomicAdd(counters + kvh, 1u);
         const bool last = prev + 1 == static_cast<uint32_t>(ns);

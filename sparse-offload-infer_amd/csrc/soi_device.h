@@ -290,6 +290,18 @@ __device__ __forceinline__ int reduce_rows_row(uint32_t lane) {
     return 0;
 }
 
+// Workgroup arrival, release side: every wave waits until its own stores have
+// completed (reached L2; a workgroup-scope fence does not wait for them), the
+// barrier makes that true for the whole workgroup, and then ONE device-scope
+// release fence by thread 0 writes the L2 lines back before thread 0 signals
+// (a release fence in every wave costs one L2 write-back per wave). Thread 0
+// must perform the signalling atomic right after this returns.
+__device__ __forceinline__ void arrive_release() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 // number of set bits of a 64-bit wave mask strictly below this lane

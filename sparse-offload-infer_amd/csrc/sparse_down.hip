@@ -4,18 +4,24 @@
 // form gemv_dip_fused.cu:116-154:
 //   y[c] = sum_{j<k} (h_j * s[j, c/gs]) * q[j, c],  fp32 accumulation, fp16 out.
 // The reference runs one thread per output column over all k rows, which
-// touches 4 bytes per row per thread and uses a handful of CUs. Here:
-//   pass 1 (partial): workgroup g owns rows [g*R, (g+1)*R) (R chosen so that
-//     k rows spread over ~256 workgroups); its 4 waves take blocks of U = 4
-//     rows in turn; lane l owns a 16-byte chunk (32 consecutive columns) of a
-//     2048-column slab, so each row is read as one coalesced 1 KB wave load.
-//     Each lane keeps 32 fp32 sums; per row: coef = fl(h_j*s),
-//     acc_c = fma(coef, q_c, acc_c) with q_c an exact binary16 integer
-//     (v_fma_mix_f32). The waves are summed in LDS in wave order and the
-//     workgroup's partial row is written to the workspace.
-//   pass 2 (reduce): y[c] = fp16(sum over g of partial[g,c]): 8 interleaved
-//     groups of g per column, each summed in ascending g with its loads
-//     issued 8 at a time, then the 8 group sums in a fixed order.
+// touches 4 bytes per row per thread and uses a handful of CUs. Here one
+// launch tiles (column slice) x (row chunk):
+//   * a slice is 256 columns = 8 16-byte chunks (128 bytes of each packed
+//     row); lane l of a wave owns chunk (l & 7) of row (l >> 3) of an 8-row
+//     group, so one wave-wide 16-byte load reads 8 rows x 128 bytes;
+//   * a workgroup (4 waves) owns rows [r*rpc, (r+1)*rpc) of its slice; wave w
+//     takes the 8-row groups w, w+4, w+8, ..., U groups per batch, all loads of
+//     a batch issued before any arithmetic. Each lane keeps 32 fp32 sums; per
+//     row: coef = fl(h_j*s), acc_c = fma(coef, q_c, acc_c) with q_c an exact
+//     binary16 integer;
+//   * the 32 (wave, row-in-group) partials of each column are summed through
+//     LDS in a fixed order and the workgroup writes one fp32 partial row of
+//     256 columns to the workspace;
+//   * arrival (arrive_release): every wave waits for its partial stores to
+//     complete, then one thread releases them at device scope and counts the
+//     workgroup in on the slice's counter; the last of the slice's R
+//     workgroups acquires, sums the R partial rows of the slice in ascending
+//     r and writes fp16 y, and resets the counter to zero.
 // Fixed partition and fixed order: deterministic, and every row source
 // (gathered rows, hot cache + staging descriptors, resident index list) gives
 // bit-identical results for the same logical rows.
@@ -27,24 +33,31 @@ namespace soi {
 
 constexpr int kDownWaves = 4;
 constexpr int kDownThreads = kDownWaves * kWave;
-constexpr int kSlabCols = kWave * 32;  // columns covered by one wave-wide row load
-constexpr int kRedPad = kWave + 1;      // LDS row pitch (floats) for the wave-sum transpose
+constexpr int kSliceChunks = 8;                 // 16-byte chunks per slice
+constexpr int kSliceCols = kSliceChunks * 32;   // 256 columns
+constexpr int kGroupRows = kWave / kSliceChunks;  // 8 rows per wave-wide load
+constexpr int kRedPitch = 33;                   // LDS floats per (row lane, chunk): conflict-free columns
+constexpr int kDownU = 3;                       // 8-row groups per wave per batch
 
-// U rows per wave per batch, all loads of a batch issued before arithmetic
-// (a lane with no chunk or a row past the range reads g_zero16 instead).
+// U groups per wave per batch (a lane with no chunk or a row past the range
+// reads g_zero16 instead, so the loads are issued unconditionally).
 template <int U, bool VEC, bool CHUNK_SCALE, class Rows>
-__global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows rows, const uint16_t* __restrict__ h,
-                                                                            float* __restrict__ partial, int64_t k,
-                                                                            int H, int gs, int rows_per_wg) {
+__global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, const uint16_t* __restrict__ h,
+                                                                    uint16_t* __restrict__ y, float* __restrict__ partial,
+                                                                    uint32_t* __restrict__ counters, int64_t k, int H,
+                                                                    int gs, int rpc, int R) {
     constexpr int SC = CHUNK_SCALE ? 1 : 4;
-    __shared__ float red[kDownWaves * 32 * kRedPad];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float red[kDownWaves * kGroupRows * kSliceChunks * kRedPitch];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rs = lane >> 3, cc = lane & (kSliceChunks - 1);
+    const int slice = blockIdx.x, r = blockIdx.y;
     const int words = (H + 7) >> 3;
     const int chunks = (words + 3) >> 2;
-    const int c = blockIdx.y * kWave + lane;
+    const int c = slice * kSliceChunks + cc;
     const bool cvalid = c < chunks;
-    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
-    const int64_t j1 = (j0 + rows_per_wg < k) ? j0 + rows_per_wg : k;
+    const int64_t j0 = static_cast<int64_t>(r) * rpc;
+    const int64_t j1 = (j0 + rpc < k) ? j0 + rpc : k;
     const uint32_t* z = g_zero16;
     const float* zf = reinterpret_cast<const float*>(g_zero16);
 
@@ -52,16 +65,17 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows 
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] = 0.0f;
 
-    for (int64_t jb = j0 + static_cast<int64_t>(wave) * U; jb < j1; jb += static_cast<int64_t>(kDownWaves) * U) {
+    constexpr int kBatchRows = kDownWaves * kGroupRows * U;
+    for (int64_t jb = j0 + static_cast<int64_t>(wave) * kGroupRows; jb < j1; jb += kBatchRows) {
         uint32_t wv[U][4];
         float coef[U][SC];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t j = jb + u;
+            const int64_t j = jb + static_cast<int64_t>(u) * kDownWaves * kGroupRows + rs;
             const bool in = j < j1;
             const RowRef ref = rows.get(in ? j : j0);
             const bool ok = in && ref.ok && cvalid;
-            const float hj = in ? f16_bits_to_f32(h[in ? j : j0]) : 0.0f;
+            const float hj = in ? f16_bits_to_f32(ldg(h + (in ? j : j0))) : 0.0f;
             if (VEC) {
                 const u32x4 t = __builtin_nontemporal_load(ok ? reinterpret_cast<const u32x4*>(ref.w) + c
                                                               : reinterpret_cast<const u32x4*>(z));
@@ -99,132 +113,113 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_partial_kernel(Rows 
         }
     }
 
+    // partial row of the slice: column (cc, i) summed over (wave, rs) in ascending order
+    float* red_lane = red + ((wave * kGroupRows + rs) * kSliceChunks + cc) * kRedPitch;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) red[(wave * 32 + i) * kRedPad + lane] = acc[i];
+    for (int i = 0; i < 32; ++i) red_lane[i] = acc[i];
     __syncthreads();
-    // 2048 slab values, 4 per thread; value v -> (lane l = v/32, column-in-chunk i = v%32)
-    const int64_t out_base = static_cast<int64_t>(blockIdx.x) * H + static_cast<int64_t>(blockIdx.y) * kSlabCols;
+    const int tc = tid >> 5, ti = tid & 31;  // thread tid <-> slice column tid = 32*tc + ti
+    float part = 0.0f;
 #pragma unroll
-    for (int m = 0; m < (kSlabCols / kDownThreads); ++m) {
-        const int v = threadIdx.x + m * kDownThreads;
-        const int l = v >> 5, i = v & 31;
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kDownWaves; ++w) s += red[(w * 32 + i) * kRedPad + l];
-        const int col = blockIdx.y * kSlabCols + v;
-        if (col < H) partial[out_base + v] = s;
-    }
-}
+    for (int g = 0; g < kDownWaves * kGroupRows; ++g) part += red[(g * kSliceChunks + tc) * kRedPitch + ti];
+    const int64_t col = static_cast<int64_t>(slice) * kSliceCols + tid;
+    if (col < H) stg(partial + static_cast<int64_t>(r) * H + col, part);
 
-// Thread (c4, t): columns 4*c4..4*c4+3, partial rows g = t, t+8, t+16, ...;
-// the 8 group sums are then added in t order through LDS. A fixed order for a
-// given G: deterministic. G == 0 writes zeros (the empty sum).
-constexpr int kRedGroups = 8;
-constexpr int kRedCols = 128;  // columns per workgroup (32 threads x 4)
-
-__global__ __launch_bounds__(256) void sparse_down_reduce_kernel(const float* __restrict__ partial, int G, int H,
-                                                                  uint16_t* __restrict__ y, int vec_ok) {
-    __shared__ f32x4 s_part[kRedGroups][kRedCols / 4];
-    const int c4 = threadIdx.x & 31, t = threadIdx.x >> 5;
-    const int col = blockIdx.x * kRedCols + 4 * c4;
-    const bool vec = vec_ok != 0;  // H % 4 == 0 and a 16-byte aligned workspace
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (col < H) {
-        int g = t;
-        for (; g + 7 * kRedGroups < G; g += 8 * kRedGroups) {
-            f32x4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float* p = partial + static_cast<int64_t>(g + u * kRedGroups) * H + col;
-                v[u] = vec ? ldg(reinterpret_cast<const f32x4*>(p))
-                           : f32x4{ldg(p), col + 1 < H ? ldg(p + 1) : 0.0f, col + 2 < H ? ldg(p + 2) : 0.0f,
-                                    col + 3 < H ? ldg(p + 3) : 0.0f};
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                acc.x += v[u].x;
-                acc.y += v[u].y;
-                acc.z += v[u].z;
-                acc.w += v[u].w;
-            }
-        }
-        for (; g < G; g += kRedGroups) {
-            const float* p = partial + static_cast<int64_t>(g) * H + col;
-            const f32x4 v = vec ? ldg(reinterpret_cast<const f32x4*>(p))
-                                 : f32x4{ldg(p), col + 1 < H ? ldg(p + 1) : 0.0f, col + 2 < H ? ldg(p + 2) : 0.0f,
-                                          col + 3 < H ? ldg(p + 3) : 0.0f};
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
+    // arrival: the last of the slice's R workgroups sums the partial rows
+    arrive_release();
+    if (tid == 0) {
+        const uint32_t prev = atomicAdd(counters + slice, 1u);
+        const bool last = prev + 1 == static_cast<uint32_t>(R);
+        if (last) atomicExch(counters + slice, 0u);
+        s_last = last ? 1 : 0;
     }
-    s_part[t][c4] = acc;
     __syncthreads();
-    if (t == 0 && col < H) {
-        f32x4 s = s_part[0][c4];
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other workgroups' partial rows
+    if (col >= H) return;
+    const float* pc = partial + col;
+    float sum = 0.0f;
+    int rr = 0;
+    for (; rr + 8 <= R; rr += 8) {
+        float v[8];
 #pragma unroll
-        for (int u = 1; u < kRedGroups; ++u) {
-            const f32x4 o = s_part[u][c4];
-            s.x += o.x;
-            s.y += o.y;
-            s.z += o.z;
-            s.w += o.w;
-        }
-        const float r[4] = {s.x, s.y, s.z, s.w};
+        for (int u = 0; u < 8; ++u) v[u] = ldg(pc + static_cast<int64_t>(rr + u) * H);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (col + e < H) stg(y + col + e, f32_to_f16_bits(r[e]));
+        for (int u = 0; u < 8; ++u) sum += v[u];
     }
+    for (; rr < R; ++rr) sum += ldg(pc + static_cast<int64_t>(rr) * H);
+    stg(y + col, f32_to_f16_bits(sum));
 }
 
-// Rows per workgroup: a multiple of waves x U (one batch per wave at least),
-// chosen to spread k rows over ~256 workgroups (one per CU).
-constexpr int kDownU = 4;  // rows per wave per batch
-
-static int64_t pick_rows_per_wg(int64_t k) {
-    const int64_t step = static_cast<int64_t>(kDownWaves) * kDownU;
-    int64_t r = ceil_div64(k, 256);
-    if (r < step) r = step;
-    return ceil_div64(r, step) * step;
+// k == 0: y = 0 (the empty sum, as the reference's loop yields); a fill kernel
+// rather than a memset so the call stays capturable in a HIP graph.
+__global__ __launch_bounds__(256) void sparse_down_zero_kernel(uint16_t* __restrict__ y, int64_t H) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < H) stg(y + i, uint16_t(0));
 }
 
-static int64_t num_splits(int64_t k) { return k == 0 ? 0 : ceil_div64(k, pick_rows_per_wg(k)); }
+// Partition: S = ceil(chunks / 8) slices; rows per chunk a multiple of 32 (one
+// 8-row group per wave) spreading k over about 256 / S chunks (at least 4).
+struct DownPlan {
+    int64_t S, R, rpc;
+};
+
+static DownPlan down_plan(int64_t H, int64_t k) {
+    const int64_t chunks = ceil_div64(ceil_div64(H, 8), 4);
+    DownPlan p;
+    p.S = ceil_div64(chunks, kSliceChunks);
+    int64_t target = 256 / p.S;
+    if (target < 4) target = 4;
+    const int64_t step = static_cast<int64_t>(kDownWaves) * kGroupRows;
+    p.rpc = ceil_div64(ceil_div64(k, target), step) * step;
+    p.R = ceil_div64(k, p.rpc);
+    return p;
+}
+
+// Workspace: the S arrival counters first (their place depends on H only, so
+// calls with any k can share a workspace), then the R x H fp32 partial rows.
+constexpr size_t kDownAlign = 256;
+
+static size_t down_counter_bytes(const DownPlan& p) {
+    return (static_cast<size_t>(p.S) * sizeof(uint32_t) + kDownAlign - 1) / kDownAlign * kDownAlign;
+}
+
+static size_t down_workspace_bytes(int64_t H, int64_t k) {
+    if (H <= 0 || k <= 0) return 0;
+    const DownPlan p = down_plan(H, k);
+    return down_counter_bytes(p) + static_cast<size_t>(p.R) * static_cast<size_t>(H) * sizeof(float);
+}
 
 template <class Rows>
 static int launch_sparse_down(const Rows& rows, int64_t k, const uint16_t* h, uint16_t* y, int64_t H, int64_t gs,
                               bool vec, void* workspace, size_t ws_bytes, hipStream_t st, const char* what) {
-    const int64_t G = num_splits(k);
-    const size_t need = static_cast<size_t>(G) * static_cast<size_t>(H) * sizeof(float);
-    if (k > 0) {
-        if (!workspace || ws_bytes < need) {
-            set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, ws_bytes);
-            return SOI_ERR_WORKSPACE;
-        }
-        const int64_t rpw = pick_rows_per_wg(k);
-        const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(ceil_div64(H, kSlabCols)));
-        float* partial = static_cast<float*>(workspace);
-        const bool cs = (gs % 32) == 0;
-        const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(rpw);
-#define SOI_D(V, CS)                                                                                             \
-    hipLaunchKernelGGL((sparse_down_partial_kernel<kDownU, V, CS, Rows>), grid, dim3(kDownThreads), 0, st, rows, h, partial, \
-                       k, Hi, gi, ri)
-        if (vec) {
-            if (cs) SOI_D(true, true); else SOI_D(true, false);
-        } else {
-            if (cs) SOI_D(false, true); else SOI_D(false, false);
-        }
-#undef SOI_D
-        int s = launch_status(what);
-        if (s) return s;
-        hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, kRedCols))), dim3(256), 0,
-                           st, partial, static_cast<int>(G), Hi, y, (H % 4 == 0 && aligned16(partial)) ? 1 : 0);
+    if (k == 0) {
+        hipLaunchKernelGGL(sparse_down_zero_kernel, dim3(static_cast<unsigned>(ceil_div64(H, 256))), dim3(256), 0, st,
+                           y, H);
         return launch_status(what);
     }
-    // k == 0: y = 0 (empty sum), as the reference's loop yields; a fill kernel
-    // rather than a memset so the call stays capturable in a HIP graph.
-    hipLaunchKernelGGL(sparse_down_reduce_kernel, dim3(static_cast<unsigned>(ceil_div64(H, kRedCols))), dim3(256), 0, st,
-                       static_cast<const float*>(nullptr), 0, static_cast<int>(H), y, 0);
+    const size_t need = down_workspace_bytes(H, k);
+    if (!workspace || ws_bytes < need) {
+        set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, ws_bytes);
+        return SOI_ERR_WORKSPACE;
+    }
+    const DownPlan p = down_plan(H, k);
+    SOI_REQUIRE(p.R <= 65535 && p.S <= (int64_t(1) << 31) - 1, "%s: partition out of range", what);
+    uint32_t* counters = static_cast<uint32_t*>(workspace);
+    float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + down_counter_bytes(p));
+    const dim3 grid(static_cast<unsigned>(p.S), static_cast<unsigned>(p.R));
+    const bool cs = (gs % 32) == 0;
+    const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(p.rpc),
+              Ri = static_cast<int>(p.R);
+#define SOI_D(V, CS)                                                                                           \
+    hipLaunchKernelGGL((sparse_down_kernel<kDownU, V, CS, Rows>), grid, dim3(kDownThreads), 0, st, rows, h, y, \
+                       partial, counters, k, Hi, gi, ri, Ri)
+    if (vec) {
+        if (cs) SOI_D(true, true); else SOI_D(true, false);
+    } else {
+        if (cs) SOI_D(false, true); else SOI_D(false, false);
+    }
+#undef SOI_D
     return launch_status(what);
 }
 
@@ -241,10 +236,7 @@ static int check_down(int64_t H, int64_t k, int64_t gs, int64_t G, const char* w
 
 using namespace soi;
 
-extern "C" size_t soi_sparse_accumulate_workspace_bytes(int64_t H, int64_t k) {
-    if (H <= 0 || k <= 0) return 0;
-    return static_cast<size_t>(num_splits(k)) * static_cast<size_t>(H) * sizeof(float);
-}
+extern "C" size_t soi_sparse_accumulate_workspace_bytes(int64_t H, int64_t k) { return down_workspace_bytes(H, k); }
 
 extern "C" int soi_gemv_w4a16_sparse_accumulate(const uint8_t* Wq_sel, const float* scale_sel, const uint16_t* h_sel,
                                                 uint16_t* y, int64_t H, int64_t k, int64_t group_size,

@@ -237,6 +237,27 @@ def test_indexed_equals_gathered(ops, k):
     assert torch.equal(y1, y2)
 
 
+def test_sparse_down_workspace_reused_across_calls(ops):
+    """One zero-filled workspace serves calls of different k at the same H: the arrival counters at its start are
+    left at zero by every call, and each result equals a call with a fresh workspace (and the oracle)."""
+    from soinfer import _C
+
+    H, gs, I = 2048, 128, 6144
+    p = int4_problem(I, H, gs, seed=11)
+    ws = torch.zeros(_C.sparse_accumulate_workspace_bytes(H, 3072), dtype=torch.uint8, device="cuda")
+    y = torch.empty(H, dtype=torch.float16, device="cuda")
+    g = torch.Generator().manual_seed(3)
+    for k in (3072, 768, 3072, 100, 1, 1536):
+        idx = torch.sort(torch.randperm(I, generator=g)[:k]).values
+        h = torch.randn(k, generator=g).half().cuda()
+        _C.gemv_w4a16_indexed_accumulate_into(p["Wq_d"], p["s_d"], idx.int().cuda(), h, y, H, gs, ws)
+        fresh = ops.gemv_w4a16_indexed_accumulate(p["Wq_d"], p["s_d"], idx.int().cuda(), h, H, gs)
+        assert torch.equal(y, fresh), f"k={k}"
+        assert_close(y, O.sparse_accumulate_f64(p["Wq"][idx.numpy()], p["s"][idx.numpy()], h.cpu().numpy(), H, gs),
+                     f"sparse down k={k}")
+        assert int(ws[:256].count_nonzero()) == 0, "arrival counters left non-zero"
+
+
 def _layer(H=2048, I=6144, gs=128, seed=0):
     from soinfer.runtime.dip import DipMLPWeights
 
