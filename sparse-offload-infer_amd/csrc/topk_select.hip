@@ -91,13 +91,45 @@ __device__ __forceinline__ uint32_t wave_prefix_u32(uint32_t x) {
 // Value sources: fp32 values as given, or |x| of binary16 values (the fp32
 // conversion and the absolute value are exact, so selecting over F16Abs(g)
 // equals selecting over g.float().abs()).
+// Each source also defines an order-preserving radix key (0 = NaN / padding,
+// never counted), the value of a key, and the digits of the radix passes.
 struct F32Values {
+    // Every bisection midpoint is > 0 (lo >= 0, hi >= 1e-3 / 2^24), so all values <= 0 compare alike: they share
+    // key 1, a positive value v has key bits(v) + 1 (<= 0x7f800001), NaN 0. 31-bit keys, digits of 11, 10, 10
+    // bits (8 bins per octave in the first pass).
+    static constexpr int kPasses = 3;
     const float* p;
     __device__ __forceinline__ float operator[](int i) const { return ldg(p + i); }
+    __device__ __forceinline__ float load(int i) const { return ldg(p + i); }
+    __device__ __forceinline__ static uint32_t key_of(float v) {
+        const uint32_t kp = __builtin_bit_cast(uint32_t, v) + 1u;
+        const uint32_t k1 = v > 0.0f ? kp : 1u;
+        return v == v ? k1 : 0u;
+    }
+    __device__ __forceinline__ static float value_of(uint32_t key) {
+        return key >= 2u ? __builtin_bit_cast(float, key - 1u) : 0.0f;
+    }
+    __host__ __device__ static constexpr int shift(int pass) { return pass == 0 ? 20 : (pass == 1 ? 10 : 0); }
+    __host__ __device__ static constexpr int bits(int pass) { return pass == 0 ? 11 : 10; }
 };
 struct F16AbsValues {
+    // |binary16| orders like its 15-bit pattern (exponent, mantissa): key = 0x8000 | pattern, NaN -> 0;
+    // digits of 9 and 6 bits (16 bins per octave in the first pass)
+    static constexpr int kPasses = 2;
     const uint16_t* p;
     __device__ __forceinline__ float operator[](int i) const { return fabsf(f16_bits_to_f32(ldg(p + i))); }
+    __device__ __forceinline__ float load(int i) const {
+        return f16_bits_to_f32(static_cast<uint16_t>(ldg(p + i) & 0x7fffu));
+    }
+    __device__ __forceinline__ static uint32_t key_of(float v) {  // v = |h|: its binary16 pattern back, exactly
+        const uint32_t m = __builtin_bit_cast(uint16_t, static_cast<f16>(v));
+        return v == v ? (m | 0x8000u) : 0u;
+    }
+    __device__ __forceinline__ static float value_of(uint32_t key) {
+        return f16_bits_to_f32(static_cast<uint16_t>(key & 0x7fffu));
+    }
+    __host__ __device__ static constexpr int shift(int pass) { return pass == 0 ? 6 : 0; }
+    __host__ __device__ static constexpr int bits(int pass) { return pass == 0 ? 9 : 6; }
 };
 
 template <int E, class Values>
@@ -115,9 +147,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const Va
     float val[E];
     float local_max = 0.0f;
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
+    for (int j = 0; j < E; ++j) {  // clamped index: every load is issued unconditionally, no branch per load
         const int i = base_i + j * kWave;
-        val[j] = (i < n) ? v[i] : -__builtin_inff();
+        const float x = v[i < n ? i : n - 1];
+        val[j] = (i < n) ? x : -__builtin_inff();
         local_max = fmaxf(local_max, val[j]);
     }
     const float total_max = block_max_from(local_max, s_max, wave, lane);
@@ -212,6 +245,179 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rule_a_regs_kernel(const Va
     if (tid == 0) *out_count = static_cast<int32_t>(total < static_cast<uint32_t>(k) ? total : k);
 }
 
+// Radix form (n <= 512*32): rule A depends on the values only through v_(k),
+// the k-th largest value: count(v >= mid) >= k exactly when v_(k) >= mid. So
+// the kernel finds v_(k) exactly by a radix select on order-preserving keys
+// (NaN and padding map to key 0 and never count; see the value sources),
+// replays the 24 bisection steps on it in fp32 (the reference's op
+// sequence), and compacts.
+//
+// One workgroup of 8 waves, E values per lane in registers, element
+// (j, lane) of wave w = w*64E + 64j + lane. Every pass: candidates (keys that
+// match the digits found so far) add 1 to an LDS histogram of their next
+// digit, one barrier, then EVERY wave scans the histogram itself (lane l
+// reads the contiguous bins l*B..l*B+B-1 counted from the top, a DPP prefix
+// over lanes finds the lane holding the rank, then B lanes re-read that
+// lane's bins and a second prefix finds the bin), so the passes need no
+// further barrier. Histograms are zeroed up front and padded by one word per
+// 32 bins (conflict-free lane reads); a lane whose element is not a
+// candidate adds to a private dummy word instead of branching. fp32 keys take
+// digits of 11, 10 and 10 bits; a binary16 magnitude's key is its 15-bit
+// pattern, two digits of 9 and 6 bits (16 bins per octave in the first pass,
+// so gate magnitudes spread over many bins: few same-address LDS atomics).
+// Four (binary16) or five (fp32) barriers in all, against nine for the
+// bisection-histogram form. Every global load is issued unconditionally
+// (clamped index): a branch per load serialises them.
+constexpr int kRadixThreads = 512;
+constexpr int kRadixWaves = kRadixThreads / kWave;
+
+__device__ __forceinline__ int hist_slot(int bin) { return bin + (bin >> 5); }
+__host__ __device__ constexpr int hist_words(int nb) { return nb + nb / 32; }
+
+template <class Values>
+__host__ __device__ constexpr int radix_hist_offset(int p) {
+    int w = 0;
+    for (int q = 0; q < p; ++q) w += hist_words(1 << Values::bits(q)) + kWave;  // + one dummy word per lane
+    return w;
+}
+
+// One radix pass over digit (key >> SHIFT) & (2^BITS - 1) of the candidate keys
+// (key & pmask == prefix): histogram, barrier, then every wave finds the digit
+// holding the rank on its own. Lane l reads its B = 2^BITS / 64 contiguous bins
+// (counted from the top) into registers; the lane prefix over lanes is then a
+// suffix count over bins. Returns false if fewer than `rank` candidates exist
+// (only possible in the first pass: fewer than k valid values).
+template <int SHIFT, int BITS, int E>
+__device__ __forceinline__ bool radix_pass(const uint32_t (&key)[E], uint32_t* hist, uint32_t& prefix, uint32_t& pmask,
+                                           uint32_t& rank, int lane) {
+    constexpr int NB = 1 << BITS;
+    constexpr int B = NB / kWave;
+    // branch-free: a non-candidate adds to its lane's private dummy word after the histogram instead
+    // (a branch per element costs more than the extra conflict-free LDS add)
+    const int dummy = hist_words(NB) + lane;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const uint32_t kk = key[j];
+        const bool cand = kk != 0u && (kk & pmask) == prefix;
+        atomicAdd(&hist[cand ? hist_slot(static_cast<int>((kk >> SHIFT) & (NB - 1))) : dummy], 1u);
+    }
+    __syncthreads();
+    const int top = NB - B * lane - 1;
+    uint32_t c[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) c[b] = hist[hist_slot(top - b)];
+#pragma unroll
+    for (int w = 1; w < B; w *= 2)  // pairwise tree: c[0] ends with the lane's total
+#pragma unroll
+        for (int b = 0; b + w < B; b += 2 * w) c[b] += c[b + w];
+    const uint32_t t = c[0];
+    const uint32_t incl = wave_prefix_u32(t);
+    const uint32_t reach = popc64(ballot(incl >= rank));  // lanes [64 - reach, 63] reach the rank
+    if (reach == 0u) return false;
+    const int L = kWave - static_cast<int>(reach);
+    // the bin inside lane L's range: lane b < B takes bin topL - b, a lane prefix over those gives the running
+    // count from the top, and the first lane whose running count reaches the rank holds the digit
+    const int topL = NB - B * L - 1;
+    const uint32_t base = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl - t), L));
+    const uint32_t cb_all = hist[hist_slot(topL - (lane < B ? lane : 0))];
+    const uint32_t cb = lane < B ? cb_all : 0u;
+    const uint32_t run = base + wave_prefix_u32(cb);
+    const uint64_t hitm = ballot(lane < B && run >= rank);
+    const int hb = static_cast<int>(__builtin_ctzll(hitm));
+    const uint32_t d = static_cast<uint32_t>(topL - hb);
+    const uint32_t above = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run - cb), hb));
+    prefix |= d << SHIFT;
+    pmask |= static_cast<uint32_t>(NB - 1) << SHIFT;
+    rank -= above;
+    return true;
+}
+
+template <int E, class Values>
+__global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(const Values v, int n, int k,
+                                                                   int32_t* __restrict__ out_idx,
+                                                                   int32_t* __restrict__ out_count) {
+    constexpr int NPASS = Values::kPasses;
+    constexpr int kWords = radix_hist_offset<Values>(NPASS);
+    __shared__ uint32_t s_hist[kWords];
+    __shared__ float s_max[kRadixWaves];
+    __shared__ uint32_t s_tot[kRadixWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int base_i = wave * kWave * E + lane;
+
+    float val[E];
+    uint32_t key[E];
+    float local_max = 0.0f;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {  // clamped index: every load is issued unconditionally, no branch per load
+        const int i = base_i + j * kWave;
+        val[j] = v.load(i < n ? i : n - 1);
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int i = base_i + j * kWave;
+        val[j] = (i < n) ? val[j] : __builtin_nanf("");
+        key[j] = Values::key_of(val[j]);
+        local_max = fmaxf(local_max, val[j]);
+    }
+    for (int i = tid; i < kWords; i += kRadixThreads) s_hist[i] = 0u;
+    const float wmax = wave_max_bcast(local_max);
+    if (lane == 0) s_max[wave] = wmax;
+    __syncthreads();
+
+    uint32_t prefix = 0u, pmask = 0u, rank = static_cast<uint32_t>(k);
+    bool found = radix_pass<Values::shift(0), Values::bits(0)>(key, s_hist, prefix, pmask, rank, lane);
+    if (found)
+        found = radix_pass<Values::shift(1), Values::bits(1)>(key, s_hist + radix_hist_offset<Values>(1), prefix,
+                                                              pmask, rank, lane);
+    if (NPASS == 3 && found)
+        found = radix_pass<Values::shift(NPASS == 3 ? 2 : 1), Values::bits(NPASS == 3 ? 2 : 1)>(
+            key, s_hist + radix_hist_offset<Values>(NPASS == 3 ? 2 : 1), prefix, pmask, rank, lane);
+
+    float total_max = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRadixWaves; ++w) total_max = fmaxf(total_max, s_max[w]);
+    const float vk = Values::value_of(prefix | (NPASS == 2 ? 0x8000u : 0u));
+    // 24 steps of mid = fl(0.5f * fl(lo + hi)), lo = mid if v_(k) >= mid else hi = mid. Both possible next
+    // sums are formed while the comparison resolves (the same fp32 operations, fewer dependent steps).
+    float lo = 0.0f;
+    float hi = total_max + 1e-3f;
+    float sum = lo + hi;
+#pragma unroll
+    for (int it = 0; it < kBisectionSteps; ++it) {
+        const float mid = 0.5f * sum;
+        const bool right = found && vk >= mid;
+        const float s_right = mid + hi, s_left = lo + mid;
+        lo = right ? mid : lo;
+        hi = right ? hi : mid;
+        sum = right ? s_right : s_left;
+    }
+    const float tau = lo;
+
+    // ordered compaction (the ballots are recomputed rather than kept: E masks would not fit in SGPRs)
+    uint32_t wave_total = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) wave_total += popc64(ballot(val[j] >= tau));
+    if (lane == 0) s_tot[wave] = wave_total;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kRadixWaves; ++w) {
+        const uint32_t c = s_tot[w];
+        before += (w < wave) ? c : 0u;
+        total += c;
+    }
+    uint32_t running = before;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const bool sel = val[j] >= tau;
+        const uint64_t mk = ballot(sel);
+        const uint32_t pos = running + mask_prefix(mk);
+        if (sel && pos < static_cast<uint32_t>(k)) out_idx[pos] = base_i + j * kWave;
+        running += popc64(mk);
+    }
+    if (tid == 0) *out_count = static_cast<int32_t>(total < static_cast<uint32_t>(k) ? total : k);
+}
+
 // Any n: values streamed from global memory (L2-resident after the first
 // pass) in blocks of 1024, same arithmetic and same output order.
 template <class Values>
@@ -274,18 +480,27 @@ static int launch_topk(const Values v, int64_t n, int64_t k, int32_t* out_indice
     SOI_REQUIRE(v.p && out_indices && out_count, "%s: null pointer", what);
     hipStream_t st = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
+    const int64_t er = ceil_div64(n, kRadixThreads);
+    if (er <= 32) {
+#define SOI_R(EE) \
+    hipLaunchKernelGGL((topk_radix_kernel<EE, Values>), dim3(1), dim3(kRadixThreads), 0, st, v, ni, ki, \
+                       out_indices, out_count)
+        if (er <= 1) SOI_R(1);
+        else if (er <= 2) SOI_R(2);
+        else if (er <= 4) SOI_R(4);
+        else if (er <= 8) SOI_R(8);
+        else if (er <= 12) SOI_R(12);
+        else if (er <= 16) SOI_R(16);
+        else if (er <= 24) SOI_R(24);
+        else SOI_R(32);
+#undef SOI_R
+        return launch_status(what);
+    }
     const int64_t e = ceil_div64(n, kTopkThreads);
 #define SOI_T(EE)                                                                                               \
     hipLaunchKernelGGL((topk_rule_a_regs_kernel<EE, Values>), dim3(1), dim3(kTopkThreads), 0, st, v, ni, ki, \
                        out_indices, out_count)
-    if (e <= 1) SOI_T(1);
-    else if (e <= 2) SOI_T(2);
-    else if (e <= 4) SOI_T(4);
-    else if (e <= 6) SOI_T(6);
-    else if (e <= 8) SOI_T(8);
-    else if (e <= 12) SOI_T(12);
-    else if (e <= 16) SOI_T(16);
-    else if (e <= 24) SOI_T(24);
+    if (e <= 24) SOI_T(24);  // n in (16384, 24576]
     else if (e <= 32) SOI_T(32);
     else
         hipLaunchKernelGGL((topk_rule_a_stream_kernel<Values>), dim3(1), dim3(kTopkThreads), 0, st, v, ni, ki,

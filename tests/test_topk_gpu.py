@@ -59,6 +59,53 @@ def test_fp16_gate_magnitudes_with_ties(C, k, seed):
     _check(C, v, k, f"fp16 gates seed={seed} k={k}")
 
 
+def _special(n: int, seed: int, kind: str) -> np.ndarray:
+    g = np.random.default_rng(seed)
+    v = g.uniform(0.0, 5.0, n).astype(np.float32)
+    if kind == "nan":
+        v[g.choice(n, n // 10, replace=False)] = np.nan
+    elif kind == "mostly_nan":  # fewer valid values than k: every bisection decision is "no", tau = 0
+        v[g.choice(n, n - n // 20, replace=False)] = np.nan
+    elif kind == "signed":  # negatives, -0.0 and +0.0 next to positives (abs_g is unchecked in the reference)
+        v = g.uniform(-5.0, 5.0, n).astype(np.float32)
+        v[g.choice(n, 64, replace=False)] = -0.0
+        v[g.choice(n, 64, replace=False)] = 0.0
+    elif kind == "inf":
+        v[g.choice(n, 40, replace=False)] = np.inf
+        v[g.choice(n, 40, replace=False)] = -np.inf
+    elif kind == "tiny":  # zeros and subnormals only
+        v = (g.integers(0, 50, n) * np.float32(1e-45)).astype(np.float32)
+    elif kind == "equal":
+        v[:] = np.float32(0.3)
+    return v
+
+
+@pytest.mark.parametrize("kind", ["nan", "mostly_nan", "signed", "inf", "tiny", "equal"])
+@pytest.mark.parametrize("n,k", [(6144, 3072), (6144, 1), (6144, 6144), (16384, 777), (300, 30), (20000, 30)])
+def test_special_values_match_rule_a(C, kind, n, k):
+    """NaN (never counted), negatives and signed zeros, infinities, subnormals and all-equal inputs: the indices
+    and count equal the rule-A oracle's on the same fp32 array (n up to 16384 takes the radix-select kernel,
+    20000 the bisection-histogram kernel)."""
+    _check(C, _special(n, n + k, kind), k, f"{kind} n={n} k={k}")
+
+
+@pytest.mark.parametrize("kind", ["nan", "mostly_nan", "inf", "tiny", "equal"])
+@pytest.mark.parametrize("k", [1, 768, 3072, 6144])
+def test_f16abs_special_values_equal_fp32_abs(C, kind, k):
+    """The binary16-gate form (two radix passes) equals the fp32 form on gate.float().abs() for the same gates."""
+    v = _special(6144, k, kind)
+    sign = np.where(np.random.default_rng(k).random(6144) < 0.5, -1.0, 1.0).astype(np.float32)
+    gate = torch.from_numpy(v * sign).half().cuda()
+    idx_ref, cnt_ref = C.topk_threshold_select(gate.float().abs(), k)
+    idx = torch.zeros(k, dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    C.topk_threshold_select_f16abs_into(gate, k, idx, cnt)
+    n = int(cnt_ref.item())
+    assert int(cnt.item()) == n
+    assert torch.equal(idx[:n], idx_ref[:n])
+    _check(C, gate.float().abs().cpu().numpy(), k, f"f16 {kind} k={k}")
+
+
 def test_heavy_ties(C):
     g = torch.Generator().manual_seed(1)
     v = torch.randint(0, 10, (8192,), generator=g).float().numpy()
