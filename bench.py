@@ -454,7 +454,7 @@ def bench_kernels(dev, gen):
     qn = torch.ones(HD, dtype=f16, device=dev)
     cos_t, sin_t = ops.rope_tables(HD, 1e6, S, dev)
     out = torch.empty(NQ, HD, dtype=f16, device=dev)
-    ws_at = torch.empty(_C.decode_attention_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
+    ws_at = torch.zeros(_C.decode_attention_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
     ws_step = torch.zeros(_C.decode_attention_step_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
     for L in (192, 2048):
         pos = torch.tensor([L - 1], dtype=i32, device=dev)

@@ -226,9 +226,15 @@ int soi_gemv_w4a16_indexed_accumulate(const uint8_t* Wq_T, const float* scale_T,
  * kvh = h / (NQ/NKV), t < cur_len. q: fp16 [NQ, hd]; k_cache, v_cache:
  * fp16 [NKV, max_seq, hd]; out: fp16 [NQ, hd]; 1 <= cur_len <= max_seq,
  * NQ % NKV == 0. `scale` is the score multiplier (the binding passes
- * 1/sqrt(hd)). Split over the KV sequence with a fixed-order combine.
- * Replaces launch_decode_attention (csrc/kernels/decode_attention.cu:57-63;
- * binding csrc/bindings.cpp:468-488).
+ * 1/sqrt(hd)). One launch: a short context is one workgroup per KV head; a
+ * long one is split over the KV sequence and the last split of each KV head
+ * combines the split states in a fixed order. The workspace
+ * (soi_decode_attention_workspace_bytes, 16-byte aligned) holds the split
+ * states and ends in arrival counters that must be zero before the first
+ * call (e.g. zero-filled once); every call leaves them zero, so a workspace
+ * is reused across calls and graph replays (calls that overlap on one
+ * workspace race). Replaces launch_decode_attention
+ * (csrc/kernels/decode_attention.cu:57-63; binding csrc/bindings.cpp:468-488).
  * ------------------------------------------------------------------------ */
 size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t cur_len);
 int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
@@ -237,9 +243,11 @@ int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint1
 
 /* Device-position form of soi_decode_attention: cur_len = pos[0] + 1 read on
  * the device (clamped to [1, max_seq]), so one captured graph serves every
- * position. The split plan is the one for cur_len = max_seq; splits past the
- * current length contribute nothing. Workspace: soi_decode_attention_workspace_bytes
- * (NQ, NKV, head_dim, max_seq). Used by the decode engine. */
+ * position. The grid covers cur_len = max_seq and the split plan of the
+ * current length is made on the device (the host form's formula: identical
+ * outputs); workgroups past it exit at once. Workspace (same rules):
+ * soi_decode_attention_workspace_bytes(NQ, NKV, head_dim, max_seq). Used by
+ * the decode engine. */
 int soi_decode_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
                             int64_t NQ, int64_t NKV, int64_t max_seq, int64_t head_dim, const int32_t* pos,
                             float scale, void* workspace, size_t workspace_bytes, void* stream);
@@ -250,12 +258,11 @@ int soi_decode_attention_at(const uint16_t* q, const uint16_t* k_cache, const ui
  * q/k RMSNorm (q_norm / k_norm) + RoPE (tables cos/sin [max_seq, hd/2]), the
  * KV append of k, v at p, and attention of the NQ query heads over p + 1
  * timesteps into out [NQ, hd]. Same binary16 rounding points as
- * soi_qk_norm_rope_append followed by soi_decode_attention_at. The workspace
- * (soi_decode_attention_step_workspace_bytes, 16-byte aligned) ends in a
- * 256-byte block of counters that must be zero before the first call; every
- * call leaves it zero, so a workspace is reused across calls and graph
- * replays (calls that overlap on one workspace race). Returns
- * SOI_ERR_UNSUPPORTED for head sizes outside the fast path. */
+ * soi_qk_norm_rope_append followed by soi_decode_attention_at, and the same
+ * attention kernel and split plan, so the outputs are identical. Workspace:
+ * soi_decode_attention_step_workspace_bytes, under the rules above. Returns
+ * SOI_ERR_UNSUPPORTED for head sizes outside the fast path (head_dim a
+ * power of two in [8, 256], at most 8 query heads per KV head). */
 size_t soi_decode_attention_step_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_dim, int64_t max_seq);
 int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
                               const float* cos_table, const float* sin_table, const int32_t* pos, uint16_t* k_cache,

@@ -52,11 +52,7 @@ uint16_t* h16m(torch::Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr
 
 int64_t expected_num_groups(int64_t k_dim, int64_t group_size) { return (k_dim + group_size - 1) / group_size; }
 
-torch::Tensor workspace(const torch::Tensor& like, size_t bytes) {
-    return torch::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(torch::kUInt8));
-}
-
-// a workspace whose arrival counters must start at zero (the sparse down projection)
+// workspaces end (attention) or start (sparse down) with arrival counters that must start at zero
 torch::Tensor zeroed_workspace(const torch::Tensor& like, size_t bytes) {
     return torch::zeros({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(torch::kUInt8));
 }
@@ -453,7 +449,7 @@ torch::Tensor decode_attention(torch::Tensor q, torch::Tensor k_cache, torch::Te
     auto out = torch::empty({NQ, hd}, q.options());
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
     const size_t wsb = soi_decode_attention_workspace_bytes(NQ, NKV, hd, cur_len);
-    auto ws = workspace(q, wsb);
+    auto ws = zeroed_workspace(q, wsb);
     check_status(soi_decode_attention(h16(q), h16(k_cache), h16(v_cache), h16m(out), NQ, NKV, S, hd, cur_len, scale,
                                       ws.data_ptr<uint8_t>(), wsb, cur_stream(q)),
                  "decode_attention");

@@ -90,4 +90,4 @@ def test_workspace_queries(lib):
     lib.soi_decode_attention_workspace_bytes.restype = C.c_size_t
     lib.soi_decode_attention_workspace_bytes.argtypes = [C.c_int64] * 4
     a = lib.soi_decode_attention_workspace_bytes(16, 8, 128, 2048)
-    assert a > 0 and a % (16 * 130 * 4) == 0
+    assert a >= 16 * 130 * 4 and a % 256 == 0  # split states (256-byte aligned) + arrival counters

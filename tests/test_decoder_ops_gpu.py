@@ -208,7 +208,7 @@ def test_qk_norm_rope_append_equals_separate_ops(C, ops, NQ, NKV, hd, S, pos):
 def test_decode_attention_at_matches_oracle(C, NQ, NKV, hd, S, L):
     q = rnd((NQ, hd), 30).cuda()
     kc, vc = rnd((NKV, S, hd), 31).cuda(), rnd((NKV, S, hd), 32).cuda()
-    ws = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
     out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
     C.decode_attention_at(q, kc, vc, torch.tensor([L - 1], dtype=torch.int32, device="cuda"), out, ws)
     ref = O.decode_attention_f64(q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy(), L)
@@ -341,7 +341,7 @@ def test_fused_up_silu_equals_fused_up_then_silu(C, ops):
     assert torch.equal(h, want)
 
 
-@pytest.mark.parametrize("NQ,NKV,hd,S,positions", [(16, 8, 128, 2048, [0, 1, 63, 64, 65, 700]),
+@pytest.mark.parametrize("NQ,NKV,hd,S,positions", [(16, 8, 128, 2048, [0, 1, 63, 64, 65, 254, 255, 256, 700]),
                                                    (4, 2, 64, 64, [0, 5, 63]), (8, 8, 128, 256, [0, 200])])
 def test_attention_step_equals_separate_ops(C, ops, NQ, NKV, hd, S, positions):
     """One-launch attention == qk_norm_rope_append + decode_attention_at, bit for bit (outputs and both caches),
@@ -352,7 +352,7 @@ def test_attention_step_equals_separate_ops(C, ops, NQ, NKV, hd, S, positions):
     vc_a = rnd((NKV, S, hd), 25).cuda()
     kc_b, vc_b = kc_a.clone(), vc_a.clone()
     ws_step = torch.zeros(C.decode_attention_step_workspace_bytes(NQ, NKV, hd, S), dtype=torch.uint8, device="cuda")
-    ws_at = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    ws_at = torch.zeros(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
     q = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
     out_a = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
     out_b = torch.empty_like(out_a)
@@ -373,8 +373,8 @@ def test_attention_device_position_equals_host_length(C, ops, NQ, NKV, hd, S):
     """The device-position form plans its splits at run time with the host form's formula: identical outputs."""
     q = rnd((NQ, hd), 40).cuda()
     kc, vc = rnd((NKV, S, hd), 41).cuda(), rnd((NKV, S, hd), 42).cuda()
-    ws = torch.empty(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(1, C.decode_attention_workspace_bytes(NQ, NKV, hd, S)), dtype=torch.uint8, device="cuda")
     out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
-    for L in sorted(L for L in {1, 2, 15, 16, 17, 100, S // 2, S - 1, S} if L <= S):
+    for L in sorted(L for L in {1, 2, 15, 16, 17, 100, 255, 256, 257, S // 2, S - 1, S} if L <= S):
         C.decode_attention_at(q, kc, vc, torch.tensor([L - 1], dtype=torch.int32, device="cuda"), out, ws)
         assert torch.equal(out, ops.decode_attention(q, kc, vc, L)), f"length {L}"
