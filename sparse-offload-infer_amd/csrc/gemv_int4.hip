@@ -184,6 +184,12 @@ struct SwigluY {
     uint16_t* y;
 };
 
+// Streaming GEMV kernels ask the compiler for at least 6 resident waves per
+// SIMD (<= 80 VGPRs, no spills at these tile sizes): with the default
+// allocation the 8-row tile takes ~120 VGPRs (4 waves), and the extra waves'
+// loads in flight are worth ~5% of HBM bandwidth on the gate/up batch.
+#define SOI_GEMV_OCCUPANCY __attribute__((amdgpu_waves_per_eu(6, 8)))
+
 // R rows per wave; PU passes (64 chunks each) loaded per batch, so a wave has
 // R*PU 1 KB row segments in flight before it does any arithmetic.
 template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class XS, class EP>
@@ -204,6 +210,12 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
             ref[r] = rows.get(in ? row0 + r : N - 1);
             if (!in) ref[r].ok = false;
         }
+    }
+    // the rows of a tile are the same for every lane: keep their addresses in scalar registers
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ref[r].w = uniform_ptr(ref[r].w);
+        ref[r].s = uniform_ptr(ref[r].s);
     }
     bool valid[R];  // row exists and resolved (else y untouched / NaN)
 #pragma unroll
@@ -323,11 +335,11 @@ __global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, con
 // memory; a problem whose pointers are not 16-byte aligned (when the vector
 // path is compiled in) or null writes nothing.
 template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
-__global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* const* __restrict__ Wp,
-                                                               const float* const* __restrict__ Sp,
-                                                               const uint16_t* const* __restrict__ Xp,
-                                                               uint16_t* const* __restrict__ Yp, int64_t N, int K,
-                                                               int gs, int G, int tiles) {
+__device__ __forceinline__ void gemv_int4_batched_body(const uint8_t* const* __restrict__ Wp,
+                                                       const float* const* __restrict__ Sp,
+                                                       const uint16_t* const* __restrict__ Xp,
+                                                       uint16_t* const* __restrict__ Yp, int64_t N, int K, int gs, int G,
+                                                       int tiles) {
     const int p = blockIdx.x / tiles;
     const int tile = blockIdx.x - p * tiles;
     const uint8_t* W = ldg(Wp + p);
@@ -341,6 +353,20 @@ __global__ __launch_bounds__(64) void gemv_int4_batched_kernel(const uint8_t* co
     gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,
                                                        static_cast<int64_t>(tile) * R);
 }
+
+#define SOI_BATCHED_PARAMS                                                                                     \
+    const uint8_t* const* __restrict__ Wp, const float* const* __restrict__ Sp,                              \
+        const uint16_t* const* __restrict__ Xp, uint16_t* const* __restrict__ Yp, int64_t N, int K, int gs, int G, \
+        int tiles
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int4_batched_kernel(SOI_BATCHED_PARAMS) {
+    gemv_int4_batched_body<R, PU, VEC, CHUNK_SCALE, FULL>(Wp, Sp, Xp, Yp, N, K, gs, G, tiles);
+}
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) SOI_GEMV_OCCUPANCY void gemv_int4_batched_occ_kernel(SOI_BATCHED_PARAMS) {
+    gemv_int4_batched_body<R, PU, VEC, CHUNK_SCALE, FULL>(Wp, Sp, Xp, Yp, N, K, gs, G, tiles);
+}
+#undef SOI_BATCHED_PARAMS
 
 // Decode-step form: y = W . rmsnorm(a + d, w) with the residual add and the
 // RMSNorm done on load. Every workgroup computes inv = 1/sqrt(mean((a+d)^2) +
@@ -460,11 +486,11 @@ struct GroupClasses {
 };
 
 template <int R, bool VEC, bool CHUNK_SCALE, bool FULL>
-__global__ __launch_bounds__(64) void gemv_int4_grouped_kernel(const uint8_t* const* __restrict__ Wp,
-                                                               const float* const* __restrict__ Sp,
-                                                               const uint16_t* const* __restrict__ Xp,
-                                                               uint16_t* const* __restrict__ Yp, GroupClasses cl,
-                                                               int gs) {
+__device__ __forceinline__ void gemv_int4_grouped_body(const uint8_t* const* __restrict__ Wp,
+                                                       const float* const* __restrict__ Sp,
+                                                       const uint16_t* const* __restrict__ Xp,
+                                                       uint16_t* const* __restrict__ Yp, const GroupClasses& cl,
+                                                       int gs) {
     const int b = blockIdx.x;
     int first = cl.first_wg[0], tiles = cl.tiles[0], p0 = cl.first_problem[0];
     int N = cl.N[0], K = cl.K[0], G = cl.G[0];
@@ -493,6 +519,48 @@ __global__ __launch_bounds__(64) void gemv_int4_grouped_kernel(const uint8_t* co
     DenseRows rows{W, S, row_bytes, G};
     gemv_int4_tile<R, 1, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,
                                                       static_cast<int64_t>(tile) * R);
+}
+
+#define SOI_GROUPED_PARAMS                                                                                   \
+    const uint8_t* const* __restrict__ Wp, const float* const* __restrict__ Sp,                            \
+        const uint16_t* const* __restrict__ Xp, uint16_t* const* __restrict__ Yp, GroupClasses cl, int gs
+template <int R, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int4_grouped_kernel(SOI_GROUPED_PARAMS) {
+    gemv_int4_grouped_body<R, VEC, CHUNK_SCALE, FULL>(Wp, Sp, Xp, Yp, cl, gs);
+}
+template <int R, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) SOI_GEMV_OCCUPANCY void gemv_int4_grouped_occ_kernel(SOI_GROUPED_PARAMS) {
+    gemv_int4_grouped_body<R, VEC, CHUNK_SCALE, FULL>(Wp, Sp, Xp, Yp, cl, gs);
+}
+#undef SOI_GROUPED_PARAMS
+
+// The occupancy hint is applied where the tile fits its register budget
+// without spilling (checked on the compiler's output): vector loads, one
+// scale per chunk, and one pass per batch (or at most 4 row segments).
+constexpr bool occ_fits(int R, int PU, bool VEC, bool CS, bool FULL) {
+    return VEC && CS && (PU == 1 || (R * PU <= 4 && FULL));
+}
+
+template <int R, int PU, bool V, bool CS, bool FL>
+static void launch_batched_kernel(dim3 grid, hipStream_t st, const uint8_t* const* Wp, const float* const* Sp,
+                                  const uint16_t* const* Xp, uint16_t* const* Yp, int64_t N, int K, int gs, int G,
+                                  int tiles) {
+    if constexpr (occ_fits(R, PU, V, CS, FL))
+        hipLaunchKernelGGL((gemv_int4_batched_occ_kernel<R, PU, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp,
+                           N, K, gs, G, tiles);
+    else
+        hipLaunchKernelGGL((gemv_int4_batched_kernel<R, PU, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, N, K,
+                           gs, G, tiles);
+}
+
+template <int R, bool V, bool CS, bool FL>
+static void launch_grouped_kernel(dim3 grid, hipStream_t st, const uint8_t* const* Wp, const float* const* Sp,
+                                  const uint16_t* const* Xp, uint16_t* const* Yp, const GroupClasses& cl, int gs) {
+    if constexpr (occ_fits(R, 1, V, CS, FL))
+        hipLaunchKernelGGL((gemv_int4_grouped_occ_kernel<R, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, cl,
+                           gs);
+    else
+        hipLaunchKernelGGL((gemv_int4_grouped_kernel<R, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, cl, gs);
 }
 
 // ---------------------------------------------------------------------------
@@ -576,9 +644,7 @@ static int launch_int4_batched(const uint8_t* const* Wp, const float* const* Sp,
     const bool full = vec && cs && (N % pl.R == 0) && ((K / 32) % (64 * pl.PU) == 0);
     const dim3 grid(static_cast<unsigned>(tiles * P));
     const int Ki = static_cast<int>(K), gi = static_cast<int>(gs), Gi = static_cast<int>(G), ti = static_cast<int>(tiles);
-#define SOI_B(RR, PP, V, CS, FL)                                                                             \
-    hipLaunchKernelGGL((gemv_int4_batched_kernel<RR, PP, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, N, Ki, \
-                       gi, Gi, ti)
+#define SOI_B(RR, PP, V, CS, FL) launch_batched_kernel<RR, PP, V, CS, FL>(grid, st, Wp, Sp, Xp, Yp, N, Ki, gi, Gi, ti)
 #define SOI_BCS(RR, PP, V)                        \
     if (V && full) SOI_B(RR, PP, V, true, true);  \
     else if (cs) SOI_B(RR, PP, V, true, false);   \
@@ -729,9 +795,7 @@ extern "C" int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float
     const int gi = static_cast<int>(group_size);
     const bool cs = (group_size % 32) == 0;
     hipStream_t st = as_stream(stream);
-#define SOI_G(V, CS, FL) \
-    hipLaunchKernelGGL((gemv_int4_grouped_kernel<R, V, CS, FL>), grid, dim3(64), 0, st, Wq_ptrs, scale_ptrs, x_ptrs, \
-                       y_ptrs, cl, gi)
+#define SOI_G(V, CS, FL) launch_grouped_kernel<R, V, CS, FL>(grid, st, Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs, cl, gi)
     if (full) SOI_G(true, true, true);
     else if (vec && cs) SOI_G(true, true, false);
     else if (vec) SOI_G(true, false, false);
