@@ -596,7 +596,7 @@ def main() -> int:
     n_wg = sum(c * (nn // 8) for c, nn in zip(group.class_count, group.class_N))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": read_traffic(),
-                "kernel": f"soi::gemv_int4_grouped_kernel<8,true,true,true> (196 GEMVs in 4 shape classes, "
+                "kernel": f"soi::gemv_int4_grouped_occ_kernel<8,true,true,true> (196 GEMVs in 4 shape classes, "
                           f"{n_wg} workgroups of 64)",
                 "bytes_per_launch": step_bytes, "avg_launch_us": round(dom_us, 3),
                 "timing": "HIP events around 30 back-to-back launches on the launching stream"}
