@@ -247,13 +247,16 @@ def bench_decode_chain(ops, layers, step_bytes):
     del chain, graph
     return decode_chain
 
-def mlp_bytes(L, I: int, H: int, k=None) -> int:
+def mlp_bytes(L, I: int, H: int, k=None, dense_up: bool = False) -> int:
     """Algorithmic bytes of one layer's MLP: dense reads gate|up and down; DIP reads gate, k rows of up and
-    k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes."""
+    k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes; the dense-up DIP schedule
+    reads every up row."""
     row = L.gu_Wq.shape[1] + 4 * L.gu_scale.shape[1]
     if k is None:
         return 2 * I * row + L.down_Wq.numel() + 4 * L.down_scale.numel() + 2 * (H + 3 * I + H)
     row_t = L.down_T_Wq.shape[1] + 4 * L.down_T_scale.shape[1]
+    if dense_up:
+        return 2 * I * row + k * row_t + 2 * (H + 2 * I + 2 * k + H) + 4 * (I + k)
     return I * row + k * (row + row_t) + 2 * (H + I + 2 * k + H) + 4 * (I + k)
 
 
@@ -338,9 +341,10 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     out, toks = {}, {}
     L0 = w.layers[0]
     attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
-    for mode in ("dense", "dip", "cached_dip"):
-        eng = D.DecodeEngine(w, mode, dip_k=None if mode == "dense" else k,
-                             hot_channels=hot if mode == "cached_dip" else None, max_new_tokens=n_new)
+    for mode in ("dense", "dip", "dip_dense_up", "cached_dip"):
+        eng = D.DecodeEngine(w, "dip" if mode == "dip_dense_up" else mode, dip_k=None if mode == "dense" else k,
+                             hot_channels=hot if mode == "cached_dip" else None, max_new_tokens=n_new,
+                             dip_dense_up=mode == "dip_dense_up")
         eng.capture()
         eng.generate(prompt[:8], 8)  # warm up the graphs
         torch.cuda.synchronize()
@@ -353,7 +357,7 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if mode == "dense" else k)
+        mlp = mlp_bytes(L0, I, c.hidden, None if mode == "dense" else k, dense_up=mode == "dip_dense_up")
         per_tok = c.layers * (attn_w + mlp) + w.lm_head.numel() * 2
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
@@ -364,6 +368,10 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
     out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"]
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
+    out["dip_dense_up_tokens_equal_dip"] = toks["dip"] == toks["dip_dense_up"]
+    assert out["dip_dense_up_tokens_equal_dip"], "the dense-up DIP schedule must generate the same tokens as DIP"
+    out["dip_dense_up"]["schedule"] = ("gate and up of every channel in one launch, top-k on gate, sparse down "
+                                       "with the SiLU gating of the selected channels on the fly")
     out["config"] = {"prompt_tokens": n_prompt, "new_tokens": n_new, "dip_k": k, "hot_fraction": 0.2,
                      "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed and LM head",
                      "kv": "fp16, max_seq 2048"}

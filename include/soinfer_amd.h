@@ -351,6 +351,18 @@ int soi_advance_position(int32_t* pos, int32_t delta, void* stream);
  *   [0, min(num_rows, n_gate))).
  * soi_gemv_dip_fused_up_silu: the same epilogue on soi_gemv_dip_fused_up
  *   (descriptor rows; sel = the selected channel indices).
+ * soi_gemv_w4a16_rmsnorm_gate_up: soi_gemv_w4a16_rmsnorm over the interleaved
+ *   gate|up rows (8-row tiles as above, N % 8 == 0) writing both halves
+ *   unfused: gate_out[i] = fp16(gate_i), up_out[i] = fp16(up_i), i < N/2,
+ *   each equal to the plain GEMV of that row.
+ * soi_gemv_w4a16_indexed_accumulate_gated: soi_gemv_w4a16_indexed_accumulate
+ *   with h_sel computed on the fly: h_sel[j] = fp16(silu(gate[c]) * up[c]),
+ *   c = idx[j] (NaN for c outside [0, num_channels)), the rounding of
+ *   soi_gemv_w4a16_indexed_silu, so the two-step and the fused forms give
+ *   identical y. Workspace rules of soi_gemv_w4a16_sparse_accumulate.
+ *   Together they are a DIP MLP schedule for resident weights: gate and up of
+ *   every channel in one launch, top-k on gate, then the gated sparse down
+ *   (one launch fewer than the indexed up GEMV; up is read for all channels).
  * ------------------------------------------------------------------------ */
 int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
                            const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out, uint16_t* y,
@@ -363,6 +375,15 @@ int soi_gemv_dip_fused_up_silu(const uint8_t* cache_Wq, const float* cache_scale
                                const int32_t* desc, const int32_t* sel, int64_t k, const uint16_t* x,
                                const uint16_t* gate, int64_t n_gate, uint16_t* h_sel, int64_t K, int64_t group_size,
                                int64_t num_groups, void* stream);
+int soi_gemv_w4a16_rmsnorm_gate_up(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
+                                   const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out,
+                                   uint16_t* gate_out, uint16_t* up_out, int64_t N, int64_t K, int64_t group_size,
+                                   int64_t num_groups, void* stream);
+int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
+                                            const int32_t* idx, int64_t k, const uint16_t* gate, const uint16_t* up,
+                                            int64_t num_channels, uint16_t* y, int64_t H, int64_t group_size,
+                                            int64_t num_groups, void* workspace, size_t workspace_bytes,
+                                            void* stream);
 
 #ifdef __cplusplus
 }

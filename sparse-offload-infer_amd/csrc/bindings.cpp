@@ -1014,6 +1014,64 @@ void gemv_w4a16_rmsnorm_into(torch::Tensor Wq, torch::Tensor scale, torch::Tenso
                  n);
 }
 
+void gemv_w4a16_rmsnorm_gate_up_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x,
+                                     c10::optional<torch::Tensor> delta, torch::Tensor norm_weight, double eps,
+                                     c10::optional<torch::Tensor> x_out, torch::Tensor gate_out, torch::Tensor up_out,
+                                     int64_t K, int64_t group_size) {
+    const char* n = "gemv_w4a16_rmsnorm_gate_up_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(x, torch::kFloat16, x, n, "x");
+    need(norm_weight, torch::kFloat16, x, n, "norm_weight");
+    need(gate_out, torch::kFloat16, x, n, "gate_out");
+    need(up_out, torch::kFloat16, x, n, "up_out");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K && norm_weight.numel() == K, n,
+                ": Wq / x / norm_weight shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0), n, ": scale must be [N, num_groups]");
+    TORCH_CHECK(gate_out.numel() == Wq.size(0) / 2 && up_out.numel() == Wq.size(0) / 2, n,
+                ": gate_out and up_out must have N/2 values");
+    const uint16_t* dp = nullptr;
+    uint16_t* xo = nullptr;
+    if (delta.has_value()) {
+        need(*delta, torch::kFloat16, x, n, "delta");
+        TORCH_CHECK(delta->numel() == K, n, ": delta must be [K]");
+        dp = h16(*delta);
+    }
+    if (x_out.has_value()) {
+        need(*x_out, torch::kFloat16, x, n, "x_out");
+        TORCH_CHECK(x_out->numel() == K, n, ": x_out must be [K]");
+        xo = h16m(*x_out);
+    }
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_rmsnorm_gate_up(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), dp,
+                                                h16(norm_weight), static_cast<float>(eps), xo, nullptr,
+                                                h16m(gate_out), h16m(up_out), Wq.size(0), K, group_size,
+                                                scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void gemv_w4a16_indexed_accumulate_gated_into(torch::Tensor Wq_T, torch::Tensor scale_T, torch::Tensor idx,
+                                              torch::Tensor gate, torch::Tensor up, torch::Tensor y, int64_t H,
+                                              int64_t group_size, torch::Tensor workspace_buf) {
+    const char* n = "gemv_w4a16_indexed_accumulate_gated_into";
+    need(Wq_T, torch::kUInt8, gate, n, "Wq_T");
+    need(scale_T, torch::kFloat32, gate, n, "scale_T");
+    need(idx, torch::kInt32, gate, n, "idx");
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(up, torch::kFloat16, gate, n, "up");
+    need(y, torch::kFloat16, gate, n, "y");
+    need(workspace_buf, torch::kUInt8, gate, n, "workspace");
+    TORCH_CHECK(Wq_T.dim() == 2 && Wq_T.size(1) == ((H + 7) / 8) * 4 && y.numel() == H, n, ": Wq_T / y mismatch");
+    TORCH_CHECK(scale_T.dim() == 2 && scale_T.size(0) == Wq_T.size(0), n, ": scale_T shape mismatch");
+    TORCH_CHECK(up.numel() == gate.numel(), n, ": gate and up must have the same length");
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_gemv_w4a16_indexed_accumulate_gated(
+                     Wq_T.data_ptr<uint8_t>(), scale_T.data_ptr<float>(), Wq_T.size(0), idx.data_ptr<int32_t>(),
+                     idx.numel(), h16(gate), h16(up), gate.numel(), h16m(y), H, group_size, scale_T.size(1),
+                     workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(gate)),
+                 n);
+}
+
 void gemv_w4a16_indexed_silu_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
                                   torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
     const char* n = "gemv_w4a16_indexed_silu_into";
@@ -1109,6 +1167,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_w4a16_rmsnorm_into", &gemv_w4a16_rmsnorm_into,
           "INT4 GEMV of rmsnorm(x + delta) (optionally with the interleaved SwiGLU epilogue)");
     m.def("gemv_w4a16_indexed_silu_into", &gemv_w4a16_indexed_silu_into, "DIP up GEMV with SiLU gating");
+    m.def("gemv_w4a16_rmsnorm_gate_up_into", &gemv_w4a16_rmsnorm_gate_up_into,
+          "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows, both halves written");
+    m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
+          "sparse down over selected rows with the SiLU gating computed on the fly");
     m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");
     m.def("version", []() { return std::string(soi_version()); });
 }

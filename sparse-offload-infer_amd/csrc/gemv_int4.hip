@@ -184,6 +184,21 @@ struct SwigluY {
     uint16_t* y;
 };
 
+// SplitGUY (rows interleaved by 8-row tiles as for SwigluY): row 8t + i goes to
+// gate[4t + i] for i < 4 and to up[4t + i - 4] otherwise, each fp16(total) as
+// StoreY would write it, so both halves equal the plain GEMV of those rows.
+struct SplitGUY {
+    static constexpr bool kSwiglu = false;
+    uint16_t* gate;
+    uint16_t* up;
+    __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
+        const int64_t t = row >> 3;
+        const int i = static_cast<int>(row & 7);
+        uint16_t* dst = i < 4 ? gate + 4 * t + i : up + 4 * t + (i - 4);
+        stg(dst, valid ? f32_to_f16_bits(total) : uint16_t(0x7e00u));
+    }
+};
+
 // Streaming GEMV kernels ask the compiler for at least 6 resident waves per
 // SIMD (<= 80 VGPRs, no spills at these tile sizes): with the default
 // allocation the 8-row tile takes ~120 VGPRs (4 waves), and the extra waves'
@@ -816,6 +831,45 @@ extern "C" int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float
     SOI_REQUIRE(Wq_ptrs && scale_ptrs && x_ptrs && y_ptrs, "%s: null pointer table", what);
     return launch_int4_batched(Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs, P, N, K, group_size, num_groups,
                                as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_w4a16_rmsnorm_gate_up(const uint8_t* Wq, const float* scale, const uint16_t* x,
+                                              const uint16_t* delta, const uint16_t* norm_weight, float eps,
+                                              uint16_t* x_out, uint16_t* h_out, uint16_t* gate_out, uint16_t* up_out,
+                                              int64_t N, int64_t K, int64_t group_size, int64_t num_groups,
+                                              void* stream) {
+    const char* what = "soi_gemv_w4a16_rmsnorm_gate_up";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1 && N % 8 == 0, "%s: N must be a multiple of 8 (8-row tiles)",
+                what);
+    SOI_REQUIRE(K % 32 == 0, "%s: K must be a multiple of 32", what);
+    SOI_REQUIRE(Wq && scale && x && norm_weight && gate_out && up_out, "%s: null pointer", what);
+    SOI_REQUIRE(aligned16(Wq) && aligned16(x) && aligned16(norm_weight) && (!delta || aligned16(delta)) &&
+                    (!x_out || aligned16(x_out)) && (!h_out || aligned16(h_out)),
+                "%s: vectors and weights must be 16-byte aligned", what);
+    const void* ins[2] = {x, delta};
+    for (const void* o : {static_cast<const void*>(x_out), static_cast<const void*>(h_out)})
+        for (const void* i : ins) SOI_REQUIRE(!o || o != i, "%s: x_out / h_out must not alias x or delta", what);
+    if (N == 0) return SOI_OK;
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    DenseRows rows{Wq, scale, row_bytes, num_groups};
+    hipStream_t s = as_stream(stream);
+    const bool cs = (group_size % 32) == 0;
+    const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size);
+    const bool full_k = (K / 32) % 64 == 0;
+    const bool one = cs && K == 2048;
+    const dim3 grid(static_cast<unsigned>(N / 8));
+    const SplitGUY ep{gate_out, up_out};
+#define SOI_N(CS, FL, OP)                                                                                          \
+    hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, OP, SplitGUY>), grid, dim3(64), 0, s, rows, N, x, delta,   \
+                       norm_weight, eps, x_out, h_out, ep, Ki, gi)
+    if (one) SOI_N(true, true, true);
+    else if (cs && full_k) SOI_N(true, true, false);
+    else if (cs) SOI_N(true, false, false);
+    else SOI_N(false, false, false);
+#undef SOI_N
+    return launch_status(what);
 }
 
 extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,

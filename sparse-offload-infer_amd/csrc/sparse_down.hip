@@ -31,6 +31,29 @@
 
 namespace soi {
 
+// Coefficient sources: h_sel given (PlainH), or the SiLU gating of the
+// selected channels computed on the fly (GatedH: h_j = fp16(silu(gate[c]) *
+// up[c]), c = idx[j], the rounding of the indexed SiLU GEMV epilogue and of
+// generate.py:304-305; a channel outside [0, n) gives NaN).
+struct PlainH {
+    const uint16_t* h;
+    __device__ __forceinline__ float get(int64_t j) const { return f16_bits_to_f32(ldg(h + j)); }
+};
+struct GatedH {
+    const uint16_t* gate;
+    const uint16_t* up;
+    const int32_t* idx;
+    int n;
+    __device__ __forceinline__ float get(int64_t j) const {
+        const int c = ldg(idx + j);
+        const bool ok = c >= 0 && c < n;
+        const int cc = ok ? c : 0;
+        const float g = f16_bits_to_f32(ldg(gate + cc));
+        const float u = f16_bits_to_f32(ldg(up + cc));
+        return ok ? f16_bits_to_f32(f32_to_f16_bits(silu_f32(g) * u)) : __builtin_nanf("");
+    }
+};
+
 constexpr int kDownWaves = 4;
 constexpr int kDownThreads = kDownWaves * kWave;
 constexpr int kSliceChunks = 8;                 // 16-byte chunks per slice
@@ -41,8 +64,8 @@ constexpr int kDownU = 3;                       // 8-row groups per wave per bat
 
 // U groups per wave per batch (a lane with no chunk or a row past the range
 // reads g_zero16 instead, so the loads are issued unconditionally).
-template <int U, bool VEC, bool CHUNK_SCALE, class Rows>
-__global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, const uint16_t* __restrict__ h,
+template <int U, bool VEC, bool CHUNK_SCALE, class Rows, class HS>
+__global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, const HS hs,
                                                                     uint16_t* __restrict__ y, float* __restrict__ partial,
                                                                     uint32_t* __restrict__ counters, int64_t k, int H,
                                                                     int gs, int rpc, int R) {
@@ -75,7 +98,7 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, co
             const bool in = j < j1;
             const RowRef ref = rows.get(in ? j : j0);
             const bool ok = in && ref.ok && cvalid;
-            const float hj = in ? f16_bits_to_f32(ldg(h + (in ? j : j0))) : 0.0f;
+            const float hj = in ? hs.get(in ? j : j0) : 0.0f;
             if (VEC) {
                 const u32x4 t = __builtin_nontemporal_load(ok ? reinterpret_cast<const u32x4*>(ref.w) + c
                                                               : reinterpret_cast<const u32x4*>(z));
@@ -190,8 +213,8 @@ static size_t down_workspace_bytes(int64_t H, int64_t k) {
     return down_counter_bytes(p) + static_cast<size_t>(p.R) * static_cast<size_t>(H) * sizeof(float);
 }
 
-template <class Rows>
-static int launch_sparse_down(const Rows& rows, int64_t k, const uint16_t* h, uint16_t* y, int64_t H, int64_t gs,
+template <class Rows, class HS>
+static int launch_sparse_down(const Rows& rows, int64_t k, const HS& h, uint16_t* y, int64_t H, int64_t gs,
                               bool vec, void* workspace, size_t ws_bytes, hipStream_t st, const char* what) {
     if (k == 0) {
         hipLaunchKernelGGL(sparse_down_zero_kernel, dim3(static_cast<unsigned>(ceil_div64(H, 256))), dim3(256), 0, st,
@@ -212,7 +235,7 @@ static int launch_sparse_down(const Rows& rows, int64_t k, const uint16_t* h, ui
     const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(p.rpc),
               Ri = static_cast<int>(p.R);
 #define SOI_D(V, CS)                                                                                           \
-    hipLaunchKernelGGL((sparse_down_kernel<kDownU, V, CS, Rows>), grid, dim3(kDownThreads), 0, st, rows, h, y, \
+    hipLaunchKernelGGL((sparse_down_kernel<kDownU, V, CS, Rows, HS>), grid, dim3(kDownThreads), 0, st, rows, h, y, \
                        partial, counters, k, Hi, gi, ri, Ri)
     if (vec) {
         if (cs) SOI_D(true, true); else SOI_D(true, false);
@@ -249,8 +272,8 @@ extern "C" int soi_gemv_w4a16_sparse_accumulate(const uint8_t* Wq_sel, const flo
     const int64_t row_bytes = ceil_div64(H, 8) * 4;
     const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_sel);
     DenseRows rows{Wq_sel, scale_sel, row_bytes, num_groups};
-    return launch_sparse_down(rows, k, h_sel, y, H, group_size, vec, workspace, workspace_bytes, as_stream(stream),
-                              what);
+    return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
+                              as_stream(stream), what);
 }
 
 extern "C" int soi_gemv_dip_fused_down(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
@@ -268,8 +291,26 @@ extern "C" int soi_gemv_dip_fused_down(const uint8_t* cache_Wq, const float* cac
                      (staging_rows == 0 || aligned16(staging_Wq));
     DescRows rows{cache_Wq, cache_scale, cache_rows, staging_Wq, staging_scale, staging_rows, desc, row_bytes,
                   num_groups};
-    return launch_sparse_down(rows, k, h_sel, y, H, group_size, vec, workspace, workspace_bytes, as_stream(stream),
-                              what);
+    return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
+                              as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
+                                                       const int32_t* idx, int64_t k, const uint16_t* gate,
+                                                       const uint16_t* up, int64_t num_channels, uint16_t* y,
+                                                       int64_t H, int64_t group_size, int64_t num_groups,
+                                                       void* workspace, size_t workspace_bytes, void* stream) {
+    const char* what = "soi_gemv_w4a16_indexed_accumulate_gated";
+    int s = check_down(H, k, group_size, num_groups, what);
+    if (s) return s;
+    SOI_REQUIRE(num_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
+                "%s: negative or too large row / channel count", what);
+    SOI_REQUIRE(y && (k == 0 || (Wq_T && scale_T && idx && gate && up)), "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(H, 8) * 4;
+    const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_T);
+    IndexRows rows{Wq_T, scale_T, num_rows, idx, row_bytes, num_groups};
+    return launch_sparse_down(rows, k, GatedH{gate, up, idx, static_cast<int>(num_channels)}, y, H, group_size, vec,
+                              workspace, workspace_bytes, as_stream(stream), what);
 }
 
 extern "C" int soi_gemv_w4a16_indexed_accumulate(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
@@ -284,6 +325,6 @@ extern "C" int soi_gemv_w4a16_indexed_accumulate(const uint8_t* Wq_T, const floa
     const int64_t row_bytes = ceil_div64(H, 8) * 4;
     const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_T);
     IndexRows rows{Wq_T, scale_T, num_rows, idx, row_bytes, num_groups};
-    return launch_sparse_down(rows, k, h_sel, y, H, group_size, vec, workspace, workspace_bytes, as_stream(stream),
-                              what);
+    return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
+                              as_stream(stream), what);
 }

@@ -149,9 +149,16 @@ class DecodeEngine:
     and are captured into HIP graphs by capture()."""
 
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
-                 hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True):
+                 hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
+                 dip_dense_up: bool = False):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
+        if dip_dense_up and mode != "dip":
+            raise ValueError("dip_dense_up applies to mode 'dip' (weights resident)")
+        # DIP schedule for resident weights: gate and up of every channel in one launch, top-k on gate, then the
+        # sparse down with the SiLU gating of the selected channels computed on the fly (one launch fewer per layer
+        # than the indexed up GEMV; the selected h values and hence every output are identical)
+        self.dip_dense_up = dip_dense_up
         c = w.config
         self.w, self.c, self.mode, self.fused = w, c, mode, fused
         dev = w.embed.device
@@ -197,7 +204,7 @@ class DecodeEngine:
             if hot_channels is None or len(hot_channels) != c.layers:
                 raise ValueError("cached_dip needs one hot-channel list per layer")
             self._setup_cache(hot_channels)
-        if fused and mode == "dense":
+        if fused and (mode == "dense" or dip_dense_up):
             # gate|up rows interleaved by 8-row tiles (gate 4t..4t+3, up 4t..4t+3) for the SwiGLU epilogue
             t = torch.arange(I // 4, device=dev)
             perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
@@ -247,10 +254,17 @@ class DecodeEngine:
         gate = self.gu[:I]
         gW, gS = L.gate(I)
         _C.gemv_w4a16_into(gW, gS, self.h, gate, H, gs)
+        if self.dip_dense_up:
+            uW, uS = L.up(I)
+            _C.gemv_w4a16_into(uW, uS, self.h, self.gu[I:], H, gs)
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         if self.counts is not None:
             self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
                                                                      device=self.device))
+        if self.dip_dense_up:
+            _C.gemv_w4a16_indexed_accumulate_gated_into(L.down_T_Wq, L.down_T_scale, self.idx, gate, self.gu[I:],
+                                                        self.down, H, gs, self.sd_ws)
+            return
         if self.mode == "dip":
             uW, uS = L.up(I)
             _C.gemv_w4a16_indexed_into(uW, uS, self.idx, self.h, self.u_sel, H, gs)
@@ -338,6 +352,18 @@ class DecodeEngine:
                 _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
                 continue
             gate = self.gu[:I]
+            if self.dip_dense_up:
+                gW, gS = self.gu_il[l]
+                _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
+                                                   H, gs)
+                cur, other = other, cur
+                _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
+                if self.counts is not None:
+                    self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
+                                                                             device=self.device))
+                _C.gemv_w4a16_indexed_accumulate_gated_into(L.down_T_Wq, L.down_T_scale, self.idx, gate,
+                                                            self.gu[I:], self.down, H, gs, self.sd_ws)
+                continue
             gW, gS = L.gate(I)
             _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
             cur, other = other, cur

@@ -113,7 +113,24 @@ def test_cached_dip_bit_identical_to_dip(dec, tiny, fused):
             assert torch.equal(eng.x_final, plain.x_final), f"cache {name} graph={use_graph}: hidden state differs"
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_dip_dense_up_schedule_bit_identical(dec, tiny, fused):
+    """Gate and up of every channel in one launch + the gated sparse down give the same tokens and the same hidden
+    state, bit for bit, as the indexed-up DIP schedule (eager and graph replay)."""
+    cfg = tiny.config
+    k = cfg.intermediate // 2
+    prompt = prompt_ids(6, cfg.vocab, seed=9)
+    plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
+    want = plain.generate(prompt, 6, use_graph=True)
+    eng = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused, dip_dense_up=True)
+    for use_graph in (False, True):
+        assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"graph={use_graph}"
+        assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
+
+
 def test_engine_rejects_bad_arguments(dec, tiny):
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dense", dip_dense_up=True)
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "sparse")
     with pytest.raises(ValueError):

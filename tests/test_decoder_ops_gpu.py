@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close
+from helpers import assert_close, int4_problem
 from oracle import decoder as OD
 from oracle import oracle as O
 
@@ -295,6 +295,52 @@ def test_gemv_rmsnorm_swiglu_equals_gemv_then_silu_mul(C, ops):
     want = torch.empty_like(y)
     C.silu_mul_into(gate, up, want)
     assert torch.equal(y, want)
+
+
+def test_gemv_rmsnorm_gate_up_equals_separate_gemvs(C, ops):
+    """The interleaved gate|up GEMV writing both halves == rmsnorm then the plain GEMV of the gate rows and of the
+    up rows, bit for bit."""
+    H, I = 2048, 1024
+    x, d = rnd((H,), 61).cuda(), rnd((H,), 62).cuda()
+    nw = (rnd((H,), 63) * 0.1 + 1).half().cuda()
+    g = int4_problem(I, H, 128, seed=64)
+    u = int4_problem(I, H, 128, seed=65)
+    t = torch.arange(I // 4)
+    perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1).cuda()
+    W = torch.cat([g["Wq_d"], u["Wq_d"]]).index_select(0, perm).contiguous()
+    S = torch.cat([g["s_d"], u["s_d"]]).index_select(0, perm).contiguous()
+    gate = torch.empty(I, dtype=torch.float16, device="cuda")
+    up = torch.empty_like(gate)
+    xo = torch.empty_like(x)
+    C.gemv_w4a16_rmsnorm_gate_up_into(W, S, x, d, nw, 1e-6, xo, gate, up, H, 128)
+    hx = torch.empty_like(x)
+    gref = torch.empty_like(gate)
+    C.gemv_w4a16_rmsnorm_into(g["Wq_d"], g["s_d"], x, d, nw, 1e-6, None, hx, gref, H, 128, False)
+    uref = ops.gemv_w4a16_group_lop3(u["Wq_d"], u["s_d"], hx, H, 128)
+    assert torch.equal(gate, gref) and torch.equal(up, uref)
+    assert torch.equal(xo, (x.float() + d.float()).half())
+
+
+def test_indexed_accumulate_gated_equals_silu_then_accumulate(C, ops):
+    """h_sel computed inside the sparse down == the indexed SiLU GEMV's h_sel, so y is identical; an index outside
+    the channel range gives NaN."""
+    H, I, k = 2048, 6144, 3072
+    down = int4_problem(I, H, 128, seed=71)
+    gate = (rnd((I,), 72) * 2).cuda()
+    up = (rnd((I,), 73) * 2).cuda()
+    idx = torch.sort(torch.randperm(I, generator=torch.Generator().manual_seed(74))[:k]).values.int().cuda()
+    ws = torch.zeros(C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+    y = torch.empty(H, dtype=torch.float16, device="cuda")
+    C.gemv_w4a16_indexed_accumulate_gated_into(down["Wq_d"], down["s_d"], idx, gate, up, y, H, 128, ws)
+    h = torch.empty(k, dtype=torch.float16, device="cuda")
+    C.silu_mul_indexed_into(gate, idx, up.index_select(0, idx.long()), h)
+    y2 = torch.empty_like(y)
+    C.gemv_w4a16_indexed_accumulate_into(down["Wq_d"], down["s_d"], idx, h, y2, H, 128, ws)
+    assert torch.equal(y, y2)
+    bad = idx.clone()
+    bad[5] = I + 3
+    C.gemv_w4a16_indexed_accumulate_gated_into(down["Wq_d"], down["s_d"], bad, gate, up, y, H, 128, ws)
+    assert torch.isnan(y.float()).all()
 
 
 def test_gemv_rmsnorm_rejects_aliasing(C):
