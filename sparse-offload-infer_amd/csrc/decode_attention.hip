@@ -70,10 +70,21 @@ __host__ __device__ __forceinline__ void split_plan(int64_t L, int64_t NKV, int6
     ns = static_cast<int>((L + t - 1) / t);
 }
 
+// Sum over the LPR lanes of a row group, every lane of the group gets it. Up to
+// 16 lanes this is DPP inside a 16-lane row (a few cycles per step, against
+// ~100 for an LDS-crossbar shuffle): rotations by 8 and 4 (or the 8-lane
+// mirror), then the two quad exchanges; each step doubles the lanes summed.
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int mask = 1; mask < LPR; mask <<= 1) v += __shfl_xor(v, mask, kWave);
+    if (LPR >= 16) {
+        v += dpp_f<0x128>(v);  // row_ror:8
+        v += dpp_f<0x124>(v);  // row_ror:4
+    } else if (LPR == 8) {
+        v += dpp_f<0x141>(v);  // row_half_mirror: lane i <-> 7-i
+    }
+    if (LPR >= 4) v += dpp_f<0x4e>(v);  // quad_perm [2,3,0,1]
+    if (LPR >= 2) v += dpp_f<0xb1>(v);  // quad_perm [1,0,3,2]
+    if (LPR == 32) v += __shfl_xor(v, 16, kWave);
     return v;
 }
 
