@@ -3,6 +3,10 @@
 StaticFrequencyPolicy picks the cache_size most frequently selected
 intermediate channels from calibration counts, ties broken by the lower
 channel index (reference python/soinfer/offload/hot_cache.py:67-95).
+LRUPolicy and LFUDecayPolicy are the online alternatives the reference
+evaluates against it in trace-driven simulation (hot_cache.py:98-187), and
+compare_policies runs all three over one trace (hot_cache.py:190-218). The
+simulations are host bookkeeping only.
 
 HotCache holds, for those channels in ascending order, their up_proj rows and
 down_proj^T rows (packed INT4 + fp32 scales) in device memory, and slot_of
@@ -14,8 +18,9 @@ the staged H2D gather instead (the reference's offload setting).
 """
 from __future__ import annotations
 
+from collections import OrderedDict
 from dataclasses import dataclass
-from typing import Iterable, Sequence
+from typing import Iterable, Optional, Sequence
 
 import torch
 
@@ -59,6 +64,104 @@ class StaticFrequencyPolicy:
                 total += 1
                 hits += c in self.hot_set
         return SimulationResult(self.name, self.cache_size, hits, total)
+
+
+class LRUPolicy:
+    """Least-recently-selected eviction, no calibration (hot_cache.py:98-141).
+
+    A token's selected channels are all looked up against the cache as it stood at the end of the previous
+    token (hits become most recent); only then are the token's misses inserted, in ascending channel order,
+    each evicting the least recently used entry when the cache is full. This is how the device cache behaves
+    per token (descriptors for the whole selection, then one update), and it keeps cross-token reuse visible
+    when one token selects more channels than the cache holds."""
+
+    name = "lru"
+
+    def __init__(self, cache_size: int):
+        self.cache_size = int(cache_size)
+
+    def simulate(self, trace: Iterable) -> SimulationResult:
+        cache: "OrderedDict[int, None]" = OrderedDict()  # first = least recently used
+        hits = total = 0
+        for selected in trace:
+            chans = _sorted_ints(selected)
+            total += len(chans)
+            missed = []
+            for c in chans:
+                if c in cache:
+                    cache.move_to_end(c)
+                    hits += 1
+                else:
+                    missed.append(c)
+            if self.cache_size <= 0:
+                continue
+            for c in missed:
+                if len(cache) >= self.cache_size:
+                    cache.popitem(last=False)
+                cache[c] = None
+        return SimulationResult(self.name, self.cache_size, hits, total)
+
+
+class LFUDecayPolicy:
+    """Lowest-frequency eviction with periodic decay (hot_cache.py:144-187).
+
+    Every selection adds 1 to its channel's frequency (before the lookup); a miss into a full cache evicts
+    the cached channel of lowest frequency, the higher index on ties (the lower index stays, as in
+    StaticFrequencyPolicy). After every decay_every tokens all tracked frequencies are multiplied by
+    decay in (0, 1], so stale popularity fades."""
+
+    name = "lfu_decay"
+
+    def __init__(self, cache_size: int, decay: float = 0.98, decay_every: int = 50):
+        if not (0.0 < decay <= 1.0):
+            raise ValueError("decay must be in (0, 1]")
+        self.cache_size = int(cache_size)
+        self.decay = float(decay)
+        self.decay_every = int(decay_every)
+
+    def simulate(self, trace: Iterable) -> SimulationResult:
+        freq: dict = {}
+        cache: set = set()
+        hits = total = 0
+        for step, selected in enumerate(trace):
+            for c in _sorted_ints(selected):
+                total += 1
+                freq[c] = freq.get(c, 0.0) + 1.0
+                if c in cache:
+                    hits += 1
+                    continue
+                if self.cache_size <= 0:
+                    continue
+                if len(cache) >= self.cache_size:
+                    # lowest frequency first; among equal frequencies the highest index goes
+                    cache.remove(min(cache, key=lambda x: (freq[x], -x)))
+                cache.add(c)
+            if self.decay_every > 0 and (step + 1) % self.decay_every == 0:
+                for ch in freq:
+                    freq[ch] *= self.decay
+        return SimulationResult(self.name, self.cache_size, hits, total)
+
+
+def compare_policies(trace: Sequence, cache_sizes: Sequence[int], frequencies: Optional[Sequence[int]] = None,
+                     **lfu_kwargs) -> list:
+    """Static, LRU and LFU-with-decay over the same trace at each cache size (hot_cache.py:190-218).
+
+    frequencies (for the static policy) default to the trace's own per-channel selection counts, i.e. the
+    static policy's best case; pass calibration counts to evaluate it on held-out traffic instead."""
+    trace = list(trace)
+    if frequencies is None:
+        counts: dict = {}
+        for selected in trace:
+            for c in _sorted_ints(selected):
+                counts[c] = counts.get(c, 0) + 1
+        n = max(counts) + 1 if counts else 0
+        frequencies = [counts.get(c, 0) for c in range(n)]
+    out = []
+    for size in cache_sizes:
+        out.append(StaticFrequencyPolicy(frequencies, size).simulate(trace))
+        out.append(LRUPolicy(size).simulate(trace))
+        out.append(LFUDecayPolicy(size, **lfu_kwargs).simulate(trace))
+    return out
 
 
 @dataclass
