@@ -4,11 +4,16 @@
 // y[n] = sum_k s[n*stride + k/gs] * q[n,k] * x[k], stride 0 = per-tensor
 // scale, fp32 accumulation, binary16 output.
 //
-// One wave per workgroup, R rows per wave. Lane l owns 16-byte chunk l of each
-// 64-chunk pass (16 consecutive k), so a wave-wide dwordx4 load reads 1 KB of
-// a row. Bytes become exact binary16 integers (soi_device.h), pairs are
-// accumulated with an ordered v_dot2 chain, and the scale is applied once per
-// chunk (per word when 16 does not divide group_size).
+// One wave per workgroup, R rows per wave, PU 64-chunk passes per batch.
+// Lane l owns 16-byte chunk l of each pass (16 consecutive k), so a wave-wide
+// dwordx4 load reads 1 KB of a row; R*PU such loads are issued before any
+// arithmetic. Loads are unconditional: a lane past the last chunk (or any
+// byte past K) reads the zero word instead (address select, no branch), and
+// row addresses are wave-uniform (scalar registers). Bytes become exact
+// binary16 integers (soi_device.h), pairs are accumulated with an ordered
+// v_dot2 chain, the scale is applied once per chunk (per word when 16 does
+// not divide group_size), and the R row totals come out of one transposed
+// wave reduction with a fixed order of additions.
 //
 // One deliberate difference: with num_groups == 1 every element uses the
 // row's single scale. The reference indexes scale[row*stride + k/gs] even
@@ -18,116 +23,151 @@
 
 namespace soi {
 
-template <int R, bool VEC, bool CHUNK_SCALE>
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
 __global__ __launch_bounds__(64) void gemv_int8_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
                                                        int64_t srow_stride, int64_t N, const uint16_t* __restrict__ x,
                                                        uint16_t* __restrict__ y, int K, int gs, int G) {
+    constexpr int SC = CHUNK_SCALE ? 1 : 4;
     const int lane = threadIdx.x;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
     const int chunks = (K + 15) >> 4;
+    const uint32_t* zw = g_zero16;
+    const float* zf = reinterpret_cast<const float*>(g_zero16);
+
+    // rows past N read row N-1 (never stored)
+    const uint8_t* wr[R];
+    const float* sr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t n = (FULL || row0 + r < N) ? row0 + r : N - 1;
+        wr[r] = uniform_ptr(reinterpret_cast<const uint8_t*>(W) + n * static_cast<int64_t>(K));
+        sr[r] = uniform_ptr(S + n * srow_stride);
+    }
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int c0 = 0; c0 < chunks; c0 += kWave) {
-        const int c = c0 + lane;
-        if (c >= chunks) continue;
-        const int k0 = 16 * c;
-        uint32_t wv[R][4];
+    for (int c0 = 0; c0 < chunks; c0 += kWave * PU) {
+        uint32_t wv[PU][R][4];
+        float sc[PU][R][SC];
+        f16x2 xv[PU][8];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t n = row0 + r;
-            const int8_t* row = W + (n < N ? n : 0) * static_cast<int64_t>(K);
-            if (n >= N) {
-                wv[r][0] = wv[r][1] = wv[r][2] = wv[r][3] = 0u;
-            } else if (VEC) {
-                const u32x4 t = reinterpret_cast<const u32x4*>(row)[c];
-                wv[r][0] = t.x;
-                wv[r][1] = t.y;
-                wv[r][2] = t.z;
-                wv[r][3] = t.w;
-            } else {
-                const uint8_t* rb = reinterpret_cast<const uint8_t*>(row);
+        for (int p = 0; p < PU; ++p) {
+            const int c = c0 + p * kWave + lane;
+            const bool cv = FULL || c < chunks;
+            const int k0 = 16 * c;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    uint32_t word = 0;
+            for (int r = 0; r < R; ++r) {
+                if (VEC) {
+                    const u32x4* q = reinterpret_cast<const u32x4*>(wr[r]) + c;
+                    const u32x4 t = ldg(cv ? q : reinterpret_cast<const u32x4*>(zw));
+                    wv[p][r][0] = t.x;
+                    wv[p][r][1] = t.y;
+                    wv[p][r][2] = t.z;
+                    wv[p][r][3] = t.w;
+                } else {
+                    // ragged K: bytes past K read as 0x00 -> value 0 (x there is 0 too)
+                    const uint8_t* zb = reinterpret_cast<const uint8_t*>(zw);
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int kk = k0 + 4 * i + b;
-                        // padding bytes read as 0x00 -> value 0; x there is 0 too
-                        word |= (kk < K ? static_cast<uint32_t>(rb[kk]) : 0u) << (8 * b);
+                    for (int i = 0; i < 4; ++i) {
+                        uint32_t word = 0;
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const int kk = k0 + 4 * i + b;
+                            word |= static_cast<uint32_t>(ldg((cv && kk < K) ? wr[r] + kk : zb)) << (8 * b);
+                        }
+                        wv[p][r][i] = word;
                     }
-                    wv[r][i] = word;
+                }
+                if (CHUNK_SCALE) {
+                    sc[p][r][0] = ldg(cv ? sr[r] + (G == 1 ? 0 : k0 / gs) : zf);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < SC; ++i) {
+                        const int kk = k0 + 4 * i;
+                        sc[p][r][i] = ldg((cv && kk < K) ? sr[r] + kk / gs : zf);
+                    }
                 }
             }
-        }
-        float sc[R][CHUNK_SCALE ? 1 : 4];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t n = row0 + r;
-            const float* srow = S + (n < N ? n : 0) * srow_stride;
-            if (CHUNK_SCALE) {
-                sc[r][0] = (n < N) ? srow[G == 1 ? 0 : k0 / gs] : 0.0f;
+            if (VEC) {  // K % 16 == 0: a valid chunk is fully inside x
+                const u32x4* xp = reinterpret_cast<const u32x4*>(x + k0);
+                const u32x4* z4 = reinterpret_cast<const u32x4*>(zw);
+                const u32x4 a = ldg(cv ? xp : z4), b = ldg(cv ? xp + 1 : z4);
+                xv[p][0] = as_f16x2(a.x);
+                xv[p][1] = as_f16x2(a.y);
+                xv[p][2] = as_f16x2(a.z);
+                xv[p][3] = as_f16x2(a.w);
+                xv[p][4] = as_f16x2(b.x);
+                xv[p][5] = as_f16x2(b.y);
+                xv[p][6] = as_f16x2(b.z);
+                xv[p][7] = as_f16x2(b.w);
             } else {
+                const uint16_t* zh = reinterpret_cast<const uint16_t*>(zw);
 #pragma unroll
-                for (int i = 0; i < (CHUNK_SCALE ? 1 : 4); ++i) {
-                    const int kk = k0 + 4 * i;
-                    sc[r][i] = (n < N && kk < K) ? srow[kk / gs] : 0.0f;
+                for (int e = 0; e < 8; ++e) {
+                    const int ka = k0 + 2 * e, kb = ka + 1;
+                    const uint32_t lo = ldg((cv && ka < K) ? x + ka : zh);
+                    const uint32_t hi = ldg((cv && kb < K) ? x + kb : zh);
+                    xv[p][e] = as_f16x2(lo | (hi << 16));
                 }
             }
         }
-        f16x2 xv[8];
-        if (VEC && k0 + 16 <= K) {
-            const u32x4* xp = reinterpret_cast<const u32x4*>(x + k0);
-            const u32x4 a = xp[0], b = xp[1];
-            xv[0] = as_f16x2(a.x);
-            xv[1] = as_f16x2(a.y);
-            xv[2] = as_f16x2(a.z);
-            xv[3] = as_f16x2(a.w);
-            xv[4] = as_f16x2(b.x);
-            xv[5] = as_f16x2(b.y);
-            xv[6] = as_f16x2(b.z);
-            xv[7] = as_f16x2(b.w);
-        } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int ka = k0 + 2 * e, kb = ka + 1;
-                const uint32_t lo = (ka < K) ? x[ka] : 0u;
-                const uint32_t hi = (kb < K) ? x[kb] : 0u;
-                xv[e] = as_f16x2(lo | (hi << 16));
-            }
-        }
+        for (int p = 0; p < PU; ++p) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (CHUNK_SCALE) {
-                float t = 0.0f;
+            for (int r = 0; r < R; ++r) {
+                if (CHUNK_SCALE) {
+                    float t = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    f16x2 q[2];
-                    dequant_int8x4(wv[r][i], q);
-                    t = dot2(q[0], xv[2 * i], t);
-                    t = dot2(q[1], xv[2 * i + 1], t);
-                }
-                acc[r] = fmaf(sc[r][0], t, acc[r]);
-            } else {
+                    for (int i = 0; i < 4; ++i) {
+                        f16x2 q[2];
+                        dequant_int8x4(wv[p][r][i], q);
+                        t = dot2(q[0], xv[p][2 * i], t);
+                        t = dot2(q[1], xv[p][2 * i + 1], t);
+                    }
+                    acc[r] = fmaf(sc[p][r][0], t, acc[r]);
+                } else {
 #pragma unroll
-                for (int i = 0; i < (CHUNK_SCALE ? 1 : 4); ++i) {
-                    f16x2 q[2];
-                    dequant_int8x4(wv[r][i], q);
-                    float t = dot2(q[0], xv[2 * i], 0.0f);
-                    t = dot2(q[1], xv[2 * i + 1], t);
-                    acc[r] = fmaf(sc[r][i], t, acc[r]);
+                    for (int i = 0; i < SC; ++i) {
+                        f16x2 q[2];
+                        dequant_int8x4(wv[p][r][i], q);
+                        float t = dot2(q[0], xv[p][2 * i], 0.0f);
+                        t = dot2(q[1], xv[p][2 * i + 1], t);
+                        acc[r] = fmaf(sc[p][r][i], t, acc[r]);
+                    }
                 }
             }
         }
     }
 
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float total = wave_sum_lane63(acc[r]);
-        if (lane == 63 && row0 + r < N) y[row0 + r] = f32_to_f16_bits(total);
+    const float total = reduce_rows<R>(acc);
+    const int r = reduce_rows_row<R>(static_cast<uint32_t>(lane));
+    if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) stg(y + row0 + r, f32_to_f16_bits(total));
+}
+
+struct Int8Plan {
+    int R, PU;
+};
+
+// PU: passes per batch, the largest of 4, 3, 2 that divides the pass count
+// (all of them when there are fewer than 4); R: the most rows per wave with
+// R*PU <= 8 1 KB row segments in flight that still leaves >= 2048 waves in the
+// grid (swept on the Qwen3-1.7B shapes: more waves beat more rows per wave).
+static Int8Plan plan_int8(int64_t N, int64_t K, bool vec) {
+    const int64_t passes = ceil_div64(ceil_div64(K, 16), kWave);
+    Int8Plan p{1, 1};
+    if (vec) {
+        if (passes <= 4) p.PU = static_cast<int>(passes);
+        else if (passes % 4 == 0) p.PU = 4;
+        else if (passes % 3 == 0) p.PU = 3;
+        else if (passes % 2 == 0) p.PU = 2;
+        else p.PU = 4;
     }
+    int R = 8;
+    while (R > 1 && (R * p.PU > 8 || N / R < 2048)) R >>= 1;
+    p.R = R;
+    return p;
 }
 
 }  // namespace soi
@@ -152,25 +192,41 @@ extern "C" int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16
     SOI_REQUIRE(Wq && scale && x && y, "%s: null pointer", what);
     const bool vec = (K % 16 == 0) && aligned16(Wq) && aligned16(x);
     const bool chunk_scale = (num_groups == 1) || (group_size % 16 == 0);
-    const int R = N >= 4096 ? 4 : (N >= 2048 ? 2 : 1);
-    const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
+    const Int8Plan pl = plan_int8(N, K, vec);
+    const bool full = vec && (N % pl.R == 0) && ((K / 16) % (kWave * pl.PU) == 0);
+    const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
     hipStream_t st = as_stream(stream);
     const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size), Gi = static_cast<int>(num_groups);
-#define SOI_L(RR, V, CS)                                                                                          \
-    hipLaunchKernelGGL((gemv_int8_kernel<RR, V, CS>), grid, dim3(64), 0, st, Wq, scale, scale_row_stride, N, x, y, \
-                       Ki, gi, Gi)
-#define SOI_LR(V, CS)                    \
-    switch (R) {                         \
-        case 4: SOI_L(4, V, CS); break;  \
-        case 2: SOI_L(2, V, CS); break;  \
-        default: SOI_L(1, V, CS); break; \
-    }
+#define SOI_L(RR, PP, V, CS, FL)                                                                                   \
+    hipLaunchKernelGGL((gemv_int8_kernel<RR, PP, V, CS, FL>), grid, dim3(64), 0, st, Wq, scale, scale_row_stride, N, \
+                       x, y, Ki, gi, Gi)
+#define SOI_CS(RR, PP, V)                                     \
+    if (V && full && chunk_scale) SOI_L(RR, PP, V, true, true); \
+    else if (chunk_scale) SOI_L(RR, PP, V, true, false);        \
+    else SOI_L(RR, PP, V, false, false)
     if (vec) {
-        if (chunk_scale) { SOI_LR(true, true) } else { SOI_LR(true, false) }
+        switch (pl.R * 10 + pl.PU) {
+            case 81: SOI_CS(8, 1, true); break;
+            case 41: SOI_CS(4, 1, true); break;
+            case 21: SOI_CS(2, 1, true); break;
+            case 11: SOI_CS(1, 1, true); break;
+            case 42: SOI_CS(4, 2, true); break;
+            case 22: SOI_CS(2, 2, true); break;
+            case 12: SOI_CS(1, 2, true); break;
+            case 23: SOI_CS(2, 3, true); break;
+            case 13: SOI_CS(1, 3, true); break;
+            case 24: SOI_CS(2, 4, true); break;
+            default: SOI_CS(1, 4, true); break;
+        }
     } else {
-        if (chunk_scale) { SOI_LR(false, true) } else { SOI_LR(false, false) }
+        switch (pl.R) {
+            case 8: SOI_CS(8, 1, false); break;
+            case 4: SOI_CS(4, 1, false); break;
+            case 2: SOI_CS(2, 1, false); break;
+            default: SOI_CS(1, 1, false); break;
+        }
     }
-#undef SOI_LR
+#undef SOI_CS
 #undef SOI_L
     return launch_status(what);
 }

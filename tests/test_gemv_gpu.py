@@ -128,7 +128,10 @@ def test_w8_basis_vectors_exact(ops, gran, gs):
 
 
 @pytest.mark.parametrize("gran,gs", W8 + [("group", 32), ("group", 4), ("group", 12)])
-@pytest.mark.parametrize("N,K", [(512, 4096), (6144, 2048), (2048, 6144), (1024, 2048), (7, 96)])
+# tiles: (512, 4096) 1 row x 4 passes; (6144, 2048) 4 x 2; (2048, 6144) 2 x 3; (1024, 2048) 1 x 2 -- all full;
+# (4097, 3072) 2 x 3 with a partial last tile; (8200, 1040) 4 x 2 with idle lanes; (2049, 100) and (7, 96) ragged
+@pytest.mark.parametrize("N,K", [(512, 4096), (6144, 2048), (2048, 6144), (1024, 2048), (7, 96), (4097, 3072),
+                                 (8200, 1040), (2049, 100)])
 def test_w8_matches_oracle(ops, gran, gs, N, K):
     if gs and K % gs:
         pytest.skip("K not a multiple of the group size in this grid")
