@@ -910,7 +910,9 @@ extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, con
 #undef SOI_N
         return launch_status(what);
     }
-    const int R = N >= 8 * 1024 ? 8 : N >= 4 * 1024 ? 4 : N >= 2 * 1024 ? 2 : 1;
+    // each wave normalises the whole vector before its rows, so larger tiles than the plain GEMV's pay here
+    // (swept at K = 2048: N = 4096 / 6144 / 2048 best at 8 / 8 / 4 rows per wave)
+    const int R = N >= 4 * 1024 ? 8 : N >= 2 * 1024 ? 4 : N >= 1024 ? 2 : 1;
     const bool full = cs && full_k && N % R == 0;
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
     const StoreY ep{y};

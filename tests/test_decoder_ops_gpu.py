@@ -261,7 +261,8 @@ def int4_mat(N, K, seed, gs=128):
     return int4_problem(N, K, gs, seed=seed)
 
 
-@pytest.mark.parametrize("N,with_delta", [(4096, True), (6144, False), (1000, True), (37, True)])
+@pytest.mark.parametrize("N,with_delta", [(4096, True), (6144, False), (1000, True), (37, True), (2050, False),
+                                          (1030, True)])
 def test_gemv_rmsnorm_equals_norm_then_gemv(C, ops, N, with_delta):
     K = 2048
     p = int4_mat(N, K, 50 + N)
