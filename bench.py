@@ -469,11 +469,11 @@ def bench_kernels(dev, gen):
         nb = 4096 * L + 8192
         t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_at(q, kc, vc, pos, out, ws_at),
                                   list(zip(KC, VC)))
-        res[f"attention_L{L}"] = entry(nb, t["mean_us"], kernel="attn_split + attn_combine (2 launches)")
+        res[f"attention_L{L}"] = entry(nb, t["mean_us"], kernel="attn_kernel, device position (1 launch)")
         t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_step(qkv, qn, qn, cos_t, sin_t, pos, kc, vc, out,
                                                                           1e-6, ws_step), list(zip(KC, VC)))
         res[f"attention_step_L{L}"] = entry(nb + 2 * (NQ + 2 * NKV) * HD, t["mean_us"],
-                                            kernel="attn_step (norm + RoPE + append + attention, 1 launch)")
+                                            kernel="attn_kernel with q/k norm + RoPE + KV append (1 launch)")
     del KC, VC
     torch.cuda.empty_cache()
 
