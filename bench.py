@@ -313,17 +313,22 @@ def bench_dip_mlp(D, w, hot, dev):
             y_dip = eng.down.clone()
         del eng
     k = I // 2
-    eng = D.DecodeEngine(w, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=1)
-    us = run(eng)
-    assert torch.equal(eng.down, y_dip), "cache-aware DIP must equal DIP bit for bit"
-    misses = int(eng.miss_cnt.item())
-    nb = mlp_bytes(w.layers[0], I, H, k)
-    res[f"cached_dip_k{k}"] = {"k_over_I": 0.5, "hot_fraction": 0.2, "us": round(us, 2),
-                               "misses_last_layer": misses, "bit_identical_to_dip": True,
-                               "host_bytes_last_layer": misses * (w.layers[0].gu_Wq.shape[1] +
-                                                                  w.layers[0].down_T_Wq.shape[1]),
-                               "note": "misses read from pinned host memory by an in-graph device gather"}
-    del eng
+    notes = {"direct": "misses read in place from the pinned host arena by the up GEMV and the down accumulate "
+                       "(no descriptors, gathers or staging)",
+             "staged": "descriptors, then in-graph device gathers of the misses from pinned host memory into "
+                       "staging, then the descriptor kernels (the reference's shape)"}
+    for path in ("direct", "staged"):
+        eng = D.DecodeEngine(w, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=1, miss_path=path)
+        us = run(eng)
+        assert torch.equal(eng.down, y_dip), "cache-aware DIP must equal DIP bit for bit"
+        import soinfer.ops as ops
+        misses = int(ops.build_dip_descriptors(eng.idx, eng.caches[-1].slot_of)[2].item())
+        key = f"cached_dip_k{k}" if path == "direct" else f"cached_dip_staged_k{k}"
+        res[key] = {"k_over_I": 0.5, "hot_fraction": 0.2, "us": round(us, 2), "misses_last_layer": misses,
+                    "bit_identical_to_dip": True,
+                    "host_bytes_last_layer": misses * (w.layers[0].gu_Wq.shape[1] + w.layers[0].down_T_Wq.shape[1]),
+                    "note": notes[path]}
+        del eng
     return res
 
 
@@ -341,10 +346,12 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     out, toks = {}, {}
     L0 = w.layers[0]
     attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
-    for mode in ("dense", "dip", "dip_dense_up", "cached_dip"):
-        eng = D.DecodeEngine(w, "dip" if mode == "dip_dense_up" else mode, dip_k=None if mode == "dense" else k,
-                             hot_channels=hot if mode == "cached_dip" else None, max_new_tokens=n_new,
-                             dip_dense_up=mode == "dip_dense_up")
+    for mode in ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged"):
+        base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip"}.get(mode, mode)
+        eng = D.DecodeEngine(w, base, dip_k=None if mode == "dense" else k,
+                             hot_channels=hot if base == "cached_dip" else None, max_new_tokens=n_new,
+                             dip_dense_up=mode == "dip_dense_up",
+                             miss_path="staged" if mode == "cached_dip_staged" else "direct")
         eng.capture()
         eng.generate(prompt[:8], 8)  # warm up the graphs
         torch.cuda.synchronize()
@@ -366,8 +373,10 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         del eng
         torch.cuda.empty_cache()
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
-    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"]
+    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"] == toks["cached_dip_staged"]
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
+    out["cached_dip"]["miss_path"] = "direct: misses read in place from the pinned host arena inside the GEMVs"
+    out["cached_dip_staged"]["miss_path"] = "staged: device gathers of the misses into staging, then descriptors"
     out["dip_dense_up_tokens_equal_dip"] = toks["dip"] == toks["dip_dense_up"]
     assert out["dip_dense_up_tokens_equal_dip"], "the dense-up DIP schedule must generate the same tokens as DIP"
     out["dip_dense_up"]["schedule"] = ("gate and up of every channel in one launch, top-k on gate, sparse down "

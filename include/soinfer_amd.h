@@ -385,6 +385,43 @@ int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* sc
                                             int64_t num_groups, void* workspace, size_t workspace_bytes,
                                             void* stream);
 
+/* --------------------------------------------------------------------------
+ * Hot-cache GEMVs that read the misses in place (cache-aware DIP without a
+ * staging copy). Row j of the logical selected matrix is channel ch = sel[j]:
+ * cache row slot_of[ch] when slot_of[ch] >= 0 (cache_Wq / cache_scale, as
+ * built by HotCache), else row ch of the full matrix full_Wq [num_channels,
+ * row_bytes] with scales full_scale [num_channels, G]. full_Wq is normally
+ * the device address of pinned host memory (hipHostGetDevicePointer), so a
+ * miss row crosses PCIe once, inside the GEMV that consumes it, while the
+ * hits stream from HBM in the same launch; no descriptors, gathers or
+ * staging buffers. slot_of: int32 [num_channels]. A channel outside
+ * [0, num_channels) or a slot outside [0, cache_rows) yields NaN for that row.
+ * The row bytes and arithmetic are those of the descriptor forms, so results
+ * equal soi_build_dip_descriptors + gathers + soi_gemv_dip_fused_up /
+ * _up_silu / _down bit for bit, and equal plain DIP over resident weights.
+ * No reference counterpart: replaces the staged miss path of
+ * run_decoder_layer_cached_dip (generate.py:367-404: descriptors, a host sync,
+ * gather_rows_staged of the misses, then gemv_dip_fused_up / _down).
+ *   soi_gemv_dip_cached_up: y[k] = rows @ x.
+ *   soi_gemv_dip_cached_up_silu: h_sel[j] = fp16(silu(gate[sel[j]]) * fp16(row_j . x)).
+ *   soi_gemv_dip_cached_down: y[H] = sum_j h_sel[j] * row_j (rows of down^T);
+ *     workspace rules of soi_gemv_w4a16_sparse_accumulate.
+ * ------------------------------------------------------------------------ */
+int soi_gemv_dip_cached_up(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                           const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
+                           const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x, uint16_t* y,
+                           int64_t K, int64_t group_size, int64_t num_groups, void* stream);
+int soi_gemv_dip_cached_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                                const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
+                                const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x,
+                                const uint16_t* gate, uint16_t* h_sel, int64_t K, int64_t group_size,
+                                int64_t num_groups, void* stream);
+int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                             const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
+                             const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* h_sel,
+                             uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

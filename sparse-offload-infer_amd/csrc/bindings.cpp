@@ -1112,6 +1112,109 @@ void gemv_dip_fused_up_silu_into(torch::Tensor cache_Wq, torch::Tensor cache_sca
                  n);
 }
 
+namespace {
+
+// Device-visible address of a weight matrix read in place: a CUDA tensor, or pinned host memory through its
+// device mapping (the mapping of the allocation's base plus the view's offset, so views into one pinned arena
+// work).
+const uint8_t* readable_rows(const torch::Tensor& W, int64_t row_bytes, const torch::Tensor& dev, const char* name) {
+    TORCH_CHECK(W.scalar_type() == torch::kUInt8 && W.dim() == 2 && W.is_contiguous() && W.size(1) == row_bytes,
+                name, "(full_Wq): must be a contiguous 2D uint8 tensor [num_channels, ceil(row_dim/8)*4]");
+    if (W.is_cuda()) {
+        check_same_device(dev, W, name);
+        return W.data_ptr<uint8_t>();
+    }
+    TORCH_CHECK(W.is_cpu() && W.is_pinned(), name, "(full_Wq): must be a CUDA tensor or pinned host memory");
+    const auto* base = static_cast<const uint8_t*>(W.storage().data());
+    const auto* at = static_cast<const uint8_t*>(W.data_ptr());
+    void* dp = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dp, const_cast<uint8_t*>(base), 0);
+    TORCH_CHECK(e == hipSuccess && dp != nullptr, name, ": hipHostGetDevicePointer failed: ", hipGetErrorString(e));
+    return static_cast<const uint8_t*>(dp) + (at - base);
+}
+
+struct CachedArgs {
+    const uint8_t* full;
+    int64_t cache_rows;
+    int64_t num_channels;
+};
+
+CachedArgs check_cached_common(const torch::Tensor& cache_Wq, const torch::Tensor& cache_scale,
+                               const torch::Tensor& full_Wq, const torch::Tensor& full_scale,
+                               const torch::Tensor& slot_of, const torch::Tensor& sel, int64_t row_dim,
+                               const char* name) {
+    const int64_t row_bytes = ((row_dim + 7) / 8) * 4;
+    TORCH_CHECK(cache_Wq.is_cuda() && cache_Wq.scalar_type() == torch::kUInt8 && cache_Wq.dim() == 2 &&
+                    cache_Wq.is_contiguous() && cache_Wq.size(1) == row_bytes,
+                name, "(cache_Wq): must be a contiguous 2D uint8 CUDA tensor [C, ceil(row_dim/8)*4]");
+    need(cache_scale, torch::kFloat32, sel, name, "cache_scale");
+    need(full_scale, torch::kFloat32, sel, name, "full_scale");
+    need(slot_of, torch::kInt32, sel, name, "slot_of");
+    need(sel, torch::kInt32, sel, name, "sel");
+    check_same_device(sel, cache_Wq, name);
+    TORCH_CHECK(cache_scale.dim() == 2 && full_scale.dim() == 2 && cache_scale.size(1) == full_scale.size(1), name,
+                ": cache_scale and full_scale must be 2D with the same num_groups");
+    TORCH_CHECK(cache_scale.size(0) >= cache_Wq.size(0), name, ": cache_scale must have a row per cache_Wq row");
+    TORCH_CHECK(full_scale.size(0) == full_Wq.size(0) && slot_of.numel() == full_Wq.size(0), name,
+                ": full_Wq, full_scale and slot_of must have one entry per channel");
+    return {readable_rows(full_Wq, row_bytes, sel, name), cache_Wq.size(0), full_Wq.size(0)};
+}
+
+}  // namespace
+
+void gemv_dip_cached_up_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor full_Wq,
+                             torch::Tensor full_scale, torch::Tensor slot_of, torch::Tensor sel, torch::Tensor x,
+                             torch::Tensor y, int64_t K, int64_t group_size) {
+    const char* n = "gemv_dip_cached_up_into";
+    const CachedArgs a = check_cached_common(cache_Wq, cache_scale, full_Wq, full_scale, slot_of, sel, K, n);
+    need(x, torch::kFloat16, sel, n, "x");
+    need(y, torch::kFloat16, sel, n, "y");
+    TORCH_CHECK(x.numel() == K && y.numel() == sel.numel(), n, ": shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_dip_cached_up(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), a.cache_rows,
+                                        a.full, full_scale.data_ptr<float>(), a.num_channels,
+                                        slot_of.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), sel.numel(), h16(x),
+                                        h16m(y), K, group_size, cache_scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void gemv_dip_cached_up_silu_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor full_Wq,
+                                  torch::Tensor full_scale, torch::Tensor slot_of, torch::Tensor sel, torch::Tensor x,
+                                  torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
+    const char* n = "gemv_dip_cached_up_silu_into";
+    const CachedArgs a = check_cached_common(cache_Wq, cache_scale, full_Wq, full_scale, slot_of, sel, K, n);
+    need(x, torch::kFloat16, sel, n, "x");
+    need(gate, torch::kFloat16, sel, n, "gate");
+    need(h_sel, torch::kFloat16, sel, n, "h_sel");
+    TORCH_CHECK(x.numel() == K && h_sel.numel() == sel.numel() && gate.numel() == a.num_channels, n,
+                ": shape mismatch");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_dip_cached_up_silu(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(),
+                                             a.cache_rows, a.full, full_scale.data_ptr<float>(), a.num_channels,
+                                             slot_of.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), sel.numel(),
+                                             h16(x), h16(gate), h16m(h_sel), K, group_size, cache_scale.size(1),
+                                             cur_stream(x)),
+                 n);
+}
+
+void gemv_dip_cached_down_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor full_Wq,
+                               torch::Tensor full_scale, torch::Tensor slot_of, torch::Tensor sel, torch::Tensor h_sel,
+                               torch::Tensor y, int64_t H, int64_t group_size, torch::Tensor workspace_buf) {
+    const char* n = "gemv_dip_cached_down_into";
+    const CachedArgs a = check_cached_common(cache_Wq, cache_scale, full_Wq, full_scale, slot_of, sel, H, n);
+    need(h_sel, torch::kFloat16, sel, n, "h_sel");
+    need(y, torch::kFloat16, sel, n, "y");
+    need(workspace_buf, torch::kUInt8, sel, n, "workspace");
+    TORCH_CHECK(h_sel.numel() == sel.numel() && y.numel() == H, n, ": h_sel / y shape mismatch");
+    const at::DeviceGuard guard(h_sel.device());
+    check_status(soi_gemv_dip_cached_down(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), a.cache_rows,
+                                          a.full, full_scale.data_ptr<float>(), a.num_channels,
+                                          slot_of.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), sel.numel(),
+                                          h16(h_sel), h16m(y), H, group_size, cache_scale.size(1),
+                                          workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(h_sel)),
+                 n);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "soinfer MI355X (gfx950) quantized decode hot path";
     m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
@@ -1172,5 +1275,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
           "sparse down over selected rows with the SiLU gating computed on the fly");
     m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");
+    m.def("gemv_dip_cached_up_into", &gemv_dip_cached_up_into, "hot-cache up GEMV, misses read in place");
+    m.def("gemv_dip_cached_up_silu_into", &gemv_dip_cached_up_silu_into,
+          "hot-cache up GEMV with SiLU gating, misses read in place");
+    m.def("gemv_dip_cached_down_into", &gemv_dip_cached_down_into, "hot-cache down accumulate, misses read in place");
     m.def("version", []() { return std::string(soi_version()); });
 }

@@ -954,6 +954,54 @@ extern "C" int soi_gemv_w4a16_indexed_silu(const uint8_t* Wq, const float* scale
                              as_stream(stream), what);
 }
 
+static int check_cached(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows, const uint8_t* full_Wq,
+                        const float* full_scale, int64_t num_channels, const int32_t* slot_of, const int32_t* sel,
+                        int64_t k, const char* what) {
+    SOI_REQUIRE(k >= 0 && k <= (int64_t(1) << 31) - 1, "%s: k out of range", what);
+    SOI_REQUIRE(cache_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
+                "%s: negative or too large row / channel count", what);
+    if (k == 0) return SOI_OK;
+    SOI_REQUIRE(sel && slot_of && full_Wq && full_scale, "%s: null pointer", what);
+    SOI_REQUIRE(cache_rows == 0 || (cache_Wq && cache_scale), "%s: null cache", what);
+    return SOI_OK;
+}
+
+extern "C" int soi_gemv_dip_cached_up(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                                      const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
+                                      const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x,
+                                      uint16_t* y, int64_t K, int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_dip_cached_up";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    st = check_cached(cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, slot_of, sel, k, what);
+    if (st || k == 0) return st;
+    SOI_REQUIRE(x && y, "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    const bool vec = (K % 32 == 0) && aligned16(x) && aligned16(full_Wq) && (cache_rows == 0 || aligned16(cache_Wq));
+    SlotRows rows{cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, sel, slot_of, row_bytes,
+                  num_groups};
+    return launch_int4<true>(rows, k, x, StoreY{y}, K, group_size, vec, as_stream(stream), what);
+}
+
+extern "C" int soi_gemv_dip_cached_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
+                                           const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
+                                           const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x,
+                                           const uint16_t* gate, uint16_t* h_sel, int64_t K, int64_t group_size,
+                                           int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_dip_cached_up_silu";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    st = check_cached(cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, slot_of, sel, k, what);
+    if (st || k == 0) return st;
+    SOI_REQUIRE(x && gate && h_sel, "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    const bool vec = (K % 32 == 0) && aligned16(x) && aligned16(full_Wq) && (cache_rows == 0 || aligned16(cache_Wq));
+    SlotRows rows{cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, sel, slot_of, row_bytes,
+                  num_groups};
+    return launch_int4<true>(rows, k, x, SiluIdxY{h_sel, gate, sel, static_cast<int>(num_channels)}, K, group_size,
+                             vec, as_stream(stream), what);
+}
+
 extern "C" int soi_gemv_dip_fused_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
                                           const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
                                           const int32_t* desc, const int32_t* sel, int64_t k, const uint16_t* x,

@@ -47,6 +47,35 @@ struct DescRows {
     }
 };
 
+// row j = channel idx[j] through a hot-channel cache: slot_of[ch] >= 0 -> cache
+// row slot_of[ch], else row ch of the full matrix (usually a device mapping of
+// pinned host memory, read in place) with its scales from the full scale
+// matrix. Same logical rows as DescRows over a staging copy of the misses, so
+// the GEMV results are identical; a channel outside [0, fN) or a slot outside
+// [0, cN) is unresolvable.
+struct SlotRows {
+    const uint8_t* cW;
+    const float* cS;
+    int64_t cN;
+    const uint8_t* fW;
+    const float* fS;
+    int64_t fN;
+    const int32_t* idx;
+    const int32_t* slot_of;
+    int64_t row_bytes;
+    int64_t G;
+    __device__ __forceinline__ RowRef get(int64_t j) const {
+        const int32_t ch = idx[j];
+        if (ch < 0 || ch >= fN) return {nullptr, nullptr, false};
+        const int32_t s = slot_of[ch];
+        if (s >= 0) {
+            if (s < cN) return {cW + static_cast<int64_t>(s) * row_bytes, cS + static_cast<int64_t>(s) * G, true};
+            return {nullptr, nullptr, false};
+        }
+        return {fW + static_cast<int64_t>(ch) * row_bytes, fS + static_cast<int64_t>(ch) * G, true};
+    }
+};
+
 // row j = row idx[j] of a resident [num_rows, row_bytes] matrix
 struct IndexRows {
     const uint8_t* W;

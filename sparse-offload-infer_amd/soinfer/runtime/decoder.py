@@ -24,10 +24,14 @@ into preallocated buffers, and one decode step (LM head + argmax + 28 layers)
 is captured once as a HIP graph and replayed, so generation needs no host
 round trip until the end. The residual add is fused into the following
 RMSNorm and q/k-norm + RoPE + KV append into one launch; both give the same
-binary16 values as the separate ops. The cache-aware DIP mode keeps the
-up / down^T rows of non-hot channels in pinned host memory and fetches the
-misses inside the graph with a device gather from the host mapping, so its
-output is bit-identical to DIP with everything resident.
+binary16 values as the separate ops. The cache-aware DIP mode keeps every
+layer's up / down^T matrices in one pinned host arena (PinnedWeightStore) and
+the hot rows in HBM; the up GEMV and the down accumulate read each selected
+channel from the cache or, for a miss, straight from the arena's device
+mapping (miss_path "direct"), or the misses are first gathered into device
+staging buffers and read through descriptors (miss_path "staged", the
+reference's shape). Either way the output is bit-identical to DIP with
+everything resident.
 """
 from __future__ import annotations
 
@@ -39,6 +43,7 @@ import torch
 from .. import _C
 from .. import ops
 from ..offload.hot_cache import HotCache
+from ..offload.weight_store import PinnedWeightStore, plan_bytes
 from ..quant import formats, pack
 
 
@@ -143,16 +148,20 @@ def random_decoder(config: DecoderConfig = QWEN3_1P7B, seed: int = 0, device="cu
 
 class DecodeEngine:
     """Greedy decoder over DecoderWeights. mode: "dense", "dip" (top dip_k channels per layer, weights
-    resident) or "cached_dip" (hot channels resident, the rest fetched from pinned host memory).
+    resident) or "cached_dip" (hot channels resident, the rest in pinned host memory; miss_path "direct" reads
+    the misses in place inside the up / down kernels, "staged" gathers them into device staging first).
 
     All buffers are allocated here; decode steps launch only this package's kernels on the current stream
     and are captured into HIP graphs by capture()."""
 
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
-                 dip_dense_up: bool = False):
+                 dip_dense_up: bool = False, miss_path: str = "direct"):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
+        if miss_path not in ("direct", "staged"):
+            raise ValueError(f"unknown miss_path {miss_path!r}")
+        self.miss_path = miss_path
         if dip_dense_up and mode != "dip":
             raise ValueError("dip_dense_up applies to mode 'dip' (weights resident)")
         # DIP schedule for resident weights: gate and up of every channel in one launch, top-k on gate, then the
@@ -218,18 +227,21 @@ class DecodeEngine:
     def _setup_cache(self, hot_channels):
         c, dev, k = self.c, self.device, self.k
         I = c.intermediate
+        # one pinned arena for all layers' up and down^T rows, registered in the order the layers use them
+        shapes = []
+        for L in self.w.layers:
+            shapes += [tuple(L.up(I)[0].shape), tuple(L.down_T_Wq.shape)]
+        self.store = PinnedWeightStore(plan_bytes(shapes))
         self.caches, self.host_up, self.host_down, self.host_up_ptr, self.host_down_ptr = [], [], [], [], []
-        for L, hot in zip(self.w.layers, hot_channels):
+        for l, (L, hot) in enumerate(zip(self.w.layers, hot_channels)):
             up_Wq, up_s = L.up(I)
             self.caches.append(HotCache.build(up_Wq, up_s, L.down_T_Wq, L.down_T_scale, hot))
-            hu = torch.empty(up_Wq.shape, dtype=torch.uint8, pin_memory=True)
-            hd_ = torch.empty(L.down_T_Wq.shape, dtype=torch.uint8, pin_memory=True)
-            hu.copy_(up_Wq)
-            hd_.copy_(L.down_T_Wq)
-            self.host_up.append(hu)
-            self.host_down.append(hd_)
-            self.host_up_ptr.append(_C.host_device_pointer(hu))
-            self.host_down_ptr.append(_C.host_device_pointer(hd_))
+            hu = self.store.register(f"model.layers.{l}.mlp.up_proj.weight", up_Wq)
+            hd_ = self.store.register(f"model.layers.{l}.mlp.down_proj_T.weight", L.down_T_Wq)
+            self.host_up.append(self.store.matrix_view(hu))
+            self.host_down.append(self.store.matrix_view(hd_))
+            self.host_up_ptr.append(self.store.device_address(hu))
+            self.host_down_ptr.append(self.store.device_address(hd_))
         row_up = self.w.layers[0].gu_Wq.shape[1]
         row_dn = self.w.layers[0].down_T_Wq.shape[1]
         G = self.w.layers[0].gu_scale.shape[1]
@@ -274,6 +286,13 @@ class DecodeEngine:
             return
         cache = self.caches[l]
         _, uS = L.up(I)
+        if self.miss_path == "direct":
+            _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of, self.idx,
+                                       self.h, self.u_sel, H, gs)
+            _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
+            _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
+                                         cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws)
+            return
         self._fetch_misses(l, L, uS)
         _C.gemv_dip_fused_up_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc, self.h,
                                   self.u_sel, H, gs)
@@ -378,6 +397,12 @@ class DecodeEngine:
                                                       H, gs, self.sd_ws)
                 continue
             cache = self.caches[l]
+            if self.miss_path == "direct":
+                _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of,
+                                                self.idx, self.h, gate, self.h_sel, H, gs)
+                _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
+                                             cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws)
+                continue
             self._fetch_misses(l, L, uS)
             _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc,
                                            self.idx, self.h, gate, self.h_sel, H, gs)

@@ -129,6 +129,32 @@ def cached_dip_mlp(w: DipMLPWeights, cache: HotCache, x: torch.Tensor, dip_k: in
     return y, idx, mc
 
 
+def cached_dip_mlp_direct(w: DipMLPWeights, cache: HotCache, x: torch.Tensor, dip_k: int,
+                          full_up: Optional[torch.Tensor] = None, full_down_T: Optional[torch.Tensor] = None,
+                          workspace: Optional[torch.Tensor] = None):
+    """Cache-aware DIP MLP with the misses read in place: the up GEMV and the down accumulate resolve every
+    selected channel through cache.slot_of themselves, reading hits from the cache and misses from full_up /
+    full_down_T (pinned host memory read through its device mapping, or device tensors; default: the
+    resident weights). No descriptors, no gather, no staging buffer and no host sync; the SiLU gating is the
+    up GEMV's epilogue. Bit-identical to dip_mlp and cached_dip_mlp. Returns (y, idx)."""
+    from .. import _C
+
+    gate, idx = select_channels(w, x, dip_k)
+    full_up = w.up_Wq if full_up is None else full_up
+    full_down_T = w.down_T_Wq if full_down_T is None else full_down_T
+    H, gs = w.hidden_size, w.group_size
+    h = torch.empty(dip_k, dtype=torch.float16, device=x.device)
+    _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, full_up, w.up_scale, cache.slot_of, idx, x, gate,
+                                    h, H, gs)
+    if workspace is None:
+        workspace = torch.zeros(max(1, _C.sparse_accumulate_workspace_bytes(H, dip_k)), dtype=torch.uint8,
+                                device=x.device)
+    y = torch.empty(H, dtype=torch.float16, device=x.device)
+    _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, full_down_T, w.down_T_scale, cache.slot_of, idx,
+                                 h, y, H, gs, workspace)
+    return y, idx
+
+
 def calibrate_channel_frequencies(w: DipMLPWeights, xs: torch.Tensor, dip_k: int) -> torch.Tensor:
     """counts[c] = number of calibration inputs whose DIP selection contains channel c
     (generate.py:579-609, one layer). xs: [n, H] fp16."""

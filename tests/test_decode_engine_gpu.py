@@ -94,8 +94,9 @@ def test_graph_replay_equals_eager(dec, tiny, mode, k, fused):
         _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
 
 
+@pytest.mark.parametrize("miss_path", ["direct", "staged"])
 @pytest.mark.parametrize("fused", [True, False])
-def test_cached_dip_bit_identical_to_dip(dec, tiny, fused):
+def test_cached_dip_bit_identical_to_dip(dec, tiny, fused, miss_path):
     cfg = tiny.config
     k = cfg.intermediate // 2
     prompt = prompt_ids(6, cfg.vocab, seed=5)
@@ -106,7 +107,9 @@ def test_cached_dip_bit_identical_to_dip(dec, tiny, fused):
     assert all(len(h) == round(0.2 * cfg.intermediate) for h in hot20)
     for name, hot in (("0%", [[] for _ in range(cfg.layers)]), ("20%", hot20),
                       ("100%", [list(range(cfg.intermediate)) for _ in range(cfg.layers)])):
-        eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6, fused=fused)
+        eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6, fused=fused,
+                               miss_path=miss_path)
+        assert eng.store.arena.is_pinned() and eng.store.bytes_used == eng.store.bytes_total
         for use_graph in (False, True):
             got = eng.generate(prompt, 6, use_graph=use_graph)
             assert got == want, f"cache {name} graph={use_graph}"
@@ -137,6 +140,8 @@ def test_engine_rejects_bad_arguments(dec, tiny):
         dec.DecodeEngine(tiny, "dip", dip_k=0)
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "cached_dip", dip_k=8, hot_channels=[[]])  # one list per layer
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dip", dip_k=8, miss_path="zero_copy")
     eng = dec.DecodeEngine(tiny, "dense", max_new_tokens=4)
     with pytest.raises(ValueError):
         eng.generate(prompt_ids(10, tiny.config.vocab), 60)  # longer than max_seq

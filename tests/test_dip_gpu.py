@@ -317,3 +317,104 @@ def test_cached_dip_from_pinned_host_matches(ops):
     y, _, mc = dip.cached_dip_mlp(w, cache, x, k, host_up=up_host, host_down_T=down_host, staging=staging)
     assert mc > 0
     assert torch.equal(y, y_ref)
+
+
+# ---------------------------------------------------------------------------
+# hot-cache GEMVs reading the misses in place (no descriptors / staging)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("C", [0, 1229, 6144])
+@pytest.mark.parametrize("source", ["cuda", "pinned", "pinned_arena_view"])
+def test_cached_direct_equals_staged_and_resident(ops, C, source):
+    """soi_gemv_dip_cached_up / _up_silu / _down: bit-identical to the descriptor + staging kernels and to the
+    index-driven resident kernels on the same selection, with the full matrices on the device, in pinned host
+    memory, or as views at an offset inside one pinned arena."""
+    from soinfer import _C
+    from soinfer.offload.hot_cache import HotCache
+    from soinfer.runtime import dip
+
+    w = _layer(seed=5)
+    k, H, gs = 3072, 2048, 128
+    x = torch.randn(H, generator=torch.Generator().manual_seed(9)).half().cuda()
+    gate, idx = dip.select_channels(w, x, k)
+    hot = sorted(np.random.default_rng(C).choice(6144, C, replace=False).tolist())
+    cache = HotCache.build(w.up_Wq, w.up_scale, w.down_T_Wq, w.down_T_scale, hot)
+    if source == "cuda":
+        full_up, full_dn = w.up_Wq, w.down_T_Wq
+    elif source == "pinned":
+        full_up, full_dn = w.up_Wq.cpu().pin_memory(), w.down_T_Wq.cpu().pin_memory()
+    else:
+        rows, rb = w.up_Wq.shape
+        arena = torch.empty(4096 + 2 * rows * rb, dtype=torch.uint8).pin_memory()
+        full_up = arena[4096:4096 + rows * rb].view(rows, rb)
+        full_dn = arena[4096 + rows * rb:].view(rows, rb)
+        full_up.copy_(w.up_Wq.cpu())
+        full_dn.copy_(w.down_T_Wq.cpu())
+    # staged reference: descriptors, device gathers of the misses, descriptor kernels
+    desc, miss, mcnt = ops.build_dip_descriptors(idx, cache.slot_of)
+    mc = int(mcnt.item())
+    ml = miss[:mc].long()
+    up_st = w.up_Wq.index_select(0, ml).contiguous()
+    dn_st = w.down_T_Wq.index_select(0, ml).contiguous()
+    u_ref = ops.gemv_dip_fused_up(cache.up_Wq, cache.up_scale, up_st, w.up_scale.index_select(0, ml), desc, x, H, gs)
+    u = torch.empty(k, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, full_up, w.up_scale, cache.slot_of, idx, x, u, H, gs)
+    assert torch.equal(u, u_ref), "cached up differs from the descriptor form"
+    assert torch.equal(u, ops.gemv_w4a16_indexed(w.up_Wq, w.up_scale, idx, x, H, gs)), "cached up != resident"
+    h_ref = torch.empty(k, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, up_st, w.up_scale.index_select(0, ml), desc, idx,
+                                   x, gate, h_ref, H, gs)
+    h = torch.empty(k, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, full_up, w.up_scale, cache.slot_of, idx, x, gate,
+                                    h, H, gs)
+    assert torch.equal(h, h_ref), "cached up + SiLU differs from the descriptor form"
+    y_ref = ops.gemv_dip_fused_down(cache.down_Wq, cache.down_scale, dn_st, w.down_T_scale.index_select(0, ml), desc,
+                                    h, H, gs)
+    ws = torch.zeros(_C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+    y = torch.empty(H, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, full_dn, w.down_T_scale, cache.slot_of, idx, h, y,
+                                 H, gs, ws)
+    assert torch.equal(y, y_ref), "cached down differs from the descriptor form"
+    # and the whole MLP equals resident DIP
+    y_mlp, idx_mlp = dip.cached_dip_mlp_direct(w, cache, x, k, full_up, full_dn)
+    y_res, idx_res = dip.dip_mlp(w, x, k)
+    assert torch.equal(idx_mlp, idx_res) and torch.equal(y_mlp, y_res)
+    sel = idx.long().cpu().numpy()
+    assert_close(y, O.sparse_accumulate_f64(w.down_T_Wq.cpu().numpy()[sel], w.down_T_scale.cpu().numpy()[sel],
+                                            h.cpu().numpy(), H, gs), f"cached down C={C}")
+
+
+def test_cached_direct_edge_cases_and_rejections(ops):
+    from soinfer import _C
+    from soinfer.offload.hot_cache import HotCache
+
+    w = _layer(seed=6)
+    H, gs, I = 2048, 128, 6144
+    x = torch.randn(H, generator=torch.Generator().manual_seed(1)).half().cuda()
+    cache = HotCache.build(w.up_Wq, w.up_scale, w.down_T_Wq, w.down_T_scale, list(range(0, I, 3)))
+    # out-of-range channels give NaN rows, never a read
+    sel = torch.tensor([5, -1, I, 7], dtype=torch.int32, device="cuda")
+    u = torch.zeros(4, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, w.up_Wq, w.up_scale, cache.slot_of, sel, x, u, H, gs)
+    assert not torch.isnan(u[0]) and torch.isnan(u[1]) and torch.isnan(u[2]) and not torch.isnan(u[3])
+    # k = 0: the down accumulate writes zeros
+    empty = torch.empty(0, dtype=torch.int32, device="cuda")
+    y = torch.full((H,), 1.0, dtype=torch.float16, device="cuda")
+    ws = torch.zeros(1, dtype=torch.uint8, device="cuda")
+    _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, w.down_T_Wq, w.down_T_scale, cache.slot_of, empty,
+                                 torch.empty(0, dtype=torch.float16, device="cuda"), y, H, gs, ws)
+    assert int(y.count_nonzero()) == 0
+    sel = torch.arange(8, dtype=torch.int32, device="cuda")
+    u = torch.empty(8, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError):  # full matrix in pageable host memory
+        _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, w.up_Wq.cpu(), w.up_scale, cache.slot_of, sel, x, u,
+                                   H, gs)
+    with pytest.raises(RuntimeError):  # slot_of shorter than the channel count
+        _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, w.up_Wq, w.up_scale, cache.slot_of[:100], sel, x, u,
+                                   H, gs)
+    with pytest.raises(RuntimeError):  # scale groups differ between cache and full matrix
+        _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, w.up_Wq, w.up_scale[:, :8].contiguous(),
+                                   cache.slot_of, sel, x, u, H, gs)
+    with pytest.raises(RuntimeError):  # workspace too small
+        _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, w.down_T_Wq, w.down_T_scale, cache.slot_of, sel,
+                                     u, torch.empty(H, dtype=torch.float16, device="cuda"), H, gs, ws)
