@@ -150,15 +150,22 @@ class DecodeEngine:
     """Greedy decoder over DecoderWeights. mode: "dense", "dip" (top dip_k channels per layer, weights
     resident) or "cached_dip" (hot channels resident, the rest in pinned host memory; miss_path "direct" reads
     the misses in place inside the up / down kernels, "staged" gathers them into device staging first).
+    offload=True keeps the dense weights of every layer (q|k|v, o, and gate|up + down for dense or gate for
+    cached DIP) in a pinned host arena and copies each layer's block into one of two device slots right before
+    the layer runs (hipMemcpyAsync on the compute stream, captured in the graph): the reference's streamed
+    configuration (WeightPipeline, generate.py:85-138). Scales, norms, embedding and LM head stay in HBM.
 
     All buffers are allocated here; decode steps launch only this package's kernels on the current stream
     and are captured into HIP graphs by capture()."""
 
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
-                 dip_dense_up: bool = False, miss_path: str = "direct"):
+                 dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
+        if offload and mode == "dip":
+            raise ValueError("offload streams the dense weights; for DIP with every selected row read from host "
+                             "memory use mode 'cached_dip' with empty hot-channel lists")
         if miss_path not in ("direct", "staged"):
             raise ValueError(f"unknown miss_path {miss_path!r}")
         self.miss_path = miss_path
@@ -219,6 +226,9 @@ class DecodeEngine:
             perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
             self.gu_il = [(L.gu_Wq.index_select(0, perm).contiguous(), L.gu_scale.index_select(0, perm).contiguous())
                           for L in w.layers]
+        self.offload = offload
+        if offload:
+            self._setup_offload()
         self._x_final = self.x
         self._graph_layers = None
         self._graph_gen = None
@@ -253,6 +263,56 @@ class DecodeEngine:
         self.st_dn = torch.zeros(k, row_dn, dtype=u8, device=dev)
         self.st_up_s = torch.zeros(k, G, dtype=f32, device=dev)
         self.st_dn_s = torch.zeros(k, G, dtype=f32, device=dev)
+
+    # ---- offloaded dense weights: pinned arena, two device slots, one copy per layer ----
+    def _streamed(self, l: int, L: LayerWeights) -> list:
+        """(field, tensor) of the packed matrices layer l streams, in the order the layer uses them."""
+        I = self.c.intermediate
+        out = [("qkv_Wq", L.qkv_Wq), ("o_Wq", L.o_Wq)]
+        if self.mode == "dense":
+            out.append(("gu_il", self.gu_il[l][0]) if self.fused else ("gu_Wq", L.gu_Wq))
+            out.append(("down_Wq", L.down_Wq))
+        else:
+            out.append(("gu_Wq", L.gu_Wq[:I]))  # gate rows; up / down^T rows come from the cache or host arena
+        return out
+
+    def _setup_offload(self):
+        blocks = [self._streamed(l, L) for l, L in enumerate(self.w.layers)]
+        self.wstore = PinnedWeightStore(plan_bytes(tuple(t.shape) for b in blocks for _, t in b))
+        self._blocks = []  # per layer: (arena offset, bytes)
+        for l, b in enumerate(blocks):
+            first = None
+            for name, t in b:
+                h = self.wstore.register(f"model.layers.{l}.{name}", t.contiguous())
+                first = h.offset if first is None else first
+            self._blocks.append((first, self.wstore.bytes_used - first))
+        nbytes = max(n for _, n in self._blocks)
+        self.slots = [torch.empty(nbytes, dtype=torch.uint8, device=self.device) for _ in range(2)]
+        # the views of a slot for each layer (same shapes every layer)
+        self._slot_views = []
+        for slot in self.slots:
+            views, off = {}, 0
+            for name, t in blocks[0]:
+                n = t.numel()
+                views[name] = slot[off:off + n].view(t.shape)
+                off += n
+            self._slot_views.append(views)
+
+    def _layer(self, l: int, L: LayerWeights):
+        """Layer l's weights for this step. With offload, first copies the layer's block from the pinned arena
+        into slot l % 2 (stream-ordered before the layer's kernels) and returns views of the slot with the
+        resident scales and norms."""
+        if not self.offload:
+            return L, (self.gu_il[l] if hasattr(self, "gu_il") else None)
+        off, n = self._blocks[l]
+        slot = self.slots[l % 2]
+        slot[:n].copy_(self.wstore.arena[off:off + n], non_blocking=True)
+        v = self._slot_views[l % 2]
+        Ls = LayerWeights(L.in_norm, L.post_norm, L.q_norm, L.k_norm, v["qkv_Wq"], L.qkv_scale, v["o_Wq"], L.o_scale,
+                          v.get("gu_Wq", L.gu_Wq), L.gu_scale, v.get("down_Wq", L.down_Wq), L.down_scale,
+                          L.down_T_Wq, L.down_T_scale)
+        gu = (v["gu_il"], self.gu_il[l][1]) if "gu_il" in v else None
+        return Ls, gu
 
     # ---- one layer ----
     def _mlp(self, l: int, L: LayerWeights):
@@ -324,6 +384,7 @@ class DecodeEngine:
         H, gs = c.hidden, c.group_size
         _C.embed_lookup_into(self.w.embed, self.token, self.x)
         for l, L in enumerate(self.w.layers):
+            L, _ = self._layer(l, L)
             if l == 0:
                 _C.rmsnorm_into(self.x, L.in_norm, self.h, eps)
             else:
@@ -347,6 +408,7 @@ class DecodeEngine:
         cur, other = self.x, self.x2
         _C.embed_lookup_into(self.w.embed, self.token, cur)
         for l, L in enumerate(self.w.layers):
+            L, gu_il = self._layer(l, L)
             if l == 0:
                 _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, None, L.in_norm, eps, None, None, self.qkv,
                                            H, gs, False)
@@ -364,7 +426,7 @@ class DecodeEngine:
                 _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
             if self.mode == "dense":
-                gW, gS = self.gu_il[l]
+                gW, gS = gu_il
                 _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, None, self.mlp_h, H, gs,
                                            True)
                 cur, other = other, cur
@@ -372,7 +434,7 @@ class DecodeEngine:
                 continue
             gate = self.gu[:I]
             if self.dip_dense_up:
-                gW, gS = self.gu_il[l]
+                gW, gS = gu_il
                 _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
                                                    H, gs)
                 cur, other = other, cur

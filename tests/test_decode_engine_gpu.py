@@ -131,6 +131,34 @@ def test_dip_dense_up_schedule_bit_identical(dec, tiny, fused):
         assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_offloaded_dense_weights_bit_identical(dec, fused):
+    """Dense weights streamed per layer from the pinned arena into two device slots (the reference's streamed
+    configuration) give the resident engine's tokens and hidden state bit for bit: dense, DIP with every selected
+    row read from host memory (empty caches), and cache-aware DIP; eager and graph replays. Three layers, so a
+    slot is reused within a step."""
+    tiny = dec.random_decoder(dec.DecoderConfig(**{**TINY, "layers": 3}), seed=4, linear_std=0.05, norm_jitter=0.1)
+    cfg = tiny.config
+    k = cfg.intermediate // 2
+    prompt = prompt_ids(6, cfg.vocab, seed=21)
+    dense = dec.DecodeEngine(tiny, "dense", max_new_tokens=6, fused=fused)
+    want_dense = dense.generate(prompt, 6, use_graph=True)
+    dip = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
+    want_dip = dip.generate(prompt, 6, use_graph=True)
+    hot = [list(range(0, cfg.intermediate, 4)) for _ in range(cfg.layers)]
+    cases = (("dense", dense, want_dense, dict()),
+             ("dip_offload", dip, want_dip, dict(dip_k=k, hot_channels=[[] for _ in range(cfg.layers)])),
+             ("cached_offload", dip, want_dip, dict(dip_k=k, hot_channels=hot)))
+    for name, ref, want, kw in cases:
+        mode = "dense" if name == "dense" else "cached_dip"
+        eng = dec.DecodeEngine(tiny, mode, max_new_tokens=6, fused=fused, offload=True, **kw)
+        assert eng.wstore.bytes_used == eng.wstore.bytes_total and eng.wstore.arena.is_pinned()
+        for use_graph in (False, True, True):
+            assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"{name} graph={use_graph}"
+            assert torch.equal(eng.x_final, ref.x_final), f"{name} graph={use_graph}: hidden state differs"
+            _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+
+
 def test_engine_rejects_bad_arguments(dec, tiny):
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "dense", dip_dense_up=True)
@@ -142,6 +170,8 @@ def test_engine_rejects_bad_arguments(dec, tiny):
         dec.DecodeEngine(tiny, "cached_dip", dip_k=8, hot_channels=[[]])  # one list per layer
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "dip", dip_k=8, miss_path="zero_copy")
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dip", dip_k=8, offload=True)  # DIP offload = cached_dip with empty caches
     eng = dec.DecodeEngine(tiny, "dense", max_new_tokens=4)
     with pytest.raises(ValueError):
         eng.generate(prompt_ids(10, tiny.config.vocab), 60)  # longer than max_seq
