@@ -222,7 +222,7 @@ __global__ __launch_bounds__(64) void gemv_f16_kernel(const uint16_t* __restrict
             const bool ok = FULL || c < chunks;
             xv[p] = ldg(ok ? x4 + c : z);
 #pragma unroll
-            for (int r = 0; r < R; ++r) wv[p][r] = ldg(ok ? wr[r] + c : z);
+            for (int r = 0; r < R; ++r) wv[p][r] = ldg_stream(ok ? wr[r] + c : z);
         }
 #pragma unroll
         for (int p = 0; p < PU; ++p) {

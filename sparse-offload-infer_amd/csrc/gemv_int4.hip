@@ -49,7 +49,7 @@ __device__ __forceinline__ void load_w_chunk(const uint8_t* __restrict__ row, bo
     if (VEC) {
         const u32x4* p = reinterpret_cast<const u32x4*>(row) + c;
         if (!FULL) p = ok ? p : reinterpret_cast<const u32x4*>(z);
-        const u32x4 t = ldg(p);
+        const u32x4 t = ldg_stream(p);  // weights are read once: non-temporal
         wv[0] = t.x;
         wv[1] = t.y;
         wv[2] = t.z;

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(64) void gemv_int8_kernel(const int8_t* __restrict_
             for (int r = 0; r < R; ++r) {
                 if (VEC) {
                     const u32x4* q = reinterpret_cast<const u32x4*>(wr[r]) + c;
-                    const u32x4 t = ldg(cv ? q : reinterpret_cast<const u32x4*>(zw));
+                    const u32x4 t = ldg_stream(cv ? q : reinterpret_cast<const u32x4*>(zw));
                     wv[p][r][0] = t.x;
                     wv[p][r][1] = t.y;
                     wv[p][r][2] = t.z;
