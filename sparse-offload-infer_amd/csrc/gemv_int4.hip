@@ -586,17 +586,19 @@ struct Int4Plan {
     int R, PU;
 };
 
-// PU: passes per batch (all of them up to 4); R: rows per wave, so that a
-// wave has R*PU <= 8 row segments in flight and the grid keeps >= ~1024 waves.
+// PU: passes per batch (all of them up to 4); R: rows per wave, 8 for a
+// one-pass tile over >= 4096 rows, else 2 from 2048 rows, else 1. Swept on
+// single cold launches of the Qwen3-1.7B shapes: 4-row tiles were slower than
+// both 8- and 2-row tiles at every shape (gate/up 6144x2048: 3.39 / 3.93 /
+// 3.53 us for 8 / 4 / 2 rows), and more than 8 row segments in flight per
+// wave did not pay.
 static Int4Plan plan_int4(int64_t N, int64_t K, bool vec) {
     const int64_t chunks = ceil_div64(ceil_div64(K, 8), 4);
     const int64_t passes = ceil_div64(chunks, kWave);
     Int4Plan p{1, 1};
     p.PU = vec ? static_cast<int>(passes < 4 ? passes : 4) : 1;
     if (p.PU == 3 && passes > 3) p.PU = 4;
-    int R = N >= 8 * 1024 ? 8 : N >= 4 * 1024 ? 4 : N >= 2 * 1024 ? 2 : 1;
-    while (R * p.PU > 8) R >>= 1;
-    p.R = R < 1 ? 1 : R;
+    p.R = (N >= 4 * 1024 && p.PU == 1) ? 8 : N >= 2 * 1024 ? 2 : 1;
     return p;
 }
 
@@ -620,10 +622,8 @@ static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP&
     if (vec) {
         switch (key) {
             case 81: SOI_CS(8, 1, true); break;
-            case 41: SOI_CS(4, 1, true); break;
             case 21: SOI_CS(2, 1, true); break;
             case 11: SOI_CS(1, 1, true); break;
-            case 42: SOI_CS(4, 2, true); break;
             case 22: SOI_CS(2, 2, true); break;
             case 12: SOI_CS(1, 2, true); break;
             case 23: SOI_CS(2, 3, true); break;
@@ -634,7 +634,6 @@ static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP&
     } else {
         switch (pl.R) {
             case 8: SOI_CS(8, 1, false); break;
-            case 4: SOI_CS(4, 1, false); break;
             case 2: SOI_CS(2, 1, false); break;
             default: SOI_CS(1, 1, false); break;
         }
@@ -668,10 +667,8 @@ static int launch_int4_batched(const uint8_t* const* Wp, const float* const* Sp,
     if (vec) {
         switch (key) {
             case 81: SOI_BCS(8, 1, true); break;
-            case 41: SOI_BCS(4, 1, true); break;
             case 21: SOI_BCS(2, 1, true); break;
             case 11: SOI_BCS(1, 1, true); break;
-            case 42: SOI_BCS(4, 2, true); break;
             case 22: SOI_BCS(2, 2, true); break;
             case 12: SOI_BCS(1, 2, true); break;
             case 23: SOI_BCS(2, 3, true); break;
@@ -682,7 +679,6 @@ static int launch_int4_batched(const uint8_t* const* Wp, const float* const* Sp,
     } else {
         switch (pl.R) {
             case 8: SOI_BCS(8, 1, false); break;
-            case 4: SOI_BCS(4, 1, false); break;
             case 2: SOI_BCS(2, 1, false); break;
             default: SOI_BCS(1, 1, false); break;
         }
