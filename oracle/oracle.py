@@ -56,6 +56,7 @@ def _declare(L):
     L.soi_ref_unpack_int4.argtypes = [_p, _i64, _i64, _p]
     L.soi_ref_gemv_w4_f64.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _p]
     L.soi_ref_gemv_w4_f32.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _p]
+    L.soi_ref_gemv_w4_f64_mt.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _p, C.c_int]
     L.soi_ref_dequant_int4.argtypes = [_p, _p, _i64, _i64, _i64, _i64, _p]
     L.soi_ref_gemv_w8_f64.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _p]
     L.soi_ref_topk_tau_rule_a.restype = C.c_float
@@ -166,13 +167,18 @@ def dequant_int4(Wq: np.ndarray, scale: np.ndarray, K: int, group_size: int) -> 
 # R4/R5: dense GEMVs
 # --------------------------------------------------------------------------
 
-def gemv_w4_f64(Wq: np.ndarray, scale: np.ndarray, x: np.ndarray, K: int, group_size: int) -> np.ndarray:
-    """y = dequant(Wq, scale) @ x in binary64 (gemv_w4a16_group.cu:23-127 arithmetic)."""
+def gemv_w4_f64(Wq: np.ndarray, scale: np.ndarray, x: np.ndarray, K: int, group_size: int,
+                threads: int = 1) -> np.ndarray:
+    """y = dequant(Wq, scale) @ x in binary64 (gemv_w4a16_group.cu:23-127 arithmetic). threads > 1 splits the rows
+    over POSIX threads (same result: each row is summed by one thread in ascending k)."""
     Wq, scale = _c(Wq, np.uint8), _c(scale, np.float32)
     xb = _c(x, np.float16).view(np.uint16)
     N, G = scale.shape
     y = np.empty(N, np.float64)
-    lib().soi_ref_gemv_w4_f64(_ptr(Wq), _ptr(scale), _ptr(xb), N, K, group_size, G, _ptr(y))
+    if threads > 1:
+        lib().soi_ref_gemv_w4_f64_mt(_ptr(Wq), _ptr(scale), _ptr(xb), N, K, group_size, G, _ptr(y), threads)
+    else:
+        lib().soi_ref_gemv_w4_f64(_ptr(Wq), _ptr(scale), _ptr(xb), N, K, group_size, G, _ptr(y))
     return y
 
 
@@ -291,7 +297,7 @@ def decode_attention_f64(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray
 
 
 def threads_used() -> int:
-    """The oracle is single-threaded scalar C."""
+    """The oracle is scalar C; every function runs on one thread except gemv_w4_f64 with threads > 1."""
     return 1
 
 

@@ -18,6 +18,7 @@
 #include <fenv.h>
 #include <float.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -256,6 +257,43 @@ EXPORT void soi_ref_gemv_w4_f64(const uint8_t* Wq, const float* scale, const uin
         y[n] = acc;
     }
     free(xf);
+}
+
+/* The same GEMV with its rows split over `threads` POSIX threads (contiguous row ranges). Every row is
+ * still summed in ascending k by one thread, so the output equals soi_ref_gemv_w4_f64 exactly; this form
+ * exists only to time the CPU baseline on several host cores. */
+typedef struct {
+    const uint8_t* Wq;
+    const float* scale;
+    const uint16_t* x;
+    int64_t n0, n1, K, gs, G;
+    double* y;
+} soi_gemv_w4_job;
+
+static void* soi_gemv_w4_worker(void* arg) {
+    const soi_gemv_w4_job* j = (const soi_gemv_w4_job*)arg;
+    const int64_t row_bytes = ((j->K + 7) / 8) * 4;
+    soi_ref_gemv_w4_f64(j->Wq + j->n0 * row_bytes, j->scale + j->n0 * j->G, j->x, j->n1 - j->n0, j->K, j->gs, j->G,
+                        j->y + j->n0);
+    return NULL;
+}
+
+EXPORT void soi_ref_gemv_w4_f64_mt(const uint8_t* Wq, const float* scale, const uint16_t* x, int64_t N, int64_t K,
+                                   int64_t gs, int64_t G, double* y, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    if ((int64_t)threads > N) threads = (int)(N > 0 ? N : 1);
+    pthread_t tid[64];
+    soi_gemv_w4_job job[64];
+    for (int t = 0; t < threads; ++t) {
+        job[t] = (soi_gemv_w4_job){Wq, scale, x, N * t / threads, N * (t + 1) / threads, K, gs, G, y};
+    }
+    int started = 0;
+    for (int t = 1; t < threads; ++t, ++started)
+        if (pthread_create(&tid[t], NULL, soi_gemv_w4_worker, &job[t]) != 0) break;
+    soi_gemv_w4_worker(&job[0]);
+    for (int t = 1; t <= started; ++t) pthread_join(tid[t], NULL);
+    for (int t = started + 1; t < threads; ++t) soi_gemv_w4_worker(&job[t]); /* threads that failed to start */
 }
 
 EXPORT void soi_ref_gemv_w4_f32(const uint8_t* Wq, const float* scale, const uint16_t* x, int64_t N, int64_t K,

@@ -363,3 +363,15 @@ def test_decoder_oracle_gemv_f16():
     x = np.random.default_rng(5).standard_normal(96).astype(np.float16)
     ref = W.astype(np.float64) @ x.astype(np.float64)
     assert np.allclose(OD.gemv_f16(W, x).astype(np.float64), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_threaded_gemv_equals_single_thread():
+    """The row-split form used for the multi-core CPU baseline gives the single-thread result exactly (each row is
+    still summed by one thread in ascending k), including more threads than rows."""
+    r = np.random.default_rng(12)
+    for N, K, threads in ((37, 96, 8), (3, 256, 8), (1000, 2048, 5)):
+        q = r.integers(-8, 8, (N, K)).astype(np.int8)
+        Wq = O.pack_int4(q)
+        s = r.random((N, -(-K // 32)), dtype=np.float32)
+        x = r.standard_normal(K).astype(np.float16)
+        assert np.array_equal(O.gemv_w4_f64(Wq, s, x, K, 32, threads=threads), O.gemv_w4_f64(Wq, s, x, K, 32))
