@@ -404,8 +404,17 @@ int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* sc
  * gather_rows_staged of the misses, then gemv_dip_fused_up / _down).
  *   soi_gemv_dip_cached_up: y[k] = rows @ x.
  *   soi_gemv_dip_cached_up_silu: h_sel[j] = fp16(silu(gate[sel[j]]) * fp16(row_j . x)).
+ *     With copy_src / copy_dst (both or neither): the same waves also copy,
+ *     for every miss j, row sel[j] of copy_src ([num_channels,
+ *     copy_row_bytes], e.g. the pinned down^T matrix) to row j of copy_dst
+ *     (device staging [k, copy_row_bytes]); copy_row_bytes a multiple of 16,
+ *     at most 4096, both 16-byte aligned. The copy's loads are issued before
+ *     the GEMV's, so the down^T misses cross PCIe as whole-row reads while
+ *     the up rows stream; rows of hits are not written.
  *   soi_gemv_dip_cached_down: y[H] = sum_j h_sel[j] * row_j (rows of down^T);
- *     workspace rules of soi_gemv_w4a16_sparse_accumulate.
+ *     a miss reads row j of staging_Wq when it is given (as filled by the
+ *     copy above), else row sel[j] of full_Wq in place; scales always from
+ *     full_scale. Workspace rules of soi_gemv_w4a16_sparse_accumulate.
  * ------------------------------------------------------------------------ */
 int soi_gemv_dip_cached_up(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
                            const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
@@ -415,12 +424,13 @@ int soi_gemv_dip_cached_up_silu(const uint8_t* cache_Wq, const float* cache_scal
                                 const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
                                 const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x,
                                 const uint16_t* gate, uint16_t* h_sel, int64_t K, int64_t group_size,
-                                int64_t num_groups, void* stream);
+                                int64_t num_groups, const uint8_t* copy_src, int64_t copy_row_bytes,
+                                uint8_t* copy_dst, void* stream);
 int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
                              const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
                              const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* h_sel,
-                             uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups, void* workspace,
-                             size_t workspace_bytes, void* stream);
+                             uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups,
+                             const uint8_t* staging_Wq, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1180,7 +1180,8 @@ void gemv_dip_cached_up_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, 
 
 void gemv_dip_cached_up_silu_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor full_Wq,
                                   torch::Tensor full_scale, torch::Tensor slot_of, torch::Tensor sel, torch::Tensor x,
-                                  torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
+                                  torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size,
+                                  c10::optional<torch::Tensor> copy_src, c10::optional<torch::Tensor> copy_dst) {
     const char* n = "gemv_dip_cached_up_silu_into";
     const CachedArgs a = check_cached_common(cache_Wq, cache_scale, full_Wq, full_scale, slot_of, sel, K, n);
     need(x, torch::kFloat16, sel, n, "x");
@@ -1188,29 +1189,53 @@ void gemv_dip_cached_up_silu_into(torch::Tensor cache_Wq, torch::Tensor cache_sc
     need(h_sel, torch::kFloat16, sel, n, "h_sel");
     TORCH_CHECK(x.numel() == K && h_sel.numel() == sel.numel() && gate.numel() == a.num_channels, n,
                 ": shape mismatch");
+    TORCH_CHECK(copy_src.has_value() == copy_dst.has_value(), n, ": copy_src and copy_dst go together");
+    const uint8_t* csrc = nullptr;
+    uint8_t* cdst = nullptr;
+    int64_t crow = 0;
+    if (copy_src.has_value()) {
+        const torch::Tensor& cd = *copy_dst;
+        crow = copy_src->dim() == 2 ? copy_src->size(1) : -1;
+        TORCH_CHECK(crow > 0 && copy_src->size(0) == a.num_channels, n,
+                    "(copy_src): must be 2D with one row per channel");
+        csrc = readable_rows(*copy_src, crow, sel, n);
+        need(cd, torch::kUInt8, sel, n, "copy_dst");
+        TORCH_CHECK(cd.dim() == 2 && cd.size(0) >= sel.numel() && cd.size(1) == crow, n,
+                    "(copy_dst): must be [>= k, copy row bytes]");
+        cdst = cd.data_ptr<uint8_t>();
+    }
     const at::DeviceGuard guard(x.device());
     check_status(soi_gemv_dip_cached_up_silu(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(),
                                              a.cache_rows, a.full, full_scale.data_ptr<float>(), a.num_channels,
                                              slot_of.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), sel.numel(),
-                                             h16(x), h16(gate), h16m(h_sel), K, group_size, cache_scale.size(1),
-                                             cur_stream(x)),
+                                             h16(x), h16(gate), h16m(h_sel), K, group_size, cache_scale.size(1), csrc,
+                                             crow, cdst, cur_stream(x)),
                  n);
 }
 
 void gemv_dip_cached_down_into(torch::Tensor cache_Wq, torch::Tensor cache_scale, torch::Tensor full_Wq,
                                torch::Tensor full_scale, torch::Tensor slot_of, torch::Tensor sel, torch::Tensor h_sel,
-                               torch::Tensor y, int64_t H, int64_t group_size, torch::Tensor workspace_buf) {
+                               torch::Tensor y, int64_t H, int64_t group_size, torch::Tensor workspace_buf,
+                               c10::optional<torch::Tensor> staging_Wq) {
     const char* n = "gemv_dip_cached_down_into";
     const CachedArgs a = check_cached_common(cache_Wq, cache_scale, full_Wq, full_scale, slot_of, sel, H, n);
     need(h_sel, torch::kFloat16, sel, n, "h_sel");
     need(y, torch::kFloat16, sel, n, "y");
     need(workspace_buf, torch::kUInt8, sel, n, "workspace");
     TORCH_CHECK(h_sel.numel() == sel.numel() && y.numel() == H, n, ": h_sel / y shape mismatch");
+    const uint8_t* stg_p = nullptr;
+    if (staging_Wq.has_value()) {
+        const torch::Tensor& st = *staging_Wq;
+        need(st, torch::kUInt8, sel, n, "staging_Wq");
+        TORCH_CHECK(st.dim() == 2 && st.size(0) >= sel.numel() && st.size(1) == full_Wq.size(1), n,
+                    "(staging_Wq): must be [>= k, row bytes]");
+        stg_p = st.data_ptr<uint8_t>();
+    }
     const at::DeviceGuard guard(h_sel.device());
     check_status(soi_gemv_dip_cached_down(cache_Wq.data_ptr<uint8_t>(), cache_scale.data_ptr<float>(), a.cache_rows,
                                           a.full, full_scale.data_ptr<float>(), a.num_channels,
                                           slot_of.data_ptr<int32_t>(), sel.data_ptr<int32_t>(), sel.numel(),
-                                          h16(h_sel), h16m(y), H, group_size, cache_scale.size(1),
+                                          h16(h_sel), h16m(y), H, group_size, cache_scale.size(1), stg_p,
                                           workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(h_sel)),
                  n);
 }
@@ -1277,7 +1302,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");
     m.def("gemv_dip_cached_up_into", &gemv_dip_cached_up_into, "hot-cache up GEMV, misses read in place");
     m.def("gemv_dip_cached_up_silu_into", &gemv_dip_cached_up_silu_into,
-          "hot-cache up GEMV with SiLU gating, misses read in place");
-    m.def("gemv_dip_cached_down_into", &gemv_dip_cached_down_into, "hot-cache down accumulate, misses read in place");
+          "hot-cache up GEMV with SiLU gating, misses read in place (optionally copying the down^T miss rows)",
+          py::arg("cache_Wq"), py::arg("cache_scale"), py::arg("full_Wq"), py::arg("full_scale"), py::arg("slot_of"),
+          py::arg("sel"), py::arg("x"), py::arg("gate"), py::arg("h_sel"), py::arg("K"), py::arg("group_size"),
+          py::arg("copy_src") = py::none(), py::arg("copy_dst") = py::none());
+    m.def("gemv_dip_cached_down_into", &gemv_dip_cached_down_into,
+          "hot-cache down accumulate, misses read in place or from staging", py::arg("cache_Wq"),
+          py::arg("cache_scale"), py::arg("full_Wq"), py::arg("full_scale"), py::arg("slot_of"), py::arg("sel"),
+          py::arg("h_sel"), py::arg("y"), py::arg("H"), py::arg("group_size"), py::arg("workspace"),
+          py::arg("staging_Wq") = py::none());
     m.def("version", []() { return std::string(soi_version()); });
 }

@@ -338,11 +338,68 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
     }
 }
 
-template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY>
+// Side copies done by a GEMV's waves for their own rows. NoCopy: none.
+// MissCopy<CH>: for each row j of the wave's tile whose channel c = sel[j] is
+// not in the hot cache (slot_of[c] < 0), row c of src (row_bytes, typically
+// pinned host memory read in place) is copied to row j of dst (device
+// staging). The copy's loads (CH 16-byte chunks per lane per row: rows up to
+// CH KB) are issued before the GEMV's, so both round trips overlap, and every
+// row crosses PCIe as whole 1 KB wave reads.
+struct NoCopy {
+    static constexpr int kChunks = 0;
+};
+
+template <int CH>
+struct MissCopy {
+    static constexpr int kChunks = CH;
+    const int32_t* sel;
+    const int32_t* slot_of;
+    int64_t num_channels;
+    const uint8_t* src;
+    uint8_t* dst;
+    int64_t row_bytes;  // multiple of 16, at most CH * 1024
+    __device__ __forceinline__ int32_t miss_channel(int64_t j) const {
+        const int32_t c = ldg(sel + j);
+        return (c >= 0 && c < num_channels && ldg(slot_of + c) < 0) ? c : -1;
+    }
+};
+
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY,
+          class CP = NoCopy>
 __global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x, EP ep,
-                                                       int K, int gs) {
-    gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, PlainX{x}, ep, K, gs,
-                                                           static_cast<int64_t>(blockIdx.x) * R);
+                                                       int K, int gs, CP cp = CP{}) {
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+    if constexpr (CP::kChunks > 0) {
+        constexpr int CH = CP::kChunks;
+        const int lane = threadIdx.x;
+        const int64_t nchunks = cp.row_bytes >> 4;
+        const u32x4* z = reinterpret_cast<const u32x4*>(g_zero16);
+        u32x4 buf[R][CH];
+        int32_t ch[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ch[r] = (row0 + r < N) ? cp.miss_channel(row0 + r) : -1;
+            const u32x4* src =
+                reinterpret_cast<const u32x4*>(cp.src + static_cast<int64_t>(ch[r] >= 0 ? ch[r] : 0) * cp.row_bytes);
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int64_t c = lane + 64 * i;
+                buf[r][i] = ldg_stream((ch[r] >= 0 && c < nchunks) ? src + c : z);
+            }
+        }
+        gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, PlainX{x}, ep, K, gs, row0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            u32x4* dst = reinterpret_cast<u32x4*>(cp.dst + (row0 + r) * cp.row_bytes);
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int64_t c = lane + 64 * i;
+                if (ch[r] >= 0 && c < nchunks) stg(dst + c, buf[r][i]);
+            }
+        }
+    } else {
+        gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, PlainX{x}, ep, K, gs, row0);
+    }
 }
 
 // Batched form: P independent problems of one shape [N, K]; workgroup b takes
@@ -602,9 +659,9 @@ static Int4Plan plan_int4(int64_t N, int64_t K, bool vec) {
     return p;
 }
 
-template <bool BITFIELD, class Rows, class EP = StoreY>
+template <bool BITFIELD, class Rows, class EP = StoreY, class CP = NoCopy>
 static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP& ep, int64_t K, int64_t gs, bool vec,
-                       hipStream_t st, const char* what) {
+                       hipStream_t st, const char* what, const CP& cp = CP{}) {
     if (N == 0) return SOI_OK;
     const Int4Plan pl = plan_int4(N, K, vec);
     const bool cs = (gs % 32) == 0;
@@ -612,8 +669,8 @@ static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP&
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
     const int Ki = static_cast<int>(K), gi = static_cast<int>(gs);
 #define SOI_L(RR, PP, V, CS, FL)                                                                                \
-    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows, EP>), grid, dim3(64), 0, st, rows, N, x, ep, \
-                       Ki, gi)
+    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows, EP, CP>), grid, dim3(64), 0, st, rows, N, x, \
+                       ep, Ki, gi, cp)
 #define SOI_CS(RR, PP, V)                    \
     if (V && full) SOI_L(RR, PP, V, true, true); \
     else if (cs) SOI_L(RR, PP, V, true, false);  \
@@ -983,19 +1040,33 @@ extern "C" int soi_gemv_dip_cached_up_silu(const uint8_t* cache_Wq, const float*
                                            const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
                                            const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* x,
                                            const uint16_t* gate, uint16_t* h_sel, int64_t K, int64_t group_size,
-                                           int64_t num_groups, void* stream) {
+                                           int64_t num_groups, const uint8_t* copy_src, int64_t copy_row_bytes,
+                                           uint8_t* copy_dst, void* stream) {
     const char* what = "soi_gemv_dip_cached_up_silu";
     int st = check_int4_common(K, group_size, num_groups, what);
     if (st) return st;
     st = check_cached(cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, slot_of, sel, k, what);
     if (st || k == 0) return st;
     SOI_REQUIRE(x && gate && h_sel, "%s: null pointer", what);
+    SOI_REQUIRE((copy_src == nullptr) == (copy_dst == nullptr), "%s: copy_src and copy_dst go together", what);
     const int64_t row_bytes = ceil_div64(K, 8) * 4;
     const bool vec = (K % 32 == 0) && aligned16(x) && aligned16(full_Wq) && (cache_rows == 0 || aligned16(cache_Wq));
     SlotRows rows{cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, sel, slot_of, row_bytes,
                   num_groups};
-    return launch_int4<true>(rows, k, x, SiluIdxY{h_sel, gate, sel, static_cast<int>(num_channels)}, K, group_size,
-                             vec, as_stream(stream), what);
+    const SiluIdxY ep{h_sel, gate, sel, static_cast<int>(num_channels)};
+    hipStream_t s = as_stream(stream);
+    if (!copy_src) return launch_int4<true>(rows, k, x, ep, K, group_size, vec, s, what);
+    SOI_REQUIRE(copy_row_bytes > 0 && copy_row_bytes % 16 == 0 && copy_row_bytes <= 4096 && aligned16(copy_src) &&
+                    aligned16(copy_dst),
+                "%s: copied rows must be 16-byte aligned, a multiple of 16 bytes and at most 4096 bytes", what);
+    if (copy_row_bytes <= 1024)
+        return launch_int4<true>(rows, k, x, ep, K, group_size, vec, s, what,
+                                 MissCopy<1>{sel, slot_of, num_channels, copy_src, copy_dst, copy_row_bytes});
+    if (copy_row_bytes <= 2048)
+        return launch_int4<true>(rows, k, x, ep, K, group_size, vec, s, what,
+                                 MissCopy<2>{sel, slot_of, num_channels, copy_src, copy_dst, copy_row_bytes});
+    return launch_int4<true>(rows, k, x, ep, K, group_size, vec, s, what,
+                             MissCopy<4>{sel, slot_of, num_channels, copy_src, copy_dst, copy_row_bytes});
 }
 
 extern "C" int soi_gemv_dip_fused_up_silu(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,

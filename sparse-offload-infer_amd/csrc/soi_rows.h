@@ -76,6 +76,31 @@ struct SlotRows {
     }
 };
 
+// SlotRows with the misses already copied to staging row j (device memory):
+// a miss reads row j of stW, its scales still come from row ch of fS.
+struct SlotStageRows {
+    const uint8_t* cW;
+    const float* cS;
+    int64_t cN;
+    const uint8_t* stW;
+    const float* fS;
+    int64_t fN;
+    const int32_t* idx;
+    const int32_t* slot_of;
+    int64_t row_bytes;
+    int64_t G;
+    __device__ __forceinline__ RowRef get(int64_t j) const {
+        const int32_t ch = idx[j];
+        if (ch < 0 || ch >= fN) return {nullptr, nullptr, false};
+        const int32_t s = slot_of[ch];
+        if (s >= 0) {
+            if (s < cN) return {cW + static_cast<int64_t>(s) * row_bytes, cS + static_cast<int64_t>(s) * G, true};
+            return {nullptr, nullptr, false};
+        }
+        return {stW + j * row_bytes, fS + static_cast<int64_t>(ch) * G, true};
+    }
+};
+
 // row j = row idx[j] of a resident [num_rows, row_bytes] matrix
 struct IndexRows {
     const uint8_t* W;

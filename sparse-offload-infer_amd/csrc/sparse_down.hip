@@ -299,21 +299,30 @@ extern "C" int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* ca
                                         const uint8_t* full_Wq, const float* full_scale, int64_t num_channels,
                                         const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* h_sel,
                                         uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups,
-                                        void* workspace, size_t workspace_bytes, void* stream) {
+                                        const uint8_t* staging_Wq, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
     const char* what = "soi_gemv_dip_cached_down";
     int s = check_down(H, k, group_size, num_groups, what);
     if (s) return s;
     SOI_REQUIRE(cache_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
                 "%s: negative or too large row / channel count", what);
-    SOI_REQUIRE(y && (k == 0 || (sel && slot_of && full_Wq && full_scale && h_sel)), "%s: null pointer", what);
+    SOI_REQUIRE(y && (k == 0 || (sel && slot_of && (full_Wq || staging_Wq) && full_scale && h_sel)),
+                "%s: null pointer", what);
     SOI_REQUIRE(k == 0 || cache_rows == 0 || (cache_Wq && cache_scale), "%s: null cache", what);
     const int64_t row_bytes = ceil_div64(H, 8) * 4;
-    const bool vec = (row_bytes % 16 == 0) && (k == 0 || aligned16(full_Wq)) &&
+    const uint8_t* miss_src = staging_Wq ? staging_Wq : full_Wq;
+    const bool vec = (row_bytes % 16 == 0) && (k == 0 || aligned16(miss_src)) &&
                      (cache_rows == 0 || aligned16(cache_Wq));
+    hipStream_t st = as_stream(stream);
+    if (staging_Wq) {
+        SlotStageRows rows{cache_Wq, cache_scale, cache_rows, staging_Wq, full_scale, num_channels, sel, slot_of,
+                           row_bytes, num_groups};
+        return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes, st,
+                                  what);
+    }
     SlotRows rows{cache_Wq, cache_scale, cache_rows, full_Wq, full_scale, num_channels, sel, slot_of, row_bytes,
                   num_groups};
-    return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
-                              as_stream(stream), what);
+    return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes, st, what);
 }
 
 extern "C" int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,

@@ -160,7 +160,8 @@ class DecodeEngine:
 
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
-                 dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False):
+                 dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
+                 down_copy: bool = True):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         if offload and mode == "dip":
@@ -169,6 +170,9 @@ class DecodeEngine:
         if miss_path not in ("direct", "staged"):
             raise ValueError(f"unknown miss_path {miss_path!r}")
         self.miss_path = miss_path
+        # direct path, fused layers: the up GEMV also copies the down^T miss rows to staging (False: the down
+        # accumulate reads them in place)
+        self.down_copy = down_copy
         if dip_dense_up and mode != "dip":
             raise ValueError("dip_dense_up applies to mode 'dip' (weights resident)")
         # DIP schedule for resident weights: gate and up of every channel in one launch, top-k on gate, then the
@@ -460,10 +464,14 @@ class DecodeEngine:
                 continue
             cache = self.caches[l]
             if self.miss_path == "direct":
+                # the up GEMV's waves also copy their down^T miss rows to staging (whole-row PCIe reads, overlapped
+                # with the up rows); the down accumulate then reads hits from the cache and misses from staging
+                cp = (self.host_down[l], self.st_dn) if self.down_copy else (None, None)
                 _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of,
-                                                self.idx, self.h, gate, self.h_sel, H, gs)
+                                                self.idx, self.h, gate, self.h_sel, H, gs, *cp)
                 _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
-                                             cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws)
+                                             cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws,
+                                             self.st_dn if self.down_copy else None)
                 continue
             self._fetch_misses(l, L, uS)
             _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc,

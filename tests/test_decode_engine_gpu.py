@@ -114,6 +114,11 @@ def test_cached_dip_bit_identical_to_dip(dec, tiny, fused, miss_path):
             got = eng.generate(prompt, 6, use_graph=use_graph)
             assert got == want, f"cache {name} graph={use_graph}"
             assert torch.equal(eng.x_final, plain.x_final), f"cache {name} graph={use_graph}: hidden state differs"
+        if miss_path == "direct" and fused:  # down^T misses read in place instead of copied by the up GEMV
+            eng = dec.DecodeEngine(tiny, "cached_dip", dip_k=k, hot_channels=hot, max_new_tokens=6, fused=fused,
+                                   down_copy=False)
+            assert eng.generate(prompt, 6, use_graph=True) == want, f"cache {name} in-place down"
+            assert torch.equal(eng.x_final, plain.x_final)
 
 
 @pytest.mark.parametrize("fused", [True, False])

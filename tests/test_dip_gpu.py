@@ -375,6 +375,21 @@ def test_cached_direct_equals_staged_and_resident(ops, C, source):
     _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, full_dn, w.down_T_scale, cache.slot_of, idx, h, y,
                                  H, gs, ws)
     assert torch.equal(y, y_ref), "cached down differs from the descriptor form"
+    # the up GEMV copying the down^T miss rows to staging: same h; staging row j = down^T row sel[j] for every miss
+    # (hit rows untouched); the down accumulate reading misses from that staging gives the same y
+    stage = torch.full((k, w.down_T_Wq.shape[1]), 0xAB, dtype=torch.uint8, device="cuda")
+    h2 = torch.empty(k, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, full_up, w.up_scale, cache.slot_of, idx, x, gate,
+                                    h2, H, gs, full_dn, stage)
+    assert torch.equal(h2, h_ref), "cached up + SiLU with the miss copy differs"
+    is_miss = cache.slot_of[idx.long()] < 0
+    assert int(is_miss.sum()) == mc
+    assert torch.equal(stage[is_miss], w.down_T_Wq[idx.long()[is_miss]]), "staged miss rows differ"
+    assert bool((stage[~is_miss] == 0xAB).all()), "hit rows of the staging buffer were written"
+    y2 = torch.empty(H, dtype=torch.float16, device="cuda")
+    _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, full_dn, w.down_T_scale, cache.slot_of, idx, h, y2,
+                                 H, gs, ws, stage)
+    assert torch.equal(y2, y_ref), "cached down from the copied staging differs"
     # and the whole MLP equals resident DIP
     y_mlp, idx_mlp = dip.cached_dip_mlp_direct(w, cache, x, k, full_up, full_dn)
     y_res, idx_res = dip.dip_mlp(w, x, k)
@@ -415,6 +430,15 @@ def test_cached_direct_edge_cases_and_rejections(ops):
     with pytest.raises(RuntimeError):  # scale groups differ between cache and full matrix
         _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, w.up_Wq, w.up_scale[:, :8].contiguous(),
                                    cache.slot_of, sel, x, u, H, gs)
+    with pytest.raises(RuntimeError):  # copy destination without a source
+        _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, w.up_Wq, w.up_scale, cache.slot_of, sel, x,
+                                        torch.zeros(I, dtype=torch.float16, device="cuda"), u, H, gs, None,
+                                        torch.empty(8, 1024, dtype=torch.uint8, device="cuda"))
+    with pytest.raises(RuntimeError):  # staging narrower than a row
+        _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, w.down_T_Wq, w.down_T_scale, cache.slot_of, sel,
+                                     u, torch.empty(H, dtype=torch.float16, device="cuda"), H, gs,
+                                     torch.zeros(1 << 16, dtype=torch.uint8, device="cuda"),
+                                     torch.empty(8, 512, dtype=torch.uint8, device="cuda"))
     with pytest.raises(RuntimeError):  # workspace too small
         _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, w.down_T_Wq, w.down_T_scale, cache.slot_of, sel,
                                      u, torch.empty(H, dtype=torch.float16, device="cuda"), H, gs, ws)
