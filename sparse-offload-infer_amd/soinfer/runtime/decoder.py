@@ -282,6 +282,9 @@ class DecodeEngine:
 
     def _setup_offload(self):
         blocks = [self._streamed(l, L) for l, L in enumerate(self.w.layers)]
+        shapes0 = [(name, tuple(t.shape)) for name, t in blocks[0]]
+        if any([(name, tuple(t.shape)) for name, t in b] != shapes0 for b in blocks):
+            raise ValueError("offload needs the same streamed matrix shapes in every layer (one slot layout)")
         self.wstore = PinnedWeightStore(plan_bytes(tuple(t.shape) for b in blocks for _, t in b))
         self._blocks = []  # per layer: (arena offset, bytes)
         for l, b in enumerate(blocks):
