@@ -81,6 +81,31 @@ def test_argument_checks_return_before_launch(lib):
     assert gr(None, None, None, None, 0, None, None, None, 128, None) == 0  # nothing to do
 
 
+def test_cached_dip_argument_checks(lib):
+    """The hot-cache GEMVs reject missing sources, half-given copy arguments and oversized copied rows before any
+    launch; k = 0 is a no-op for the up form."""
+    lib.soi_last_error.restype = C.c_char_p
+    i64, vp = C.c_int64, C.c_void_p
+    up = lib.soi_gemv_dip_cached_up_silu
+    up.argtypes = [vp, vp, i64, vp, vp, i64, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp, i64, vp, vp]
+    b = (C.c_uint8 * 4096)()
+    p = C.addressof(b)
+    # k > 0 with a null selection
+    assert up(None, None, 0, p, p, 64, p, None, 8, p, p, p, 2048, 128, 16, None, 0, None, None) == 1
+    # copy destination without a source
+    assert up(None, None, 0, p, p, 64, p, p, 8, p, p, p, 2048, 128, 16, None, 1024, p, None) == 1
+    assert b"copy_src and copy_dst" in lib.soi_last_error()
+    # copied rows over 4096 bytes
+    assert up(None, None, 0, p, p, 64, p, p, 8, p, p, p, 2048, 128, 16, p, 8192, p, None) == 1
+    assert up(None, None, 0, None, None, 64, None, None, 0, None, None, None, 2048, 128, 16, None, 0, None,
+              None) == 0  # k = 0
+    dn = lib.soi_gemv_dip_cached_down
+    dn.argtypes = [vp, vp, i64, vp, vp, i64, vp, vp, i64, vp, vp, i64, i64, i64, vp, vp, C.c_size_t, vp]
+    # neither the full matrix nor staging for the misses
+    assert dn(None, None, 0, None, p, 64, p, p, 8, p, p, 2048, 128, 16, None, p, 4096, None) == 1
+    assert b"null pointer" in lib.soi_last_error()
+
+
 def test_workspace_queries(lib):
     lib.soi_sparse_accumulate_workspace_bytes.restype = C.c_size_t
     lib.soi_sparse_accumulate_workspace_bytes.argtypes = [C.c_int64, C.c_int64]
