@@ -630,6 +630,9 @@ def main() -> int:
     import numpy as np
     import torch
 
+    from __graft_entry__ import ensure_built
+
+    ensure_built()
     import soinfer.ops as ops
 
     dev = torch.device("cuda:0")

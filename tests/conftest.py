@@ -24,16 +24,9 @@ def pytest_configure(config):
 def pytest_sessionstart(session):
     """A fresh checkout has no built libraries (they are not committed): build them in-tree once, before any test
     imports soinfer. An existing build is used as it is."""
-    import importlib.util
+    from __graft_entry__ import ensure_built
 
-    lib_dir = PKG / "soinfer"
-    if (lib_dir / "libsoinfer_hip.so").exists() and any(lib_dir.glob("_C*.so")):
-        return
-    spec = importlib.util.spec_from_file_location("soinfer_build", PKG / "build.py")
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
-    mod.build_hip()
-    mod.build_ext()
+    ensure_built()
 
 
 @pytest.fixture(scope="session")
