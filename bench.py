@@ -571,8 +571,28 @@ def bench_kernels(dev, gen):
                                                                                       else ")"))
         del Ws, Ss
         torch.cuda.empty_cache()
-    return res
 
+    # --- host gathers from pinned memory (R8: the reference's staged vs per-row forms), wall clock incl. sync ---
+    host = torch.randint(0, 256, (I, row), dtype=torch.uint8, generator=torch.Generator().manual_seed(5)).pin_memory()
+    staging = torch.empty(I * row, dtype=torch.uint8).pin_memory()
+    for k in (768, 3072):
+        sel = torch.sort(torch.randperm(I, generator=torch.Generator().manual_seed(k))[:k]).values
+        dst = torch.empty(k, row, dtype=torch.uint8, device=dev)
+        for name, fn in (("staged", lambda: ops.gather_rows_staged(host, sel, staging, dst)),
+                         ("naive", lambda: ops.gather_rows_naive(host, sel, dst))):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(10):
+                fn()
+                torch.cuda.synchronize()
+            us = (time.perf_counter() - t0) / 10 * 1e6
+            res[f"gather_rows_{name}_k{k}"] = {"bytes": k * row, "us": round(us, 2),
+                                               "GBps": round(k * row / us / 1e3, 2),
+                                               "kernel": f"gather_rows_{name} (host pinned -> device, synchronized)"}
+        assert torch.equal(dst.cpu(), host[sel]), "host gather bytes"
+    del host, staging
+    return res
 
 
 def _cpu_model() -> str:
