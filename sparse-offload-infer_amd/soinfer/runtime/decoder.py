@@ -146,6 +146,46 @@ def random_decoder(config: DecoderConfig = QWEN3_1P7B, seed: int = 0, device="cu
     return DecoderWeights(c, embed, lm_head, norm(H), layers)
 
 
+def decoder_weights_from_arena(store, matrices, config: DecoderConfig, embed: torch.Tensor, lm_head: torch.Tensor,
+                               final_norm: torch.Tensor, layer_norms: list, device=None) -> DecoderWeights:
+    """DecoderWeights over a checkpoint loaded by offload.load_hf_checkpoint.stream_load_layers (with
+    include_down_proj_t=True): q|k|v and gate|up are views of consecutive arena rows (the loader registers them
+    in that order), scales are concatenated on the GPU. device=None keeps every packed matrix in the pinned
+    arena (for DecodeEngine(offload=True)); a device copies them there (resident modes). embed / lm_head /
+    final_norm: fp16 on the GPU; layer_norms[l]: dict with input_layernorm, post_attention_layernorm, q_norm,
+    k_norm (fp16 on the GPU), as the reference keeps them (generate.py:60-80)."""
+    from ..offload.load_hf_checkpoint import DOWN_PROJ_T_SUFFIX
+
+    def span(names):
+        hs = [matrices[n].handle for n in names]
+        rb = hs[0].row_nbytes
+        for a, b in zip(hs, hs[1:]):
+            if b.offset != a.offset + a.nbytes or b.row_nbytes != rb:
+                raise ValueError(f"{names}: not consecutive rows of one width in the arena")
+        rows = sum(h.num_rows for h in hs)
+        v = store.arena[hs[0].offset:hs[0].offset + rows * rb].view(rows, rb)
+        return v if device is None else v.to(device)
+
+    def scales(names):
+        return torch.cat([matrices[n].scale for n in names]).contiguous()
+
+    def one(name):
+        v = store.matrix_view(matrices[name].handle)
+        return v if device is None else v.to(device)
+
+    layers = []
+    for l in range(config.layers):
+        p = f"model.layers.{l}."
+        qkv = [p + f"self_attn.{x}_proj.weight" for x in ("q", "k", "v")]
+        gu = [p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"]
+        o, down, down_T = p + "self_attn.o_proj.weight", p + "mlp.down_proj.weight", p + DOWN_PROJ_T_SUFFIX
+        nm = layer_norms[l]
+        layers.append(LayerWeights(nm["input_layernorm"], nm["post_attention_layernorm"], nm["q_norm"], nm["k_norm"],
+                                   span(qkv), scales(qkv), one(o), matrices[o].scale, span(gu), scales(gu),
+                                   one(down), matrices[down].scale, one(down_T), matrices[down_T].scale))
+    return DecoderWeights(config, embed, lm_head, final_norm, layers)
+
+
 class DecodeEngine:
     """Greedy decoder over DecoderWeights. mode: "dense", "dip" (top dip_k channels per layer, weights
     resident) or "cached_dip" (hot channels resident, the rest in pinned host memory; miss_path "direct" reads
@@ -228,9 +268,14 @@ class DecodeEngine:
             # gate|up rows interleaved by 8-row tiles (gate 4t..4t+3, up 4t..4t+3) for the SwiGLU epilogue
             t = torch.arange(I // 4, device=dev)
             perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
-            self.gu_il = [(L.gu_Wq.index_select(0, perm).contiguous(), L.gu_scale.index_select(0, perm).contiguous())
-                          for L in w.layers]
+            self.gu_il = [(L.gu_Wq.index_select(0, perm.to(L.gu_Wq.device)).contiguous(),
+                           L.gu_scale.index_select(0, perm).contiguous()) for L in w.layers]
         self.offload = offload
+        if not offload:
+            packed = [t for L in w.layers for t in (L.qkv_Wq, L.o_Wq, L.gu_Wq, L.down_Wq)]
+            if any(t.device != dev for t in packed):
+                raise ValueError("resident modes need every packed weight on the engine's device (use offload=True "
+                                 "for weights in host memory)")
         if offload:
             self._setup_offload()
         self._x_final = self.x
@@ -249,11 +294,15 @@ class DecodeEngine:
         self.caches, self.host_up, self.host_down, self.host_up_ptr, self.host_down_ptr = [], [], [], [], []
         for l, (L, hot) in enumerate(zip(self.w.layers, hot_channels)):
             up_Wq, up_s = L.up(I)
-            self.caches.append(HotCache.build(up_Wq, up_s, L.down_T_Wq, L.down_T_scale, hot))
             hu = self.store.register(f"model.layers.{l}.mlp.up_proj.weight", up_Wq)
             hd_ = self.store.register(f"model.layers.{l}.mlp.down_proj_T.weight", L.down_T_Wq)
             self.host_up.append(self.store.matrix_view(hu))
             self.host_down.append(self.store.matrix_view(hd_))
+            if up_Wq.is_cuda and L.down_T_Wq.is_cuda:
+                self.caches.append(HotCache.build(up_Wq, up_s, L.down_T_Wq, L.down_T_scale, hot))
+            else:  # weights in host memory: fill the cache from the pinned arena
+                self.caches.append(HotCache.from_host(self.host_up[l], up_s, self.host_down[l], L.down_T_scale, hot,
+                                                      device=dev))
             self.host_up_ptr.append(self.store.device_address(hu))
             self.host_down_ptr.append(self.store.device_address(hd_))
         row_up = self.w.layers[0].gu_Wq.shape[1]

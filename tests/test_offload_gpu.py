@@ -183,3 +183,49 @@ def test_stream_load_layers_arena_bytes_and_gemv(off, tmp_path, H, I):
     y = ops.gemv_w4a16_group_lop3(store.matrix_view(m.handle).cuda(), m.scale, x.cuda(), m.packed_k, 128)
     ref = O.gemv_w4_f64(store.matrix_view(m.handle).numpy(), m.scale.cpu().numpy(), x.numpy(), m.packed_k, 128)
     assert_close(y, ref, "loaded gate_proj")
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_engine_runs_a_loaded_checkpoint_from_host_memory(off, tmp_path, fused):
+    """stream_load_layers -> decoder_weights_from_arena -> DecodeEngine: with the packed weights left in the pinned
+    arena (offload=True; dense, DIP with no cache, cache-aware DIP) the engine generates exactly the tokens and
+    hidden state of the resident engine over device copies of the same arena bytes."""
+    from soinfer.runtime import decoder as D
+
+    _, _, ld = off
+    cfg = D.DecoderConfig(hidden=256, layers=3, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=1000,
+                          group_size=128, max_seq=64)
+    _write_checkpoint(tmp_path, cfg.layers, cfg.hidden, cfg.intermediate, cfg.q_heads * cfg.head_dim,
+                      cfg.kv_heads * cfg.head_dim, seed=77)
+    store, mats = ld.stream_load_layers(str(tmp_path), cfg.layers, group_size=128, log_every=0,
+                                        include_down_proj_t=True)
+    g = torch.Generator(device="cuda").manual_seed(5)
+
+    def vec(n, std=1.0, base=0.0):
+        return (torch.randn(n, generator=g, device="cuda") * std + base).half()
+
+    embed = vec(cfg.vocab * cfg.hidden).view(cfg.vocab, cfg.hidden)
+    lm_head = vec(cfg.vocab * cfg.hidden, 0.05).view(cfg.vocab, cfg.hidden)
+    norms = [{"input_layernorm": vec(cfg.hidden, 0.1, 1.0), "post_attention_layernorm": vec(cfg.hidden, 0.1, 1.0),
+              "q_norm": vec(cfg.head_dim, 0.1, 1.0), "k_norm": vec(cfg.head_dim, 0.1, 1.0)} for _ in range(cfg.layers)]
+    final = vec(cfg.hidden, 0.1, 1.0)
+    w_dev = D.decoder_weights_from_arena(store, mats, cfg, embed, lm_head, final, norms, device="cuda")
+    w_host = D.decoder_weights_from_arena(store, mats, cfg, embed, lm_head, final, norms)
+    assert not w_host.layers[0].qkv_Wq.is_cuda and w_host.layers[0].qkv_Wq.is_pinned()
+    prompt = torch.randint(0, cfg.vocab, (5,), generator=torch.Generator().manual_seed(9)).tolist()
+    k = cfg.intermediate // 2
+    hot = [list(range(0, cfg.intermediate, 3)) for _ in range(cfg.layers)]
+    dense = D.DecodeEngine(w_dev, "dense", max_new_tokens=6, fused=fused)
+    want_dense = dense.generate(prompt, 6)
+    dip = D.DecodeEngine(w_dev, "dip", dip_k=k, max_new_tokens=6, fused=fused)
+    want_dip = dip.generate(prompt, 6)
+    for mode, kw, want, ref in (("dense", {}, want_dense, dense),
+                                ("cached_dip", dict(dip_k=k, hot_channels=[[] for _ in range(cfg.layers)]), want_dip,
+                                 dip),
+                                ("cached_dip", dict(dip_k=k, hot_channels=hot), want_dip, dip)):
+        eng = D.DecodeEngine(w_host, mode, max_new_tokens=6, fused=fused, offload=True, **kw)
+        for use_graph in (False, True):
+            assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"{mode} {kw.keys()} graph={use_graph}"
+            assert torch.equal(eng.x_final, ref.x_final)
+    with pytest.raises(ValueError):
+        D.DecodeEngine(w_host, "dense")  # resident modes need the weights on the device
