@@ -287,6 +287,10 @@ int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const
  *   pos. Replaces launch_kv_cache_append (kv_cache.cu:22-27; bindings.cpp:450-466).
  * soi_gemv_f16: y[N] = W[N,K] x[K] with fp16 W (the LM head). Replaces
  *   launch_gemv_fp16_v3 (gemv_fp16.cu:89-93; bindings.cpp:201-208).
+ * soi_swiglu_gate_up: h[I] = fp16(silu(g) * u), g = gate_W[I,H] x and
+ *   u = up_W[I,H] x summed in fp32 over fp16 products, silu(t) = t/(1+exp(-t)),
+ *   one pass over x for both matrices. Replaces launch_swiglu_gate_up
+ *   (swiglu_fused.cu:15-56; bindings.cpp:434-448).
  * soi_argmax_f16: index of the largest of n binary16 values (NaN above every
  *   number, ties to the lowest index: torch.argmax, generate.py:446). Writes
  *   out_index[0]; if log/log_len are given, also log[log_len[0]] = index and
@@ -318,6 +322,8 @@ int soi_rope_apply(uint16_t* x, const float* cos_vals, const float* sin_vals, in
 int soi_kv_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
                         int64_t num_kv_heads, int64_t max_seq, int64_t head_dim, int64_t pos, void* stream);
 int soi_gemv_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, int64_t N, int64_t K, void* stream);
+int soi_swiglu_gate_up(const uint16_t* gate_W, const uint16_t* up_W, const uint16_t* x, uint16_t* h, int64_t I,
+                       int64_t H, void* stream);
 size_t soi_argmax_workspace_bytes(int64_t n);
 int soi_argmax_f16(const uint16_t* x, int64_t n, int32_t* out_index, int32_t* log, int32_t* log_len, int64_t log_cap,
                    void* workspace, size_t workspace_bytes, void* stream);

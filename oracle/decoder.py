@@ -15,7 +15,7 @@ Follows python/soinfer/runtime/generate.py of the reference:
   * generation (generate_streaming :429-463): prompt tokens one at a time,
     then final rmsnorm -> fp16 LM head GEMV -> argmax (first maximum).
 Kernels restated: rmsnorm.cu:9-48 (x * rsqrt(mean(x^2) + eps) * w),
-rope.cu:5-25, kv_cache.cu:7-27, gemv_fp16.cu:60-95. Every op rounds its
+rope.cu:5-25, kv_cache.cu:7-27, gemv_fp16.cu:60-95, swiglu_fused.cu:15-51. Every op rounds its
 output to binary16, as the reference's ops do; the arithmetic inside an op is
 binary64 here (the reference's is fp32), so results agree to the fp16
 rounding of each op, not bit for bit.
@@ -76,6 +76,15 @@ def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
 def gemv_f16(W: np.ndarray, x: np.ndarray) -> np.ndarray:
     """gemv_fp16.cu:60-95 (the LM head): fp16(W @ x)."""
     return f16(np.asarray(W, np.float64) @ np.asarray(x, np.float64))
+
+
+def swiglu_gate_up(gate_W: np.ndarray, up_W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """swiglu_fused.cu:15-51 (ops.py:112-116): fp16(silu(gate_W @ x) * (up_W @ x)), silu on the unrounded gate
+    sum (the kernel keeps both sums in fp32 and rounds only h)."""
+    xd = np.asarray(x, np.float64)
+    g = np.asarray(gate_W, np.float64) @ xd
+    u = np.asarray(up_W, np.float64) @ xd
+    return f16(silu(g) * u)
 
 
 def argmax_first(v: np.ndarray) -> int:

@@ -545,6 +545,26 @@ torch::Tensor gemv_fp16_v3(torch::Tensor W, torch::Tensor x) {
     return y;
 }
 
+// reference bindings.cpp:434-448 (same checks and messages)
+torch::Tensor swiglu_gate_up(torch::Tensor gate_W, torch::Tensor up_W, torch::Tensor x) {
+    check_f16_cuda_contiguous(gate_W, "swiglu_gate_up(gate_W)");
+    check_f16_cuda_contiguous(up_W, "swiglu_gate_up(up_W)");
+    check_f16_cuda_contiguous(x, "swiglu_gate_up(x)");
+    TORCH_CHECK(gate_W.dim() == 2 && up_W.dim() == 2, "swiglu_gate_up: gate_W and up_W must be 2D [I, H]");
+    TORCH_CHECK(gate_W.sizes() == up_W.sizes(), "swiglu_gate_up: gate_W and up_W must have the same shape");
+    TORCH_CHECK(x.dim() == 1 && x.size(0) == gate_W.size(1),
+                "swiglu_gate_up: x must be 1D [H] matching the weights' H");
+    TORCH_CHECK(gate_W.size(1) % 8 == 0, "swiglu_gate_up: H must be a multiple of 8 (float4-vectorized loads)");
+    check_same_device(gate_W, x, "swiglu_gate_up");
+    check_same_device(up_W, x, "swiglu_gate_up");
+    const at::DeviceGuard guard(x.device());
+    auto h = torch::empty({gate_W.size(0)}, x.options());
+    check_status(soi_swiglu_gate_up(h16(gate_W), h16(up_W), h16(x), h16m(h), gate_W.size(0), gate_W.size(1),
+                                    cur_stream(x)),
+                 "swiglu_gate_up");
+    return h;
+}
+
 void kv_cache_append(torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor k_new, torch::Tensor v_new,
                      int64_t pos) {
     check_f16_cuda_contiguous(k_cache, "kv_cache_append(k_cache)");
@@ -1261,6 +1281,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gather_rows_naive", &gather_rows_naive, "pinned-host row gather, per row");
     m.def("rmsnorm", &rmsnorm, "RMSNorm over the last dim (reference rmsnorm)");
     m.def("gemv_fp16_v3", &gemv_fp16_v3, "fp16 GEMV (LM head)");
+    m.def("swiglu_gate_up", &swiglu_gate_up, "h = silu(gate_W @ x) * (up_W @ x), one fused pass (fp16)");
     m.def("kv_cache_append", &kv_cache_append, "KV cache append at pos");
     m.def("rope_apply", &rope_apply, "RoPE in place (rotate-half)");
     m.def("rmsnorm_into", &rmsnorm_into, "RMSNorm into a caller buffer");

@@ -254,6 +254,86 @@ __global__ __launch_bounds__(64) void gemv_f16_simple_kernel(const uint16_t* __r
     if (threadIdx.x == 0) stg(y + row, f32_to_f16_bits(a));
 }
 
+// h[i] = fp16(silu(g_i) * u_i) with g = gate_W x and u = up_W x summed in fp32 over fp16 products. Both matrices'
+// rows i stream through one wave, which reads each x chunk once for both; the SiLU and the product run on the
+// reduced sums, so only h is written. R rows of each matrix per wave: R = 2 keeps 4 weight rows in flight, the
+// same as the fp16 GEMV's 4-row tile, so the register footprint (and occupancy) matches it.
+template <int R, int PU, bool FULL>
+__global__ __launch_bounds__(64) void swiglu_gate_up_kernel(const uint16_t* __restrict__ Wg,
+                                                            const uint16_t* __restrict__ Wu,
+                                                            const uint16_t* __restrict__ x,
+                                                            uint16_t* __restrict__ h, int64_t I, int H) {
+    const int lane = threadIdx.x;
+    const int chunks = H >> 3;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+    const u32x4* z = reinterpret_cast<const u32x4*>(g_zero16);
+    const u32x4* x4 = reinterpret_cast<const u32x4*>(x);
+    const u32x4 *gr[R], *ur[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = (FULL || row0 + r < I) ? row0 + r : I - 1;
+        gr[r] = reinterpret_cast<const u32x4*>(Wg + row * H);
+        ur[r] = reinterpret_cast<const u32x4*>(Wu + row * H);
+    }
+    float ga[R], ua[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) ga[r] = ua[r] = 0.0f;
+    for (int c0 = 0; c0 < chunks; c0 += kWave * PU) {
+        u32x4 gv[PU][R], uv[PU][R], xv[PU];
+#pragma unroll
+        for (int p = 0; p < PU; ++p) {
+            const int c = c0 + p * kWave + lane;
+            const bool ok = FULL || c < chunks;
+            xv[p] = ldg(ok ? x4 + c : z);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                gv[p][r] = ldg_stream(ok ? gr[r] + c : z);
+                uv[p][r] = ldg_stream(ok ? ur[r] + c : z);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PU; ++p) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float a = ga[r], b = ua[r];
+                a = dot2(as_f16x2(gv[p][r].x), as_f16x2(xv[p].x), a);
+                b = dot2(as_f16x2(uv[p][r].x), as_f16x2(xv[p].x), b);
+                a = dot2(as_f16x2(gv[p][r].y), as_f16x2(xv[p].y), a);
+                b = dot2(as_f16x2(uv[p][r].y), as_f16x2(xv[p].y), b);
+                a = dot2(as_f16x2(gv[p][r].z), as_f16x2(xv[p].z), a);
+                b = dot2(as_f16x2(uv[p][r].z), as_f16x2(xv[p].z), b);
+                a = dot2(as_f16x2(gv[p][r].w), as_f16x2(xv[p].w), a);
+                b = dot2(as_f16x2(uv[p][r].w), as_f16x2(xv[p].w), b);
+                ga[r] = a;
+                ua[r] = b;
+            }
+        }
+    }
+    const float g = reduce_rows<R>(ga);
+    const float u = reduce_rows<R>(ua);
+    const int r = reduce_rows_row<R>(static_cast<uint32_t>(lane));
+    if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < I)) stg(h + row0 + r, f32_to_f16_bits(silu_f32(g) * u));
+}
+
+// Any H / alignment: one wave per row, lanes stride over k.
+__global__ __launch_bounds__(64) void swiglu_gate_up_simple_kernel(const uint16_t* __restrict__ Wg,
+                                                                   const uint16_t* __restrict__ Wu,
+                                                                   const uint16_t* __restrict__ x,
+                                                                   uint16_t* __restrict__ h, int H) {
+    const int64_t row = blockIdx.x;
+    const uint16_t* g = Wg + row * H;
+    const uint16_t* u = Wu + row * H;
+    float a = 0.0f, b = 0.0f;
+    for (int k = threadIdx.x; k < H; k += kWave) {
+        const float xk = f16_bits_to_f32(ldg(x + k));
+        a = fmaf(f16_bits_to_f32(ldg(g + k)), xk, a);
+        b = fmaf(f16_bits_to_f32(ldg(u + k)), xk, b);
+    }
+    a = wave_sum_bcast(a);
+    b = wave_sum_bcast(b);
+    if (threadIdx.x == 0) stg(h + row, f32_to_f16_bits(silu_f32(a) * b));
+}
+
 // argmax with torch.argmax's order: NaN above every number, ties -> lowest index.
 __device__ __forceinline__ bool arg_better(float av, int ai, float bv, int bi) {
     const bool an = av != av, bn = bv != bv;
@@ -540,6 +620,33 @@ extern "C" int soi_gemv_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, i
         hipLaunchKernelGGL((gemv_f16_kernel<R, 2, false>), grid, dim3(64), 0, st, W, x, y, N, Ki);
     else
         hipLaunchKernelGGL((gemv_f16_kernel<R, 1, false>), grid, dim3(64), 0, st, W, x, y, N, Ki);
+    return launch_status(what);
+}
+
+extern "C" int soi_swiglu_gate_up(const uint16_t* gate_W, const uint16_t* up_W, const uint16_t* x, uint16_t* h,
+                                  int64_t I, int64_t H, void* stream) {
+    const char* what = "soi_swiglu_gate_up";
+    SOI_REQUIRE(I >= 0 && I <= (int64_t(1) << 31) - 1, "%s: I out of range", what);
+    SOI_REQUIRE(H >= 1 && H <= (int64_t(1) << 30), "%s: H must be in [1, 2^30]", what);
+    if (I == 0) return SOI_OK;
+    SOI_REQUIRE(gate_W && up_W && x && h, "%s: null pointer", what);
+    hipStream_t st = as_stream(stream);
+    const int Hi = static_cast<int>(H);
+    if (!vec_ok(H, {gate_W, up_W, x})) {
+        hipLaunchKernelGGL(swiglu_gate_up_simple_kernel, dim3(static_cast<unsigned>(I)), dim3(64), 0, st, gate_W,
+                           up_W, x, h, Hi);
+        return launch_status(what);
+    }
+    constexpr int R = 2;
+    const int64_t chunks = H / 8;
+    const int64_t passes = ceil_div64(chunks, kWave);
+    const dim3 grid(static_cast<unsigned>(ceil_div64(I, R)));
+    if (passes >= 4 && I % R == 0 && chunks % (4 * kWave) == 0)
+        hipLaunchKernelGGL((swiglu_gate_up_kernel<R, 4, true>), grid, dim3(64), 0, st, gate_W, up_W, x, h, I, Hi);
+    else if (passes >= 2)
+        hipLaunchKernelGGL((swiglu_gate_up_kernel<R, 2, false>), grid, dim3(64), 0, st, gate_W, up_W, x, h, I, Hi);
+    else
+        hipLaunchKernelGGL((swiglu_gate_up_kernel<R, 1, false>), grid, dim3(64), 0, st, gate_W, up_W, x, h, I, Hi);
     return launch_status(what);
 }
 

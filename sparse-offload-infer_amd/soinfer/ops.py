@@ -228,6 +228,36 @@ def gemv_fp16_v3(W: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return _C.gemv_fp16_v3(W, x)
 
 
+def swiglu_gate_up(gate_W: torch.Tensor, up_W: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """h = silu(gate_W @ x) * (up_W @ x) (reference ops.py:112-116). gate_W, up_W: [I, H] fp16 of the same
+    shape, x: [H] fp16, H % 8 == 0. One kernel: each wave streams rows of both matrices against one read of x,
+    sums in fp32 and applies silu(g) * u = g / (1 + exp(-g)) * u to the sums; only h is written."""
+    return _C.swiglu_gate_up(gate_W, up_W, x)
+
+
+def fused_swiglu_mlp(gate_W: torch.Tensor, up_W: torch.Tensor, down_W: torch.Tensor,
+                     x: torch.Tensor) -> torch.Tensor:
+    """y = down_W @ (silu(gate_W @ x) * (up_W @ x)), the fp16 SwiGLU MLP (reference ops.py:119-125): gate_W, up_W
+    [I, H], down_W [H, I], x [H]. swiglu_gate_up, then gemv_fp16_v3 for the down projection, which needs all of
+    h before any output row can finish."""
+    return gemv_fp16_v3(down_W, swiglu_gate_up(gate_W, up_W, x))
+
+
+def concat_qkv_weights(Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tensor) -> torch.Tensor:
+    """[q_dim + 2 kv_dim, H] = rows of Wq, then Wk, then Wv (reference ops.py:128-132), built once at load time
+    for fused_qkv_projection."""
+    return torch.cat([Wq, Wk, Wv], dim=0).contiguous()
+
+
+def fused_qkv_projection(qkv_W: torch.Tensor, x: torch.Tensor, q_dim: int,
+                         kv_dim: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """q, k, v = split(qkv_W @ x, [q_dim, kv_dim, kv_dim]) (reference ops.py:135-149): one fp16 GEMV over the
+    concatenated weight from concat_qkv_weights, one pass over x; q, k, v are views of its output (a row count
+    other than q_dim + 2 kv_dim makes the split raise, as in the reference)."""
+    q, k, v = gemv_fp16_v3(qkv_W, x).split([q_dim, kv_dim, kv_dim])
+    return q, k, v
+
+
 def precompute_rope_cos_sin(head_dim: int, theta: float, pos: int, device, dtype=torch.float32):
     """cos/sin [head_dim/2] at absolute position pos: inv_freq[i] = 1 / theta^(2i/head_dim),
     angle_i = pos * inv_freq[i], computed in fp32 (the Qwen3 / HF rotary convention)."""

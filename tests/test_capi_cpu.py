@@ -79,6 +79,12 @@ def test_argument_checks_return_before_launch(lib):
     assert b"num_classes" in lib.soi_last_error()
     assert gr(None, None, None, None, 1, cnt, n, k, 12, None) == 1  # group_size not a multiple of 8
     assert gr(None, None, None, None, 0, None, None, None, 128, None) == 0  # nothing to do
+    sw = lib.soi_swiglu_gate_up
+    sw.argtypes = [C.c_void_p] * 4 + [i64, i64, C.c_void_p]
+    assert sw(None, None, None, None, 16, 0, None) == 1  # H < 1
+    assert sw(None, None, None, None, 16, 64, None) == 1  # rows to write, null pointers
+    assert b"null pointer" in lib.soi_last_error()
+    assert sw(None, None, None, None, 0, 64, None) == 0  # I = 0: nothing to do
 
 
 def test_cached_dip_argument_checks(lib):

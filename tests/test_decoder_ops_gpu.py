@@ -110,6 +110,71 @@ def test_gemv_fp16_v3_requires_k_multiple_of_8(ops):
         ops.gemv_fp16_v3(rnd((4, 12), 0).cuda(), rnd((12,), 1).cuda())
 
 
+# (6144, 2048): the Qwen3-1.7B MLP (full tiles, 4 passes); (2048, 6144): 12 passes; (4095, 256): a ragged last
+# tile; (33, 64): one partial pass; (7, 8): a single chunk per row
+@pytest.mark.parametrize("I,H", [(6144, 2048), (2048, 6144), (4095, 256), (33, 64), (7, 8)])
+def test_swiglu_gate_up_matches_oracle(ops, I, H):
+    Wg, Wu, x = rnd((I, H), 30 + I, 0.05), rnd((I, H), 31 + H, 0.05), rnd((H,), 32)
+    h = ops.swiglu_gate_up(Wg.cuda(), Wu.cuda(), x.cuda())
+    assert h.dtype == torch.float16 and h.shape == (I,)
+    assert_close(h, OD.swiglu_gate_up(Wg.numpy(), Wu.numpy(), x.numpy()).astype(np.float64), f"swiglu {I}x{H}")
+
+
+def test_swiglu_gate_up_unaligned_rows(ops):
+    """Weights starting 8 bytes into their storage take the per-element kernel; same results to the tolerance."""
+    I, H = 100, 512
+    Wg_s, Wu_s, x = rnd((I * H + 4,), 33, 0.05), rnd((I * H + 4,), 34, 0.05), rnd((H,), 35)
+    Wg, Wu = Wg_s[4:].view(I, H), Wu_s[4:].view(I, H)
+    h = ops.swiglu_gate_up(Wg_s.cuda()[4:].view(I, H), Wu_s.cuda()[4:].view(I, H), x.cuda())
+    assert_close(h, OD.swiglu_gate_up(Wg.numpy(), Wu.numpy(), x.numpy()).astype(np.float64), "swiglu unaligned")
+
+
+def test_swiglu_gate_up_rejects_bad_arguments(ops):
+    W, x = rnd((16, 64), 36).cuda(), rnd((64,), 37).cuda()
+    with pytest.raises(RuntimeError, match="same shape"):
+        ops.swiglu_gate_up(W, rnd((8, 64), 38).cuda(), x)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        ops.swiglu_gate_up(rnd((4, 12), 0).cuda(), rnd((4, 12), 1).cuda(), rnd((12,), 2).cuda())
+    with pytest.raises(RuntimeError, match="matching"):
+        ops.swiglu_gate_up(W, W, rnd((32,), 39).cuda())
+    with pytest.raises(RuntimeError):
+        ops.swiglu_gate_up(W.float(), W.float(), x)
+
+
+def test_fused_swiglu_mlp_equals_gate_up_then_down(ops):
+    H, I = 2048, 6144
+    Wg, Wu, Wd, x = (rnd((I, H), 40, 0.05).cuda(), rnd((I, H), 41, 0.05).cuda(), rnd((H, I), 42, 0.02).cuda(),
+                     rnd((H,), 43).cuda())
+    y = ops.fused_swiglu_mlp(Wg, Wu, Wd, x)
+    assert torch.equal(y, ops.gemv_fp16_v3(Wd, ops.swiglu_gate_up(Wg, Wu, x)))
+    # against the binary64 MLP: h is rounded to fp16 between the two kernels, so each h_j may carry up to one
+    # binary16 rounding (2^-11 relative) plus its fp32 sums' error; the down sum propagates that as at most
+    # 2^-10 sum_j |Wd_ij h_j|, and y itself rounds once more (2^-11 |y_i|)
+    Wg64, Wu64, Wd64 = (t.cpu().numpy().astype(np.float64) for t in (Wg, Wu, Wd))
+    x64 = x.cpu().numpy().astype(np.float64)
+    g = Wg64 @ x64
+    h64 = g / (1 + np.exp(-g)) * (Wu64 @ x64)
+    y64 = Wd64 @ h64
+    bound = 2.0 ** -10 * (np.abs(Wd64) @ np.abs(h64)) + 2.0 ** -11 * np.abs(y64) + 2.0 ** -24
+    err = np.abs(y.cpu().numpy().astype(np.float64) - y64)
+    assert (err <= bound).all(), f"fused_swiglu_mlp: {int((err > bound).sum())} outputs beyond the propagated bound"
+
+
+def test_fused_qkv_projection_equals_separate_gemvs(ops):
+    H, q_dim, kv_dim = 2048, 2048, 1024
+    Wq, Wk, Wv = rnd((q_dim, H), 44, 0.05), rnd((kv_dim, H), 45, 0.05), rnd((kv_dim, H), 46, 0.05)
+    x = rnd((H,), 47).cuda()
+    qkv_W = ops.concat_qkv_weights(Wq.cuda(), Wk.cuda(), Wv.cuda())
+    assert qkv_W.shape == (q_dim + 2 * kv_dim, H) and qkv_W.is_contiguous()
+    q, k, v = ops.fused_qkv_projection(qkv_W, x, q_dim, kv_dim)
+    # each output row is the same row-independent GEMV whichever matrix holds the row
+    assert torch.equal(q, ops.gemv_fp16_v3(Wq.cuda(), x))
+    assert torch.equal(k, ops.gemv_fp16_v3(Wk.cuda(), x))
+    assert torch.equal(v, ops.gemv_fp16_v3(Wv.cuda(), x))
+    with pytest.raises(RuntimeError):
+        ops.fused_qkv_projection(qkv_W, x, q_dim, kv_dim + 1)
+
+
 def argmax_dev(C, x):
     ws = torch.empty(C.argmax_workspace_bytes(x.numel()), dtype=torch.uint8, device="cuda")
     out = torch.full((1,), -1, dtype=torch.int32, device="cuda")

@@ -365,6 +365,33 @@ def test_decoder_oracle_gemv_f16():
     assert np.allclose(OD.gemv_f16(W, x).astype(np.float64), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
 
 
+def test_decoder_oracle_swiglu_gate_up():
+    from oracle import decoder as OD
+
+    rng = np.random.default_rng(6)
+    Wg = (rng.standard_normal((48, 64)) * 2).astype(np.float16)
+    Wu = rng.standard_normal((48, 64)).astype(np.float16)
+    # a unit x picks column j of both matrices: silu applies to the gate column only, times the up column
+    e = np.zeros(64, np.float16)
+    e[5] = 1.0
+    assert np.array_equal(OD.swiglu_gate_up(Wg, Wu, e), OD.silu_mul(Wg[:, 5], Wu[:, 5]))
+    assert not np.array_equal(OD.swiglu_gate_up(Wu, Wg, e), OD.swiglu_gate_up(Wg, Wu, e))
+    # closed forms at the ends of silu: gate sum 0 -> 0, a gate of +30 passes u * 30 (1 + e^-30 = 1 in binary64
+    # to 1e-13), a gate of -30 leaves |h| < 30 e^-30 |u|
+    Wg2 = np.zeros((3, 64), np.float16)
+    Wg2[1, 5], Wg2[2, 5] = 30.0, -30.0
+    Wu2 = np.zeros((3, 64), np.float16)
+    Wu2[:, 5] = 0.5
+    h = OD.swiglu_gate_up(Wg2, Wu2, e).astype(np.float64)
+    assert h[0] == 0.0 and h[1] == 15.0 and abs(h[2]) < 1e-11
+    # binary64 sums of the full product: against a float64 matmul within the one final fp16 rounding
+    x = rng.standard_normal(64).astype(np.float16)
+    g = Wg.astype(np.float64) @ x.astype(np.float64)
+    u = Wu.astype(np.float64) @ x.astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    assert np.allclose(OD.swiglu_gate_up(Wg, Wu, x).astype(np.float64), ref, rtol=2 ** -11, atol=2 ** -24)
+
+
 def test_threaded_gemv_equals_single_thread():
     """The row-split form used for the multi-core CPU baseline gives the single-thread result exactly (each row is
     still summed by one thread in ascending k), including more threads than rows."""
