@@ -351,6 +351,15 @@ def bench_dip_mlp(D, w, hot, dev):
         if frac == 0.5:
             y_dip = y_unfused
         del eng
+        # dense-up schedule: gate and up GEMVs of every channel, then the selection and the gated sparse down in
+        # one launch (3 launches); same selection and bit-identical y
+        eng = D.DecodeEngine(w, "dip", dip_k=k, max_new_tokens=1, dip_dense_up=True)
+        us_du = run(eng)
+        assert torch.equal(eng.down, y_unfused), "dense-up DIP must equal DIP bit for bit"
+        res[f"dip_k{k}"]["dense_up_us"] = round(us_du, 2)
+        res[f"dip_k{k}"]["dense_up_schedule"] = ("gate GEMV, up GEMV, selection + gated sparse down in one launch "
+                                                 "(3 launches)")
+        del eng
     k = I // 2
     notes = {"direct": "misses read in place from the pinned host arena by the up GEMV and the down accumulate "
                        "(no descriptors, gathers or staging)",
@@ -483,6 +492,20 @@ def bench_kernels(dev, gen):
                                   list(zip(Wt, St)))
         res[f"up_indexed_silu_k{k}"] = entry(k * (row + 4 * G + 4 + 2 + 2) + 2 * H, t["mean_us"],
                                              kernel="gemv_int4 IndexRows + SiLU epilogue")
+        upv = torch.randn(I, generator=gen, device=dev).half()
+        sel_i, sel_c = torch.empty(k, dtype=i32, device=dev), torch.empty(1, dtype=i32, device=dev)
+
+        def two_launches(W, S):
+            _C.topk_threshold_select_f16abs_into(gate, k, sel_i, sel_c)
+            _C.gemv_w4a16_indexed_accumulate_gated_into(W, S, sel_i, gate, upv, y, H, GS, ws)
+
+        t2 = time_graph_per_launch(two_launches, list(zip(Wt, St)))
+        t = time_graph_per_launch(
+            lambda W, S: _C.dip_select_gated_down_into(gate, upv, k, W, S, sel_i, sel_c, y, H, GS, ws),
+            list(zip(Wt, St)))
+        res[f"dip_select_gated_down_k{k}"] = entry(
+            k * (row + 4 * G + 2 + 4) + 2 * I + 2 * H, t["mean_us"], two_launch_us=round(t2["mean_us"], 3),
+            kernel="DIP selection over |gate| + gated sparse down (1 launch); two_launch_us: top-k, then gated down")
         dst = torch.empty(k, row, dtype=torch.uint8, device=dev)
         kcount = torch.full((1,), k, dtype=i32, device=dev)
         t = time_graph_per_launch(lambda W: _C.gather_rows_device_counted(W.data_ptr(), I, row, idx, kcount, dst),

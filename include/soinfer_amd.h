@@ -390,6 +390,24 @@ int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* sc
                                             int64_t num_channels, uint16_t* y, int64_t H, int64_t group_size,
                                             int64_t num_groups, void* workspace, size_t workspace_bytes,
                                             void* stream);
+/* soi_dip_select_gated_down: the DIP selection and the gated sparse down of
+ *   one MLP in ONE launch. Equals soi_topk_threshold_select_f16abs(gate, n =
+ *   num_channels, k) -> (out_indices, out_count) followed by
+ *   soi_gemv_w4a16_indexed_accumulate_gated over those indices, bit for bit
+ *   (indices, count and y); a selection of fewer than k channels (NaN gates)
+ *   sums over the selected ones only. Fuses the reference's
+ *   topk_threshold_select (csrc/bindings.cpp:507-518), the SiLU gating of
+ *   python/soinfer/runtime/generate.py:304-305 and gemv_w4a16_sparse_accumulate
+ *   (csrc/bindings.cpp:311-339). Every workgroup of the down grid computes the
+ *   selection itself and keeps its own rows' channels in LDS. Requires
+ *   num_rows >= num_channels and 1 <= k <= num_channels; workspace rules of
+ *   soi_gemv_w4a16_sparse_accumulate. Sizes past the fused kernel's limits
+ *   (num_channels > 8192, a row chunk over 1024 rows, or rows / scales that
+ *   the vector path cannot read) run the two kernels instead, same results. */
+int soi_dip_select_gated_down(const uint16_t* gate, const uint16_t* up, int64_t num_channels, int64_t k,
+                              const uint8_t* Wq_T, const float* scale_T, int64_t num_rows, int32_t* out_indices,
+                              int32_t* out_count, uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* --------------------------------------------------------------------------
  * Hot-cache GEMVs that read the misses in place (cache-aware DIP without a

@@ -1092,6 +1092,36 @@ void gemv_w4a16_indexed_accumulate_gated_into(torch::Tensor Wq_T, torch::Tensor 
                  n);
 }
 
+// DIP selection + gated sparse down in one launch: idx_out / count_out as
+// topk_threshold_select_f16abs_into(gate, k), y as
+// gemv_w4a16_indexed_accumulate_gated_into over those indices.
+void dip_select_gated_down_into(torch::Tensor gate, torch::Tensor up, int64_t k, torch::Tensor Wq_T,
+                                torch::Tensor scale_T, torch::Tensor idx_out, torch::Tensor count_out, torch::Tensor y,
+                                int64_t H, int64_t group_size, torch::Tensor workspace_buf) {
+    const char* n = "dip_select_gated_down_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(up, torch::kFloat16, gate, n, "up");
+    need(Wq_T, torch::kUInt8, gate, n, "Wq_T");
+    need(scale_T, torch::kFloat32, gate, n, "scale_T");
+    need(idx_out, torch::kInt32, gate, n, "idx_out");
+    need(count_out, torch::kInt32, gate, n, "count_out");
+    need(y, torch::kFloat16, gate, n, "y");
+    need(workspace_buf, torch::kUInt8, gate, n, "workspace");
+    TORCH_CHECK(k >= 1 && k <= gate.numel(), n, ": k must be in [1, n]");
+    need_numel(idx_out, k, n, "idx_out");
+    need_numel(count_out, 1, n, "count_out");
+    TORCH_CHECK(up.numel() == gate.numel(), n, ": gate and up must have the same length");
+    TORCH_CHECK(Wq_T.dim() == 2 && Wq_T.size(1) == ((H + 7) / 8) * 4 && y.numel() == H, n, ": Wq_T / y mismatch");
+    TORCH_CHECK(scale_T.dim() == 2 && scale_T.size(0) == Wq_T.size(0), n, ": scale_T shape mismatch");
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_dip_select_gated_down(h16(gate), h16(up), gate.numel(), k, Wq_T.data_ptr<uint8_t>(),
+                                           scale_T.data_ptr<float>(), Wq_T.size(0), idx_out.data_ptr<int32_t>(),
+                                           count_out.data_ptr<int32_t>(), h16m(y), H, group_size, scale_T.size(1),
+                                           workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(),
+                                           cur_stream(gate)),
+                 n);
+}
+
 void gemv_w4a16_indexed_silu_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
                                   torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
     const char* n = "gemv_w4a16_indexed_silu_into";
@@ -1320,6 +1350,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows, both halves written");
     m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
           "sparse down over selected rows with the SiLU gating computed on the fly");
+    m.def("dip_select_gated_down_into", &dip_select_gated_down_into,
+          "DIP selection over |gate| and the gated sparse down in one launch");
     m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");
     m.def("gemv_dip_cached_up_into", &gemv_dip_cached_up_into, "hot-cache up GEMV, misses read in place");
     m.def("gemv_dip_cached_up_silu_into", &gemv_dip_cached_up_silu_into,

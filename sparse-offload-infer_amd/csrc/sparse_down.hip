@@ -28,6 +28,7 @@
 #include "soi_device.h"
 #include "soi_host.h"
 #include "soi_rows.h"
+#include "soi_select.h"
 
 namespace soi {
 
@@ -64,14 +65,17 @@ constexpr int kDownU = 3;                       // 8-row groups per wave per bat
 
 // U groups per wave per batch (a lane with no chunk or a row past the range
 // reads g_zero16 instead, so the loads are issued unconditionally).
+constexpr int kRedFloats = kDownWaves * kGroupRows * kSliceChunks * kRedPitch;
+
+// One workgroup's share: rows [r*rpc, min((r+1)*rpc, k)) of slice blockIdx.x,
+// r = blockIdx.y, then the partial row, the arrival and (last workgroup of the
+// slice) the combine. red: kRedFloats floats of LDS; s_last: one LDS word.
 template <int U, bool VEC, bool CHUNK_SCALE, class Rows, class HS>
-__global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, const HS hs,
-                                                                    uint16_t* __restrict__ y, float* __restrict__ partial,
-                                                                    uint32_t* __restrict__ counters, int64_t k, int H,
-                                                                    int gs, int rpc, int R) {
+__device__ __forceinline__ void sparse_down_body(const Rows& rows, const HS& hs, uint16_t* __restrict__ y,
+                                                 float* __restrict__ partial, uint32_t* __restrict__ counters,
+                                                 int64_t k, int H, int gs, int rpc, int R, float* red, int* s_last_p) {
     constexpr int SC = CHUNK_SCALE ? 1 : 4;
-    __shared__ float red[kDownWaves * kGroupRows * kSliceChunks * kRedPitch];
-    __shared__ int s_last;
+    int& s_last = *s_last_p;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rs = lane >> 3, cc = lane & (kSliceChunks - 1);
     const int slice = blockIdx.x, r = blockIdx.y;
@@ -174,11 +178,110 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, co
     stg(y + col, f32_to_f16_bits(sum));
 }
 
+template <int U, bool VEC, bool CHUNK_SCALE, class Rows, class HS>
+__global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, const HS hs,
+                                                                    uint16_t* __restrict__ y, float* __restrict__ partial,
+                                                                    uint32_t* __restrict__ counters, int64_t k, int H,
+                                                                    int gs, int rpc, int R) {
+    __shared__ float red[kRedFloats];
+    __shared__ int s_last;
+    sparse_down_body<U, VEC, CHUNK_SCALE>(rows, hs, y, partial, counters, k, H, gs, rpc, R, red, &s_last);
+}
+
 // k == 0: y = 0 (the empty sum, as the reference's loop yields); a fill kernel
 // rather than a memset so the call stays capturable in a HIP graph.
 __global__ __launch_bounds__(256) void sparse_down_zero_kernel(uint16_t* __restrict__ y, int64_t H) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i < H) stg(y + i, uint16_t(0));
+}
+
+// Fused DIP selection + gated down projection. Every workgroup of the sparse
+// down grid first computes the rule-A selection over |gate| itself (the
+// top-k radix select of soi_select.h over n <= 256*E binary16 gates, read
+// from L2), keeps the channels (and raw gates) of its own row chunk in LDS,
+// and then runs the gated sparse down on them: no top-k launch and no global
+// index round trip. The row partition, coefficients and arithmetic are those
+// of sparse_down_kernel over IndexRows + GatedH, so y equals the top-k launch
+// followed by the gated down bit for bit; the selection equals the top-k
+// kernel's (slice-0 workgroups write the indices of their chunks, workgroup
+// (0, 0) the count). Positions at or past the selected count contribute
+// nothing.
+constexpr int kFusedMaxRpc = 1024;
+
+struct LdsIndexRows {
+    const uint8_t* W;
+    const float* S;
+    const int32_t* ch;  // LDS: channel of row j0 + i
+    int64_t j0;
+    int64_t row_bytes;
+    int64_t G;
+    __device__ __forceinline__ RowRef get(int64_t j) const {
+        const int64_t c = ch[j - j0];
+        return {W + c * row_bytes, S + c * G, true};
+    }
+};
+struct LdsGatedH {
+    const uint16_t* g;  // LDS: raw binary16 gate of row j0 + i
+    const int32_t* ch;  // LDS: its channel
+    const uint16_t* up;
+    int64_t j0;
+    __device__ __forceinline__ float get(int64_t j) const {
+        const float gv = f16_bits_to_f32(g[j - j0]);
+        const float u = f16_bits_to_f32(ldg(up + ch[j - j0]));
+        return f16_bits_to_f32(f32_to_f16_bits(silu_f32(gv) * u));
+    }
+};
+
+template <int E, bool VEC, bool CHUNK_SCALE>
+__global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int n, int k, int32_t* __restrict__ out_idx,
+    int32_t* __restrict__ out_count, const uint8_t* __restrict__ W, const float* __restrict__ S, int64_t row_bytes,
+    int64_t G, uint16_t* __restrict__ y, float* __restrict__ partial, uint32_t* __restrict__ counters, int H, int gs,
+    int rpc, int R) {
+    __shared__ float red[kRedFloats];
+    __shared__ int s_last;
+    __shared__ uint32_t s_hist[radix_hist_offset<F16AbsValues>(F16AbsValues::kPasses)];
+    __shared__ float s_max[kDownWaves];
+    __shared__ uint32_t s_tot[kDownWaves];
+    __shared__ int32_t s_ch[kFusedMaxRpc];
+    __shared__ uint16_t s_g[kFusedMaxRpc];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int base_i = wave * kWave * E + lane;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.y) * rpc;
+    const int64_t j1 = (j0 + rpc < k) ? j0 + rpc : static_cast<int64_t>(k);
+
+    uint32_t raw[E];
+    float val[E];
+    uint32_t key[E];
+    float local_max = 0.0f;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {  // clamped index: every load is issued unconditionally
+        const int i = base_i + j * kWave;
+        raw[j] = ldg(gate + (i < n ? i : n - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int i = base_i + j * kWave;
+        val[j] = (i < n) ? f16_bits_to_f32(static_cast<uint16_t>(raw[j] & 0x7fffu)) : __builtin_nanf("");
+        key[j] = F16AbsValues::key_of(val[j]);
+        local_max = fmaxf(local_max, val[j]);
+    }
+    const float tau = rule_a_tau<E, kDownWaves, F16AbsValues>(key, local_max, s_hist, s_max, k, tid);
+    const bool writer = blockIdx.x == 0;
+    const uint32_t total = rule_a_compact<E, kDownWaves>(val, tau, s_tot, tid, [&](uint32_t pos, int j) {
+        if (pos >= j0 && pos < j1) {
+            const int c = base_i + j * kWave;
+            s_ch[pos - j0] = c;
+            s_g[pos - j0] = static_cast<uint16_t>(raw[j]);
+            if (writer) stg(out_idx + pos, static_cast<int32_t>(c));
+        }
+    });
+    const int64_t kk = total < static_cast<uint32_t>(k) ? static_cast<int64_t>(total) : static_cast<int64_t>(k);
+    if (writer && blockIdx.y == 0 && tid == 0) stg(out_count, static_cast<int32_t>(kk));
+    __syncthreads();  // s_ch / s_g of the chunk complete
+    sparse_down_body<kDownU, VEC, CHUNK_SCALE>(LdsIndexRows{W, S, s_ch, j0, row_bytes, G},
+                                               LdsGatedH{s_g, s_ch, up, j0}, y, partial, counters, kk, H, gs, rpc,
+                                               R, red, &s_last);
 }
 
 // Partition: S = ceil(chunks / 8) slices; rows per chunk a multiple of 32 (one
@@ -357,4 +460,54 @@ extern "C" int soi_gemv_w4a16_indexed_accumulate(const uint8_t* Wq_T, const floa
     IndexRows rows{Wq_T, scale_T, num_rows, idx, row_bytes, num_groups};
     return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
                               as_stream(stream), what);
+}
+
+extern "C" int soi_dip_select_gated_down(const uint16_t* gate, const uint16_t* up, int64_t num_channels, int64_t k,
+                                         const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
+                                         int32_t* out_indices, int32_t* out_count, uint16_t* y, int64_t H,
+                                         int64_t group_size, int64_t num_groups, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+    const char* what = "soi_dip_select_gated_down";
+    int s = check_down(H, k, group_size, num_groups, what);
+    if (s) return s;
+    SOI_REQUIRE(num_channels >= 1 && num_channels <= (int64_t(1) << 30), "%s: num_channels must be in [1, 2^30]",
+                what);
+    SOI_REQUIRE(k >= 1 && k <= num_channels, "%s: k must be in [1, num_channels]", what);
+    SOI_REQUIRE(num_rows >= num_channels, "%s: down_proj^T has %lld rows, fewer than the %lld channels", what,
+                (long long)num_rows, (long long)num_channels);
+    SOI_REQUIRE(gate && up && Wq_T && scale_T && out_indices && out_count && y, "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(H, 8) * 4;
+    const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_T) && (group_size % 32) == 0;
+    const size_t need = down_workspace_bytes(H, k);
+    if (!workspace || workspace_bytes < need) {  // checked before either path launches anything
+        set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+        return SOI_ERR_WORKSPACE;
+    }
+    const DownPlan p = down_plan(H, k);
+    const int64_t E = ceil_div64(num_channels, kDownThreads);
+    if (!vec || E > 32 || p.rpc > kFusedMaxRpc) {
+        // outside the fused kernel's limits: the top-k kernel, then the gated down over its indices
+        s = soi_topk_threshold_select_f16abs(gate, num_channels, k, out_indices, out_count, stream);
+        if (s) return s;
+        return soi_gemv_w4a16_indexed_accumulate_gated(Wq_T, scale_T, num_rows, out_indices, k, gate, up,
+                                                       num_channels, y, H, group_size, num_groups, workspace,
+                                                       workspace_bytes, stream);
+    }
+    SOI_REQUIRE(p.R <= 65535, "%s: partition out of range", what);
+    uint32_t* counters = static_cast<uint32_t*>(workspace);
+    float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + down_counter_bytes(p));
+    const dim3 grid(static_cast<unsigned>(p.S), static_cast<unsigned>(p.R));
+    const int ni = static_cast<int>(num_channels), ki = static_cast<int>(k), Hi = static_cast<int>(H),
+              gi = static_cast<int>(group_size), ri = static_cast<int>(p.rpc), Ri = static_cast<int>(p.R);
+    hipStream_t st = as_stream(stream);
+#define SOI_F(EE)                                                                                                  \
+    hipLaunchKernelGGL((dip_select_down_kernel<EE, true, true>), grid, dim3(kDownThreads), 0, st, gate, up, ni, ki, \
+                       out_indices, out_count, Wq_T, scale_T, row_bytes, num_groups, y, partial, counters, Hi, gi, ri, \
+                       Ri)
+    if (E <= 8) SOI_F(8);
+    else if (E <= 16) SOI_F(16);
+    else if (E <= 24) SOI_F(24);
+    else SOI_F(32);
+#undef SOI_F
+    return launch_status(what);
 }

@@ -385,14 +385,13 @@ class DecodeEngine:
         if self.dip_dense_up:
             uW, uS = L.up(I)
             _C.gemv_w4a16_into(uW, uS, self.h, self.gu[I:], H, gs)
-        _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
-        if self.counts is not None:
-            self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
-                                                                     device=self.device))
-        if self.dip_dense_up:
-            _C.gemv_w4a16_indexed_accumulate_gated_into(L.down_T_Wq, L.down_T_scale, self.idx, gate, self.gu[I:],
-                                                        self.down, H, gs, self.sd_ws)
+            # selection and gated sparse down in one launch (indices and count still written)
+            _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx, self.cnt,
+                                          self.down, H, gs, self.sd_ws)
+            self._count_selection(l)
             return
+        _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
+        self._count_selection(l)
         if self.mode == "dip":
             uW, uS = L.up(I)
             _C.gemv_w4a16_indexed_into(uW, uS, self.idx, self.h, self.u_sel, H, gs)
@@ -415,6 +414,12 @@ class DecodeEngine:
         _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
         _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
                                     self.h_sel, self.down, H, gs, self.sd_ws)
+
+    def _count_selection(self, l: int):
+        """Calibration: add this layer's selected channels to its frequency counts."""
+        if self.counts is not None:
+            self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
+                                                                     device=self.device))
 
     def _fetch_misses(self, l: int, L: LayerWeights, uS: torch.Tensor):
         """Descriptors for this layer's selection, then the miss rows into staging: packed rows from pinned
@@ -494,20 +499,15 @@ class DecodeEngine:
                 _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
                                                    H, gs)
                 cur, other = other, cur
-                _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
-                if self.counts is not None:
-                    self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
-                                                                             device=self.device))
-                _C.gemv_w4a16_indexed_accumulate_gated_into(L.down_T_Wq, L.down_T_scale, self.idx, gate,
-                                                            self.gu[I:], self.down, H, gs, self.sd_ws)
+                _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx,
+                                              self.cnt, self.down, H, gs, self.sd_ws)
+                self._count_selection(l)
                 continue
             gW, gS = L.gate(I)
             _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
             cur, other = other, cur
             _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
-            if self.counts is not None:
-                self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
-                                                                         device=self.device))
+            self._count_selection(l)
             uW, uS = L.up(I)
             if self.mode == "dip":
                 _C.gemv_w4a16_indexed_silu_into(uW, uS, self.idx, self.h, gate, self.h_sel, H, gs)

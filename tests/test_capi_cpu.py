@@ -112,6 +112,27 @@ def test_cached_dip_argument_checks(lib):
     assert b"null pointer" in lib.soi_last_error()
 
 
+def test_dip_select_gated_down_argument_checks(lib):
+    """The fused selection + gated down rejects k outside [1, n], a down^T with fewer rows than channels, null
+    pointers and a short workspace before any launch."""
+    lib.soi_last_error.restype = C.c_char_p
+    i64, vp = C.c_int64, C.c_void_p
+    f = lib.soi_dip_select_gated_down
+    f.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp, C.c_size_t, vp]
+    b = (C.c_uint8 * 4096)()
+    p = C.addressof(b)
+    assert f(p, p, 6144, 0, p, p, 6144, p, p, p, 2048, 128, 16, p, 4096, None) == 1  # k < 1
+    assert f(p, p, 6144, 6145, p, p, 6144, p, p, p, 2048, 128, 16, p, 4096, None) == 1  # k > n
+    assert f(p, p, 6144, 3072, p, p, 6143, p, p, p, 2048, 128, 16, p, 4096, None) == 1  # rows < channels
+    assert b"fewer than" in lib.soi_last_error()
+    assert f(p, None, 6144, 3072, p, p, 6144, p, p, p, 2048, 128, 16, p, 4096, None) == 1  # null up
+    assert b"null pointer" in lib.soi_last_error()
+    assert f(p, p, 6144, 3072, p, p, 6144, p, p, p, 2048, 128, 15, p, 4096, None) == 1  # num_groups != H/gs
+    # a workspace below the partial rows' size (either path)
+    assert f(p, p, 6144, 3072, p, p, 6144, p, p, p, 2048, 128, 16, p, 4096, None) == 2
+    assert b"workspace" in lib.soi_last_error()
+
+
 def test_workspace_queries(lib):
     lib.soi_sparse_accumulate_workspace_bytes.restype = C.c_size_t
     lib.soi_sparse_accumulate_workspace_bytes.argtypes = [C.c_int64, C.c_int64]

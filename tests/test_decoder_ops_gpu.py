@@ -409,6 +409,82 @@ def test_indexed_accumulate_gated_equals_silu_then_accumulate(C, ops):
     assert torch.isnan(y.float()).all()
 
 
+def _fused_select_down(C, gate, up, k, down, H, ws):
+    idx = torch.full((k,), -7, dtype=torch.int32, device="cuda")
+    cnt = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    y = torch.full((H,), float("nan"), dtype=torch.float16, device="cuda")
+    C.dip_select_gated_down_into(gate, up, k, down["Wq_d"], down["s_d"], idx, cnt, y, H, 128, ws)
+    return idx, cnt, y
+
+
+@pytest.mark.parametrize("I,H,k,ties", [(6144, 2048, 3072, False), (6144, 2048, 768, True), (6144, 2048, 1536, False),
+                                        (6144, 2048, 6144, False), (6144, 2048, 1, False), (1000, 256, 333, True),
+                                        (8192, 1024, 4096, True), (9728, 2048, 4864, False)])
+def test_dip_select_gated_down_equals_topk_then_gated_down(C, I, H, k, ties):
+    """One-launch selection + gated sparse down == the top-k launch followed by the gated down, bit for bit
+    (indices, count, y); the indices are the oracle's rule-A selection and y matches the oracle's binary64 sum
+    over them. Ragged sizes, tie-heavy gates (quarter steps), k = 1 and k = n; 9728 channels exceed the fused
+    kernel and run the two-kernel path."""
+    down = int4_problem(I, H, 128, seed=81 + k)
+    g = rnd((I,), 82 + k) * 2
+    if ties:
+        g = ((g.float() * 4).round() / 4).half()
+    u = rnd((I,), 83 + k) * 2
+    gate, up = g.cuda(), u.cuda()
+    ws = torch.zeros(C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+    idx, cnt, y = _fused_select_down(C, gate, up, k, down, H, ws)
+    idx2 = torch.empty(k, dtype=torch.int32, device="cuda")
+    cnt2 = torch.empty(1, dtype=torch.int32, device="cuda")
+    C.topk_threshold_select_f16abs_into(gate, k, idx2, cnt2)
+    y2 = torch.empty(H, dtype=torch.float16, device="cuda")
+    C.gemv_w4a16_indexed_accumulate_gated_into(down["Wq_d"], down["s_d"], idx2, gate, up, y2, H, 128, ws)
+    assert torch.equal(idx, idx2) and torch.equal(cnt, cnt2) and torch.equal(y, y2)
+    ref_idx = O.topk_rule_a(np.abs(g.float().numpy()), k)
+    assert int(cnt.item()) == ref_idx.size == k
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    h = OD.silu_mul(g.numpy()[ref_idx], u.numpy()[ref_idx])
+    y_ref = O.sparse_accumulate_f64(down["Wq"][ref_idx], down["s"][ref_idx], h, H, 128)
+    assert_close(y, y_ref, f"fused select + down I={I} k={k}")
+    # the arrival counters are left at zero: a second call on the same workspace is identical
+    assert all(torch.equal(a, b) for a, b in zip(_fused_select_down(C, gate, up, k, down, H, ws), (idx, cnt, y)))
+
+
+def test_dip_select_gated_down_fewer_than_k_selected(C):
+    """With NaN gates fewer than k channels can be selected: the count says how many, only those indices are
+    written, and y sums over exactly those rows (as the oracle's sum over the rule-A selection)."""
+    I, H, k = 1000, 256, 995
+    down = int4_problem(I, H, 128, seed=91)
+    g = rnd((I,), 92) * 2
+    g[torch.arange(3, I, 97)] = float("nan")  # 11 NaN gates: 989 valid channels
+    u = rnd((I,), 93) * 2
+    ws = torch.zeros(C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+    idx, cnt, y = _fused_select_down(C, g.cuda(), u.cuda(), k, down, H, ws)
+    ref_idx = O.topk_rule_a(np.abs(g.float().numpy()), k)
+    n = ref_idx.size
+    assert n == 989 and int(cnt.item()) == n
+    assert np.array_equal(idx[:n].cpu().numpy(), ref_idx) and bool((idx[n:] == -7).all())
+    h = OD.silu_mul(g.numpy()[ref_idx], u.numpy()[ref_idx])
+    assert_close(y, O.sparse_accumulate_f64(down["Wq"][ref_idx], down["s"][ref_idx], h, H, 128), "fused, count < k")
+
+
+def test_dip_select_gated_down_rejections(C):
+    I, H, k = 1024, 256, 100
+    down = int4_problem(I, H, 128, seed=94)
+    gate, up = (rnd((I,), 95)).cuda(), (rnd((I,), 96)).cuda()
+    ws = torch.zeros(C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError):  # k = 0
+        _fused_select_down(C, gate, up, 0, down, H, ws)
+    with pytest.raises(RuntimeError):  # k > n
+        _fused_select_down(C, gate, up, I + 1, down, H, ws)
+    with pytest.raises(RuntimeError):  # fewer down^T rows than channels
+        short = {"Wq_d": down["Wq_d"][: I - 1], "s_d": down["s_d"][: I - 1]}
+        _fused_select_down(C, gate, up, k, short, H, ws)
+    with pytest.raises(RuntimeError):  # workspace too small
+        _fused_select_down(C, gate, up, k, down, H, ws[:16])
+    with pytest.raises(RuntimeError):  # up shorter than gate
+        _fused_select_down(C, gate, up[:-1], k, down, H, ws)
+
+
 def test_gemv_rmsnorm_rejects_aliasing(C):
     K = 256
     p = int4_mat(64, K, 70)
