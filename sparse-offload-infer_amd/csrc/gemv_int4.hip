@@ -97,6 +97,7 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int
 // base(): a K-element fp16 vector (2K bytes), a legal read target for a row
 // that cannot be resolved (its K/2 packed bytes and K/gs scales fit in it).
 struct PlainX {
+    static constexpr bool kSinglePass = false;
     const uint16_t* x;
     __device__ __forceinline__ const uint16_t* base() const { return x; }
     template <bool VEC, bool FULL>
@@ -106,6 +107,7 @@ struct PlainX {
 };
 
 struct NormX {
+    static constexpr bool kSinglePass = false;
     const uint16_t* a;
     const uint16_t* d;  // may be null
     const uint16_t* w;
@@ -140,6 +142,7 @@ struct NormX {
 // RegX: the lane's x chunk already in registers (single-pass shapes: K == 2048,
 // lane l owns chunk l), computed by the caller.
 struct RegX {
+    static constexpr bool kSinglePass = false;
     const f16x2* v;     // 16 pairs held by this lane
     const uint16_t* b;  // a K-element vector for unresolvable rows
     __device__ __forceinline__ const uint16_t* base() const { return b; }
@@ -147,6 +150,59 @@ struct RegX {
     __device__ __forceinline__ void load(int, int, bool, f16x2 xv[16]) const {
 #pragma unroll
         for (int e = 0; e < 16; ++e) xv[e] = v[e];
+    }
+};
+
+// RegNormX (K == 2048 with one pass: lane l's GEMV chunk is elements
+// 32l..32l+31): the lane's chunks of a, d and the norm weight w are loaded
+// into registers before the tile issues its weight loads, and load() does
+// the residual add, the RMSNorm (one wave reduction) and, when x_out / h_out
+// are given (workgroup 0 only), their stores. So the norm's arithmetic runs
+// while the weight loads are in flight instead of before they are issued.
+// Same operations in the same order as the separate norm, so the same x.
+struct RegNormX {
+    static constexpr bool kSinglePass = true;
+    u32x4 t[4], e[4], g[4];  // a, d (when has_d), w
+    bool has_d;
+    float eps;
+    int K;
+    uint16_t* x_out;
+    uint16_t* h_out;
+    const uint16_t* b;  // a K-element vector for unresolvable rows
+    __device__ __forceinline__ const uint16_t* base() const { return b; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int, int, bool, f16x2 xv[16]) const {
+        const int lane = threadIdx.x;
+        u32x4 s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[i] = t[i];
+            if (has_d) {
+                s[i].x = add_f16x2(t[i].x, e[i].x);
+                s[i].y = add_f16x2(t[i].y, e[i].y);
+                s[i].z = add_f16x2(t[i].z, e[i].z);
+                s[i].w = add_f16x2(t[i].w, e[i].w);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ss += sumsq_f16x2(s[i].x) + sumsq_f16x2(s[i].y) + sumsq_f16x2(s[i].z) + sumsq_f16x2(s[i].w);
+        const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(K) + eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u32x4 r;
+            r.x = norm_f16x2(s[i].x, g[i].x, inv);
+            r.y = norm_f16x2(s[i].y, g[i].y, inv);
+            r.z = norm_f16x2(s[i].z, g[i].z, inv);
+            r.w = norm_f16x2(s[i].w, g[i].w, inv);
+            xv[4 * i + 0] = as_f16x2(r.x);
+            xv[4 * i + 1] = as_f16x2(r.y);
+            xv[4 * i + 2] = as_f16x2(r.z);
+            xv[4 * i + 3] = as_f16x2(r.w);
+            if (x_out) stg(reinterpret_cast<u32x4*>(x_out) + 4 * lane + i, s[i]);
+            if (h_out) stg(reinterpret_cast<u32x4*>(h_out) + 4 * lane + i, r);
+        }
     }
 };
 
@@ -250,7 +306,8 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int c0 = 0; c0 < chunks; c0 += kWave * PU) {
+    const int c_end = XS::kSinglePass ? kWave * PU : chunks;  // single pass: no loop for the compiler to keep
+    for (int c0 = 0; c0 < c_end; c0 += kWave * PU) {
         uint32_t wv[PU][R][4];
         float sc[PU][R][SC];
         f16x2 xv[PU][16];
@@ -274,6 +331,8 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
                     }
                 }
             }
+            // a single-pass x source computes x from registers: keep that work after the weight loads
+            if constexpr (XS::kSinglePass) __builtin_amdgcn_sched_barrier(0);
             xsrc.template load<VEC, FULL>(K, c, cv, xv[p]);
             const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 #pragma unroll
@@ -456,48 +515,25 @@ __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int6
     const u32x4* a4 = reinterpret_cast<const u32x4*>(a);
     const u32x4* d4 = reinterpret_cast<const u32x4*>(d);
     const u32x4* w4 = reinterpret_cast<const u32x4*>(w);
-    if (ONEPASS) {
-        // K == 2048: lane l's 32 elements are exactly its GEMV chunk; keep them in registers
-        u32x4 t[4], g[4];
+    if constexpr (ONEPASS) {
+        // K == 2048: lane l's 32 elements are exactly its GEMV chunk. Its a / d / w chunks are requested here, the
+        // tile then issues the weight loads, and the add + RMSNorm run while those are in flight (RegNormX).
+        static_assert(FULL, "the one-pass norm form needs the full tile");
+        RegNormX xs;
+        const u32x4* e4 = d ? d4 : a4;  // unconditional loads (a branch around a load makes the wave wait there)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            t[i] = ldg(a4 + 4 * lane + i);
-            g[i] = ldg(w4 + 4 * lane + i);
+            xs.t[i] = ldg(a4 + 4 * lane + i);
+            xs.g[i] = ldg(w4 + 4 * lane + i);
+            xs.e[i] = ldg(e4 + 4 * lane + i);
         }
-        if (d) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4 e = ldg(d4 + 4 * lane + i);
-                t[i].x = add_f16x2(t[i].x, e.x);
-                t[i].y = add_f16x2(t[i].y, e.y);
-                t[i].z = add_f16x2(t[i].z, e.z);
-                t[i].w = add_f16x2(t[i].w, e.w);
-            }
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            ss += sumsq_f16x2(t[i].x) + sumsq_f16x2(t[i].y) + sumsq_f16x2(t[i].z) + sumsq_f16x2(t[i].w);
-        const float inv = rsqrtf(wave_sum_bcast(ss) / static_cast<float>(K) + eps);
-        f16x2 hv[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            u32x4 r;
-            r.x = norm_f16x2(t[i].x, g[i].x, inv);
-            r.y = norm_f16x2(t[i].y, g[i].y, inv);
-            r.z = norm_f16x2(t[i].z, g[i].z, inv);
-            r.w = norm_f16x2(t[i].w, g[i].w, inv);
-            hv[4 * i + 0] = as_f16x2(r.x);
-            hv[4 * i + 1] = as_f16x2(r.y);
-            hv[4 * i + 2] = as_f16x2(r.z);
-            hv[4 * i + 3] = as_f16x2(r.w);
-            if (blockIdx.x == 0) {
-                if (x_out) stg(reinterpret_cast<u32x4*>(x_out) + 4 * lane + i, t[i]);
-                if (h_out) stg(reinterpret_cast<u32x4*>(h_out) + 4 * lane + i, r);
-            }
-        }
-        gemv_int4_tile<R, 1, true, CHUNK_SCALE, true, FULL>(rows, N, RegX{hv, a}, ep, K, gs,
-                                                           static_cast<int64_t>(blockIdx.x) * R);
+        xs.has_d = d != nullptr;
+        xs.eps = eps;
+        xs.K = K;
+        xs.x_out = blockIdx.x == 0 ? x_out : nullptr;
+        xs.h_out = blockIdx.x == 0 ? h_out : nullptr;
+        xs.b = a;
+        gemv_int4_tile<R, 1, true, CHUNK_SCALE, true, FULL>(rows, N, xs, ep, K, gs, static_cast<int64_t>(blockIdx.x) * R);
         return;
     }
     const int n8 = K >> 3;
