@@ -334,7 +334,13 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
             // a single-pass x source computes x from registers: keep that work after the weight loads
             if constexpr (XS::kSinglePass) __builtin_amdgcn_sched_barrier(0);
             xsrc.template load<VEC, FULL>(K, c, cv, xv[p]);
-            const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+        }
+        // the x sums only after every pass's loads are issued (summing pass p's x first would make the wave wait
+        // for it before requesting pass p + 1); with several passes the order is pinned for the scheduler too
+        if constexpr (PU > 1) __builtin_amdgcn_sched_barrier(0);
+        const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+        for (int p = 0; p < PU; ++p) {
 #pragma unroll
             for (int i = 0; i < SC; ++i) {
                 float t = 0.0f;
@@ -423,10 +429,9 @@ struct MissCopy {
     }
 };
 
-template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY,
-          class CP = NoCopy>
-__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x, EP ep,
-                                                       int K, int gs, CP cp = CP{}) {
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP, class CP>
+__device__ __forceinline__ void gemv_int4_body(const Rows& rows, int64_t N, const uint16_t* __restrict__ x,
+                                               const EP& ep, int K, int gs, const CP& cp) {
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
     if constexpr (CP::kChunks > 0) {
         constexpr int CH = CP::kChunks;
@@ -459,6 +464,25 @@ __global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, con
     } else {
         gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, PlainX{x}, ep, K, gs, row0);
     }
+}
+
+// Single-pass tiles: the default register budget (occupancy-driven scheduling).
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY,
+          class CP = NoCopy>
+__global__ __launch_bounds__(64) void gemv_int4_kernel(Rows rows, int64_t N, const uint16_t* __restrict__ x, EP ep,
+                                                       int K, int gs, CP cp = CP{}) {
+    gemv_int4_body<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, x, ep, K, gs, cp);
+}
+
+// Multi-pass tiles (PU > 1: rows longer than 64 chunks, e.g. down_proj at K = 6144): at decode sizes a launch
+// has about one wave per SIMD, so occupancy buys nothing, while every pass's loads must be in flight at once
+// (R*PU weight chunks + PU x chunks, ~90 VGPRs). With the default budget the scheduler kept 5 waves per SIMD by
+// reusing registers, which serialised the passes' loads into several round trips.
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool BITFIELD, bool FULL, class Rows, class EP = StoreY,
+          class CP = NoCopy>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv_int4_mp_kernel(
+    Rows rows, int64_t N, const uint16_t* __restrict__ x, EP ep, int K, int gs, CP cp = CP{}) {
+    gemv_int4_body<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, x, ep, K, gs, cp);
 }
 
 // Batched form: P independent problems of one shape [N, K]; workgroup b takes
@@ -695,6 +719,17 @@ static Int4Plan plan_int4(int64_t N, int64_t K, bool vec) {
     return p;
 }
 
+template <int RR, int PP, bool V, bool CS, bool BF, bool FL, class Rows, class EP, class CP>
+static void launch_int4_kernel(dim3 grid, hipStream_t st, const Rows& rows, int64_t N, const uint16_t* x, const EP& ep,
+                               int K, int gs, const CP& cp) {
+    if constexpr (PP > 1)
+        hipLaunchKernelGGL((gemv_int4_mp_kernel<RR, PP, V, CS, BF, FL, Rows, EP, CP>), grid, dim3(64), 0, st, rows, N,
+                           x, ep, K, gs, cp);
+    else
+        hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BF, FL, Rows, EP, CP>), grid, dim3(64), 0, st, rows, N, x,
+                           ep, K, gs, cp);
+}
+
 template <bool BITFIELD, class Rows, class EP = StoreY, class CP = NoCopy>
 static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP& ep, int64_t K, int64_t gs, bool vec,
                        hipStream_t st, const char* what, const CP& cp = CP{}) {
@@ -704,9 +739,8 @@ static int launch_int4(const Rows& rows, int64_t N, const uint16_t* x, const EP&
     const bool full = vec && cs && (N % pl.R == 0) && ((K / 32) % (64 * pl.PU) == 0);
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
     const int Ki = static_cast<int>(K), gi = static_cast<int>(gs);
-#define SOI_L(RR, PP, V, CS, FL)                                                                                \
-    hipLaunchKernelGGL((gemv_int4_kernel<RR, PP, V, CS, BITFIELD, FL, Rows, EP, CP>), grid, dim3(64), 0, st, rows, N, x, \
-                       ep, Ki, gi, cp)
+#define SOI_L(RR, PP, V, CS, FL) \
+    launch_int4_kernel<RR, PP, V, CS, BITFIELD, FL>(grid, st, rows, N, x, ep, Ki, gi, cp)
 #define SOI_CS(RR, PP, V)                    \
     if (V && full) SOI_L(RR, PP, V, true, true); \
     else if (cs) SOI_L(RR, PP, V, true, false);  \
