@@ -1084,6 +1084,7 @@ static int check_cached(const uint8_t* cache_Wq, const float* cache_scale, int64
     SOI_REQUIRE(cache_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
                 "%s: negative or too large row / channel count", what);
     if (k == 0) return SOI_OK;
+    SOI_REQUIRE(num_channels >= 1, "%s: a selection needs at least one channel", what);
     SOI_REQUIRE(sel && slot_of && full_Wq && full_scale, "%s: null pointer", what);
     SOI_REQUIRE(cache_rows == 0 || (cache_Wq && cache_scale), "%s: null cache", what);
     return SOI_OK;

@@ -3,6 +3,12 @@
 // index-driven (resident weights) variants only differ in where row j's
 // packed bytes and scales live, so they share every arithmetic step and
 // return bit-identical results on the same logical rows.
+// get() is branch-free (an unresolvable row gets a clamped in-range address
+// and ok = false): a branch around a load makes the wave wait for it at the
+// merge, which serialised the per-lane row lookups of the sparse down.
+// get(j) == resolve(key(j), j): key() is the first load of a lookup (index or
+// descriptor), resolve() the rest, so a kernel can issue every row's key
+// before any row's dependent loads (loads complete in order).
 #pragma once
 
 #include <stdint.h>
@@ -21,7 +27,9 @@ struct DenseRows {
     const float* S;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const { return {W + j * row_bytes, S + j * G, true}; }
+    __device__ __forceinline__ int64_t key(int64_t j) const { return j; }
+    __device__ __forceinline__ RowRef resolve(int64_t k, int64_t) const { return {W + k * row_bytes, S + k * G, true}; }
+    __device__ __forceinline__ RowRef get(int64_t j) const { return resolve(key(j), j); }
 };
 
 // row j resolved by descriptor: top bit set -> staging row, else cache row
@@ -35,15 +43,15 @@ struct DescRows {
     const int32_t* desc;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const {
-        const uint32_t d = static_cast<uint32_t>(desc[j]);
+    __device__ __forceinline__ int64_t key(int64_t j) const { return static_cast<uint32_t>(desc[j]); }
+    __device__ __forceinline__ RowRef get(int64_t j) const { return resolve(key(j), j); }
+    __device__ __forceinline__ RowRef resolve(int64_t kd, int64_t) const {
+        const uint32_t d = static_cast<uint32_t>(kd);
         const int64_t off = static_cast<int64_t>(d & 0x7fffffffu);
-        if (d >> 31) {
-            if (off < sN) return {sW + off * row_bytes, sS + off * G, true};
-        } else {
-            if (off < cN) return {cW + off * row_bytes, cS + off * G, true};
-        }
-        return {nullptr, nullptr, false};
+        const bool st = (d >> 31) != 0;
+        const bool ok = off < (st ? sN : cN);
+        const int64_t o = ok ? off : 0;
+        return {(st ? sW : cW) + o * row_bytes, (st ? sS : cS) + o * G, ok};
     }
 };
 
@@ -64,15 +72,16 @@ struct SlotRows {
     const int32_t* slot_of;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const {
-        const int32_t ch = idx[j];
-        if (ch < 0 || ch >= fN) return {nullptr, nullptr, false};
-        const int32_t s = slot_of[ch];
-        if (s >= 0) {
-            if (s < cN) return {cW + static_cast<int64_t>(s) * row_bytes, cS + static_cast<int64_t>(s) * G, true};
-            return {nullptr, nullptr, false};
-        }
-        return {fW + static_cast<int64_t>(ch) * row_bytes, fS + static_cast<int64_t>(ch) * G, true};
+    __device__ __forceinline__ int64_t key(int64_t j) const { return idx[j]; }
+    __device__ __forceinline__ RowRef get(int64_t j) const { return resolve(key(j), j); }
+    __device__ __forceinline__ RowRef resolve(int64_t ch, int64_t) const {
+        const bool cok = ch >= 0 && ch < fN;
+        const int64_t c = cok ? ch : 0;
+        const int32_t s = slot_of[c];
+        const bool hit = s >= 0;
+        const bool ok = cok && (!hit || s < cN);
+        const int64_t r = hit ? (ok ? s : 0) : c;
+        return {(hit ? cW : fW) + r * row_bytes, (hit ? cS : fS) + r * G, ok};
     }
 };
 
@@ -89,15 +98,16 @@ struct SlotStageRows {
     const int32_t* slot_of;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const {
-        const int32_t ch = idx[j];
-        if (ch < 0 || ch >= fN) return {nullptr, nullptr, false};
-        const int32_t s = slot_of[ch];
-        if (s >= 0) {
-            if (s < cN) return {cW + static_cast<int64_t>(s) * row_bytes, cS + static_cast<int64_t>(s) * G, true};
-            return {nullptr, nullptr, false};
-        }
-        return {stW + j * row_bytes, fS + static_cast<int64_t>(ch) * G, true};
+    __device__ __forceinline__ int64_t key(int64_t j) const { return idx[j]; }
+    __device__ __forceinline__ RowRef get(int64_t j) const { return resolve(key(j), j); }
+    __device__ __forceinline__ RowRef resolve(int64_t ch, int64_t j) const {
+        const bool cok = ch >= 0 && ch < fN;
+        const int64_t c = cok ? ch : 0;
+        const int32_t s = slot_of[c];
+        const bool hit = s >= 0;
+        const bool ok = cok && (!hit || s < cN);
+        const int64_t r = ok ? s : 0;
+        return {hit ? cW + r * row_bytes : stW + j * row_bytes, hit ? cS + r * G : fS + c * G, ok};
     }
 };
 
@@ -109,10 +119,12 @@ struct IndexRows {
     const int32_t* idx;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const {
-        const int32_t r = idx[j];
-        if (r >= 0 && r < nrows) return {W + static_cast<int64_t>(r) * row_bytes, S + static_cast<int64_t>(r) * G, true};
-        return {nullptr, nullptr, false};
+    __device__ __forceinline__ int64_t key(int64_t j) const { return idx[j]; }
+    __device__ __forceinline__ RowRef get(int64_t j) const { return resolve(key(j), j); }
+    __device__ __forceinline__ RowRef resolve(int64_t r, int64_t) const {
+        const bool ok = r >= 0 && r < nrows;
+        const int64_t rr = ok ? r : 0;
+        return {W + rr * row_bytes, S + rr * G, ok};
     }
 };
 

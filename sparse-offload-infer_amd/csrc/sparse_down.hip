@@ -35,23 +35,37 @@ namespace soi {
 // Coefficient sources: h_sel given (PlainH), or the SiLU gating of the
 // selected channels computed on the fly (GatedH: h_j = fp16(silu(gate[c]) *
 // up[c]), c = idx[j], the rounding of the indexed SiLU GEMV epilogue and of
-// generate.py:304-305; a channel outside [0, n) gives NaN).
+// generate.py:304-305; a channel outside [0, n) gives NaN). As for the row
+// sources, key(j) is the first load, fetch() the dependent loads and value()
+// the arithmetic, so a kernel can issue every row's loads before using any.
 struct PlainH {
     const uint16_t* h;
-    __device__ __forceinline__ float get(int64_t j) const { return f16_bits_to_f32(ldg(h + j)); }
+    struct Raw {
+        uint16_t b;
+    };
+    __device__ __forceinline__ int64_t key(int64_t j) const { return j; }
+    __device__ __forceinline__ Raw fetch(int64_t k) const { return {ldg(h + k)}; }
+    __device__ __forceinline__ static float value(Raw r) { return f16_bits_to_f32(r.b); }
 };
 struct GatedH {
     const uint16_t* gate;
     const uint16_t* up;
     const int32_t* idx;
     int n;
-    __device__ __forceinline__ float get(int64_t j) const {
-        const int c = ldg(idx + j);
+    struct Raw {
+        uint16_t g, u;
+        bool ok;
+    };
+    __device__ __forceinline__ int64_t key(int64_t j) const { return ldg(idx + j); }
+    __device__ __forceinline__ Raw fetch(int64_t c) const {
         const bool ok = c >= 0 && c < n;
-        const int cc = ok ? c : 0;
-        const float g = f16_bits_to_f32(ldg(gate + cc));
-        const float u = f16_bits_to_f32(ldg(up + cc));
-        return ok ? f16_bits_to_f32(f32_to_f16_bits(silu_f32(g) * u)) : __builtin_nanf("");
+        const int64_t cc = ok ? c : 0;
+        return {ldg(gate + cc), ldg(up + cc), ok};
+    }
+    __device__ __forceinline__ static float value(Raw r) {
+        const float g = f16_bits_to_f32(r.g);
+        const float u = f16_bits_to_f32(r.u);
+        return r.ok ? f16_bits_to_f32(f32_to_f16_bits(silu_f32(g) * u)) : __builtin_nanf("");
     }
 };
 
@@ -96,34 +110,60 @@ __device__ __forceinline__ void sparse_down_body(const Rows& rows, const HS& hs,
     for (int64_t jb = j0 + static_cast<int64_t>(wave) * kGroupRows; jb < j1; jb += kBatchRows) {
         uint32_t wv[U][4];
         float coef[U][SC];
+        // Loads complete in order, so a lookup issued after another row's weight chunk could only be used once
+        // that chunk had arrived too. Every group's loads are therefore issued level by level (keys, dependent
+        // lookups, weight chunks and scales), with scheduling barriers between the levels, before any arithmetic.
+        int64_t jc[U], rk[U], hk[U];
+        bool in[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t j = jb + static_cast<int64_t>(u) * kDownWaves * kGroupRows + rs;
-            const bool in = j < j1;
-            const RowRef ref = rows.get(in ? j : j0);
-            const bool ok = in && ref.ok && cvalid;
-            const float hj = in ? hs.get(in ? j : j0) : 0.0f;
+            in[u] = j < j1;
+            jc[u] = in[u] ? j : j0;  // unconditional loads from a clamped row: no branch around a load
+            rk[u] = rows.key(jc[u]);
+            hk[u] = hs.key(jc[u]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        RowRef ref[U];
+        typename HS::Raw hr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            ref[u] = rows.resolve(rk[u], jc[u]);
+            hr[u] = hs.fetch(hk[u]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float sv[U][SC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool ok = in[u] && ref[u].ok && cvalid;
             if (VEC) {
-                const u32x4 t = __builtin_nontemporal_load(ok ? reinterpret_cast<const u32x4*>(ref.w) + c
+                const u32x4 t = __builtin_nontemporal_load(ok ? reinterpret_cast<const u32x4*>(ref[u].w) + c
                                                               : reinterpret_cast<const u32x4*>(z));
                 wv[u][0] = t.x;
                 wv[u][1] = t.y;
                 wv[u][2] = t.z;
                 wv[u][3] = t.w;
             } else {
-                const uint32_t* rw = reinterpret_cast<const uint32_t*>(ref.w);
+                const uint32_t* rw = reinterpret_cast<const uint32_t*>(ref[u].w);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) wv[u][i] = *((ok && 4 * c + i < words) ? rw + 4 * c + i : z);
             }
-            const float bad = (in && !ref.ok) ? __builtin_nanf("") : 1.0f;  // unresolvable row -> NaN
 #pragma unroll
             for (int i = 0; i < SC; ++i) {
                 const int wi = 4 * c + i;
-                const float sv = CHUNK_SCALE ? *(ok ? ref.s + (32 * c) / gs : zf)
-                                             : *((ok && wi < words) ? ref.s + (8 * wi) / gs : zf);
-                coef[u][i] = (hj * sv) * bad;
+                sv[u][i] = CHUNK_SCALE ? *(ok ? ref[u].s + (32 * c) / gs : zf)
+                                       : *((ok && wi < words) ? ref[u].s + (8 * wi) / gs : zf);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float hj = in[u] ? HS::value(hr[u]) : 0.0f;
+            const float bad = (in[u] && !ref[u].ok) ? __builtin_nanf("") : 1.0f;  // unresolvable row -> NaN
+#pragma unroll
+            for (int i = 0; i < SC; ++i) coef[u][i] = (hj * sv[u][i]) * bad;
+        }
+        // Phase 3: the accumulation
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -215,20 +255,21 @@ struct LdsIndexRows {
     int64_t j0;
     int64_t row_bytes;
     int64_t G;
-    __device__ __forceinline__ RowRef get(int64_t j) const {
-        const int64_t c = ch[j - j0];
-        return {W + c * row_bytes, S + c * G, true};
-    }
+    __device__ __forceinline__ int64_t key(int64_t j) const { return ch[j - j0]; }
+    __device__ __forceinline__ RowRef resolve(int64_t c, int64_t) const { return {W + c * row_bytes, S + c * G, true}; }
 };
 struct LdsGatedH {
     const uint16_t* g;  // LDS: raw binary16 gate of row j0 + i
     const int32_t* ch;  // LDS: its channel
     const uint16_t* up;
     int64_t j0;
-    __device__ __forceinline__ float get(int64_t j) const {
-        const float gv = f16_bits_to_f32(g[j - j0]);
-        const float u = f16_bits_to_f32(ldg(up + ch[j - j0]));
-        return f16_bits_to_f32(f32_to_f16_bits(silu_f32(gv) * u));
+    struct Raw {
+        uint16_t g, u;
+    };
+    __device__ __forceinline__ int64_t key(int64_t j) const { return j - j0; }
+    __device__ __forceinline__ Raw fetch(int64_t i) const { return {g[i], ldg(up + ch[i])}; }
+    __device__ __forceinline__ static float value(Raw r) {
+        return f16_bits_to_f32(f32_to_f16_bits(silu_f32(f16_bits_to_f32(r.g)) * f16_bits_to_f32(r.u)));
     }
 };
 
@@ -409,6 +450,7 @@ extern "C" int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* ca
     if (s) return s;
     SOI_REQUIRE(cache_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
                 "%s: negative or too large row / channel count", what);
+    SOI_REQUIRE(k == 0 || num_channels >= 1, "%s: a selection needs at least one channel", what);
     SOI_REQUIRE(y && (k == 0 || (sel && slot_of && (full_Wq || staging_Wq) && full_scale && h_sel)),
                 "%s: null pointer", what);
     SOI_REQUIRE(k == 0 || cache_rows == 0 || (cache_Wq && cache_scale), "%s: null cache", what);
@@ -438,6 +480,7 @@ extern "C" int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, cons
     if (s) return s;
     SOI_REQUIRE(num_rows >= 0 && num_channels >= 0 && num_channels <= (int64_t(1) << 31) - 1,
                 "%s: negative or too large row / channel count", what);
+    SOI_REQUIRE(k == 0 || num_channels >= 1, "%s: a selection needs at least one channel", what);
     SOI_REQUIRE(y && (k == 0 || (Wq_T && scale_T && idx && gate && up)), "%s: null pointer", what);
     const int64_t row_bytes = ceil_div64(H, 8) * 4;
     const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_T);
