@@ -214,29 +214,53 @@ struct RegNormX {
 // y[4*tile + i] = fp16(silu(fp16(gate_i)) * fp16(up_i)) (generate.py:178).
 struct StoreY {
     static constexpr bool kSwiglu = false;
+    static constexpr bool kPrefetch = false;
+    struct Pre {};
     uint16_t* y;
     __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
         stg(y + row, valid ? f32_to_f16_bits(total) : uint16_t(0x7e00u));
     }
 };
 
+// SiluIdxY requests its gate value before the tile's weight loads: the tile's
+// R channels are read with wave-uniform (scalar) loads, the lane's one is
+// selected and gate[c] is requested right away, instead of two dependent
+// loads after the dot products.
 struct SiluIdxY {
     static constexpr bool kSwiglu = false;
+    static constexpr bool kPrefetch = true;
     uint16_t* y;
     const uint16_t* gate;
     const int32_t* idx;
     int n_gate;
-    __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
-        const int c = ldg(idx + row);
-        const bool ok = valid && c >= 0 && c < n_gate;
+    struct Pre {
+        uint16_t g;
+        bool ok;
+    };
+    // rows row0 .. row0 + R - 1 (clamped to N - 1); the lane stores row row0 + r_lane
+    template <int R>
+    __device__ __forceinline__ Pre prefetch(int64_t row0, int r_lane, int64_t N) const {
+        int32_t c = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int32_t cr = ldg(idx + (row0 + r < N ? row0 + r : N - 1));
+            c = r == r_lane ? cr : c;
+        }
+        const bool ok = c >= 0 && c < n_gate;
+        return {ldg(gate + (ok ? c : 0)), ok};
+    }
+    __device__ __forceinline__ void store(int64_t row, float total, bool valid, Pre p) const {
+        const bool ok = valid && p.ok;
         const float u = f16_bits_to_f32(f32_to_f16_bits(total));
-        const float g = ok ? f16_bits_to_f32(ldg(gate + c)) : 0.0f;
+        const float g = ok ? f16_bits_to_f32(p.g) : 0.0f;
         stg(y + row, ok ? f32_to_f16_bits(silu_f32(g) * u) : uint16_t(0x7e00u));
     }
 };
 
 struct SwigluY {
     static constexpr bool kSwiglu = true;
+    static constexpr bool kPrefetch = false;
+    struct Pre {};
     uint16_t* y;
 };
 
@@ -245,6 +269,8 @@ struct SwigluY {
 // StoreY would write it, so both halves equal the plain GEMV of those rows.
 struct SplitGUY {
     static constexpr bool kSwiglu = false;
+    static constexpr bool kPrefetch = false;
+    struct Pre {};
     uint16_t* gate;
     uint16_t* up;
     __device__ __forceinline__ void store(int64_t row, float total, bool valid) const {
@@ -301,6 +327,10 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
             }
         }
     }
+
+    // epilogue operands that do not depend on the result are requested before the weights
+    typename EP::Pre pre{};
+    if constexpr (EP::kPrefetch) pre = ep.template prefetch<R>(row0, reduce_rows_row<R>(static_cast<uint32_t>(lane)), N);
 
     float acc[R];
 #pragma unroll
@@ -399,7 +429,12 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
             stg(ep.y + (row0 >> 1) + (r - 4), (vr && vo) ? f32_to_f16_bits(silu_f32(g) * u) : uint16_t(0x7e00u));
         }
     } else {
-        if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) ep.store(row0 + r, total, vr);
+        if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) {
+            if constexpr (EP::kPrefetch)
+                ep.store(row0 + r, total, vr, pre);
+            else
+                ep.store(row0 + r, total, vr);
+        }
     }
 }
 
