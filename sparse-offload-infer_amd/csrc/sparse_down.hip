@@ -75,7 +75,7 @@ constexpr int kSliceChunks = 8;                 // 16-byte chunks per slice
 constexpr int kSliceCols = kSliceChunks * 32;   // 256 columns
 constexpr int kGroupRows = kWave / kSliceChunks;  // 8 rows per wave-wide load
 constexpr int kRedPitch = 33;                   // LDS floats per (row lane, chunk): conflict-free columns
-constexpr int kDownU = 3;                       // 8-row groups per wave per batch
+constexpr int kDownU = 6;                       // 8-row groups per wave per batch
 
 // U groups per wave per batch (a lane with no chunk or a row past the range
 // reads g_zero16 instead, so the loads are issued unconditionally).
@@ -325,8 +325,15 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
                                                R, red, &s_last);
 }
 
-// Partition: S = ceil(chunks / 8) slices; rows per chunk a multiple of 32 (one
-// 8-row group per wave) spreading k over about 256 / S chunks (at least 4).
+// Partition: S = ceil(chunks / 8) slices; each slice's k rows split into R
+// chunks of rpc rows (a multiple of 32: one 8-row group per wave), R as small
+// as one load batch per wave allows (rpc <= 4 waves x 8 rows x kDownU = 192),
+// but at least 64 workgroups in all (at least 4 chunks per slice). Fewer,
+// fuller chunks mean fewer arrivals on each slice's counter and fewer partial
+// rows for the last workgroup to sum, while every wave still makes a single
+// round trip for its rows (swept at H = 2048: 32 chunks of 96 rows at
+// k = 3072 took 8.5 us, 16 of 192 rows 7.0 us, 8 of 384 rows (two batches)
+// 8.2 us; at k = 768, 8 chunks of 96 rows 5.7 us against 7.0 us for 24 of 32).
 struct DownPlan {
     int64_t S, R, rpc;
 };
@@ -335,9 +342,12 @@ static DownPlan down_plan(int64_t H, int64_t k) {
     const int64_t chunks = ceil_div64(ceil_div64(H, 8), 4);
     DownPlan p;
     p.S = ceil_div64(chunks, kSliceChunks);
-    int64_t target = 256 / p.S;
-    if (target < 4) target = 4;
     const int64_t step = static_cast<int64_t>(kDownWaves) * kGroupRows;
+    const int64_t batch = step * kDownU;
+    int64_t target = ceil_div64(k, batch);
+    int64_t floor_chunks = ceil_div64(64, p.S);
+    if (floor_chunks < 4) floor_chunks = 4;
+    if (target < floor_chunks) target = floor_chunks;
     p.rpc = ceil_div64(ceil_div64(k, target), step) * step;
     p.R = ceil_div64(k, p.rpc);
     return p;
