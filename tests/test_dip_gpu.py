@@ -86,7 +86,8 @@ def test_sparse_accumulate_one_hot_exact(ops):
 
 
 @pytest.mark.parametrize("k,H,gs", [(64, 512, 128), (37, 256, 64), (3072, 2048, 128), (1536, 2048, 128),
-                                    (768, 2048, 128), (200, 5120, 128), (50, 100, 8), (0, 256, 64)])
+                                    (768, 2048, 128), (200, 5120, 128), (50, 100, 8), (0, 256, 64),
+                                    (8704, 5120, 128)])  # Qwen3-14B shape at k/I = 0.5: 20 slices x 46 row chunks
 def test_sparse_accumulate_matches_oracle(ops, k, H, gs):
     p = int4_problem(max(k, 1), H, gs, seed=k + H)
     Wq, s = p["Wq"][:k], p["s"][:k]

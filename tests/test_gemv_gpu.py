@@ -41,6 +41,7 @@ def test_w4_basis_vectors_exact(ops, fn, K):
 SHAPES = [
     (512, 4096, 128), (512, 4099, 128),  # reference test shapes (4099 pads to 4224)
     (6144, 2048, 128), (2048, 6144, 128), (2048, 2048, 128), (1024, 2048, 128),  # Qwen3-1.7B
+    (2049, 6144, 128), (1000, 5120, 128),  # multi-pass tiles with a ragged last tile / a pass count of 2.5
     (37, 512, 32), (64, 256, 64), (33, 200, 8), (17, 1000, 40),  # non-32-multiple groups
     (1, 8, 8), (3, 100, 16),  # tiny / unaligned rows
 ]
