@@ -30,7 +30,8 @@ Also reported:
                   DIP MLP, graph-replayed over 28 distinct layers;
   decode          BASELINE config 5: greedy decode tok/s of the random-init 28-layer Qwen3-1.7B
                   shape, dense vs DIP vs cache-aware DIP at k/I = 0.5 (64-token prompt, 128 tokens);
-  cpu_baseline    the CPU oracle on a bounded sample (one thread).
+  cpu_baseline    the reference's CPU GEMV path (dequantize + fp32 torch.mv) on layer 0's GEMVs,
+                  at the job's host cores and one thread.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -628,32 +629,77 @@ def _cpu_model() -> str:
     return "unknown CPU"
 
 
-def cpu_baseline(layer_mats_cpu, budget_s: float = 8.0):
-    """The CPU oracle (scalar C) on layer 0's seven GEMVs, repeated to ~budget_s, on the host cores this job may use
-    (at most 16, the box's CPU share for one GPU) and, beside it, on one thread."""
-    from oracle import oracle as O
-
-    def run(threads):
+def _time_passes(fn, warmup: int = 20, iters: int = 100):
+    """median and p90 (seconds) of `iters` timed calls of fn after `warmup` untimed ones (bench/harness.py:36-74
+    of the reference: >= 20 warmup, >= 100 iterations)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(iters):
         t0 = time.perf_counter()
-        done_bytes, reps = 0, 0
-        while True:
-            for Wq, s, x, K in layer_mats_cpu:
-                O.gemv_w4_f64(Wq, s, x, K, GS, threads=threads)
-                done_bytes += int4_bytes(Wq.shape[0], K)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s:
-                return done_bytes / el / 1e9, reps, el
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts[min(len(ts) - 1, int(0.9 * len(ts)))]
+
+
+def cpu_baseline(layer0):
+    """The reference's CPU GEMV path (formats.dequantize, then fp32 torch.mv, rounded to fp16:
+    tests/test_m4_kernels.py:157-165, restated in oracle/cpu_path.py) over layer 0's seven GEMVs, one pass = all
+    seven, timed with 20 warmup and 100 timed passes (median and p90) on the host cores this job may use (at most
+    16, the box's CPU share for one GPU) and on one thread; beside it the matmul alone on pre-dequantized fp32
+    weights, and the C oracle's binary64 GEMV (the tests' checker) for reference. layer0: (q int8 [N, K],
+    scale fp32 [N, K/gs], Wq packed, x fp16 [K], K) per GEMV."""
+    import torch
+
+    from oracle import cpu_path
+    from oracle import oracle as O
 
     avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     cores = max(1, min(16, avail))
-    v_mt, reps_mt, el_mt = run(cores)
-    v_1, reps_1, el_1 = run(1)
-    return {"value": round(v_mt, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "single_thread_value": round(v_1, 4),
-            "sample": f"oracle/soi_oracle.c soi_ref_gemv_w4_f64 (binary64 accumulation, rows split over {cores} threads) "
-                      f"over layer 0's 7 INT4 GEMVs (26.8 MB), {reps_mt} passes in {el_mt:.1f} s; one thread: "
-                      f"{reps_1} passes in {el_1:.1f} s; host: {_cpu_model()}, {avail} cores available to the job"}
+    qs = [(torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(x), K) for q, s, _, x, K in layer0]
+    pass_bytes = sum(int4_bytes(q.shape[0], K) for q, _, _, K in qs)
+    pre = [cpu_path.dequantize_group(q, s, K, GS) for q, s, _, K in qs]
+
+    def dequant_mv():
+        for q, s, x, K in qs:
+            cpu_path.gemv_dequant_mv(q, s, x, K, GS)
+
+    def mv_only():
+        for W, (_, _, x, _) in zip(pre, qs):
+            cpu_path.gemv_mv_predequantized(W, x)
+
+    saved = torch.get_num_threads()
+    figures = {}
+    try:
+        for threads in (cores, 1):
+            torch.set_num_threads(threads)
+            for name, fn in (("dequant_mv", dequant_mv), ("mv_predequantized", mv_only)):
+                med, p90 = _time_passes(fn)
+                figures[f"{name}_{threads}t"] = {"median_ms": round(med * 1e3, 3), "p90_ms": round(p90 * 1e3, 3),
+                                                 "GBps": round(pass_bytes / med / 1e9, 4)}
+    finally:
+        torch.set_num_threads(saved)
+
+    # the binary64 scalar C checker, a bounded sample
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < 2.0:
+        for q, s, Wq, x, K in layer0:
+            O.gemv_w4_f64(Wq, s, x, K, GS, threads=cores)
+        reps += 1
+    checker = round(reps * pass_bytes / (time.perf_counter() - t0) / 1e9, 4)
+    main_fig = figures[f"dequant_mv_{cores}t"]
+    return {"value": main_fig["GBps"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "median_ms_per_pass": main_fig["median_ms"], "p90_ms_per_pass": main_fig["p90_ms"],
+            "single_thread_value": figures["dequant_mv_1t"]["GBps"], "figures": figures,
+            "c_oracle_binary64_GBps": checker,
+            "sample": f"the reference's CPU GEMV path (formats.dequantize of the int8 codes and fp32 scales, then "
+                      f"fp32 torch.mv, fp16 out; tests/test_m4_kernels.py:157-165, restated in oracle/cpu_path.py) "
+                      f"over layer 0's 7 INT4 g128 GEMVs ({pass_bytes} algorithmic bytes per pass), 20 warmup + 100 "
+                      f"timed passes, median, torch.set_num_threads({cores}); GB/s = algorithmic INT4 bytes / "
+                      f"time, as the GPU figure. Also: 1 thread, the matmul alone on pre-dequantized fp32, and "
+                      f"the C oracle's binary64 GEMV (the tests' checker, not the baseline). Host: {_cpu_model()}, "
+                      f"{avail} cores available to the job"}
 
 
 def main() -> int:
@@ -825,7 +871,7 @@ def main() -> int:
 
         for _, N, K in LAYER_SHAPES:
             q, s = O.quantize_group((torch.randn(N, K, generator=g) * 0.02).numpy(), GS)
-            layer0.append((O.pack_int4(q), s, torch.randn(K, generator=g).half().numpy(), K))
+            layer0.append((q, s, O.pack_int4(q), torch.randn(K, generator=g).half().numpy(), K))
         result["cpu_baseline"] = cpu_baseline(layer0)
         log("cpu baseline done")
     print(json.dumps(result))

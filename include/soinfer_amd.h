@@ -65,8 +65,10 @@ int soi_gemv_w4a16_group_lop3(const uint8_t* Wq, const float* scale, const uint1
  * Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs are DEVICE arrays of P device pointers
  * (problem p: Wq [N, ceil(K/8)*4], scale [N, num_groups], x [K], y [N]).
  * The pointer table is trusted (the caller validated the buffers); a problem
- * whose pointers are null, or not 16-byte aligned when K % 32 == 0, is
- * skipped. Each y is bit-identical to soi_gemv_w4a16_group_lop3 on that
+ * whose pointers are null is skipped, and one whose Wq or x is not 16-byte
+ * aligned when K % 32 == 0 gets NaN in every row of y (the vector loads
+ * need the alignment; soinfer.ops.GemvBatch / GemvGroup reject such problems
+ * before launch). Each y is bit-identical to soi_gemv_w4a16_group_lop3 on that
  * problem. No reference counterpart: amortises the ~2.6 us per-launch latency
  * floor of MI355X over many GEMVs (the reference launches one per matrix). */
 int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,
@@ -79,7 +81,8 @@ int soi_gemv_w4a16_batched(const uint8_t* const* Wq_ptrs, const float* const* sc
  * [class_N[c], class_K[c]] with ceil(class_K[c]/group_size) scale columns.
  * class_count, class_N, class_K are HOST arrays of num_classes (<= 8)
  * entries. Workgroups are laid out class by class in the given order (put
- * the longest rows first to keep the tail short). Each y is bit-identical to
+ * the longest rows first to keep the tail short). Null and misaligned
+ * problems are treated as in the batched form. Each y is bit-identical to
  * soi_gemv_w4a16_group_lop3 on that problem. No reference counterpart: one
  * launch for a whole decoder's independent GEMVs. */
 int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float* const* scale_ptrs,

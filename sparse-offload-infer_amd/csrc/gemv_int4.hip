@@ -159,7 +159,11 @@ struct RegX {
 // the residual add, the RMSNorm (one wave reduction) and, when x_out / h_out
 // are given (workgroup 0 only), their stores. So the norm's arithmetic runs
 // while the weight loads are in flight instead of before they are issued.
-// Same operations in the same order as the separate norm, so the same x.
+// The rounding points are those of the separate add and norm, but the sum of
+// squares runs in another order (per lane over its 32 elements, then one wave
+// reduction; the separate norm and NormX sum in other partitions), so inv and
+// hence each x element can differ from the separate norm's by one binary16
+// rounding.
 struct RegNormX {
     static constexpr bool kSinglePass = true;
     u32x4 t[4], e[4], g[4];  // a, d (when has_d), w
@@ -520,10 +524,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     gemv_int4_body<R, PU, VEC, CHUNK_SCALE, BITFIELD, FULL>(rows, N, x, ep, K, gs, cp);
 }
 
+// A problem of the batched / grouped forms whose W or x is not 16-byte aligned
+// while the vector path is compiled in cannot be read with dwordx4 loads: its
+// rows are set to NaN, so the output is never left unwritten (the host
+// wrappers reject such problems before launching).
+template <int R>
+__device__ __forceinline__ void misaligned_rows_nan(uint16_t* y, int64_t N, int64_t row0) {
+    const int64_t r = row0 + static_cast<int64_t>(threadIdx.x);
+    if (threadIdx.x < R && r < N) stg(y + r, static_cast<uint16_t>(0x7e00u));
+}
+
 // Batched form: P independent problems of one shape [N, K]; workgroup b takes
 // row tile b % tiles of problem b / tiles. Pointer tables live in device
-// memory; a problem whose pointers are not 16-byte aligned (when the vector
-// path is compiled in) or null writes nothing.
+// memory; a problem with a null pointer writes nothing, a misaligned one NaN
+// rows (misaligned_rows_nan).
 template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
 __device__ __forceinline__ void gemv_int4_batched_body(const uint8_t* const* __restrict__ Wp,
                                                        const float* const* __restrict__ Sp,
@@ -536,8 +550,12 @@ __device__ __forceinline__ void gemv_int4_batched_body(const uint8_t* const* __r
     const float* S = ldg(Sp + p);
     const uint16_t* x = ldg(Xp + p);
     uint16_t* y = ldg(Yp + p);
+    if (!W || !S || !x || !y) return;
     const uintptr_t bad = reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x);
-    if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
+    if (VEC && (bad & 15u)) {
+        misaligned_rows_nan<R>(y, N, static_cast<int64_t>(tile) * R);
+        return;
+    }
     const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
     DenseRows rows{W, S, row_bytes, G};
     gemv_int4_tile<R, PU, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,
@@ -680,8 +698,12 @@ __device__ __forceinline__ void gemv_int4_grouped_body(const uint8_t* const* __r
     const float* S = ldg(Sp + p);
     const uint16_t* x = ldg(Xp + p);
     uint16_t* y = ldg(Yp + p);
+    if (!W || !S || !x || !y) return;
     const uintptr_t bad = reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x);
-    if (!W || !S || !x || !y || (VEC && (bad & 15u))) return;
+    if (VEC && (bad & 15u)) {
+        misaligned_rows_nan<R>(y, N, static_cast<int64_t>(tile) * R);
+        return;
+    }
     const int64_t row_bytes = static_cast<int64_t>((K + 7) >> 3) * 4;
     DenseRows rows{W, S, row_bytes, G};
     gemv_int4_tile<R, 1, VEC, CHUNK_SCALE, true, FULL>(rows, N, PlainX{x}, StoreY{y}, K, gs,

@@ -27,8 +27,9 @@ constexpr int kWave = 64;
 // 16 zero bytes: the load target of lanes / rows that have nothing to read,
 // so loads can be issued unconditionally (no branch, no serialising wait)
 // and contribute exact zeros.
-// (Never written; one private copy per code object.)
-__device__ uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
+// (Never written; one private copy per code object. 16-byte aligned: it is
+// the target of dwordx4 loads.)
+__device__ __attribute__((aligned(16))) uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
 
 // Loads through the global address space (global_load_*, not flat_load_*):
 // pointers read from memory or chosen by a select lose the address-space

@@ -1,56 +1,84 @@
-"""Copy streams with transfer-done and read-done events for double / triple buffered weight prefetch.
+"""Copy streams for double / triple buffered weight prefetch, with write-after-read protection.
 
-Same interface and semantics as the reference's StreamManager
-(python/soinfer/offload/stream_manager.py:10-86): buffer i has its own copy
-stream, an event marking "transfer into buffer i done" and an event marking
-"the last reader of buffer i done". prefetch(i) first makes the copy stream
-wait for buffer i's read-done event, so a new transfer never overwrites data a
-kernel launched earlier is still reading (the write-after-read hazard the
-reference hit once kernels got fast); wait(i) orders the current stream after
-the transfer; mark_read_done(i) records the reader's completion point.
+Public surface of the reference's StreamManager
+(python/soinfer/offload/stream_manager.py:10-86, driven by WeightPipeline in
+generate.py:85-138): prefetch(i, dst, src) starts an asynchronous copy of
+pinned host bytes into device buffer i, wait(i) orders the current stream
+after it, mark_read_done(i) records where the kernels reading buffer i were
+issued, and the next prefetch into buffer i starts only after that point, so
+a transfer never overwrites data a kernel launched earlier is still reading.
+synchronize(i) blocks the host until buffer i's copy has landed.
 
-All streams use the default priority. On MI355X the copies are
-hipMemcpyAsync from pinned host memory, executed by the SDMA engines.
+Design here: each buffer is a CopySlot that owns its copy stream and two
+events, `landed` (its latest copy is complete) and `released` (its latest
+readers were issued before this point), plus a flag telling whether
+`released` has ever been recorded: the first transfer into a buffer has no
+reader to wait for. All streams keep the default priority; the copies are
+hipMemcpyAsync from pinned memory, run by the SDMA engines.
 """
 from __future__ import annotations
+
+from dataclasses import dataclass, field
 
 import torch
 
 
+@dataclass
+class CopySlot:
+    """One prefetch buffer's stream and its two fences."""
+
+    stream: torch.cuda.Stream
+    landed: torch.cuda.Event = field(default_factory=torch.cuda.Event)
+    released: torch.cuda.Event = field(default_factory=torch.cuda.Event)
+    has_reader: bool = False
+
+    def start_copy(self, dst: torch.Tensor, src: torch.Tensor) -> None:
+        if self.has_reader:
+            self.stream.wait_event(self.released)
+        with torch.cuda.stream(self.stream):
+            dst.copy_(src, non_blocking=True)
+            self.landed.record()
+
+    def release(self, on: torch.cuda.Stream) -> None:
+        self.released.record(on)
+        self.has_reader = True
+
+
 class StreamManager:
+    """num_buffers copy slots (2 for double buffering, 3 for triple)."""
+
     def __init__(self, num_buffers: int = 2):
-        if num_buffers < 1:
-            raise ValueError("num_buffers must be >= 1")
-        self.num_buffers = num_buffers
-        self.streams = [torch.cuda.Stream() for _ in range(num_buffers)]
-        self.events = [torch.cuda.Event() for _ in range(num_buffers)]
-        # never recorded until the first mark_read_done: waiting on an unrecorded event is a no-op, which is
-        # right for a buffer's first transfer
-        self.read_done_events = [torch.cuda.Event() for _ in range(num_buffers)]
+        if int(num_buffers) < 1:
+            raise ValueError(f"StreamManager needs at least one buffer, got {num_buffers}")
+        self.num_buffers = int(num_buffers)
+        self.slots = [CopySlot(torch.cuda.Stream()) for _ in range(self.num_buffers)]
+
+    def _slot(self, buf_idx: int) -> CopySlot:
+        if not 0 <= buf_idx < self.num_buffers:
+            raise IndexError(f"buffer {buf_idx} does not exist (this manager has {self.num_buffers})")
+        return self.slots[buf_idx]
 
     def prefetch(self, buf_idx: int, gpu_buffer: torch.Tensor, host_data: torch.Tensor) -> None:
-        """Asynchronous copy host_data (pinned) -> gpu_buffer on buffer buf_idx's stream, after that buffer's
-        last reader; records the transfer-done event. Returns immediately."""
+        """Queue host_data (pinned) -> gpu_buffer on buffer buf_idx's copy stream, behind the buffer's previous
+        readers. Returns at once."""
+        slot = self._slot(buf_idx)
         if not host_data.is_pinned():
-            raise ValueError("prefetch: host_data must be pinned (PinnedWeightStore) for an asynchronous copy")
-        if gpu_buffer.shape != host_data.shape:
-            raise ValueError(f"prefetch: gpu_buffer shape {tuple(gpu_buffer.shape)} != host_data shape "
-                             f"{tuple(host_data.shape)}")
-        stream = self.streams[buf_idx]
-        stream.wait_event(self.read_done_events[buf_idx])
-        with torch.cuda.stream(stream):
-            gpu_buffer.copy_(host_data, non_blocking=True)
-        self.events[buf_idx].record(stream)
+            raise ValueError("StreamManager.prefetch: an asynchronous host->device copy needs pinned host_data "
+                             "(e.g. a PinnedWeightStore view)")
+        if tuple(gpu_buffer.shape) != tuple(host_data.shape):
+            raise ValueError(f"StreamManager.prefetch: destination {tuple(gpu_buffer.shape)} and source "
+                             f"{tuple(host_data.shape)} differ in shape")
+        slot.start_copy(gpu_buffer, host_data)
 
     def wait(self, buf_idx: int) -> None:
-        """Order the current stream after buffer buf_idx's transfer (a device-side wait, not a host sync)."""
-        torch.cuda.current_stream().wait_event(self.events[buf_idx])
+        """Make the current stream wait (on the device) for buffer buf_idx's latest copy."""
+        torch.cuda.current_stream().wait_event(self._slot(buf_idx).landed)
 
     def mark_read_done(self, buf_idx: int) -> None:
-        """Record, on the current stream, that the kernels reading buffer buf_idx have been issued; the next
-        prefetch into buf_idx waits for them."""
-        self.read_done_events[buf_idx].record(torch.cuda.current_stream())
+        """Declare that every kernel reading buffer buf_idx has been issued on the current stream; the next
+        prefetch into the buffer waits for them to finish."""
+        self._slot(buf_idx).release(torch.cuda.current_stream())
 
     def synchronize(self, buf_idx: int) -> None:
-        """Host-side wait for buffer buf_idx's transfer (tests and timing)."""
-        self.events[buf_idx].synchronize()
+        """Block the host until buffer buf_idx's latest copy has landed."""
+        self._slot(buf_idx).landed.synchronize()

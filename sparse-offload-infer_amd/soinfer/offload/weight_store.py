@@ -1,30 +1,35 @@
-"""One pinned host arena holding quantized weight matrices, rows as the addressable unit.
+"""Pinned host arena for packed weight matrices, addressable row by row.
 
-Same interface and semantics as the reference's PinnedWeightStore
-(python/soinfer/offload/weight_store.py:26-117): a single pinned allocation
-sized up front, matrices registered once in order at fixed byte offsets, each
-row one contiguous span, so any subset of a matrix's rows can be fetched
-without touching the rest.
+Public surface of the reference's PinnedWeightStore / WeightHandle
+(python/soinfer/offload/weight_store.py:26-117, used by load_hf_checkpoint.py
+:95-146, generate.py:114,287,294 and hot_cache.py:300-304): one page-locked
+allocation sized up front, matrices appended in registration order with no
+padding between them, each row one contiguous byte span, so any subset of a
+matrix's rows can be copied or read without touching the rest.
 
-On MI355X the arena is also read in place by the GPU: pinned host memory is
-mapped into the device address space, and device_address() gives the address
-kernels use (the hot-cache GEMVs and the device row gather read miss rows
-straight from it over PCIe, with no staging copy).
+Design here: the arena is a ledger of spans. Each registered matrix is a
+WeightHandle (name, byte offset, rows, row width) appended to an ordered list;
+the next free byte is the end of the last span, so the ledger is the only
+state. The arena is also a GPU-visible buffer: pinned host memory is mapped
+into the device address space, and device_address() returns where a kernel
+finds a matrix through that mapping (the hot-cache GEMVs and the device row
+gather read miss rows in place over PCIe, with no staging copy).
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterable
+from typing import Iterable, Iterator
 
 import torch
 
 
 @dataclass(frozen=True)
 class WeightHandle:
-    """One matrix's rows inside a PinnedWeightStore arena (offset is the store's business)."""
+    """Where one matrix lives in a PinnedWeightStore: rows [offset, offset + nbytes) of the arena, each
+    row_nbytes wide."""
 
     name: str
-    offset: int  # byte offset into the arena
+    offset: int
     num_rows: int
     row_nbytes: int
 
@@ -32,81 +37,100 @@ class WeightHandle:
     def nbytes(self) -> int:
         return self.num_rows * self.row_nbytes
 
+    @property
+    def end(self) -> int:
+        return self.offset + self.nbytes
+
+    def row_span(self, row: int) -> tuple[int, int]:
+        """[start, stop) arena byte range of one row."""
+        start = self.offset + row * self.row_nbytes
+        return start, start + self.row_nbytes
+
 
 def plan_bytes(shapes: Iterable[tuple[int, int]]) -> int:
-    """Arena size for matrices of the given [num_rows, row_nbytes] shapes, registered back to back."""
-    total = 0
-    for rows, row_nbytes in shapes:
-        if rows < 0 or row_nbytes < 0:
-            raise ValueError("negative matrix shape")
-        total += rows * row_nbytes
-    return total
+    """Arena bytes for matrices of the given (num_rows, row_nbytes) shapes appended back to back."""
+    need = 0
+    for shape in shapes:
+        rows, width = (int(v) for v in shape)
+        if min(rows, width) < 0:
+            raise ValueError(f"plan_bytes: a matrix shape cannot be negative, got {tuple(shape)}")
+        need += rows * width
+    return need
 
 
 class PinnedWeightStore:
-    """A single pinned host allocation holding quantized matrices row-major. total_bytes is fixed at
-    construction: pinned memory is page-locked, so the whole model gets one allocation instead of many small
-    ones."""
+    """One pinned uint8 arena of total_bytes holding row-major packed matrices. The size is fixed: the whole
+    model is page-locked in a single allocation rather than many small ones."""
 
     def __init__(self, total_bytes: int):
-        if total_bytes <= 0:
-            raise ValueError("total_bytes must be positive")
+        total_bytes = int(total_bytes)
+        if total_bytes < 1:
+            raise ValueError(f"PinnedWeightStore needs a positive size, got {total_bytes} bytes")
         self.arena = torch.empty(total_bytes, dtype=torch.uint8, pin_memory=True)
-        self._write_offset = 0
-        self._handles: dict[str, WeightHandle] = {}
-        self._device_base = None
+        self._ledger: list[WeightHandle] = []
+        self._index: dict[str, int] = {}
+        self._mapped_base: int | None = None
 
-    def register(self, name: str, data: torch.Tensor) -> WeightHandle:
-        """Copy data ([num_rows, row_nbytes] uint8, any device) into the next free span; returns its handle.
-        Registration order fixes the layout."""
-        if name in self._handles:
-            raise ValueError(f"weight {name!r} already registered")
-        if data.dtype != torch.uint8 or data.dim() != 2:
-            raise ValueError(f"register({name!r}): data must be 2D uint8 [num_rows, row_nbytes], got "
-                             f"{tuple(data.shape)} {data.dtype}")
-        num_rows, row_nbytes = data.shape
-        nbytes = num_rows * row_nbytes
-        end = self._write_offset + nbytes
-        if end > self.arena.numel():
-            raise ValueError(f"register({name!r}): arena overflow -- {nbytes} bytes requested, "
-                             f"{self.arena.numel() - self._write_offset} remain")
-        self.arena[self._write_offset:end].view(num_rows, row_nbytes).copy_(data)
-        handle = WeightHandle(name, self._write_offset, num_rows, row_nbytes)
-        self._handles[name] = handle
-        self._write_offset = end
-        return handle
-
-    def handle(self, name: str) -> WeightHandle:
-        return self._handles[name]
-
-    def matrix_view(self, handle: WeightHandle) -> torch.Tensor:
-        """[num_rows, row_nbytes] uint8 view of the pinned arena (no copy)."""
-        return self.arena[handle.offset:handle.offset + handle.nbytes].view(handle.num_rows, handle.row_nbytes)
-
-    def row_view(self, handle: WeightHandle, row: int) -> torch.Tensor:
-        """One row, [row_nbytes] uint8 view (no copy)."""
-        if not 0 <= row < handle.num_rows:
-            raise IndexError(f"row {row} out of range for {handle.name!r} (num_rows={handle.num_rows})")
-        start = handle.offset + row * handle.row_nbytes
-        return self.arena[start:start + handle.row_nbytes]
-
-    def rows_view(self, handle: WeightHandle, rows: torch.Tensor) -> torch.Tensor:
-        """The selected rows (1D int64 indices) gathered into a new contiguous tensor (a copy)."""
-        return self.matrix_view(handle).index_select(0, rows).contiguous()
-
-    def device_address(self, handle: WeightHandle) -> int:
-        """Device-visible address of the matrix's first byte (the arena's device mapping + offset), for kernels
-        that read rows in place."""
-        if self._device_base is None:
-            from .. import _C
-
-            self._device_base = _C.host_device_pointer(self.arena)
-        return self._device_base + handle.offset
-
+    # ---- layout ----
     @property
     def bytes_used(self) -> int:
-        return self._write_offset
+        return self._ledger[-1].end if self._ledger else 0
 
     @property
     def bytes_total(self) -> int:
         return self.arena.numel()
+
+    def __len__(self) -> int:
+        return len(self._ledger)
+
+    def __contains__(self, name: str) -> bool:
+        return name in self._index
+
+    def __iter__(self) -> Iterator[WeightHandle]:
+        return iter(self._ledger)
+
+    def register(self, name: str, data: torch.Tensor) -> WeightHandle:
+        """Append data ([num_rows, row_nbytes] uint8 on any device) right after the previous matrix and return
+        its handle. The registration order is the arena layout."""
+        if name in self._index:
+            raise ValueError(f"PinnedWeightStore.register: the name {name!r} is taken")
+        if not (isinstance(data, torch.Tensor) and data.dtype == torch.uint8 and data.dim() == 2):
+            got = (tuple(data.shape), data.dtype) if isinstance(data, torch.Tensor) else type(data).__name__
+            raise ValueError(f"PinnedWeightStore.register({name!r}): expected a 2-D uint8 matrix, got {got}")
+        h = WeightHandle(name, self.bytes_used, int(data.shape[0]), int(data.shape[1]))
+        if h.end > self.bytes_total:
+            raise ValueError(f"PinnedWeightStore.register({name!r}): {h.nbytes} bytes do not fit, only "
+                             f"{self.bytes_total - h.offset} of the {self.bytes_total}-byte arena are free")
+        self.matrix_view(h).copy_(data)
+        self._index[name] = len(self._ledger)
+        self._ledger.append(h)
+        return h
+
+    def handle(self, name: str) -> WeightHandle:
+        return self._ledger[self._index[name]]
+
+    # ---- views (no copies) and gathers ----
+    def matrix_view(self, handle: WeightHandle) -> torch.Tensor:
+        """The matrix as a [num_rows, row_nbytes] view of the arena."""
+        return self.arena.narrow(0, handle.offset, handle.nbytes).view(handle.num_rows, handle.row_nbytes)
+
+    def row_view(self, handle: WeightHandle, row: int) -> torch.Tensor:
+        """Row `row` of the matrix as a [row_nbytes] view of the arena."""
+        if row < 0 or row >= handle.num_rows:
+            raise IndexError(f"{handle.name!r} has rows 0..{handle.num_rows - 1}; row {row} does not exist")
+        start, _ = handle.row_span(row)
+        return self.arena.narrow(0, start, handle.row_nbytes)
+
+    def rows_view(self, handle: WeightHandle, rows: torch.Tensor) -> torch.Tensor:
+        """A new contiguous [len(rows), row_nbytes] tensor holding the listed rows (int64 indices, any order)."""
+        return torch.index_select(self.matrix_view(handle), 0, rows)
+
+    # ---- device mapping ----
+    def device_address(self, handle: WeightHandle) -> int:
+        """Address of the matrix's first byte in the GPU's mapping of the arena, for kernels that read its rows
+        in place."""
+        if self._mapped_base is None:
+            from .. import _C
+
+            self._mapped_base = int(_C.host_device_pointer(self.arena))
+        return self._mapped_base + handle.offset

@@ -39,6 +39,14 @@ def gemv_w4a16_group_lop3(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch
     return _C.gemv_w4a16_group_lop3(Wq_packed, scale, x, K, group_size)
 
 
+def _check_aligned16(what: str, K: int, W: torch.Tensor, x: torch.Tensor) -> None:
+    """The batched and grouped kernels read Wq and x with 16-byte loads when K % 32 == 0; a misaligned
+    problem there would only come back as NaN rows, so it is rejected before launch."""
+    if K % 32 == 0 and (W.data_ptr() % 16 or x.data_ptr() % 16):
+        raise RuntimeError(f"{what}: Wq and x must be 16-byte aligned when K % 32 == 0 (got Wq at "
+                           f"{W.data_ptr():#x}, x at {x.data_ptr():#x}); pass a .clone() of an offset view")
+
+
 class GemvBatch:
     """P independent INT4 GEMVs of one shape [N, K] executed in ONE kernel launch.
 
@@ -66,6 +74,7 @@ class GemvBatch:
                 raise RuntimeError("GemvBatch: every y must be a contiguous float16 [N] tensor")
             if not all(t.device == dev for t in (W, s, x, y)):
                 raise RuntimeError("GemvBatch: all tensors must be on one device")
+            _check_aligned16("GemvBatch", K, W, x)
         self._keep = (list(Wqs), list(scales), list(xs), list(ys))
         self.ys = self._keep[3]
         self.N, self.K, self.group_size = N, K, group_size
@@ -103,6 +112,7 @@ class GemvGroup:
                 raise RuntimeError("GemvGroup: every x must be a contiguous float16 [K] tensor")
             if not all(t.device == dev for t in (W, s, x)):
                 raise RuntimeError("GemvGroup: all tensors must be on one device")
+            _check_aligned16("GemvGroup", K, W, x)
             shapes.append((N, K))
         classes = sorted(set(shapes), key=lambda nk: (-nk[1], -nk[0]))
         if len(classes) > 8:

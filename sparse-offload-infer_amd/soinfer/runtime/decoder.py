@@ -281,6 +281,10 @@ class DecodeEngine:
         self._x_final = self.x
         self._graph_layers = None
         self._graph_gen = None
+        # eager runs only: called as layer_hook(l) after layer l's MLP has been issued (the MLP output is in
+        # self.down; in DIP modes gate is in self.gu[:I] and the selection in self.idx / self.cnt, and the MLP
+        # input in self.h except for the fused dense and dense-up schedules); never set while capture() runs
+        self.layer_hook = None
 
     # ---- cache-aware DIP: hot rows in HBM, the rest in pinned host memory ----
     def _setup_cache(self, hot_channels):
@@ -457,6 +461,8 @@ class DecodeEngine:
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
             _C.residual_rmsnorm_(self.x, self.o, L.post_norm, self.h, eps)
             self._mlp(l, L)
+            if self.layer_hook is not None:
+                self.layer_hook(l)
         _C.residual_rmsnorm_(self.x, self.down, self.w.final_norm, self.hn, eps)
         self._x_final = self.x
         _C.advance_position(self.pos, 1)
@@ -486,52 +492,59 @@ class DecodeEngine:
                                        self.k_cache[l], self.v_cache[l], eps)
                 _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
-            if self.mode == "dense":
-                gW, gS = gu_il
-                _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, None, self.mlp_h, H, gs,
-                                           True)
-                cur, other = other, cur
-                _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
-                continue
-            gate = self.gu[:I]
-            if self.dip_dense_up:
-                gW, gS = gu_il
-                _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
-                                                   H, gs)
-                cur, other = other, cur
-                _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx,
-                                              self.cnt, self.down, H, gs, self.sd_ws)
-                self._count_selection(l)
-                continue
-            gW, gS = L.gate(I)
-            _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
+            self._mlp_fused(l, L, gu_il, cur, other)
             cur, other = other, cur
-            _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
-            self._count_selection(l)
-            uW, uS = L.up(I)
-            if self.mode == "dip":
-                _C.gemv_w4a16_indexed_silu_into(uW, uS, self.idx, self.h, gate, self.h_sel, H, gs)
-                _C.gemv_w4a16_indexed_accumulate_into(L.down_T_Wq, L.down_T_scale, self.idx, self.h_sel, self.down,
-                                                      H, gs, self.sd_ws)
-                continue
-            cache = self.caches[l]
-            if self.miss_path == "direct":
-                # the up GEMV's waves also copy their down^T miss rows to staging (whole-row PCIe reads, overlapped
-                # with the up rows); the down accumulate then reads hits from the cache and misses from staging
-                cp = (self.host_down[l], self.st_dn) if self.down_copy else (None, None)
-                _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of,
-                                                self.idx, self.h, gate, self.h_sel, H, gs, *cp)
-                _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
-                                             cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws,
-                                             self.st_dn if self.down_copy else None)
-                continue
-            self._fetch_misses(l, L, uS)
-            _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc,
-                                           self.idx, self.h, gate, self.h_sel, H, gs)
-            _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
-                                        self.h_sel, self.down, H, gs, self.sd_ws)
+            if self.layer_hook is not None:
+                self.layer_hook(l)
         _C.final_norm_advance(cur, self.down, self.w.final_norm, self.hn, eps, self.pos)
         self._x_final = cur
+
+    def _mlp_fused(self, l: int, L: LayerWeights, gu_il, cur: torch.Tensor, other: torch.Tensor):
+        """Layer l's MLP with the residual add + RMSNorm on load: the first launch reads cur and self.o and
+        writes cur + o to other (the next residual); the output lands in self.down."""
+        c, eps = self.c, self.c.rms_eps
+        H, I, gs = c.hidden, c.intermediate, c.group_size
+        if self.mode == "dense":
+            gW, gS = gu_il
+            _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, None, self.mlp_h, H, gs,
+                                       True)
+            _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
+            return
+        gate = self.gu[:I]
+        if self.dip_dense_up:
+            gW, gS = gu_il
+            _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
+                                               H, gs)
+            _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx,
+                                          self.cnt, self.down, H, gs, self.sd_ws)
+            self._count_selection(l)
+            return
+        gW, gS = L.gate(I)
+        _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
+        _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
+        self._count_selection(l)
+        uW, uS = L.up(I)
+        if self.mode == "dip":
+            _C.gemv_w4a16_indexed_silu_into(uW, uS, self.idx, self.h, gate, self.h_sel, H, gs)
+            _C.gemv_w4a16_indexed_accumulate_into(L.down_T_Wq, L.down_T_scale, self.idx, self.h_sel, self.down,
+                                                  H, gs, self.sd_ws)
+            return
+        cache = self.caches[l]
+        if self.miss_path == "direct":
+            # the up GEMV's waves also copy their down^T miss rows to staging (whole-row PCIe reads, overlapped
+            # with the up rows); the down accumulate then reads hits from the cache and misses from staging
+            cp = (self.host_down[l], self.st_dn) if self.down_copy else (None, None)
+            _C.gemv_dip_cached_up_silu_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of,
+                                            self.idx, self.h, gate, self.h_sel, H, gs, *cp)
+            _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
+                                         cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws,
+                                         self.st_dn if self.down_copy else None)
+            return
+        self._fetch_misses(l, L, uS)
+        _C.gemv_dip_fused_up_silu_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc,
+                                       self.idx, self.h, gate, self.h_sel, H, gs)
+        _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
+                                    self.h_sel, self.down, H, gs, self.sd_ws)
 
     @property
     def x_final(self) -> torch.Tensor:
@@ -607,18 +620,26 @@ class DecodeEngine:
         return list(prompt_ids) + out
 
 
-def calibrate_hot_channels(w: DecoderWeights, dip_k: int, calib_tokens, cache_fraction: float = 0.2):
-    """Hot set per layer: the cache_fraction * I most frequently selected channels (ties to the lower index)
-    while decoding calib_tokens with the DIP engine (reference generate.py:579-609 counts selections the same
-    way; StaticFrequencyPolicy orders them)."""
-    from ..offload.hot_cache import StaticFrequencyPolicy
-
+def calibrate_channel_counts(w: DecoderWeights, dip_k: int, calib_tokens) -> list:
+    """Per layer, counts[c] = how many of the calib_tokens steps selected channel c, feeding the tokens one at a
+    time through the DIP engine (eagerly) as the reference's calibrate_channel_frequencies does
+    (generate.py:579-609). int64 [I] tensors on the engine's device; each sums to len(calib_tokens) * dip_k."""
     c = w.config
     eng = DecodeEngine(w, "dip", dip_k=dip_k, max_new_tokens=1)
     eng.counts = [torch.zeros(c.intermediate, dtype=torch.int64, device=eng.device) for _ in range(c.layers)]
     eng.reset()
     eng.prefill(calib_tokens, use_graph=False)
-    C = int(round(cache_fraction * c.intermediate))
-    hot = [StaticFrequencyPolicy(cnt.cpu(), C).hot_indices.tolist() for cnt in eng.counts]
+    counts = eng.counts
     del eng
-    return hot
+    return counts
+
+
+def calibrate_hot_channels(w: DecoderWeights, dip_k: int, calib_tokens, cache_fraction: float = 0.2):
+    """Hot set per layer: the cache_fraction * I most frequently selected channels (ties to the lower index)
+    while decoding calib_tokens with the DIP engine (calibrate_channel_counts; StaticFrequencyPolicy orders
+    them, hot_cache.py:67-95 of the reference)."""
+    from ..offload.hot_cache import StaticFrequencyPolicy
+
+    C = int(round(cache_fraction * w.config.intermediate))
+    return [StaticFrequencyPolicy(cnt.cpu(), C).hot_indices.tolist()
+            for cnt in calibrate_channel_counts(w, dip_k, calib_tokens)]

@@ -129,10 +129,11 @@ def test_w8_basis_vectors_exact(ops, gran, gs):
 
 
 @pytest.mark.parametrize("gran,gs", W8 + [("group", 32), ("group", 4), ("group", 12)])
-# tiles: (512, 4096) 1 row x 4 passes; (6144, 2048) 4 x 2; (2048, 6144) 2 x 3; (1024, 2048) 1 x 2 -- all full;
+# tiles: (512, 4096) 1 row x 4 passes; (6144, 2048) 4 x 2; (2048, 6144) 2 x 3; (2048, 2048) and (1024, 2048) x 2
+# passes (the q/o and k/v projections) -- all full;
 # (4097, 3072) 2 x 3 with a partial last tile; (8200, 1040) 4 x 2 with idle lanes; (2049, 100) and (7, 96) ragged
-@pytest.mark.parametrize("N,K", [(512, 4096), (6144, 2048), (2048, 6144), (1024, 2048), (7, 96), (4097, 3072),
-                                 (8200, 1040), (2049, 100)])
+@pytest.mark.parametrize("N,K", [(512, 4096), (6144, 2048), (2048, 6144), (2048, 2048), (1024, 2048), (7, 96),
+                                 (4097, 3072), (8200, 1040), (2049, 100)])
 def test_w8_matches_oracle(ops, gran, gs, N, K):
     if gs and K % gs:
         pytest.skip("K not a multiple of the group size in this grid")
@@ -217,3 +218,54 @@ def test_grouped_rejects_bad_arguments(ops):
     many = [int4_problem(8 * (i + 1), 64, 32, seed=i) for i in range(9)]
     with pytest.raises(RuntimeError):
         ops.GemvGroup([(p["Wq_d"], p["s_d"], p["x_d"], 64) for p in many], 32)  # 9 distinct shapes
+
+
+# ---------------------------------------------------------------------------
+# misaligned operands of the batched / grouped forms
+# ---------------------------------------------------------------------------
+
+def _offset_view(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of t starting 2 bytes past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    v = buf[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    assert v.is_contiguous() and v.data_ptr() % 16 == 2
+    return v
+
+
+def test_batched_and_grouped_reject_misaligned_views(ops):
+    p = int4_problem(1024, 2048, 128, seed=7)
+    xo = _offset_view(p["x_d"])
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ops.GemvBatch([p["Wq_d"]], [p["s_d"]], [xo], 2048, 128)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ops.GemvGroup([(p["Wq_d"], p["s_d"], xo, 2048)], 128)
+    # K % 32 != 0 takes the dword path, where any 2-byte aligned x is fine
+    r = int4_problem(33, 200, 8, seed=8)
+    xr = _offset_view(r["x_d"])
+    ys = ops.GemvGroup([(r["Wq_d"], r["s_d"], xr, r["K"])], 8).run()
+    assert torch.equal(ys[0], ops.gemv_w4a16_group_lop3(r["Wq_d"], r["s_d"], r["x_d"], r["K"], 8))
+
+
+def test_batched_table_with_misaligned_x_writes_nan_rows(ops):
+    """Through the raw pointer tables (no host check) a misaligned problem comes back as NaN rows, never as
+    unwritten memory; the aligned problem in the same launch is unaffected."""
+    from soinfer import _C
+
+    a = int4_problem(1024, 2048, 128, seed=9)
+    b = int4_problem(1024, 2048, 128, seed=10)
+    xb = _offset_view(b["x_d"])
+    ys = [torch.zeros(1024, dtype=torch.float16, device="cuda") for _ in range(2)]
+
+    def table(ts):
+        return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device="cuda")
+
+    _C.gemv_w4a16_batched(table([a["Wq_d"], b["Wq_d"]]), table([a["s_d"], b["s_d"]]), table([a["x_d"], xb]),
+                          table(ys), 1024, 2048, 128)
+    assert torch.equal(ys[0], ops.gemv_w4a16_group_lop3(a["Wq_d"], a["s_d"], a["x_d"], 2048, 128))
+    assert torch.isnan(ys[1]).all()
+    yg = [torch.zeros(1024, dtype=torch.float16, device="cuda") for _ in range(2)]
+    _C.gemv_w4a16_grouped(table([a["Wq_d"], b["Wq_d"]]), table([a["s_d"], b["s_d"]]), table([a["x_d"], xb]),
+                          table(yg), [2], [1024], [2048], 128)
+    assert torch.equal(yg[0], ys[0])
+    assert torch.isnan(yg[1]).all()

@@ -402,3 +402,48 @@ def test_threaded_gemv_equals_single_thread():
         s = r.random((N, -(-K // 32)), dtype=np.float32)
         x = r.standard_normal(K).astype(np.float16)
         assert np.array_equal(O.gemv_w4_f64(Wq, s, x, K, 32, threads=threads), O.gemv_w4_f64(Wq, s, x, K, 32))
+
+
+# ---------------------------------------------------------------------------
+# the reference's CPU GEMV path (oracle/cpu_path.py), the CPU baseline of bench.py
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K,gs", [(16, 256, 128), (9, 4099, 128), (7, 200, 8), (64, 2048, 128)])
+def test_cpu_path_dequantize_equals_c_oracle(N, K, gs):
+    """dequantize_group is fl(q*s) per element, exactly the C oracle's soi_ref_dequant_int4 on the packed bytes."""
+    from oracle import cpu_path
+
+    w = (torch.randn(N, K, generator=torch.Generator().manual_seed(N + K)) * 0.02).numpy()
+    q, s = O.quantize_group(w, gs)
+    Wd = cpu_path.dequantize_group(torch.from_numpy(q), torch.from_numpy(s), K, gs)
+    ref = O.dequant_int4(O.pack_int4(q), s, q.shape[1], gs)[:, :K]
+    assert Wd.shape == (N, K) and np.array_equal(Wd.numpy(), ref)
+
+
+@pytest.mark.parametrize("N,K,gs", [(33, 4099, 128), (6144, 2048, 128), (5, 64, 32)])
+def test_cpu_path_gemv_within_f16_rounding_of_oracle(N, K, gs):
+    from oracle import cpu_path
+
+    g = torch.Generator().manual_seed(3 + N)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    q, s = O.quantize_group(w, gs)
+    x = torch.randn(q.shape[1], generator=g).half()
+    y = cpu_path.gemv_dequant_mv(torch.from_numpy(q), torch.from_numpy(s), x, K, gs)
+    ref = O.gemv_w4_f64(O.pack_int4(q), s, x.numpy(), q.shape[1], gs)
+    err = np.abs(y.double().numpy() - ref)
+    assert err.max() <= 1e-3 * np.abs(ref).max()
+    Wd = cpu_path.dequantize_group(torch.from_numpy(q), torch.from_numpy(s), K, gs)
+    assert torch.equal(cpu_path.gemv_mv_predequantized(Wd, x), y)
+
+
+def test_cpu_path_basis_vector_gives_f16_column():
+    from oracle import cpu_path
+
+    w = (torch.randn(8, 256, generator=torch.Generator().manual_seed(1)) * 3.0).numpy()
+    q, s = O.quantize_group(w, 128)
+    Wd = O.dequant_int4(O.pack_int4(q), s, 256, 128)
+    for k in (0, 77, 255):
+        e = torch.zeros(256, dtype=torch.float16)
+        e[k] = 1.0
+        y = cpu_path.gemv_dequant_mv(torch.from_numpy(q), torch.from_numpy(s), e, 256, 128)
+        assert np.array_equal(y.numpy(), Wd[:, k].astype(np.float16))
