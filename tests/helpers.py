@@ -4,9 +4,12 @@ Tolerance for floating-point outputs (GEMV, sparse accumulate, attention): the
 HIP output (binary16) is compared with the oracle's binary64 result `ref`:
   normalized:  max|out - ref| <= 1e-3 * max|ref|
   per element: |out - ref|   <= 1e-3 * |ref| + 1e-5 * max|ref|
-Binary16 rounding alone contributes <= 2^-11 |ref| (4.9e-4); fp32 accumulation
-error is far below the 1e-5 floor at these sizes. Index, byte and descriptor
-outputs are compared exactly.
+Binary16 rounding alone contributes <= 2^-11 |ref| (4.9e-4). The INT4 GEMVs
+accumulate with v_dot2_f32_f16, whose rounding is not round-to-nearest-even:
+over K = 6144 their fp32 error reaches ~2e-5 * max|ref| at cancelling outputs
+(tests/test_gemv_gpu.py::test_int4_gemv_accumulation_error_bound measures it),
+so comparisons of long-K dense GEMVs pass floor=5e-5; elsewhere the 1e-5 floor
+holds. Index, byte and descriptor outputs are compared exactly.
 """
 from __future__ import annotations
 
@@ -19,7 +22,7 @@ TOL = 1e-3
 FLOOR = 1e-5
 
 
-def assert_close(out: torch.Tensor, ref: np.ndarray, label: str = "", tol: float = TOL) -> None:
+def assert_close(out: torch.Tensor, ref: np.ndarray, label: str = "", tol: float = TOL, floor: float = FLOOR) -> None:
     a = out.detach().float().cpu().numpy().astype(np.float64).reshape(ref.shape)
     assert np.all(np.isfinite(a)), f"{label}: non-finite output"
     scale = float(np.max(np.abs(ref))) if ref.size else 0.0
@@ -27,7 +30,7 @@ def assert_close(out: torch.Tensor, ref: np.ndarray, label: str = "", tol: float
     if ref.size == 0:
         return
     assert err.max() <= tol * scale + 1e-30, f"{label}: normalized error {err.max() / max(scale, 1e-30):.3e} > {tol}"
-    bound = tol * np.abs(ref) + FLOOR * scale
+    bound = tol * np.abs(ref) + floor * scale
     bad = np.flatnonzero(err > bound)
     assert bad.size == 0, (f"{label}: {bad.size} elements beyond tolerance, first at {bad[0]}: "
                            f"out={a.flat[bad[0]]} ref={ref.flat[bad[0]]}")
