@@ -174,6 +174,26 @@ int soi_gemv_w4a16_sparse_accumulate(const uint8_t* Wq_sel, const float* scale_s
                                      uint16_t* y, int64_t H, int64_t k, int64_t group_size, int64_t num_groups,
                                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of soi_gemv_w4a16_sparse_accumulate: same arguments
+ * without the workspace, same kernel, bit-identical y. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * calls no hipMalloc / hipFree: its workspace is a fixed device array of
+ * soi_sparse_accumulate_noalloc_max_scratch_bytes() (2 MiB) that each GPU the
+ * library runs on holds until the process ends, set up on the first call on a
+ * device (address lookup, arrival counters cleared by a fill kernel on
+ * `stream`). The array holds 16 KB of arrival counters and then the fp32
+ * partial rows; a call that needs more than that (R x H x 4 bytes, R the
+ * row-chunk count of the partition, about k / 192: H = 2048 takes k up to
+ * about 48000, H = 5120 up to about 19000) returns SOI_ERR_INVALID_ARGUMENT without
+ * launching. All calls on
+ * one GPU share the array: calls that overlap on one GPU (different streams,
+ * or graphs replayed concurrently) race; calls ordered on one stream do not. */
+size_t soi_sparse_accumulate_noalloc_max_scratch_bytes(void);
+int soi_gemv_w4a16_sparse_accumulate_noalloc(const uint8_t* Wq_sel, const float* scale_sel, const uint16_t* h_sel,
+                                             uint16_t* y, int64_t H, int64_t k, int64_t group_size,
+                                             int64_t num_groups, void* stream);
+
 /* --------------------------------------------------------------------------
  * Hot-channel cache descriptors. desc[j] = slot_of[sel[j]] when >= 0 (cache
  * row), else (m | 0x80000000) where m numbers the misses in ascending j;

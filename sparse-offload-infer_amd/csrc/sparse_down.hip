@@ -25,6 +25,8 @@
 // Fixed partition and fixed order: deterministic, and every row source
 // (gathered rows, hot cache + staging descriptors, resident index list) gives
 // bit-identical results for the same logical rows.
+#include <mutex>
+
 #include "soi_device.h"
 #include "soi_host.h"
 #include "soi_rows.h"
@@ -367,23 +369,17 @@ static size_t down_workspace_bytes(int64_t H, int64_t k) {
     return down_counter_bytes(p) + static_cast<size_t>(p.R) * static_cast<size_t>(H) * sizeof(float);
 }
 
+// counters: S zeroed words (left zero); partial: R x H floats
 template <class Rows, class HS>
-static int launch_sparse_down(const Rows& rows, int64_t k, const HS& h, uint16_t* y, int64_t H, int64_t gs,
-                              bool vec, void* workspace, size_t ws_bytes, hipStream_t st, const char* what) {
+static int launch_sparse_down_on(const Rows& rows, int64_t k, const HS& h, uint16_t* y, int64_t H, int64_t gs,
+                                 bool vec, uint32_t* counters, float* partial, hipStream_t st, const char* what) {
     if (k == 0) {
         hipLaunchKernelGGL(sparse_down_zero_kernel, dim3(static_cast<unsigned>(ceil_div64(H, 256))), dim3(256), 0, st,
                            y, H);
         return launch_status(what);
     }
-    const size_t need = down_workspace_bytes(H, k);
-    if (!workspace || ws_bytes < need) {
-        set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, ws_bytes);
-        return SOI_ERR_WORKSPACE;
-    }
     const DownPlan p = down_plan(H, k);
     SOI_REQUIRE(p.R <= 65535 && p.S <= (int64_t(1) << 31) - 1, "%s: partition out of range", what);
-    uint32_t* counters = static_cast<uint32_t*>(workspace);
-    float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + down_counter_bytes(p));
     const dim3 grid(static_cast<unsigned>(p.S), static_cast<unsigned>(p.R));
     const bool cs = (gs % 32) == 0;
     const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(p.rpc),
@@ -398,6 +394,70 @@ static int launch_sparse_down(const Rows& rows, int64_t k, const HS& h, uint16_t
     }
 #undef SOI_D
     return launch_status(what);
+}
+
+// workspace = [S counters, rounded to 256 bytes][R x H partial rows]
+template <class Rows, class HS>
+static int launch_sparse_down(const Rows& rows, int64_t k, const HS& h, uint16_t* y, int64_t H, int64_t gs,
+                              bool vec, void* workspace, size_t ws_bytes, hipStream_t st, const char* what) {
+    if (k > 0) {
+        const size_t need = down_workspace_bytes(H, k);
+        if (!workspace || ws_bytes < need) {
+            set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, ws_bytes);
+            return SOI_ERR_WORKSPACE;
+        }
+    }
+    const size_t cb = k > 0 ? down_counter_bytes(down_plan(H, k)) : 0;
+    return launch_sparse_down_on(rows, k, h, y, H, gs, vec, static_cast<uint32_t*>(workspace),
+                                 reinterpret_cast<float*>(static_cast<char*>(workspace) + cb), st, what);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free form. Its workspace is `scratch`, a file-scope device array
+// of kNoAllocScratchBytes that every GPU holds for the life of the process.
+// Host code never passes the array's name to a kernel (in host code it is a
+// stand-in, not a device address): the device address is looked up once per
+// device with hipGetSymbolAddress and kept in g_scratch_addr.
+// ---------------------------------------------------------------------------
+// Layout: a fixed 16 KB counter area first (slice s of any call uses word s,
+// so calls with different H never see another call's partial rows in their
+// counters), then the R x H partial rows.
+constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;
+constexpr size_t kNoAllocCounterBytes = size_t(16) << 10;
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[kNoAllocScratchBytes];
+
+// clears the arrival-counter area at set-up (a fill kernel, not a memset, so a
+// first call made under stream capture stays capturable)
+__global__ __launch_bounds__(256) void scratch_clear_kernel(uint32_t* __restrict__ p, int64_t words) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < words;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        stg(p + i, 0u);
+}
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kNoAllocMaxDevices] = {};
+
+// The current device's scratch address; on a device's first call, looks it up
+// and zeroes the counter area (the array is zero at load as well; every call
+// leaves its counters at zero again).
+static int noalloc_scratch(hipStream_t st, void** out, const char* what) {
+    int dev = -1;
+    SOI_HIP_TRY(hipGetDevice(&dev), what);
+    SOI_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, "%s: device %d out of range", what, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        SOI_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), what);
+        SOI_REQUIRE(p != nullptr, "%s: no device address for the scratch array", what);
+        const int64_t words = static_cast<int64_t>(kNoAllocCounterBytes / sizeof(uint32_t));
+        hipLaunchKernelGGL(scratch_clear_kernel, dim3(16), dim3(256), 0, st, static_cast<uint32_t*>(p), words);
+        const int s = launch_status(what);
+        if (s) return s;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return SOI_OK;
 }
 
 static int check_down(int64_t H, int64_t k, int64_t gs, int64_t G, const char* what) {
@@ -428,6 +488,34 @@ extern "C" int soi_gemv_w4a16_sparse_accumulate(const uint8_t* Wq_sel, const flo
     DenseRows rows{Wq_sel, scale_sel, row_bytes, num_groups};
     return launch_sparse_down(rows, k, PlainH{h_sel}, y, H, group_size, vec, workspace, workspace_bytes,
                               as_stream(stream), what);
+}
+
+extern "C" size_t soi_sparse_accumulate_noalloc_max_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int soi_gemv_w4a16_sparse_accumulate_noalloc(const uint8_t* Wq_sel, const float* scale_sel,
+                                                        const uint16_t* h_sel, uint16_t* y, int64_t H, int64_t k,
+                                                        int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_w4a16_sparse_accumulate_noalloc";
+    int s = check_down(H, k, group_size, num_groups, what);
+    if (s) return s;
+    SOI_REQUIRE(y && (k == 0 || (Wq_sel && scale_sel && h_sel)), "%s: null pointer", what);
+    if (k > 0) {
+        const DownPlan p = down_plan(H, k);
+        const size_t need = kNoAllocCounterBytes + static_cast<size_t>(p.R) * static_cast<size_t>(H) * sizeof(float);
+        SOI_REQUIRE(static_cast<size_t>(p.S) * sizeof(uint32_t) <= kNoAllocCounterBytes && need <= kNoAllocScratchBytes,
+                    "%s: H = %lld, k = %lld needs %zu bytes of scratch, more than the %zu this form holds per GPU; "
+                    "call soi_gemv_w4a16_sparse_accumulate with a workspace instead",
+                    what, (long long)H, (long long)k, need, kNoAllocScratchBytes);
+    }
+    hipStream_t st = as_stream(stream);
+    void* ws = nullptr;
+    s = noalloc_scratch(st, &ws, what);
+    if (s) return s;
+    const int64_t row_bytes = ceil_div64(H, 8) * 4;
+    const bool vec = (row_bytes % 16 == 0) && aligned16(Wq_sel);
+    DenseRows rows{Wq_sel, scale_sel, row_bytes, num_groups};
+    return launch_sparse_down_on(rows, k, PlainH{h_sel}, y, H, group_size, vec, static_cast<uint32_t*>(ws),
+                                 reinterpret_cast<float*>(static_cast<char*>(ws) + kNoAllocCounterBytes), st, what);
 }
 
 extern "C" int soi_gemv_dip_fused_down(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
