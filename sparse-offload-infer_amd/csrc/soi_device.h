@@ -300,16 +300,27 @@ __device__ __forceinline__ int reduce_rows_row(uint32_t lane) {
     return 0;
 }
 
+// Device-scope release by one thread before it signals other workgroups: the
+// fence writes this XCD's L2 back (buffer_wbl2), and the write-back must have
+// completed before the signal can be seen. The documented release sequence
+// waits on vmcnt after buffer_wbl2, but the compiler's wait insertion drops
+// that wait (observed in the gfx950 ISA of these kernels: the signalling
+// atomic or store directly follows buffer_wbl2), so the wait is explicit.
+__device__ __forceinline__ void release_agent() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // Workgroup arrival, release side: every wave waits until its own stores have
 // completed (reached L2; a workgroup-scope fence does not wait for them), the
 // barrier makes that true for the whole workgroup, and then ONE device-scope
-// release fence by thread 0 writes the L2 lines back before thread 0 signals
-// (a release fence in every wave costs one L2 write-back per wave). Thread 0
-// must perform the signalling atomic right after this returns.
+// release by thread 0 writes the L2 lines back before thread 0 signals (a
+// release in every wave costs one L2 write-back per wave). Thread 0 must
+// perform the signalling atomic right after this returns.
 __device__ __forceinline__ void arrive_release() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0) release_agent();
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
@@ -322,7 +333,15 @@ __device__ __forceinline__ uint32_t mask_prefix(uint64_t m) {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// binary32 -> binary16, round to nearest even, of a value that has been
+// rounded to binary32 first (the reference computes in fp32 and then
+// converts). The empty asm keeps the compiler from folding a producing
+// multiply into a mixed-precision instruction (v_fma_mixlo_f16) that rounds
+// once, straight to binary16: that choice is made per inlined site, so two
+// kernels evaluating the same expression could otherwise disagree in the
+// last binary16 bit.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    asm("" : "+v"(v));
     return __builtin_bit_cast(uint16_t, static_cast<f16>(v));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return static_cast<float>(__builtin_bit_cast(f16, b)); }
