@@ -413,36 +413,6 @@ int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* sc
                                             int64_t num_channels, uint16_t* y, int64_t H, int64_t group_size,
                                             int64_t num_groups, void* workspace, size_t workspace_bytes,
                                             void* stream);
-/* --------------------------------------------------------------------------
- * The DIP MLP of one decoder layer (hidden size 2048) in ONE launch: x =
- * rmsnorm(x + delta, norm_weight) on load (x_out = x + delta, h_out = the
- * normed x, both optional), gate = INT4 GEMV, rule-A top-k over |gate|
- * (out_indices, out_count), h_sel[j] = fp16(silu(gate[idx_j]) *
- * fp16(up[idx_j] . x)), y = sum_j h_sel[j] * down_T[idx_j, :]. Restates the
- * reference's run_decoder_layer_dip MLP half (python/soinfer/runtime/
- * generate.py:276-310) over gemv_w4a16_group_lop3, topk_threshold_select and
- * gemv_w4a16_sparse_accumulate (csrc/kernels/gemv_w4a16_group.cu:23-134,
- * topk_select.cu:10-102, gemv_sparse_accumulate.cu:10-47); every output is
- * bit-identical to soi_gemv_w4a16_rmsnorm + soi_topk_threshold_select_f16abs
- * + soi_gemv_w4a16_indexed_silu + soi_gemv_w4a16_indexed_accumulate on the
- * same inputs. One workgroup per CU, all resident at once, with two grid
- * barriers inside; the workspace (soi_dip_mlp_workspace_bytes(k)) holds the
- * barrier flags and the sparse-down partials and must be zero-filled once;
- * every call leaves it reusable (calls that overlap on one workspace race).
- * A barrier wait is bounded: if the workgroups were ever not all resident,
- * the wait gives up, the workspace records it and soi_dip_mlp_check (which
- * synchronises `stream`) reports SOI_ERR_HIP. Limits: H = 2048, group_size a
- * multiple of 32, I a multiple of 4 up to 12288, k up to 64 per CU.
- * ------------------------------------------------------------------------ */
-size_t soi_dip_mlp_workspace_bytes(int64_t k);
-int soi_dip_mlp(const uint16_t* x, const uint16_t* delta, const uint16_t* norm_weight, float eps, uint16_t* x_out,
-                uint16_t* h_out, const uint8_t* gate_Wq, const float* gate_scale, const uint8_t* up_Wq,
-                const float* up_scale, const uint8_t* down_T_Wq, const float* down_T_scale, int64_t I, int64_t H,
-                int64_t k, int64_t group_size, int64_t num_groups, uint16_t* gate_out, int32_t* out_indices,
-                int32_t* out_count, uint16_t* h_sel, uint16_t* y, void* workspace, size_t workspace_bytes,
-                void* stream);
-int soi_dip_mlp_check(const void* workspace, void* stream);
-
 /* soi_dip_select_gated_down: the DIP selection and the gated sparse down of
  *   one MLP in ONE launch. Equals soi_topk_threshold_select_f16abs(gate, n =
  *   num_channels, k) -> (out_indices, out_count) followed by

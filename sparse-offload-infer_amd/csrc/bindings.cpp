@@ -1122,72 +1122,6 @@ void dip_select_gated_down_into(torch::Tensor gate, torch::Tensor up, int64_t k,
                  n);
 }
 
-void dip_mlp_into(torch::Tensor x, c10::optional<torch::Tensor> delta, torch::Tensor norm_weight, double eps,
-                  c10::optional<torch::Tensor> x_out, c10::optional<torch::Tensor> h_out, torch::Tensor gate_Wq,
-                  torch::Tensor gate_scale, torch::Tensor up_Wq, torch::Tensor up_scale, torch::Tensor down_T_Wq,
-                  torch::Tensor down_T_scale, int64_t k, torch::Tensor gate_out, torch::Tensor idx_out,
-                  torch::Tensor count_out, torch::Tensor h_sel, torch::Tensor y, int64_t group_size,
-                  torch::Tensor workspace_buf) {
-    const char* n = "dip_mlp_into";
-    need(x, torch::kFloat16, x, n, "x");
-    need(norm_weight, torch::kFloat16, x, n, "norm_weight");
-    for (auto* t : {&gate_Wq, &up_Wq, &down_T_Wq}) need(*t, torch::kUInt8, x, n, "Wq");
-    for (auto* t : {&gate_scale, &up_scale, &down_T_scale}) need(*t, torch::kFloat32, x, n, "scale");
-    need(gate_out, torch::kFloat16, x, n, "gate_out");
-    need(idx_out, torch::kInt32, x, n, "idx_out");
-    need(count_out, torch::kInt32, x, n, "count_out");
-    need(h_sel, torch::kFloat16, x, n, "h_sel");
-    need(y, torch::kFloat16, x, n, "y");
-    need(workspace_buf, torch::kUInt8, x, n, "workspace");
-    const int64_t H = x.numel();
-    const int64_t I = gate_Wq.size(0);
-    TORCH_CHECK(norm_weight.numel() == H && y.numel() == H, n, ": norm_weight / y must have H values");
-    for (auto* t : {&gate_Wq, &up_Wq, &down_T_Wq})
-        TORCH_CHECK(t->dim() == 2 && t->size(0) == I && t->size(1) == ((H + 7) / 8) * 4, n,
-                    ": gate / up / down_T must be [I, ceil(H/8)*4]");
-    for (auto* t : {&gate_scale, &up_scale, &down_T_scale})
-        TORCH_CHECK(t->dim() == 2 && t->size(0) == I && t->size(1) == gate_scale.size(1), n,
-                    ": scales must be [I, num_groups]");
-    TORCH_CHECK(gate_out.numel() == I, n, ": gate_out must have I values");
-    need_numel(idx_out, k, n, "idx_out");
-    need_numel(count_out, 1, n, "count_out");
-    need_numel(h_sel, k, n, "h_sel");
-    const uint16_t* dp = nullptr;
-    uint16_t* xo = nullptr;
-    uint16_t* ho = nullptr;
-    if (delta.has_value()) {
-        need(*delta, torch::kFloat16, x, n, "delta");
-        need_numel(*delta, H, n, "delta");
-        dp = h16(*delta);
-    }
-    if (x_out.has_value()) {
-        need(*x_out, torch::kFloat16, x, n, "x_out");
-        need_numel(*x_out, H, n, "x_out");
-        xo = h16m(*x_out);
-    }
-    if (h_out.has_value()) {
-        need(*h_out, torch::kFloat16, x, n, "h_out");
-        need_numel(*h_out, H, n, "h_out");
-        ho = h16m(*h_out);
-    }
-    const at::DeviceGuard guard(x.device());
-    check_status(soi_dip_mlp(h16(x), dp, h16(norm_weight), static_cast<float>(eps), xo, ho,
-                             gate_Wq.data_ptr<uint8_t>(), gate_scale.data_ptr<float>(), up_Wq.data_ptr<uint8_t>(),
-                             up_scale.data_ptr<float>(), down_T_Wq.data_ptr<uint8_t>(), down_T_scale.data_ptr<float>(),
-                             I, H, k, group_size, gate_scale.size(1), h16m(gate_out), idx_out.data_ptr<int32_t>(),
-                             count_out.data_ptr<int32_t>(), h16m(h_sel), h16m(y), workspace_buf.data_ptr<uint8_t>(),
-                             workspace_buf.numel(), cur_stream(x)),
-                 n);
-}
-
-int64_t dip_mlp_workspace_bytes(int64_t k) { return static_cast<int64_t>(soi_dip_mlp_workspace_bytes(k)); }
-
-void dip_mlp_check(torch::Tensor workspace_buf) {
-    TORCH_CHECK(workspace_buf.is_cuda(), "dip_mlp_check: workspace must be a CUDA tensor");
-    const at::DeviceGuard guard(workspace_buf.device());
-    check_status(soi_dip_mlp_check(workspace_buf.data_ptr<uint8_t>(), cur_stream(workspace_buf)), "dip_mlp_check");
-}
-
 void gemv_w4a16_indexed_silu_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
                                   torch::Tensor gate, torch::Tensor h_sel, int64_t K, int64_t group_size) {
     const char* n = "gemv_w4a16_indexed_silu_into";
@@ -1416,9 +1350,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows, both halves written");
     m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
           "sparse down over selected rows with the SiLU gating computed on the fly");
-    m.def("dip_mlp_into", &dip_mlp_into, "the DIP MLP of one layer (norm, gate, selection, up, SiLU, down) in one launch");
-    m.def("dip_mlp_workspace_bytes", &dip_mlp_workspace_bytes, "workspace bytes of dip_mlp_into");
-    m.def("dip_mlp_check", &dip_mlp_check, "raise if a dip_mlp_into barrier wait gave up (synchronises)");
     m.def("dip_select_gated_down_into", &dip_select_gated_down_into,
           "DIP selection over |gate| and the gated sparse down in one launch");
     m.def("gemv_dip_fused_up_silu_into", &gemv_dip_fused_up_silu_into, "descriptor up GEMV with SiLU gating");

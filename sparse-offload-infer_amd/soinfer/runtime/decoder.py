@@ -201,7 +201,7 @@ class DecodeEngine:
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
                  dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
-                 down_copy: bool = True, single_launch_mlp: Optional[bool] = None):
+                 down_copy: bool = True):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         if offload and mode == "dip":
@@ -220,14 +220,6 @@ class DecodeEngine:
         # than the indexed up GEMV; the selected h values and hence every output are identical)
         self.dip_dense_up = dip_dense_up
         c = w.config
-        # DIP with resident weights, fused layers: the whole MLP (norm, gate, selection, up + SiLU, sparse down) as
-        # ONE launch (dip_mlp_into), bit-identical to the four launches it replaces; None = wherever it applies
-        fits = (mode == "dip" and fused and not dip_dense_up and c.hidden == 2048 and c.group_size % 32 == 0
-                and c.intermediate % 4 == 0 and c.intermediate <= 12288)
-        if single_launch_mlp and not fits:
-            raise ValueError("single_launch_mlp needs mode 'dip' with fused layers, hidden 2048, group_size a "
-                             "multiple of 32 and intermediate a multiple of 4 up to 12288")
-        self.single_launch_mlp = fits if single_launch_mlp is None else bool(single_launch_mlp)
         self.w, self.c, self.mode, self.fused = w, c, mode, fused
         dev = w.embed.device
         self.device = dev
@@ -260,7 +252,6 @@ class DecodeEngine:
         step_ws = _C.decode_attention_step_workspace_bytes(c.q_heads, c.kv_heads, hd, c.max_seq)
         self.step_ws = buf(step_ws, torch.uint8) if (fused and step_ws > 0) else None
         self.counts = None  # optional per-layer channel selection counts (eager calibration only)
-        self.mlp_ws = None  # single-launch MLP workspace (DIP only)
 
         if mode != "dense":
             if dip_k is None or not 1 <= dip_k <= I:
@@ -269,8 +260,6 @@ class DecodeEngine:
             self.idx, self.cnt = buf(dip_k, i32), buf(1, i32)
             self.u_sel, self.h_sel = buf(dip_k), buf(dip_k)
             self.sd_ws = buf(max(1, _C.sparse_accumulate_workspace_bytes(H, dip_k)), torch.uint8)
-            # grid-barrier flags + sparse-down partials of the single-launch MLP (zero-filled once, reusable)
-            self.mlp_ws = buf(_C.dip_mlp_workspace_bytes(dip_k), torch.uint8) if self.single_launch_mlp else None
         if mode == "cached_dip":
             if hot_channels is None or len(hot_channels) != c.layers:
                 raise ValueError("cached_dip needs one hot-channel list per layer")
@@ -531,12 +520,6 @@ class DecodeEngine:
             self._count_selection(l)
             return
         gW, gS = L.gate(I)
-        if self.single_launch_mlp:
-            uW, uS = L.up(I)
-            _C.dip_mlp_into(cur, self.o, L.post_norm, eps, other, self.h, gW, gS, uW, uS, L.down_T_Wq,
-                            L.down_T_scale, self.k, gate, self.idx, self.cnt, self.h_sel, self.down, gs, self.mlp_ws)
-            self._count_selection(l)
-            return
         _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         self._count_selection(l)
@@ -599,12 +582,6 @@ class DecodeEngine:
     def reset(self):
         self.pos.zero_()
         self.log_len.zero_()
-
-    def check(self):
-        """Synchronise and raise if a single-launch MLP call ever gave up a grid-barrier wait (its workgroups were
-        not all resident), i.e. if any output since the engine was built is not valid."""
-        if self.mlp_ws is not None:
-            _C.dip_mlp_check(self.mlp_ws)
 
     def prefill(self, prompt_ids, use_graph: bool = True):
         prompt = torch.as_tensor(list(prompt_ids), dtype=torch.int32, device=self.device)
