@@ -26,7 +26,7 @@
 //     (m, l, acc) rescaling;
 //   * short contexts (at most 8 passes: 256 timesteps at head_dim 128) run
 //     ONE workgroup per KV head, which writes the output itself; longer ones
-//     split the timesteps (about 256 workgroups), each split writes its state
+//     split the timesteps (about 128 workgroups), each split writes its state
 //     to the workspace and the last split of a KV head to arrive (a device
 //     counter) combines them in split order. Fixed order throughout:
 //     deterministic, and all forms give identical bytes for the same length.
@@ -40,6 +40,10 @@ constexpr int kAttnWaves = 8;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kAttnPassMax = 8;  // passes whose K/V rows a lane requests at once (8 x 32 bytes)
 constexpr float kNegBig = -1e30f;
+// Split contexts aim at this many workgroups in all: fewer, longer splits
+// trade stream time per workgroup against the arrival on each KV head's
+// counter and the combine, which both grow with the splits per KV head.
+constexpr int kAttnTargetGroups = 128;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -53,17 +57,17 @@ __device__ __forceinline__ int cur_len_of(int L_arg, const int32_t* pos, int S) 
 
 // Plan for a context of L timesteps, `step` = timesteps one workgroup pass
 // covers: one workgroup per KV head when L fits kAttnPassMax passes, else
-// about 256 workgroups, tps a multiple of step. The host and the device (the
-// device-position forms, which read L at run time) use this same function, so
-// both give the same partition and bit-identical results. ns <= ceil(256/NKV)
-// and ns <= ceil(L/step) for every L.
+// about kAttnTargetGroups workgroups, tps a multiple of step. The host and
+// the device (the device-position forms, which read L at run time) use this
+// same function, so both give the same partition and bit-identical results.
+// ns <= ceil(kAttnTargetGroups/NKV) and ns <= ceil(L/step) for every L.
 __host__ __device__ __forceinline__ void split_plan(int64_t L, int64_t NKV, int64_t step, int& tps, int& ns) {
     if (L <= kAttnPassMax * step) {
         tps = static_cast<int>(L);
         ns = 1;
         return;
     }
-    int64_t t = (L * NKV + 255) / 256;
+    int64_t t = (L * NKV + kAttnTargetGroups - 1) / kAttnTargetGroups;
     t = (t + step - 1) / step * step;
     if (t < step) t = step;
     tps = static_cast<int>(t);
@@ -84,7 +88,7 @@ __device__ __forceinline__ float group_sum(float v) {
     }
     if (LPR >= 4) v += dpp_f<0x4e>(v);  // quad_perm [2,3,0,1]
     if (LPR >= 2) v += dpp_f<0xb1>(v);  // quad_perm [1,0,3,2]
-    if (LPR == 32) v += __shfl_xor(v, 16, kWave);
+    if (LPR == 32) v += xor_lanes<16>(v);
     return v;
 }
 
@@ -118,6 +122,29 @@ __device__ __forceinline__ void attn_pass(AttnState<LPR, REP>& st, const f16x2 (
             st.acc[hh][2 * e + 1] = fmaf(st.acc[hh][2 * e + 1], corr, p * static_cast<float>(v2[e].y));
         }
         st.m[hh] = mn;
+    }
+}
+
+// Merge lane l's state with lane l ^ MASK's for MASK = M, 2M, ... 32.
+template <int LPR, int REP, int MASK>
+__device__ __forceinline__ void attn_merge_groups(AttnState<LPR, REP>& st, int rep) {
+    if constexpr (MASK < kWave) {
+#pragma unroll
+        for (int hh = 0; hh < REP; ++hh) {
+            if (hh >= rep) break;
+            const float mo = xor_lanes<MASK>(st.m[hh]);
+            const float lo = xor_lanes<MASK>(st.l[hh]);
+            const float mn = fmaxf(st.m[hh], mo);
+            const float ca = fast_exp2(st.m[hh] - mn), cb = fast_exp2(mo - mn);
+            st.l[hh] = st.l[hh] * ca + lo * cb;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const float ao = xor_lanes<MASK>(st.acc[hh][d]);
+                st.acc[hh][d] = st.acc[hh][d] * ca + ao * cb;
+            }
+            st.m[hh] = mn;
+        }
+        attn_merge_groups<LPR, REP, MASK * 2>(st, rep);
     }
 }
 
@@ -158,58 +185,58 @@ __device__ __forceinline__ float wave_merged(const float (*s_state)[REP][HD + 2]
 }
 
 // out[h,d] = (sum_s acc_s[d] 2^(m_s-M)) / (sum_s l_s 2^(m_s-M)) over the ns
-// split states of head h. M and the denominator are block reductions over the
-// splits; each thread then sums its dimension over the splits in ascending
-// order with the loads issued 8 at a time. Fixed order: deterministic.
-constexpr int kCombineMaxSplits = 256;  // nsplit <= 256 by construction of the plan
+// split states of the KV head's query heads h0 .. h0+rep-1, M = max_s m_s.
+// Thread o takes output (o / HD, o % HD). Its first kCombineBatch split values
+// are requested before the (m, l) pairs, which go to LDS, so both arrive in
+// one memory round trip (more only past 32 splits or 512 outputs); every sum
+// runs over the splits in ascending order: deterministic.
+constexpr int kCombineMaxSplits = kAttnTargetGroups;  // nsplit <= kAttnTargetGroups by construction of the plan
+constexpr int kCombineBatch = 32;
 
-template <int NT>
-__device__ __forceinline__ float block_reduce(float v, float* s_red, bool is_max) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    v = is_max ? wave_max_bcast(v) : wave_sum_bcast(v);
-    __syncthreads();
-    if (lane == 0) s_red[wave] = v;
-    __syncthreads();
-    float r = s_red[0];
-#pragma unroll
-    for (int w = 1; w < NT / kWave; ++w) r = is_max ? fmaxf(r, s_red[w]) : r + s_red[w];
-    return r;
-}
-
-template <int NT>
-__device__ __forceinline__ void combine_head(const float* __restrict__ part, uint16_t* __restrict__ out, int h, int hd,
-                                             int nsplit, int ns, float* s_w, float* s_red) {
+template <int NT, int HD>
+__device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint16_t* __restrict__ out, int h0, int rep,
+                                           int nsplit, int ns, float* s_m, float* s_l) {
+    constexpr int stride = HD + 2;
     const int tid = threadIdx.x;
-    const int stride = hd + 2;
-    const float* ph = part + static_cast<int64_t>(h) * nsplit * stride;
-    float m = kNegBig;
-    for (int sp = tid; sp < ns; sp += NT) m = fmaxf(m, ldg(ph + sp * stride));
-    const float M = block_reduce<NT>(m, s_red, true);
-    float lp = 0.0f;
-    for (int sp = tid; sp < ns; sp += NT) {
-        const float w = fast_exp2(ldg(ph + sp * stride) - M);
-        if (sp < kCombineMaxSplits) s_w[sp] = w;
-        lp = fmaf(ldg(ph + sp * stride + 1), w, lp);
-    }
-    const float Lsum = block_reduce<NT>(lp, s_red, false);
-    __syncthreads();  // s_w complete
-    for (int d = tid; d < hd; d += NT) {
-        float a = 0.0f;
-        int sp = 0;
-        for (; sp + 8 <= ns && sp + 8 <= kCombineMaxSplits; sp += 8) {
-            float v[8];
+    const int nout = rep * HD;
+    float v[kCombineBatch];
+    {
+        const int o = tid < nout ? tid : 0;
+        const float* po = part + static_cast<int64_t>(h0 + o / HD) * nsplit * stride + 2 + o % HD;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = ldg(ph + (sp + u) * stride + 2 + d);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) a = fmaf(v[u], s_w[sp + u], a);
-        }
-        for (; sp < ns; ++sp) {
-            const float w = sp < kCombineMaxSplits ? s_w[sp] : fast_exp2(ldg(ph + sp * stride) - M);
-            a = fmaf(ldg(ph + sp * stride + 2 + d), w, a);
-        }
-        stg(out + static_cast<int64_t>(h) * hd + d, f32_to_f16_bits(a / Lsum));
+        for (int s = 0; s < kCombineBatch; ++s) v[s] = ldg(po + static_cast<int64_t>(s < ns ? s : 0) * stride);
     }
-    __syncthreads();  // s_w / s_red reusable
+    for (int i = tid; i < rep * ns; i += NT) {
+        const int hh = i / ns, sp = i % ns;
+        const float* ps = part + (static_cast<int64_t>(h0 + hh) * nsplit + sp) * stride;
+        s_m[hh * kCombineMaxSplits + sp] = ldg(ps);
+        s_l[hh * kCombineMaxSplits + sp] = ldg(ps + 1);
+    }
+    __syncthreads();  // (m, l) of every split in LDS
+    for (int o = tid; o < nout; o += NT) {
+        const int hh = o / HD;
+        const float* sm = s_m + hh * kCombineMaxSplits;
+        const float* sl = s_l + hh * kCombineMaxSplits;
+        const float* po = part + static_cast<int64_t>(h0 + hh) * nsplit * stride + 2 + o % HD;
+        float M = kNegBig;
+        for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, sm[sp]);
+        float lsum = 0.0f, acc = 0.0f;
+        for (int b0 = 0; b0 < ns; b0 += kCombineBatch) {
+            if (o != tid || b0 > 0) {  // the first batch of the first output is already in v
+#pragma unroll
+                for (int s = 0; s < kCombineBatch; ++s)
+                    v[s] = ldg(po + static_cast<int64_t>(b0 + s < ns ? b0 + s : 0) * stride);
+            }
+#pragma unroll
+            for (int s = 0; s < kCombineBatch; ++s) {
+                if (b0 + s >= ns) break;
+                const float w = fast_exp2(sm[b0 + s] - M);
+                lsum = fmaf(sl[b0 + s], w, lsum);
+                acc = fmaf(v[s], w, acc);
+            }
+        }
+        stg(out + static_cast<int64_t>(h0 + hh) * HD + o % HD, f32_to_f16_bits(acc / lsum));
+    }
 }
 
 struct AttnArgs {
@@ -244,8 +271,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     __shared__ float s_state[kAttnWaves][REP][HD + 2];
     __shared__ __attribute__((aligned(16))) uint16_t s_q[PRE ? REP : 1][HD];
     __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][HD];
-    __shared__ float s_w[kCombineMaxSplits];
-    __shared__ float s_red[kAttnWaves];
+    __shared__ float s_cm[REP * kCombineMaxSplits], s_cl[REP * kCombineMaxSplits];
     __shared__ int s_last;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane / LPR, u = lane % LPR;
@@ -381,25 +407,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         }
     }
 
-    // merge lane groups (same u, different timesteps) inside the wave
-#pragma unroll
-    for (int mask = LPR; mask < kWave; mask <<= 1) {
-#pragma unroll
-        for (int hh = 0; hh < REP; ++hh) {
-            if (hh >= rep) break;
-            const float mo = __shfl_xor(st.m[hh], mask, kWave);
-            const float lo = __shfl_xor(st.l[hh], mask, kWave);
-            const float mn = fmaxf(st.m[hh], mo);
-            const float ca = fast_exp2(st.m[hh] - mn), cb = fast_exp2(mo - mn);
-            st.l[hh] = st.l[hh] * ca + lo * cb;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const float ao = __shfl_xor(st.acc[hh][d], mask, kWave);
-                st.acc[hh][d] = st.acc[hh][d] * ca + ao * cb;
-            }
-            st.m[hh] = mn;
-        }
-    }
+    // merge lane groups (same u, different timesteps) inside the wave: partner lane l ^ MASK for MASK = LPR,
+    // 2*LPR, ... 32 (VALU lane exchanges, not the LDS crossbar)
+    attn_merge_groups<LPR, REP, LPR>(st, rep);
     if (g == 0) {
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
@@ -438,8 +448,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' states
-    for (int hh = 0; hh < rep; ++hh)
-        combine_head<kAttnThreads>(a.part, a.out, kvh * rep + hh, HD, a.nsplit, ns, s_w, s_red);
+    combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep, rep, a.nsplit, ns, s_cm, s_cl);
 }
 
 // General shapes: one wave per query head, lanes over dims, online softmax.
@@ -506,7 +515,7 @@ static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
         p.rep_t = rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
         p.step = static_cast<int>((kWave / lpr) * kAttnWaves);  // timesteps per workgroup pass
         split_plan(L, NKV, p.step, p.tps, p.nsplit);
-        const int64_t by_len = ceil_div64(L, p.step), by_heads = ceil_div64(256, NKV);
+        const int64_t by_len = ceil_div64(L, p.step), by_heads = ceil_div64(kAttnTargetGroups, NKV);
         p.cap = static_cast<int>(by_len < by_heads ? by_len : by_heads);
         if (p.cap < p.nsplit) p.cap = p.nsplit;
         if (p.cap < 1) p.cap = 1;

@@ -176,6 +176,32 @@ __device__ __forceinline__ float dpp_f(float v) {
                                                                  false));
 }
 
+// The value of lane (l ^ MASK) in lane l, without the LDS crossbar where a VALU
+// form exists: masks 16 / 32 by v_permlane16_swap / v_permlane32_swap (with
+// both operands v, lane l's partner is in the first result when bit MASK of l
+// is set, else in the second), 8 by DPP row_ror:8 ((i + 8) mod 16 = i ^ 8
+// inside a 16-lane row), 2 and 1 by quad permutes, 4 by __shfl_xor.
+template <int MASK>
+__device__ __forceinline__ float xor_lanes(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const unsigned lane = threadIdx.x & 63;
+    if constexpr (MASK == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __builtin_bit_cast(float, (lane & 32) ? r[0] : r[1]);
+    } else if constexpr (MASK == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+    } else if constexpr (MASK == 8) {
+        return dpp_f<0x128>(v);
+    } else if constexpr (MASK == 2) {
+        return dpp_f<0x4e>(v);
+    } else if constexpr (MASK == 1) {
+        return dpp_f<0xb1>(v);
+    } else {
+        return __shfl_xor(v, MASK, 64);
+    }
+}
+
 __device__ __forceinline__ float wave_sum_lane63(float v) {
     v += dpp_f<0xb1>(v);        // quad_perm [1,0,3,2]
     v += dpp_f<0x4e>(v);        // quad_perm [2,3,0,1]
