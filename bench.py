@@ -20,7 +20,8 @@ Also reported:
                   summary committed under profiles/ (null when absent);
   batched_per_class  the same GEMVs as one launch per shape class, per class;
   copy_reference  a plain device-to-device copy of 512 MiB (the calibration
-                  kernel of the counter runs, and the box's streaming rate);
+                  kernel of the counter runs, and the box's streaming rate), and
+                  by_size: the same copy of one gate/up GEMV's bytes, of 64 MB and of a step;
   decode_chain    the 112 dependent launches of one decode step, graph-replayed;
   per_shape_cold  per-shape INT4 / INT8 single-launch times on cold copies;
   topk_us_I6144   top-k latency at I=6144;
@@ -34,6 +35,8 @@ Also reported:
                   at the job's host cores and one thread.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --traffic-set   (only the launches of the HBM counter passes whose summaries are
+                                        committed under profiles/; prints their algorithmic bytes)
 """
 from __future__ import annotations
 
@@ -573,6 +576,41 @@ def bench_kernels(dev, gen):
             res[f"fused_down_k{k}"] = entry(k * (row + 4 * G + 4 + 2) + 2 * H, t["mean_us"], hot_fraction=0.2,
                                             kernel="sparse_down DescRows (1 launch)")
             del caches, stag, args
+    # the sparse down's fixed cost: k = 32 is one 32-row chunk per slice (8 workgroups, one arrival each), so the
+    # time is the launch, one round trip of rows, the partial row, the arrival and the combine of a single row
+    k = 32
+    idx = torch.sort(torch.randperm(I, device=dev, generator=gen)[:k]).values.to(i32)
+    h = torch.randn(k, generator=gen, device=dev).half()
+    ws = torch.zeros(max(1, _C.sparse_accumulate_workspace_bytes(H, k)), dtype=torch.uint8, device=dev)
+    t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_indexed_accumulate_into(W, S, idx, h, y, H, GS, ws),
+                              list(zip(Wt, St)))
+    res[f"sparse_down_k{k}"] = entry(k * (row + 4 * G + 2) + 2 * H, t["mean_us"],
+                                     kernel="sparse_down (1 launch): the fixed cost of the arrival chain")
+    # reads of pinned host rows through the device mapping (k = 3072 of the 6144 down^T rows, 6.3 MB arena):
+    # whole 1 KB rows (the counted device gather) and the 128-byte row segments of the cached down with an empty
+    # cache (every selected row a miss read in place)
+    k = 3072
+    idx = torch.sort(torch.randperm(I, device=dev, generator=gen)[:k]).values.to(i32)
+    h = torch.randn(k, generator=gen, device=dev).half()
+    host_W = Wt[0].cpu().pin_memory()
+    addr = _C.host_device_pointer(host_W)
+    kcount = torch.full((1,), k, dtype=i32, device=dev)
+    dst = torch.empty(k, row, dtype=torch.uint8, device=dev)
+    t = time_graph_per_launch(lambda: _C.gather_rows_device_counted(addr, I, row, idx, kcount, dst), [()] * 16)
+    res[f"gather_rows_pinned_k{k}"] = {"bytes_over_pcie": k * row, "us": round(t["mean_us"], 3),
+                                       "GBps": round(k * row / t["mean_us"] / 1e3, 2),
+                                       "kernel": "gather_rows_device_counted from pinned host memory (1 KB rows)"}
+    empty_W = torch.empty(0, row, dtype=torch.uint8, device=dev)
+    empty_S = torch.empty(0, G, dtype=torch.float32, device=dev)
+    slot_none = torch.full((I,), -1, dtype=i32, device=dev)
+    ws = torch.zeros(max(1, _C.sparse_accumulate_workspace_bytes(H, k)), dtype=torch.uint8, device=dev)
+    t = time_graph_per_launch(lambda: _C.gemv_dip_cached_down_into(empty_W, empty_S, host_W, St[0], slot_none, idx,
+                                                                   h, y, H, GS, ws), [()] * 16)
+    res[f"cached_down_all_miss_pinned_k{k}"] = {
+        "bytes_over_pcie": k * row, "us": round(t["mean_us"], 3), "GBps": round(k * row / t["mean_us"] / 1e3, 2),
+        "kernel": "sparse_down SlotRows, empty cache: every row read in place from pinned memory (128-byte "
+                  "segments per workgroup)"}
+    del host_W
     del Wt, St
     torch.cuda.empty_cache()
 
@@ -738,6 +776,55 @@ def cpu_baseline(layer0):
                       f"{avail} cores available to the job"}
 
 
+def run_traffic_set(dev, gen):
+    """Launches for the HBM counter passes (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, one run each): the
+    calibration copy (copy_reference: 11 copies of 512 MiB), then 6 launches each, on separate operand copies
+    and each followed by a synchronize, of sparse_down_kernel and dip_select_down_kernel at k = 3072 and of
+    attn_kernel at L = 192 and L = 2048 (host-length form: grids of 8 and 8 x 16 workgroups). Prints the
+    algorithmic bytes each launch moves."""
+    import torch
+
+    from soinfer import _C
+
+    copy_reference()
+    H, I, G = 2048, 6144, 2048 // GS
+    row = H // 2
+    f16, i32 = torch.float16, torch.int32
+    n = 6
+    Wt = [torch.randint(0, 256, (I, row), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n)]
+    St = [(torch.rand(I, G, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n)]
+    k = 3072
+    idx = torch.sort(torch.randperm(I, device=dev, generator=gen)[:k]).values.to(i32)
+    h = torch.randn(k, generator=gen, device=dev).half()
+    y = torch.empty(H, dtype=f16, device=dev)
+    ws = torch.zeros(_C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    for W, S in zip(Wt, St):
+        _C.gemv_w4a16_indexed_accumulate_into(W, S, idx, h, y, H, GS, ws)
+        torch.cuda.synchronize()
+    gate = torch.randn(I, generator=gen, device=dev).half()
+    up = torch.randn(I, generator=gen, device=dev).half()
+    sel_i, sel_c = torch.empty(k, dtype=i32, device=dev), torch.empty(1, dtype=i32, device=dev)
+    for W, S in zip(Wt, St):
+        _C.dip_select_gated_down_into(gate, up, k, W, S, sel_i, sel_c, y, H, GS, ws)
+        torch.cuda.synchronize()
+    del Wt, St
+    NQ, NKV, HD, Smax = 16, 8, 128, 2048
+    q = torch.randn(NQ, HD, generator=gen, device=dev).half()
+    for L in (192, 2048):
+        for _ in range(n):
+            kc = torch.randn(NKV, Smax, HD, generator=gen, device=dev).half()
+            vc = torch.randn(NKV, Smax, HD, generator=gen, device=dev).half()
+            torch.cuda.synchronize()
+            _C.decode_attention(q, kc, vc, L)
+            torch.cuda.synchronize()
+    print(json.dumps({"traffic_set": {
+        "sparse_down_kernel_k3072": {"read": k * (row + 4 * G + 2 + 4), "write": 2 * H},
+        "dip_select_down_kernel_k3072": {"read": k * (row + 4 * G + 2) + 2 * I, "write": 2 * H + 4 * k + 4},
+        "attn_kernel_L192": {"read": 4096 * 192 + 2 * NQ * HD, "write": 2 * NQ * HD},
+        "attn_kernel_L2048": {"read": 4096 * 2048 + 2 * NQ * HD, "write": 2 * NQ * HD}}}))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -746,6 +833,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the decode-chain, per-shape and top-k tables")
     ap.add_argument("--no-decode", action="store_true", help="skip the DIP MLP and decode tok/s sections")
+    ap.add_argument("--traffic-set", action="store_true",
+                    help="only the launches of the HBM counter passes (calibration copy, sparse down, fused "
+                         "selection + down, attention at L = 192 and 2048), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU (the hot path is single-GPU; --gpus {args.gpus} is not "
@@ -762,6 +852,9 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
+    if args.traffic_set:
+        run_traffic_set(dev, gen)
+        return 0
 
     # ---- the 28-layer weight set, resident in HBM ----
     layers = []
@@ -845,6 +938,9 @@ def main() -> int:
         del bt
     log("per-class batched launches done")
     copy_ref = copy_reference()
+    # the same copy at the sizes the kernels here move: one gate/up GEMV's bytes, 64 MB, and a whole step
+    copy_ref["by_size"] = {str(nb): copy_reference(nb, reps=30 if nb < (256 << 20) else 10)
+                           for nb in (int4_bytes(6144, 2048), 64 << 20, step_bytes)}
     log(f"copy reference: {copy_ref['us']} us")
 
 

@@ -186,16 +186,23 @@ __device__ __forceinline__ float rule_a_tau(const uint32_t (&key)[E], float loca
 // wave w = w*64E + 64j + lane): its position is (selected elements of earlier
 // waves) + (selected elements of earlier j of this wave) + (earlier lanes of
 // this j), i.e. ascending index order. emit(pos, j) runs in every lane whose
-// element is selected; the return value is the total number selected. s_tot
-// holds NW words; one barrier.
+// element is selected and whose position lies in [lo, hi); the return value
+// is the total number selected. The first pass keeps each j's count (wave-
+// uniform), so the second pass ballots again only for the j whose positions
+// reach into the window: a workgroup that needs one chunk of the positions
+// walks the rest with a few scalar instructions per j. s_tot holds NW words;
+// one barrier.
 template <int E, int NW, class Emit>
 __device__ __forceinline__ uint32_t rule_a_compact(const float (&val)[E], float tau, uint32_t* s_tot, int tid,
-                                                   Emit&& emit) {
+                                                   uint32_t lo, uint32_t hi, Emit&& emit) {
     const int wave = tid >> 6, lane = tid & 63;
-    // the ballots are recomputed rather than kept: E masks would not fit in SGPRs
+    uint32_t cnt[E];
     uint32_t wave_total = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) wave_total += popc64(ballot(val[j] >= tau));
+    for (int j = 0; j < E; ++j) {
+        cnt[j] = popc64(ballot(val[j] >= tau));
+        wave_total += cnt[j];
+    }
     if (lane == 0) s_tot[wave] = wave_total;
     __syncthreads();
     uint32_t before = 0, total = 0;
@@ -208,12 +215,21 @@ __device__ __forceinline__ uint32_t rule_a_compact(const float (&val)[E], float 
     uint32_t running = before;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const bool sel = val[j] >= tau;
-        const uint64_t mk = ballot(sel);
-        if (sel) emit(running + mask_prefix(mk), j);
-        running += popc64(mk);
+        if (running < hi && running + cnt[j] > lo) {  // wave-uniform
+            const bool sel = val[j] >= tau;
+            const uint64_t mk = ballot(sel);
+            const uint32_t pos = running + mask_prefix(mk);
+            if (sel && pos >= lo && pos < hi) emit(pos, j);
+        }
+        running += cnt[j];
     }
     return total;
+}
+
+template <int E, int NW, class Emit>
+__device__ __forceinline__ uint32_t rule_a_compact(const float (&val)[E], float tau, uint32_t* s_tot, int tid,
+                                                   Emit&& emit) {
+    return rule_a_compact<E, NW>(val, tau, s_tot, tid, 0u, 0xffffffffu, static_cast<Emit&&>(emit));
 }
 
 }  // namespace soi

@@ -128,14 +128,14 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
     }
     const float tau = rule_a_tau<E, kDownWaves, F16AbsValues>(key, local_max, s_hist, s_max, k, tid);
     const bool writer = blockIdx.x == 0;
-    const uint32_t total = rule_a_compact<E, kDownWaves>(val, tau, s_tot, tid, [&](uint32_t pos, int j) {
-        if (pos >= j0 && pos < j1) {
+    // only this workgroup's chunk [j0, j1) of the positions is emitted
+    const uint32_t total = rule_a_compact<E, kDownWaves>(
+        val, tau, s_tot, tid, static_cast<uint32_t>(j0), static_cast<uint32_t>(j1), [&](uint32_t pos, int j) {
             const int c = base_i + j * kWave;
             s_ch[pos - j0] = c;
             s_g[pos - j0] = static_cast<uint16_t>(raw[j]);
             if (writer) stg(out_idx + pos, static_cast<int32_t>(c));
-        }
-    });
+        });
     const int64_t kk = total < static_cast<uint32_t>(k) ? static_cast<int64_t>(total) : static_cast<int64_t>(k);
     if (writer && blockIdx.y == 0 && tid == 0) stg(out_count, static_cast<int32_t>(kk));
     __syncthreads();  // s_ch / s_g of the chunk complete
