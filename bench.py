@@ -267,13 +267,14 @@ def bench_decode_chain(ops, layers, step_bytes):
 def mlp_bytes(L, I: int, H: int, k=None, dense_up: bool = False) -> int:
     """Algorithmic bytes of one layer's MLP: dense reads gate|up and down; DIP reads gate, k rows of up and
     k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes; the dense-up DIP schedule
-    reads every up row."""
+    reads every gate|up row and every down^T value (its down is a GEMV over the transposed down_proj^T: unselected
+    channels read with a zero coefficient), and writes then reads gate and h of every channel."""
     row = L.gu_Wq.shape[1] + 4 * L.gu_scale.shape[1]
     if k is None:
         return 2 * I * row + L.down_Wq.numel() + 4 * L.down_scale.numel() + 2 * (H + 3 * I + H)
     row_t = L.down_T_Wq.shape[1] + 4 * L.down_T_scale.shape[1]
     if dense_up:
-        return 2 * I * row + k * row_t + 2 * (H + 2 * I + 2 * k + H) + 4 * (I + k)
+        return 2 * I * row + I * row_t + 2 * (H + 4 * I + H)
     return I * row + k * (row + row_t) + 2 * (H + I + 2 * k + H) + 4 * (I + k)
 
 
@@ -382,21 +383,43 @@ def bench_dip_mlp(D, w, hot, dev):
         us_f = fused_dip(eng)
         assert torch.equal(eng.down, y_unfused), "fused DIP MLP must equal the unfused one"
         us_4 = norm_mlp(eng)
-        res[f"dip_k{k}"] = {"k_over_I": frac, "us": round(us_4, 2), "bytes": nb, "GBps": round(nb / us_4 / 1e3, 1),
-                            "schedule": "RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse down "
-                                        "(4 launches)",
-                            "no_norm_us": round(us_f, 2), "unfused_us": round(us, 2)}
+        idx_dip, y_norm = eng.idx.clone(), eng.down.clone()  # layer 27's selection and y on rmsnorm(x)
         if frac == 0.5:
             y_dip = y_unfused
         del eng
-        # dense-up schedule: gate and up GEMVs of every channel, then the selection and the gated sparse down in
-        # one launch (3 launches); same selection and bit-identical y
+        # dense-up schedule (the engine's dip_dense_up): one launch computes gate and h = fp16(silu(gate) * up) of
+        # every channel with the RMSNorm on load, a second the rule-A selection in each workgroup and the down
+        # projection as a GEMV over the transposed down_proj^T (2 launches); the same selection, y within the
+        # sparse accumulate's tolerance of the four-launch schedule's
         eng = D.DecodeEngine(w, "dip", dip_k=k, max_new_tokens=1, dip_dense_up=True)
-        us_du = run(eng)
-        assert torch.equal(eng.down, y_unfused), "dense-up DIP must equal DIP bit for bit"
-        res[f"dip_k{k}"]["dense_up_us"] = round(us_du, 2)
-        res[f"dip_k{k}"]["dense_up_schedule"] = ("gate GEMV, up GEMV, selection + gated sparse down in one launch "
-                                                 "(3 launches)")
+        us_du_unfused = run(eng)  # gate GEMV, up GEMV, SiLU gating, selection + down (4 launches)
+        gate, h_all = eng.gu[:I], eng.gu[I:]
+
+        def dense_up_mlp():
+            for l, L in enumerate(w.layers):
+                gW, gS = eng.gu_il[l]
+                Wt, St = eng.down_tt[l]
+                C.gemv_w4a16_rmsnorm_swiglu_gate_into(gW, gS, x, None, nw, eps, None, gate, h_all, H, c.group_size)
+                C.dip_select_dense_down_into(gate, h_all, k, Wt, St, None, None, eng.down, c.group_size)
+        us_du = graph_time_us(dense_up_mlp) / c.layers
+        # on layer 27's input x: the selection and y against the four-launch schedule's
+        C.dip_select_dense_down_into(gate, h_all, k, *eng.down_tt[c.layers - 1], eng.idx, eng.cnt, eng.down,
+                                     c.group_size)
+        torch.cuda.synchronize()
+        same_sel = bool(torch.equal(eng.idx, idx_dip))
+        ydiff = (eng.down.float() - y_norm.float()).abs().max().item() / max(y_norm.float().abs().max().item(), 1e-30)
+        res[f"dip_k{k}"] = {
+            "k_over_I": frac, "us": round(us_du, 2), "bytes": mlp_bytes(w.layers[0], I, H, k, dense_up=True),
+            "schedule": "gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the rule-A "
+                        "selection in every workgroup + the down as a GEMV over the transposed down_proj^T "
+                        "(2 launches)",
+            "selection_equal_indexed_up": same_sel, "y_normalized_diff_vs_indexed_up": round(ydiff, 6),
+            "dense_up_unfused_us": round(us_du_unfused, 2),
+            "indexed_up_us": round(us_4, 2), "indexed_up_bytes": nb,
+            "indexed_up_schedule": "RMSNorm-fused gate GEMV, top-k, up GEMV over the selected rows with the SiLU "
+                                   "epilogue, sparse down (4 launches)",
+            "indexed_up_no_norm_us": round(us_f, 2), "indexed_up_unfused_us": round(us, 2)}
+        res[f"dip_k{k}"]["GBps"] = round(res[f"dip_k{k}"]["bytes"] / us_du / 1e3, 1)
         del eng
     k = I // 2
     notes = {"direct": "misses read in place from the pinned host arena by the up GEMV and the down accumulate "
@@ -432,15 +455,17 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     out, toks = {}, {}
     L0 = w.layers[0]
     attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
-    modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
+    # "dip": the fastest resident DIP schedule (dense-up: gate|up GEMV + one-launch selection and down);
+    # "dip_indexed_up": the four-launch schedule the cache-aware engines reproduce bit for bit
+    modes = ("dense", "dip", "dip_indexed_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
              "cached_dip_offload")
     no_hot = [[] for _ in range(c.layers)]
     for mode in modes:
-        base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip",
+        base = {"dip_indexed_up": "dip", "cached_dip_staged": "cached_dip",
                 "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(mode, mode)
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
                              hot_channels=(no_hot if mode == "dip_offload" else hot) if base == "cached_dip" else None,
-                             max_new_tokens=n_new, dip_dense_up=mode == "dip_dense_up",
+                             max_new_tokens=n_new, dip_dense_up=mode == "dip",
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
                              offload=mode.endswith("_offload"))
         eng.capture()
@@ -455,7 +480,7 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=mode == "dip_dense_up")
+        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=mode == "dip")
         per_tok = c.layers * (attn_w + mlp) + w.lm_head.numel() * 2
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
@@ -467,9 +492,9 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         del eng
         torch.cuda.empty_cache()
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
-    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"] == toks["cached_dip_staged"]
+    out["cached_dip_tokens_equal_dip"] = toks["dip_indexed_up"] == toks["cached_dip"] == toks["cached_dip_staged"]
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
-    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip"), ("cached_dip_offload", "dip")):
+    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip_indexed_up"), ("cached_dip_offload", "dip_indexed_up")):
         assert toks[a] == toks[b], f"{a} must generate the same tokens as {b}"
     out["offload_tokens_equal_resident"] = True
     out["offload_note"] = ("*_offload: every layer's dense weights (q|k|v, o, gate|up and down for dense, gate for "
@@ -479,12 +504,13 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
                            "20% hot cache in HBM)")
     out["cached_dip"]["miss_path"] = "direct: misses read in place from the pinned host arena inside the GEMVs"
     out["cached_dip_staged"]["miss_path"] = "staged: device gathers of the misses into staging, then descriptors"
-    out["dip"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse down "
-                              "(4 launches per MLP)")
-    out["dip_dense_up_tokens_equal_dip"] = toks["dip"] == toks["dip_dense_up"]
-    assert out["dip_dense_up_tokens_equal_dip"], "the dense-up DIP schedule must generate the same tokens as DIP"
-    out["dip_dense_up"]["schedule"] = ("gate and up of every channel in one launch, top-k on gate, sparse down "
-                                       "with the SiLU gating of the selected channels on the fly")
+    out["dip_indexed_up"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse "
+                                         "down (4 launches per MLP)")
+    out["dip_tokens_equal_indexed_up"] = toks["dip"] == toks["dip_indexed_up"]
+    out["dip"]["schedule"] = ("gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the "
+                              "rule-A selection in every workgroup + the down as a GEMV over the transposed "
+                              "down_proj^T (2 launches per MLP); the selections of dip_indexed_up, y summed in "
+                              "another order")
     out["config"] = {"prompt_tokens": n_prompt, "new_tokens": n_new, "dip_k": k, "hot_fraction": 0.2,
                      "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed and LM head",
                      "kv": "fp16, max_seq 2048"}
@@ -779,9 +805,9 @@ def cpu_baseline(layer0):
 def run_traffic_set(dev, gen):
     """Launches for the HBM counter passes (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, one run each): the
     calibration copy (copy_reference: 11 copies of 512 MiB), then 6 launches each, on separate operand copies
-    and each followed by a synchronize, of sparse_down_kernel and dip_select_down_kernel at k = 3072 and of
-    attn_kernel at L = 192 and L = 2048 (host-length form: grids of 8 and 8 x 16 workgroups). Prints the
-    algorithmic bytes each launch moves."""
+    and each followed by a synchronize, of sparse_down_kernel, dip_select_down_kernel and dip_dense_down_kernel
+    (index list not written) at k = 3072 and of attn_kernel at L = 192 and L = 2048 (host-length form: grids of
+    8 and 8 x 16 workgroups). Prints the algorithmic bytes each launch moves."""
     import torch
 
     from soinfer import _C
@@ -809,6 +835,15 @@ def run_traffic_set(dev, gen):
         _C.dip_select_gated_down_into(gate, up, k, W, S, sel_i, sel_c, y, H, GS, ws)
         torch.cuda.synchronize()
     del Wt, St
+    # dip_dense_down_kernel: the transposed copy of the whole down^T ([H, I/2] nibbles, [G, I] scales)
+    Wd = [torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n)]
+    Sd = [(torch.rand(G, I, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n)]
+    hd = torch.randn(I, generator=gen, device=dev).half()
+    torch.cuda.synchronize()
+    for W, S in zip(Wd, Sd):
+        _C.dip_select_dense_down_into(gate, hd, k, W, S, None, None, y, GS)
+        torch.cuda.synchronize()
+    del Wd, Sd
     NQ, NKV, HD, Smax = 16, 8, 128, 2048
     q = torch.randn(NQ, HD, generator=gen, device=dev).half()
     for L in (192, 2048):
@@ -821,6 +856,7 @@ def run_traffic_set(dev, gen):
     print(json.dumps({"traffic_set": {
         "sparse_down_kernel_k3072": {"read": k * (row + 4 * G + 2 + 4), "write": 2 * H},
         "dip_select_down_kernel_k3072": {"read": k * (row + 4 * G + 2) + 2 * I, "write": 2 * H + 4 * k + 4},
+        "dip_dense_down_kernel_k3072": {"read": H * I // 2 + 4 * G * I + 2 * I + 2 * I, "write": 2 * H},
         "attn_kernel_L192": {"read": 4096 * 192 + 2 * NQ * HD, "write": 2 * NQ * HD},
         "attn_kernel_L2048": {"read": 4096 * 2048 + 2 * NQ * HD, "write": 2 * NQ * HD}}}))
 
@@ -835,7 +871,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the DIP MLP and decode tok/s sections")
     ap.add_argument("--traffic-set", action="store_true",
                     help="only the launches of the HBM counter passes (calibration copy, sparse down, fused "
-                         "selection + down, attention at L = 192 and 2048), then exit")
+                         "selection + down, dense down, attention at L = 192 and 2048), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU (the hot path is single-GPU; --gpus {args.gpus} is not "

@@ -408,6 +408,15 @@ int soi_gemv_w4a16_rmsnorm_gate_up(const uint8_t* Wq, const float* scale, const 
                                    const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out,
                                    uint16_t* gate_out, uint16_t* up_out, int64_t N, int64_t K, int64_t group_size,
                                    int64_t num_groups, void* stream);
+/* soi_gemv_w4a16_rmsnorm_swiglu_gate: soi_gemv_w4a16_rmsnorm with swiglu = 1
+ *   (y[N/2] = fp16(silu(gate) * up) over the 8-row interleaved gate|up rows)
+ *   that also writes gate_out[N/2] = fp16(gate), the value
+ *   soi_gemv_w4a16_rmsnorm_gate_up writes: the input of
+ *   soi_dip_select_dense_down. */
+int soi_gemv_w4a16_rmsnorm_swiglu_gate(const uint8_t* Wq, const float* scale, const uint16_t* x,
+                                       const uint16_t* delta, const uint16_t* norm_weight, float eps, uint16_t* x_out,
+                                       uint16_t* h_out, uint16_t* gate_out, uint16_t* y, int64_t N, int64_t K,
+                                       int64_t group_size, int64_t num_groups, void* stream);
 int soi_gemv_w4a16_indexed_accumulate_gated(const uint8_t* Wq_T, const float* scale_T, int64_t num_rows,
                                             const int32_t* idx, int64_t k, const uint16_t* gate, const uint16_t* up,
                                             int64_t num_channels, uint16_t* y, int64_t H, int64_t group_size,
@@ -478,6 +487,33 @@ int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* cache_scale, 
                              const int32_t* slot_of, const int32_t* sel, int64_t k, const uint16_t* h_sel,
                              uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups,
                              const uint8_t* staging_Wq, void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------------------
+ * soi_dip_select_dense_down: the DIP selection and down projection of one
+ * MLP over RESIDENT weights in one launch with no cross-workgroup step. It
+ * computes the reference's sparse accumulate (python/soinfer/runtime/
+ * generate.py:304-308 over gemv_w4a16_sparse_accumulate, csrc/bindings.cpp:
+ * 311-339) after its topk_threshold_select (csrc/bindings.cpp:507-518):
+ * y[col] = sum over the selected channels c of h[c] * s_T[c, col/gs] *
+ * q_T[c, col], the selection being that of soi_topk_threshold_select_f16abs
+ * (gate, num_channels, k). Inputs: gate[n] and h[n] = fp16(silu(gate) * up)
+ * of every channel (as soi_gemv_w4a16_rmsnorm_swiglu_gate writes them), and
+ * down_proj^T's quantized values stored TRANSPOSED: Wt [H, n/2] (row col holds
+ * q_T[0..n-1, col] packed like any INT4 row) and St [num_groups, n] (St[g, c]
+ * = s_T[c, g]). Every workgroup computes the selection itself while its rows
+ * load, then a GEMV of its 16 output columns with the coefficients h * s
+ * (fp32, carried as exact binary16 hi + lo pairs under a power-of-two scale).
+ * Reads all n channels' rows (the bytes of a dense down projection), needs
+ * no workspace; sums the reference's terms in another order (tolerance of
+ * the sparse accumulate). out_indices[k] / out_count, when not null, receive
+ * the selection exactly as the top-k function writes it (computed after y;
+ * leave them null when not needed). n a multiple of 32 in [32, 16384],
+ * 1 <= k <= n, group_size a multiple of 16, num_groups = ceil(H / group_size),
+ * Wt 16-byte aligned. No reference counterpart as a single entry point.
+ * ------------------------------------------------------------------------ */
+int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
+                              const uint8_t* Wt, const float* St, int32_t* out_indices, int32_t* out_count,
+                              uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups, void* stream);
 
 #ifdef __cplusplus
 }

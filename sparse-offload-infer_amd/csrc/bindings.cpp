@@ -1070,6 +1070,74 @@ void gemv_w4a16_rmsnorm_gate_up_into(torch::Tensor Wq, torch::Tensor scale, torc
                  n);
 }
 
+void gemv_w4a16_rmsnorm_swiglu_gate_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x,
+                                         c10::optional<torch::Tensor> delta, torch::Tensor norm_weight, double eps,
+                                         c10::optional<torch::Tensor> x_out, torch::Tensor gate_out, torch::Tensor y,
+                                         int64_t K, int64_t group_size) {
+    const char* n = "gemv_w4a16_rmsnorm_swiglu_gate_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(x, torch::kFloat16, x, n, "x");
+    need(norm_weight, torch::kFloat16, x, n, "norm_weight");
+    need(gate_out, torch::kFloat16, x, n, "gate_out");
+    need(y, torch::kFloat16, x, n, "y");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K && norm_weight.numel() == K, n,
+                ": Wq / x / norm_weight shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0), n, ": scale must be [N, num_groups]");
+    TORCH_CHECK(gate_out.numel() == Wq.size(0) / 2 && y.numel() == Wq.size(0) / 2, n,
+                ": gate_out and y must have N/2 values");
+    const uint16_t* dp = nullptr;
+    uint16_t* xo = nullptr;
+    if (delta.has_value()) {
+        need(*delta, torch::kFloat16, x, n, "delta");
+        TORCH_CHECK(delta->numel() == K, n, ": delta must be [K]");
+        dp = h16(*delta);
+    }
+    if (x_out.has_value()) {
+        need(*x_out, torch::kFloat16, x, n, "x_out");
+        TORCH_CHECK(x_out->numel() == K, n, ": x_out must be [K]");
+        xo = h16m(*x_out);
+    }
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_rmsnorm_swiglu_gate(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), dp,
+                                                    h16(norm_weight), static_cast<float>(eps), xo, nullptr,
+                                                    h16m(gate_out), h16m(y), Wq.size(0), K, group_size,
+                                                    scale.size(1), cur_stream(x)),
+                 n);
+}
+
+void dip_select_dense_down_into(torch::Tensor gate, torch::Tensor h, int64_t k, torch::Tensor Wt, torch::Tensor St,
+                                c10::optional<torch::Tensor> idx_out, c10::optional<torch::Tensor> count_out,
+                                torch::Tensor y, int64_t group_size) {
+    const char* n = "dip_select_dense_down_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(h, torch::kFloat16, gate, n, "h");
+    need(Wt, torch::kUInt8, gate, n, "Wt");
+    need(St, torch::kFloat32, gate, n, "St");
+    need(y, torch::kFloat16, gate, n, "y");
+    const int64_t I = gate.numel(), H = y.numel();
+    TORCH_CHECK(h.numel() == I, n, ": gate and h must have the same length");
+    TORCH_CHECK(k >= 1 && k <= I, n, ": k must be in [1, n]");
+    TORCH_CHECK(Wt.dim() == 2 && Wt.size(0) == H && Wt.size(1) == I / 2, n, ": Wt must be [H, n/2]");
+    TORCH_CHECK(St.dim() == 2 && St.size(1) == I, n, ": St must be [num_groups, n]");
+    int32_t* ip = nullptr;
+    int32_t* cp = nullptr;
+    if (idx_out.has_value()) {
+        need(*idx_out, torch::kInt32, gate, n, "idx_out");
+        need_numel(*idx_out, k, n, "idx_out");
+        ip = idx_out->data_ptr<int32_t>();
+    }
+    if (count_out.has_value()) {
+        need(*count_out, torch::kInt32, gate, n, "count_out");
+        need_numel(*count_out, 1, n, "count_out");
+        cp = count_out->data_ptr<int32_t>();
+    }
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_dip_select_dense_down(h16(gate), h16(h), I, k, Wt.data_ptr<uint8_t>(), St.data_ptr<float>(), ip,
+                                           cp, h16m(y), H, group_size, St.size(0), cur_stream(gate)),
+                 n);
+}
+
 void gemv_w4a16_indexed_accumulate_gated_into(torch::Tensor Wq_T, torch::Tensor scale_T, torch::Tensor idx,
                                               torch::Tensor gate, torch::Tensor up, torch::Tensor y, int64_t H,
                                               int64_t group_size, torch::Tensor workspace_buf) {
@@ -1348,6 +1416,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("gemv_w4a16_indexed_silu_into", &gemv_w4a16_indexed_silu_into, "DIP up GEMV with SiLU gating");
     m.def("gemv_w4a16_rmsnorm_gate_up_into", &gemv_w4a16_rmsnorm_gate_up_into,
           "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows, both halves written");
+    m.def("gemv_w4a16_rmsnorm_swiglu_gate_into", &gemv_w4a16_rmsnorm_swiglu_gate_into,
+          "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows: SwiGLU output and the gate half");
+    m.def("dip_select_dense_down_into", &dip_select_dense_down_into,
+          "DIP selection + down projection over resident transposed down^T values in one launch (index outputs "
+          "optional)",
+          py::arg("gate"), py::arg("h"), py::arg("k"), py::arg("Wt"), py::arg("St"), py::arg("idx_out"),
+          py::arg("count_out"), py::arg("y"), py::arg("group_size"));
     m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
           "sparse down over selected rows with the SiLU gating computed on the fly");
     m.def("dip_select_gated_down_into", &dip_select_gated_down_into,

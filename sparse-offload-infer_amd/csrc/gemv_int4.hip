@@ -634,11 +634,10 @@ extern "C" int soi_gemv_w4a16_rmsnorm_gate_up(const uint8_t* Wq, const float* sc
     return launch_status(what);
 }
 
-extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
-                                      const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out,
-                                      uint16_t* y, int64_t N, int64_t K, int64_t group_size, int64_t num_groups,
-                                      int swiglu, void* stream) {
-    const char* what = "soi_gemv_w4a16_rmsnorm";
+static int rmsnorm_impl(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
+                        const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out, uint16_t* gate_out,
+                        uint16_t* y, int64_t N, int64_t K, int64_t group_size, int64_t num_groups, int swiglu,
+                        void* stream, const char* what) {
     int st = check_int4_common(K, group_size, num_groups, what);
     if (st) return st;
     SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: N out of range", what);
@@ -661,7 +660,7 @@ extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, con
     const bool one = cs && K == 2048;  // one 64-chunk pass: the lane's x chunk stays in registers
     if (swiglu) {
         const dim3 grid(static_cast<unsigned>(N / 8));
-        const SwigluY ep{y};
+        const SwigluY ep{y, gate_out};
 #define SOI_N(CS, FL, OP)                                                                                          \
     hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, OP, SwigluY>), grid, dim3(64), 0, s, rows, N, x, delta,    \
                        norm_weight, eps, x_out, h_out, ep, Ki, gi)
@@ -695,6 +694,25 @@ extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, con
 #undef SOI_NR
 #undef SOI_N
     return launch_status(what);
+}
+
+extern "C" int soi_gemv_w4a16_rmsnorm(const uint8_t* Wq, const float* scale, const uint16_t* x, const uint16_t* delta,
+                                      const uint16_t* norm_weight, float eps, uint16_t* x_out, uint16_t* h_out,
+                                      uint16_t* y, int64_t N, int64_t K, int64_t group_size, int64_t num_groups,
+                                      int swiglu, void* stream) {
+    return rmsnorm_impl(Wq, scale, x, delta, norm_weight, eps, x_out, h_out, nullptr, y, N, K, group_size, num_groups,
+                        swiglu, stream, "soi_gemv_w4a16_rmsnorm");
+}
+
+extern "C" int soi_gemv_w4a16_rmsnorm_swiglu_gate(const uint8_t* Wq, const float* scale, const uint16_t* x,
+                                                  const uint16_t* delta, const uint16_t* norm_weight, float eps,
+                                                  uint16_t* x_out, uint16_t* h_out, uint16_t* gate_out, uint16_t* y,
+                                                  int64_t N, int64_t K, int64_t group_size, int64_t num_groups,
+                                                  void* stream) {
+    const char* what = "soi_gemv_w4a16_rmsnorm_swiglu_gate";
+    SOI_REQUIRE(gate_out, "%s: null pointer", what);
+    return rmsnorm_impl(Wq, scale, x, delta, norm_weight, eps, x_out, h_out, gate_out, y, N, K, group_size,
+                        num_groups, 1, stream, what);
 }
 
 extern "C" int soi_gemv_w4a16_indexed_silu(const uint8_t* Wq, const float* scale, int64_t num_rows, const int32_t* idx,

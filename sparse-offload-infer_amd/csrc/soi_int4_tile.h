@@ -248,11 +248,14 @@ struct SiluIdxY {
     }
 };
 
+// SwigluY: y[4t + i] = fp16(silu(g) * u) of the tile's gate row g = fp16(row 8t + i) and up row
+// u = fp16(row 8t + 4 + i); with gate set, also gate[4t + i] = g (the value SplitGUY writes).
 struct SwigluY {
     static constexpr bool kSwiglu = true;
     static constexpr bool kPrefetch = false;
     struct Pre {};
     uint16_t* y;
+    uint16_t* gate = nullptr;
 };
 
 // SplitGUY (rows interleaved by 8-row tiles as for SwigluY): row 8t + i goes to
@@ -415,9 +418,11 @@ __device__ __forceinline__ void gemv_int4_tile(const Rows& rows, int64_t N, cons
         const float other = __shfl_xor(total, 32, kWave);
         const bool vo = __shfl_xor(vr ? 1 : 0, 32, kWave) != 0;
         if ((lane & 7) == 0 && r >= 4) {
-            const float g = f16_bits_to_f32(f32_to_f16_bits(other));
+            const uint16_t gb = f32_to_f16_bits(other);
+            const float g = f16_bits_to_f32(gb);
             const float u = f16_bits_to_f32(f32_to_f16_bits(total));
             stg(ep.y + (row0 >> 1) + (r - 4), (vr && vo) ? f32_to_f16_bits(silu_f32(g) * u) : uint16_t(0x7e00u));
+            if (ep.gate) stg(ep.gate + (row0 >> 1) + (r - 4), vo ? gb : uint16_t(0x7e00u));
         }
     } else {
         if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) {

@@ -211,6 +211,33 @@ def gemv_w4a16_indexed_accumulate(Wq_T: torch.Tensor, scale_T: torch.Tensor, idx
     return _C.gemv_w4a16_indexed_accumulate(Wq_T, scale_T, idx, h_selected, H, group_size)
 
 
+def transposed_down_T(Wq_T: torch.Tensor, scale_T: torch.Tensor, H: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The same quantized down_proj^T values laid out for dip_select_dense_down: Wq_T [n, ceil(H/8)*4] packed
+    rows (channel c's H nibbles) -> Wt [H, n/2] (output column col's n nibbles, packed like every INT4 row,
+    n % 8 == 0), scale_T [n, G] -> St [G, n]. No rounding: Wt unpacks to the transpose of Wq_T's values."""
+    from soinfer.quant import pack
+
+    n = Wq_T.shape[0]
+    if n % 8:
+        raise ValueError("transposed_down_T: the channel count must be a multiple of 8")
+    q = pack.unpack_int4(Wq_T, H)  # int8 [n, H]
+    Wt, _ = pack.pack_int4(q.t().contiguous())
+    return Wt.contiguous(), scale_T.t().contiguous()
+
+
+def dip_select_dense_down(gate: torch.Tensor, h: torch.Tensor, k: int, Wt: torch.Tensor, St: torch.Tensor,
+                          group_size: int, with_indices: bool = True):
+    """One-launch DIP selection + down projection over resident weights (Wt, St from transposed_down_T):
+    y[H] = sum over the rule-A selection of top-k |gate| of h[c] * down_proj^T row c. Returns (y, indices,
+    count), the indices and count as topk_threshold_select gives them (None without with_indices)."""
+    H = Wt.shape[0]
+    y = torch.empty(H, dtype=torch.float16, device=gate.device)
+    idx = torch.empty(k, dtype=torch.int32, device=gate.device) if with_indices else None
+    cnt = torch.empty(1, dtype=torch.int32, device=gate.device) if with_indices else None
+    _C.dip_select_dense_down_into(gate, h, k, Wt, St, idx, cnt, y, group_size)
+    return y, idx, cnt
+
+
 def gather_rows_device(src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor) -> None:
     """dst[j, :] = src[idx[j], :] for device-resident rows (int32 indices; out-of-range -> zero row)."""
     _C.gather_rows_device(src, idx, dst)

@@ -215,9 +215,11 @@ class DecodeEngine:
         self.down_copy = down_copy
         if dip_dense_up and mode != "dip":
             raise ValueError("dip_dense_up applies to mode 'dip' (weights resident)")
-        # DIP schedule for resident weights: gate and up of every channel in one launch, top-k on gate, then the
-        # sparse down with the SiLU gating of the selected channels computed on the fly (one launch fewer per layer
-        # than the indexed up GEMV; the selected h values and hence every output are identical)
+        # DIP schedule for resident weights: one launch computes gate and h = fp16(silu(gate) * up) of every
+        # channel, a second runs the rule-A selection in each of its workgroups and the down projection as a GEMV
+        # over a transposed copy of down_proj^T's quantized values with the masked coefficients (no cross-
+        # workgroup step). The selection equals the four-launch schedule's; y sums the same terms in another order
+        # (within the sparse accumulate's tolerance, not bit for bit).
         self.dip_dense_up = dip_dense_up
         c = w.config
         self.w, self.c, self.mode, self.fused = w, c, mode, fused
@@ -264,6 +266,9 @@ class DecodeEngine:
             if hot_channels is None or len(hot_channels) != c.layers:
                 raise ValueError("cached_dip needs one hot-channel list per layer")
             self._setup_cache(hot_channels)
+        if dip_dense_up:
+            # down_proj^T's values transposed for the one-launch down (the same quantized values, no rounding)
+            self.down_tt = [ops.transposed_down_T(L.down_T_Wq, L.down_T_scale, H) for L in w.layers]
         if fused and (mode == "dense" or dip_dense_up):
             # gate|up rows interleaved by 8-row tiles (gate 4t..4t+3, up 4t..4t+3) for the SwiGLU epilogue
             t = torch.arange(I // 4, device=dev)
@@ -389,10 +394,8 @@ class DecodeEngine:
         if self.dip_dense_up:
             uW, uS = L.up(I)
             _C.gemv_w4a16_into(uW, uS, self.h, self.gu[I:], H, gs)
-            # selection and gated sparse down in one launch (indices and count still written)
-            _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx, self.cnt,
-                                          self.down, H, gs, self.sd_ws)
-            self._count_selection(l)
+            _C.silu_mul_into(gate, self.gu[I:], self.mlp_h)  # h of every channel
+            self._dense_down(l, gate, self.mlp_h)
             return
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         self._count_selection(l)
@@ -418,6 +421,15 @@ class DecodeEngine:
         _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
         _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
                                     self.h_sel, self.down, H, gs, self.sd_ws)
+
+    def _dense_down(self, l: int, gate: torch.Tensor, h: torch.Tensor):
+        """Selection + down of the dense-up schedule (h: fp16(silu(gate) * up) of every channel); the index list
+        is written only for the eager consumers that read it (calibration counts, the layer hook)."""
+        Wt, St = self.down_tt[l]
+        want = self.counts is not None or self.layer_hook is not None
+        _C.dip_select_dense_down_into(gate, h, self.k, Wt, St, self.idx if want else None,
+                                      self.cnt if want else None, self.down, self.c.group_size)
+        self._count_selection(l)
 
     def _count_selection(self, l: int):
         """Calibration: add this layer's selected channels to its frequency counts."""
@@ -513,11 +525,9 @@ class DecodeEngine:
         gate = self.gu[:I]
         if self.dip_dense_up:
             gW, gS = gu_il
-            _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
-                                               H, gs)
-            _C.dip_select_gated_down_into(gate, self.gu[I:], self.k, L.down_T_Wq, L.down_T_scale, self.idx,
-                                          self.cnt, self.down, H, gs, self.sd_ws)
-            self._count_selection(l)
+            _C.gemv_w4a16_rmsnorm_swiglu_gate_into(gW, gS, cur, self.o, L.post_norm, eps, other, gate, self.gu[I:],
+                                                   H, gs)
+            self._dense_down(l, gate, self.gu[I:])
             return
         gW, gS = L.gate(I)
         _C.gemv_w4a16_rmsnorm_into(gW, gS, cur, self.o, L.post_norm, eps, other, self.h, gate, H, gs, False)

@@ -122,18 +122,25 @@ def test_cached_dip_bit_identical_to_dip(dec, tiny, fused, miss_path):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-def test_dip_dense_up_schedule_bit_identical(dec, tiny, fused):
-    """Gate and up of every channel in one launch + the gated sparse down give the same tokens and the same hidden
-    state, bit for bit, as the indexed-up DIP schedule (eager and graph replay)."""
+def test_dip_dense_up_schedule(dec, tiny, fused):
+    """Gate and h of every channel in one launch + the one-launch selection and down over the transposed
+    down_proj^T: eager and graph replays give the same tokens and hidden state bit for bit; against the
+    indexed-up DIP schedule the tokens are the same and the hidden state agrees to the sparse accumulate's
+    tolerance (the down sums the same terms in another order)."""
     cfg = tiny.config
     k = cfg.intermediate // 2
     prompt = prompt_ids(6, cfg.vocab, seed=9)
     plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
     want = plain.generate(prompt, 6, use_graph=True)
     eng = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused, dip_dense_up=True)
-    for use_graph in (False, True):
-        assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"graph={use_graph}"
-        assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
+    got = eng.generate(prompt, 6, use_graph=False)
+    x_eager = eng.x_final.clone()
+    assert got == want
+    for _ in range(2):
+        assert eng.generate(prompt, 6, use_graph=True) == got
+        assert torch.equal(eng.x_final, x_eager), "graph replay differs from the eager run"
+    d = (eng.x_final.float() - plain.x_final.float()).abs().max().item()
+    assert d <= 1e-2 * plain.x_final.float().abs().max().item(), d
 
 
 @pytest.mark.parametrize("fused", [True, False])

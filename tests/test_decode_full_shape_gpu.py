@@ -3,9 +3,10 @@
 Counterpart of the reference's DIP / cache-aware DIP comparison (python/soinfer/runtime/generate.py:466-542,
 tests/test_m8_cached_dip_pipeline.py:103-138) at the real shape, k/I = 0.5, with a 20% hot cache calibrated
 from 64 seeded tokens (calibrate_hot_channels, generate.py:579-609):
-  * DIP (indexed up GEMV), DIP with the dense-up schedule (one-launch selection + gated down), and cache-aware
-    DIP with the misses read in place from pinned host memory (direct) or gathered into staging first (staged)
-    generate the same tokens and end with bit-identical hidden states, from HIP-graph replays;
+  * DIP (indexed up GEMV) and cache-aware DIP with the misses read in place from pinned host memory (direct)
+    or gathered into staging first (staged) generate the same tokens and end with bit-identical hidden states,
+    from HIP-graph replays; DIP with the dense-up schedule (one-launch selection + gated down) sums its down
+    terms in another order, so its tokens are checked for determinism (graph replay == eager run) only;
   * the first generated step, teacher-forced layer by layer: each layer's gate within 1e-3 of the binary64
     oracle GEMV on the layer's own MLP input, the selection equal to the oracle's rule A on the kernel's own
     |gate| (count = k), the gated up values h and the sparse down (on the kernel's own h) within the
@@ -59,6 +60,16 @@ def test_config5_dip_and_cached_dip_generate_identically(setup):
     x_ref = ref.x_final.clone()
     for name, eng in engines.items():
         got = eng.generate(prompt, N_NEW)
+        if name == "dip_dense_up":
+            # its down sums the same terms in another order: on this random-init model the logits are nearly flat
+            # and a 1e-3 difference in one layer's MLP output, carried through 28 layers, already moves the first
+            # argmax, so tokens are not compared with DIP (its per-layer agreement with the oracle on its own
+            # inputs is checked below); its own runs are deterministic: graph replays equal the eager run
+            x_du = eng.x_final.clone()
+            assert eng.generate(prompt, N_NEW, use_graph=False) == got
+            assert torch.equal(eng.x_final, x_du), f"{name}: eager run differs from the graph replay"
+            del eng
+            continue
         assert got == want, f"{name}: tokens differ from DIP"
         assert torch.equal(eng.x_final, x_ref), f"{name}: final hidden state differs from DIP"
         del eng
@@ -78,7 +89,8 @@ def _first_step_trace(eng, prompt):
 
     def hook(l):
         trace.append({"h": eng.h.clone(), "gate": eng.gu[:I].clone(), "idx": eng.idx.clone(),
-                      "cnt": eng.cnt.clone(), "h_sel": eng.h_sel.clone(), "down": eng.down.clone()})
+                      "cnt": eng.cnt.clone(), "h_sel": eng.h_sel.clone(), "down": eng.down.clone(),
+                      "h_all": eng.gu[I:].clone()})
 
     eng._head()
     eng.layer_hook = hook
@@ -123,8 +135,19 @@ def test_config5_first_step_per_layer_matches_oracle(setup):
         assert err <= 1e-3 * np.abs(y_ref).max(), f"layer {l} MLP: normalized error {err / np.abs(y_ref).max():.2e}"
         for name, tr in traces.items():
             o = tr[l]
+            if name == "dip_dense_up":
+                # its own inputs (the earlier layers' downs sum in another order): the selection is rule A on its own
+                # gate, and the down is the oracle's sparse accumulate over that selection and its own h
+                og = o["gate"].cpu().numpy()
+                oi = o["idx"].cpu().numpy()
+                assert int(o["cnt"].item()) == DIP_K
+                assert np.array_equal(oi, O.topk_rule_a(np.abs(og.astype(np.float32)), DIP_K)), f"{name} layer {l}"
+                oh = o["h_all"].cpu().numpy()[oi]
+                assert_close(o["down"], O.sparse_accumulate_f64(L.down_T_Wq.cpu().numpy()[oi],
+                                                                L.down_T_scale.cpu().numpy()[oi], oh, H, gs),
+                             f"{name} layer {l} down")
+                continue
             assert torch.equal(o["idx"], t["idx"]) and torch.equal(o["cnt"], t["cnt"]), f"{name} layer {l} idx"
             assert torch.equal(o["down"], t["down"]), f"{name} layer {l} MLP output"
-            if name != "dip_dense_up":  # the dense-up schedule writes neither the normed MLP input nor h_sel
-                assert torch.equal(o["h"], t["h"]), f"{name} layer {l} MLP input"
-                assert torch.equal(o["h_sel"], t["h_sel"]), f"{name} layer {l} gated up h"
+            assert torch.equal(o["h"], t["h"]), f"{name} layer {l} MLP input"
+            assert torch.equal(o["h_sel"], t["h_sel"]), f"{name} layer {l} gated up h"
