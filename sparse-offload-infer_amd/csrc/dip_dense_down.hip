@@ -12,38 +12,47 @@
 // column group g: the same terms as the reference's sum (fp32 products
 // h * s * q), in another order, with no cross-workgroup reduction at all.
 //
-// Workgroup = 8 waves x kDdRowsPerWave rows, consecutive output columns of
-// one column group.
-//   1. it requests the gates the selection reads, the gate / h / St[g] values
-//      of its 8-channel groups, then every packed chunk of its rows;
+// Workgroup = 8 waves, one output row per wave: 8 consecutive output columns
+// of one column group (tiles placed XCD-aware, below). Thread t owns the
+// 4-channel groups t + 512m (m < NC = n / 2048 rounded up); lane l of every
+// wave owns the 32-channel chunks l + 64i (i < NC) of its row.
+//   1. it requests the gate / h / St[g] values of its groups, then every
+//      packed chunk of its row;
 //   2. it forms every channel's coefficient h_c * St[g, c] in fp32 and their
 //      largest magnitude (handed over through the selection's first barrier);
-//   3. it runs the rule-A selection over all n gates itself (radix select and
-//      bisection replay, soi_select.h) while the row chunks land, and the cut
-//      that keeps the first k channels at or above the threshold
-//      (rule_a_cut): sel(c) = |gate_c| >= tau and c < cut;
-//   4. x_g[c] = sel(c) * coefficient is scaled by a power of two 2^e (exact;
-//      e from the largest magnitude) and split into binary16 hi + lo parts in
-//      LDS (hi = fp16(x), lo = fp16(x - hi): x to ~2^-22 relative), so the
-//      dot products run as v_dot2 on exact binary16 q values with fp32
-//      accumulation;
-//   5. each wave sums its rows over its lanes (DPP), rescales by 2^-e and
+//   3. it runs rule A's threshold search over all n gates itself (radix
+//      select and bisection replay, soi_select.h) while the row chunks land;
+//   4. x_g[c] = [|gate_c| >= tau] * coefficient is scaled by a power of two
+//      2^e (exact; e from the largest magnitude) and split into binary16
+//      hi + lo parts in LDS (hi = fp16(x), lo = fp16(x - hi): x to ~2^-22
+//      relative), and the 32-bit mask [|gate| >= tau] of every chunk goes to
+//      LDS beside them (one barrier);
+//   5. rule A keeps the first k channels with |gate| >= tau in index order:
+//      every wave counts its lanes' chunk masks in chunk order (one wave
+//      prefix sum per i), so each lane knows whether its chunk lies wholly
+//      before the k-th kept channel (kept), wholly after it (skipped) or holds
+//      it (the x values past it are masked off in that lane's registers);
+//   6. the dot products run as v_dot2 on exact binary16 q values with fp32
+//      accumulation; each wave sums over its lanes (DPP), rescales by 2^-e and
 //      stores y.
-// The index list of the selection is written only when asked for, after y.
+// The index list of the selection is written only when asked for, after y,
+// from the same chunk masks and counts.
 #include "soi_device.h"
 #include "soi_host.h"
 #include "soi_select.h"
 
 namespace soi {
 
-constexpr int kDdRowsPerWave = 1;  // output rows per wave: one, for the most workgroups per launch
-constexpr int kDdWaves = 8;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kDdWaves = 8;  // = output rows per workgroup (one per wave)
 constexpr int kDdThreads = kDdWaves * kWave;
-constexpr int kDdMaxChannels = kDdThreads * 32;    // the selection's E <= 32 keys per thread
-constexpr int kDdMaxChunks = kDdMaxChannels / 32;  // 16-byte (32-channel) chunks of a row
-constexpr int kDdMaxGroups = 4;                    // 8-channel groups per thread for the coefficients
-constexpr int kXcds = 8;                           // accelerator complex dies, each with its own L2
-constexpr int kDdPitch = 80;                       // LDS bytes per chunk of 32 binary16 x values (64 + 16)
+constexpr int kDdChannelsPerPass = kDdThreads * 4;        // one 4-channel group per thread
+constexpr int kDdMaxNC = 8;                               // 4-channel groups per thread (= chunks per lane)
+constexpr int kDdMaxChannels = kDdChannelsPerPass * kDdMaxNC;
+constexpr int kDdMaxChunks = kDdMaxChannels / 32;         // 32-channel chunks
+constexpr int kXcds = 8;                                  // accelerator complex dies, each with its own L2
+constexpr int kDdPitch = 80;                              // LDS bytes per chunk of 32 binary16 x values (64 + 16)
 
 struct DdArgs {
     const uint16_t* gate;  // [n]
@@ -56,197 +65,220 @@ struct DdArgs {
     int n, k, H, gs;
 };
 
+// Bit position of the r-th lowest set bit of x (1 <= r <= popcount(x)): a binary search on popcounts.
+__device__ __forceinline__ int nth_set_bit(uint32_t x, uint32_t r) {
+    int pos = 0;
+#pragma unroll
+    for (int w = 16; w >= 1; w >>= 1) {
+        const uint32_t low = static_cast<uint32_t>(__builtin_popcount(x & ((1u << w) - 1u)));
+        if (low < r) {
+            r -= low;
+            x >>= w;
+            pos += w;
+        }
+    }
+    return pos;
+}
+
+// OR over the 8 lanes 8j .. 8j+7 (quad swaps, then the 8-lane mirror); every lane of the 8 gets it.
+__device__ __forceinline__ uint32_t or8_lanes(uint32_t v) {
+    v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false));
+    v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, false));
+    v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xf, 0xf, false));
+    return v;
+}
+
 // x values of channels 32c .. 32c+31 at LDS byte offset kDdPitch * c: with the 80-byte pitch the 16-byte reads
-// of 16 lanes (chunks c .. c+15) cover the 64 banks once. RPW output rows per wave, 8 * RPW per workgroup.
-template <int E, int NCH, int RPW>
+// of 16 lanes (chunks c .. c+15) cover the 64 banks once.
+template <int NC>
 __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
+    constexpr int E = 4 * NC;  // selection keys per thread
     __shared__ uint32_t s_hist[radix_hist_offset<F16AbsValues>(F16AbsValues::kPasses)];
     __shared__ float s_max[kDdWaves];
-    __shared__ uint32_t s_tot[kDdWaves];
     __shared__ float s_cmax[kDdWaves];
-    __shared__ int32_t s_cut;
+    __shared__ uint32_t s_bits[kDdMaxChunks];
     __shared__ __attribute__((aligned(16))) uint8_t s_xh[kDdMaxChunks * kDdPitch];
     __shared__ __attribute__((aligned(16))) uint8_t s_xl[kDdMaxChunks * kDdPitch];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
     const int n = a.n;
     const int chunks = n >> 5;  // n % 32 == 0 (checked on the host)
-    const int groups8 = n >> 3;
+    const int groups4 = n >> 2;
     // workgroups go to the 8 XCDs round-robin by linear id; tile (b % 8) * (nb / 8) + b / 8 gives XCD x the
     // consecutive tiles x * nb/8 .. (x+1) * nb/8 - 1, so the workgroups sharing a column group (and its St row)
     // mostly share one L2 instead of fetching the row once per XCD
     const int nb = gridDim.x, b = blockIdx.x;
     const int tile = (nb % kXcds == 0) ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
-    const int row_base = tile * (kDdWaves * RPW);
-    const int g = row_base / a.gs;  // the workgroup's column group (8 * RPW divides gs)
-    const int base_i = wave * kWave * E + lane;
+    const int row = tile * kDdWaves + wave;
+    const int g = (tile * kDdWaves) / a.gs;  // the workgroup's column group (8 divides gs)
     const u32x4* z4 = reinterpret_cast<const u32x4*>(g_zero16);
+    const u32x2* z2 = reinterpret_cast<const u32x2*>(g_zero16);
 
-    // 1. requested first (loads return in order): the selection's gates (blocked: thread owns
-    // wave*64E + 64j + lane), then the gate / h / St[g] values of the thread's 8-channel groups q = tid + 512m
-    uint32_t raw[E];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int i = base_i + j * kWave;
-        raw[j] = ldg(a.gate + (i < n ? i : n - 1));
-    }
-    u32x4 gq[kDdMaxGroups], hq[kDdMaxGroups], sq0[kDdMaxGroups], sq1[kDdMaxGroups];
+    // 1. requested first (loads return in order): gate / h / St[g] of the thread's groups q = tid + 512m
+    u32x2 gq[NC], hq[NC];
+    u32x4 sq[NC];
     const float* sg = a.S + static_cast<int64_t>(g) * n;
 #pragma unroll
-    for (int m = 0; m < kDdMaxGroups; ++m) {
+    for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
-        const bool ok = q < groups8;
-        gq[m] = ldg(ok ? reinterpret_cast<const u32x4*>(a.gate) + q : z4);
-        hq[m] = ldg(ok ? reinterpret_cast<const u32x4*>(a.h) + q : z4);
-        sq0[m] = ldg(ok ? reinterpret_cast<const u32x4*>(sg) + 2 * q : z4);
-        sq1[m] = ldg(ok ? reinterpret_cast<const u32x4*>(sg) + 2 * q + 1 : z4);
+        const bool ok = q < groups4;
+        gq[m] = ldg(ok ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
+        hq[m] = ldg(ok ? reinterpret_cast<const u32x2*>(a.h) + q : z2);
+        sq[m] = ldg(ok ? reinterpret_cast<const u32x4*>(sg) + q : z4);
     }
-    // every chunk of the wave's rows (lane takes chunks lane, lane + 64, ...)
-    u32x4 wv[RPW][NCH];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const int row = row_base + wave * RPW + r;
+    // every chunk of the wave's row (lane takes chunks lane, lane + 64, ...)
+    u32x4 wv[NC];
+    {
         const u32x4* rp = reinterpret_cast<const u32x4*>(a.W + static_cast<int64_t>(row < a.H ? row : 0) * (n >> 1));
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
+        for (int i = 0; i < NC; ++i) {
             const int c = lane + i * kWave;
-            wv[r][i] = __builtin_nontemporal_load((row < a.H && c < chunks) ? rp + c : z4);
+            wv[i] = __builtin_nontemporal_load((row < a.H && c < chunks) ? rp + c : z4);
         }
     }
 
-    // 2. the coefficients h * St[g] of every channel (fp32, unmasked) and their largest magnitude, handed to
-    // the other waves through the selection's first barrier
-    float xc[kDdMaxGroups][8];
-    float cmax = 0.0f;
+    // 2. |gate| (NaN past the end: key 0, never counted or selected), the coefficients h * St[g] (fp32,
+    // unmasked) and their largest magnitude, handed to the other waves through the selection's first barrier
+    float gv[NC][4], xc[NC][4];
+    uint32_t key[E];
+    float local_max = 0.0f, cmax = 0.0f;
 #pragma unroll
-    for (int m = 0; m < kDdMaxGroups; ++m) {
+    for (int m = 0; m < NC; ++m) {
+        const bool ok = tid + m * kDdThreads < groups4;
         // vector lanes are copied to scalars before the bit cast: __builtin_bit_cast applied to a lane of an
-        // ext_vector value (sq0[m].y) was compiled as a cast of lane 0
-        const uint32_t hw[4] = {hq[m].x, hq[m].y, hq[m].z, hq[m].w};
-        const uint32_t su[8] = {sq0[m].x, sq0[m].y, sq0[m].z, sq0[m].w, sq1[m].x, sq1[m].y, sq1[m].z, sq1[m].w};
-        float sv[8];
+        // ext_vector value (sq[m].y) was compiled as a cast of lane 0
+        const uint32_t gw[2] = {gq[m].x, gq[m].y};
+        const uint32_t hw[2] = {hq[m].x, hq[m].y};
+        const uint32_t su[4] = {sq[m].x, sq[m].y, sq[m].z, sq[m].w};
 #pragma unroll
-        for (int p = 0; p < 8; ++p) sv[p] = __builtin_bit_cast(float, su[p]);
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t gb = ((gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu) | (ok ? 0u : 0x7e00u);
+            gv[m][p] = f16_bits_to_f32(static_cast<uint16_t>(gb));
+            key[4 * m + p] = F16AbsValues::key_of(gv[m][p]);
+            local_max = fmaxf(local_max, gv[m][p]);
             const uint16_t hb = static_cast<uint16_t>(hw[p >> 1] >> (16 * (p & 1)));
-            xc[m][p] = f16_bits_to_f32(hb) * sv[p];
+            xc[m][p] = f16_bits_to_f32(hb) * __builtin_bit_cast(float, su[p]);
             cmax = fmaxf(cmax, fabsf(xc[m][p]));
         }
     }
     cmax = wave_max_bcast(cmax);
     if (lane == 0) s_cmax[wave] = cmax;
 
-    // 3. tau and the cut; past the end the pattern is made a NaN (key 0, never selected) by a bit select
-    float val[E];
-    float tau;
-    int32_t cut;
-    uint32_t total;
-    {
-        uint32_t key[E];
-        float local_max = 0.0f;
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const int i = base_i + j * kWave;
-            const uint32_t bits = (raw[j] & 0x7fffu) | (i < n ? 0u : 0x7e00u);
-            val[j] = f16_bits_to_f32(static_cast<uint16_t>(bits));
-            key[j] = F16AbsValues::key_of(val[j]);
-            local_max = fmaxf(local_max, val[j]);
-        }
-        tau = rule_a_tau<E, kDdWaves, F16AbsValues>(key, local_max, s_hist, s_max, a.k, tid);
-        total = rule_a_cut<E, kDdWaves>(val, tau, a.k, s_tot, &s_cut, tid, cut);
-    }
+    // 3. tau of rule A
+    const float tau = rule_a_tau<E, kDdWaves, F16AbsValues>(key, local_max, s_hist, s_max, a.k, tid);
 
-    // 4. x_g[c] = sel(c) * h_c * St[g, c] scaled by 2^e (exact; e from the largest |h * s| of all channels, a
-    // bound for the selected ones) and split into binary16 hi + lo: 16-byte LDS stores per 8-channel group
+    // 4. x_g[c] = [|gate_c| >= tau] * h_c * St[g, c] scaled by 2^e (exact; e from the largest |h * s| of all
+    // channels, a bound for the selected ones), split into binary16 hi + lo (8-byte LDS stores per group), and
+    // the chunk masks: lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m
     float mx = s_cmax[0];
 #pragma unroll
     for (int w = 1; w < kDdWaves; ++w) mx = fmaxf(mx, s_cmax[w]);
     const int e = 15 - __builtin_amdgcn_frexp_expf(mx);  // max * 2^e < 2^15: no binary16 overflow
 #pragma unroll
-    for (int m = 0; m < kDdMaxGroups; ++m) {
+    for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
-        if (q < groups8) {
-            const uint32_t gw[4] = {gq[m].x, gq[m].y, gq[m].z, gq[m].w};
-            uint32_t hp[4], lp[4];
+        uint32_t m4 = 0u;
+        uint16_t hb[4], lb[4];
 #pragma unroll
-            for (int p2 = 0; p2 < 4; ++p2) {
-                uint16_t hb[2], lb[2];
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int p = 2 * p2 + t;
-                    const int c = 8 * q + p;
-                    const uint16_t gb = static_cast<uint16_t>(gw[p2] >> (16 * t));
-                    const float gv = f16_bits_to_f32(static_cast<uint16_t>(gb & 0x7fffu));
-                    const bool sel = gv >= tau && c < cut;  // NaN gates are never selected
-                    const float xs = sel ? __builtin_ldexpf(xc[m][p], e) : 0.0f;
-                    hb[t] = f32_to_f16_bits(xs);
-                    lb[t] = f32_to_f16_bits(xs - f16_bits_to_f32(hb[t]));  // exact difference
-                }
-                hp[p2] = static_cast<uint32_t>(hb[0]) | (static_cast<uint32_t>(hb[1]) << 16);
-                lp[p2] = static_cast<uint32_t>(lb[0]) | (static_cast<uint32_t>(lb[1]) << 16);
-            }
-            const int off = kDdPitch * (q >> 2) + 16 * (q & 3);
-            *reinterpret_cast<u32x4*>(s_xh + off) = u32x4{hp[0], hp[1], hp[2], hp[3]};
-            *reinterpret_cast<u32x4*>(s_xl + off) = u32x4{lp[0], lp[1], lp[2], lp[3]};
+        for (int p = 0; p < 4; ++p) {
+            const bool sel = gv[m][p] >= tau;  // NaN (and padding) never
+            const float xs = sel ? __builtin_ldexpf(xc[m][p], e) : 0.0f;
+            hb[p] = f32_to_f16_bits(xs);
+            lb[p] = f32_to_f16_bits(xs - f16_bits_to_f32(hb[p]));  // exact difference
+            m4 |= (sel ? 1u : 0u) << p;
+        }
+        const uint32_t cm = or8_lanes(m4 << (4 * (lane & 7)));
+        if (q < groups4) {
+            const int off = kDdPitch * (q >> 3) + 8 * (q & 7);
+            *reinterpret_cast<u32x2*>(s_xh + off) =
+                u32x2{hb[0] | (static_cast<uint32_t>(hb[1]) << 16), hb[2] | (static_cast<uint32_t>(hb[3]) << 16)};
+            *reinterpret_cast<u32x2*>(s_xl + off) =
+                u32x2{lb[0] | (static_cast<uint32_t>(lb[1]) << 16), lb[2] | (static_cast<uint32_t>(lb[3]) << 16)};
+            if ((lane & 7) == 0) s_bits[q >> 3] = cm;
         }
     }
     __syncthreads();
 
-    // 5. the wave's rows: chunk by chunk, the rows share the chunk's x values
-    float acc[RPW];
+    // 5. the first k channels with |gate| >= tau, chunk by chunk in index order (i-major, then lane):
+    // before[i] = kept channels of all earlier chunks, keep[i] = channels of the lane's chunk i that stay
+    // (0: none, 32: all; else the chunk holds the k-th kept channel and channels >= keep[i] are dropped)
+    const uint32_t k = static_cast<uint32_t>(a.k);
+    uint32_t total = 0u;
+    uint32_t before[NC], bits[NC];
+    int keep[NC];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+    for (int i = 0; i < NC; ++i) {
         const int c = lane + i * kWave;
-        if (c < chunks) {
+        bits[i] = c < chunks ? s_bits[c] : 0u;
+        const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(bits[i]));
+        const uint32_t incl = wave_prefix_u32(cnt);
+        before[i] = total + incl - cnt;
+        total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+        keep[i] = before[i] >= k ? 0 : (before[i] + cnt <= k ? 32 : nth_set_bit(bits[i], k - before[i]) + 1);
+    }
+
+    // 6. the wave's row
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + i * kWave;
+        if (c < chunks && keep[i] > 0) {
             const u32x4* ph = reinterpret_cast<const u32x4*>(s_xh + kDdPitch * c);
             const u32x4* pl = reinterpret_cast<const u32x4*>(s_xl + kDdPitch * c);
-            u32x4 xh[4], xl[4];
+            uint32_t hx[16], lx[16];
 #pragma unroll
             for (int wd = 0; wd < 4; ++wd) {
-                xh[wd] = ph[wd];
-                xl[wd] = pl[wd];
+                const u32x4 vh = ph[wd], vl = pl[wd];
+                hx[4 * wd] = vh.x, hx[4 * wd + 1] = vh.y, hx[4 * wd + 2] = vh.z, hx[4 * wd + 3] = vh.w;
+                lx[4 * wd] = vl.x, lx[4 * wd + 1] = vl.y, lx[4 * wd + 2] = vl.z, lx[4 * wd + 3] = vl.w;
             }
+            if (keep[i] < 32) {  // the chunk holding the k-th kept channel: channels >= keep[i] dropped
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                const uint32_t wq[4] = {wv[r][i].x, wv[r][i].y, wv[r][i].z, wv[r][i].w};
-                float th = 0.0f, tl = 0.0f;
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd) {
-                    f16x2 qv[4];
-                    dequant_int4x8_bitfield(wq[wd], qv);
-                    const uint32_t hx[4] = {xh[wd].x, xh[wd].y, xh[wd].z, xh[wd].w};
-                    const uint32_t lx[4] = {xl[wd].x, xl[wd].y, xl[wd].z, xl[wd].w};
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        th = dot2(qv[p], as_f16x2(hx[p]), th);
-                        tl = dot2(qv[p], as_f16x2(lx[p]), tl);
-                    }
+                for (int w = 0; w < 16; ++w) {
+                    const uint32_t mk = (2 * w < keep[i] ? 0x0000ffffu : 0u) | (2 * w + 1 < keep[i] ? 0xffff0000u : 0u);
+                    hx[w] &= mk;
+                    lx[w] &= mk;
                 }
-                acc[r] += th + tl;
             }
+            const uint32_t wq[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+            float th = 0.0f, tl = 0.0f;
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+                f16x2 qv[4];
+                dequant_int4x8_bitfield(wq[wd], qv);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    th = dot2(qv[p], as_f16x2(hx[4 * wd + p]), th);
+                    tl = dot2(qv[p], as_f16x2(lx[4 * wd + p]), tl);
+                }
+            }
+            acc += th + tl;
         }
     }
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const float t = wave_sum_bcast(acc[r]);
-        const int row = row_base + wave * RPW + r;
+    {
+        const float t = wave_sum_bcast(acc);
         if (lane == 0 && row < a.H) stg(a.y + row, f32_to_f16_bits(__builtin_ldexpf(t, -e)));
     }
 
-    // 6. the index list when asked for (after y): workgroup b writes positions [b*win, (b+1)*win)
-    const uint32_t kk = total < static_cast<uint32_t>(a.k) ? total : static_cast<uint32_t>(a.k);
-    if (blockIdx.x == 0 && tid == 0 && a.out_count) stg(a.out_count, static_cast<int32_t>(kk));
-    if (!a.out_idx) return;  // workgroup-uniform
-    const uint32_t win = (kk + gridDim.x - 1) / gridDim.x;
-    const uint32_t lo = blockIdx.x * win;
+    // 7. the index list when asked for (after y), by wave 0: workgroup b writes positions [b*win, (b+1)*win)
+    const uint32_t kk = total < k ? total : k;
+    if (b == 0 && tid == 0 && a.out_count) stg(a.out_count, static_cast<int32_t>(kk));
+    if (!a.out_idx || wave != 0) return;  // wave-uniform
+    const uint32_t win = (kk + nb - 1) / nb;
+    const uint32_t lo = b * win;
     const uint32_t hi = lo + win < kk ? lo + win : kk;
-    if (lo >= hi) return;  // workgroup-uniform
-    rule_a_compact<E, kDdWaves>(val, tau, s_tot, tid, lo, hi, [&](uint32_t pos, int j) {
-        stg(a.out_idx + pos, static_cast<int32_t>(base_i + j * kWave));
-    });
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + i * kWave;
+        uint32_t x = keep[i] >= 32 ? bits[i] : (bits[i] & ((1u << keep[i]) - 1u));
+        uint32_t pos = before[i];
+        if (c >= chunks || pos >= hi || pos + static_cast<uint32_t>(__builtin_popcount(x)) <= lo) continue;
+        while (x != 0u) {
+            if (pos >= lo && pos < hi) stg(a.out_idx + pos, static_cast<int32_t>(32 * c + __builtin_ctz(x)));
+            ++pos;
+            x &= x - 1u;
+        }
+    }
 }
 
 }  // namespace soi
@@ -263,35 +295,29 @@ extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h
                 what, kDdMaxChannels);
     SOI_REQUIRE(k >= 1 && k <= n, "%s: k must be in [1, num_channels]", what);
     SOI_REQUIRE(H >= 1 && H <= (int64_t(1) << 24), "%s: H out of range", what);
-    SOI_REQUIRE(group_size >= kDdWaves * kDdRowsPerWave && group_size % (kDdWaves * kDdRowsPerWave) == 0,
-                "%s: group_size must be a positive multiple of %d", what, kDdWaves * kDdRowsPerWave);
+    SOI_REQUIRE(group_size >= kDdWaves && group_size % kDdWaves == 0, "%s: group_size must be a positive multiple of %d",
+                what, kDdWaves);
     SOI_REQUIRE(num_groups == ceil_div64(H, group_size), "%s: num_groups must be ceil(H / group_size)", what);
     SOI_REQUIRE(gate && h && Wt && St && y, "%s: null pointer", what);
-    SOI_REQUIRE(aligned16(Wt), "%s: Wt must be 16-byte aligned", what);
+    SOI_REQUIRE(aligned16(Wt) && aligned16(St), "%s: Wt and St must be 16-byte aligned", what);
+    SOI_REQUIRE((reinterpret_cast<uintptr_t>(gate) & 7u) == 0 && (reinterpret_cast<uintptr_t>(h) & 7u) == 0,
+                "%s: gate and h must be 8-byte aligned", what);
     DdArgs a{gate, h, Wt, St, out_indices, out_count, y, static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(H), static_cast<int>(group_size)};
-    constexpr int RPW = kDdRowsPerWave;
-    const dim3 grid(static_cast<unsigned>(ceil_div64(H, kDdWaves * RPW))), block(kDdThreads);
-    const int64_t E = ceil_div64(n, kDdThreads);
-    const int64_t nch = ceil_div64(n / 32, kWave);
+    const dim3 grid(static_cast<unsigned>(ceil_div64(H, kDdWaves))), block(kDdThreads);
+    const int64_t nc = ceil_div64(n, kDdChannelsPerPass);
     hipStream_t st = as_stream(stream);
-#define SOI_DD(EE, CC) hipLaunchKernelGGL((dip_dense_down_kernel<EE, CC, RPW>), grid, block, 0, st, a)
-#define SOI_DDC(EE)                       \
-    do {                                  \
-        if (nch <= 1) SOI_DD(EE, 1);      \
-        else if (nch <= 2) SOI_DD(EE, 2); \
-        else if (nch <= 3) SOI_DD(EE, 3); \
-        else if (nch <= 4) SOI_DD(EE, 4); \
-        else if (nch <= 6) SOI_DD(EE, 6); \
-        else SOI_DD(EE, 8);               \
-    } while (0)
-    if (E <= 4) SOI_DDC(4);
-    else if (E <= 8) SOI_DDC(8);
-    else if (E <= 12) SOI_DDC(12);
-    else if (E <= 16) SOI_DDC(16);
-    else if (E <= 24) SOI_DDC(24);
-    else SOI_DDC(32);
-#undef SOI_DDC
+#define SOI_DD(NN) hipLaunchKernelGGL((dip_dense_down_kernel<NN>), grid, block, 0, st, a)
+    switch (nc) {
+        case 1: SOI_DD(1); break;
+        case 2: SOI_DD(2); break;
+        case 3: SOI_DD(3); break;
+        case 4: SOI_DD(4); break;
+        case 5: SOI_DD(5); break;
+        case 6: SOI_DD(6); break;
+        case 7: SOI_DD(7); break;
+        default: SOI_DD(8); break;
+    }
 #undef SOI_DD
     return launch_status(what);
 }

@@ -232,48 +232,4 @@ __device__ __forceinline__ uint32_t rule_a_compact(const float (&val)[E], float 
     return rule_a_compact<E, NW>(val, tau, s_tot, tid, 0u, 0xffffffffu, static_cast<Emit&&>(emit));
 }
 
-// The rule-A selection without positions: the selected elements are those
-// with val >= tau and index < cut, i.e. the first k in index order (element
-// (j, lane) of wave w is index w*64E + 64j + lane, as for rule_a_compact).
-// Returns the number with val >= tau; cut = one past the index of the k-th
-// such element, or INT32_MAX when there are at most k. Only the wave holding
-// the k-th element walks its ballots a second time. s_tot: NW words; s_cut:
-// one word; two barriers.
-template <int E, int NW>
-__device__ __forceinline__ uint32_t rule_a_cut(const float (&val)[E], float tau, int k, uint32_t* s_tot,
-                                               int32_t* s_cut, int tid, int32_t& cut) {
-    const int wave = tid >> 6, lane = tid & 63;
-    uint32_t wave_total = 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) wave_total += popc64(ballot(val[j] >= tau));
-    if (lane == 0) s_tot[wave] = wave_total;
-    if (tid == 0) *s_cut = INT32_MAX;
-    __syncthreads();
-    uint32_t before = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        const uint32_t c = s_tot[w];
-        before += (w < wave) ? c : 0u;
-        total += c;
-    }
-    const uint32_t ku = static_cast<uint32_t>(k);
-    if (total > ku && before < ku && before + wave_total >= ku) {  // wave-uniform: this wave holds the k-th
-        uint32_t r = ku - before;                                    // its 1-based rank within the wave
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const bool sel = val[j] >= tau;
-            const uint64_t mk = ballot(sel);
-            const uint32_t pc = popc64(mk);
-            if (r <= pc) {
-                if (sel && mask_prefix(mk) + 1 == r) *s_cut = wave * kWave * E + j * kWave + lane + 1;
-                break;
-            }
-            r -= pc;
-        }
-    }
-    __syncthreads();
-    cut = *s_cut;
-    return total;
-}
-
 }  // namespace soi
