@@ -21,7 +21,8 @@
 //   * scores: v_dot2 over the lane's 8 dims, then a butterfly over the row's
 //     lanes; softmax runs in the log2 domain (scores pre-multiplied by
 //     scale*log2(e), v_exp_f32) with the online max/sum recurrence of the
-//     reference (m0 = -1e30);
+//     reference (m0 = -1e30) taken one chunk of passes at a time: the
+//     chunk's scores first, one rescale, then its rows enter the sums;
 //   * lane groups, then waves (in wave order) are merged with the standard
 //     (m, l, acc) rescaling;
 //   * short contexts (at most 8 passes: 256 timesteps at head_dim 128) run
@@ -97,41 +98,50 @@ struct AttnState {
     float m[REP], l[REP], acc[REP][8];
 };
 
-// One pass: the lane's row (K kk, V vv) enters the online softmax of every query head.
+// Score of the lane's row (K kk) for every query head, pre-multiplied by scale * log2(e): v_dot2 over the
+// lane's 8 dims, then a sum over the row's lanes (every lane of the group takes part); -inf for a row past the
+// range. Heads past rep (rep not a power of two) are computed on head 0's q and never written.
 template <int LPR, int REP>
-__device__ __forceinline__ void attn_pass(AttnState<LPR, REP>& st, const f16x2 (&qv)[REP][4], int rep, bool valid,
-                                          const u32x4& kk, const u32x4& vv, float scale_log2) {
+__device__ __forceinline__ void attn_scores(float (&sc)[REP], const f16x2 (&qv)[REP][4], bool valid, const u32x4& kk,
+                                            float scale_log2) {
     const f16x2 k0 = as_f16x2(kk.x), k1 = as_f16x2(kk.y), k2 = as_f16x2(kk.z), k3 = as_f16x2(kk.w);
-    const f16x2 v2[4] = {as_f16x2(vv.x), as_f16x2(vv.y), as_f16x2(vv.z), as_f16x2(vv.w)};
 #pragma unroll
     for (int hh = 0; hh < REP; ++hh) {
-        if (hh >= rep) break;
         float part_s = dot2(qv[hh][0], k0, 0.0f);
         part_s = dot2(qv[hh][1], k1, part_s);
         part_s = dot2(qv[hh][2], k2, part_s);
         part_s = dot2(qv[hh][3], k3, part_s);
-        float sc = group_sum<LPR>(part_s) * scale_log2;  // every lane of the group takes part
-        if (!valid) sc = -__builtin_inff();
-        const float mn = fmaxf(st.m[hh], sc);
-        const float corr = fast_exp2(st.m[hh] - mn);
-        const float p = fast_exp2(sc - mn);
-        st.l[hh] = fmaf(st.l[hh], corr, p);
+        const float sc_h = group_sum<LPR>(part_s) * scale_log2;
+        sc[hh] = valid ? sc_h : -__builtin_inff();
+    }
+}
+
+// The lane's row (V vv) with weight 2^(sc - m) enters every query head's sum (m already covers sc).
+template <int LPR, int REP>
+__device__ __forceinline__ void attn_accumulate(AttnState<LPR, REP>& st, const float (&sc)[REP], const u32x4& vv) {
+    const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+    float v[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            st.acc[hh][2 * e] = fmaf(st.acc[hh][2 * e], corr, p * static_cast<float>(v2[e].x));
-            st.acc[hh][2 * e + 1] = fmaf(st.acc[hh][2 * e + 1], corr, p * static_cast<float>(v2[e].y));
-        }
-        st.m[hh] = mn;
+    for (int e = 0; e < 4; ++e) {
+        const f16x2 v2 = as_f16x2(vw[e]);
+        v[2 * e] = static_cast<float>(v2.x);
+        v[2 * e + 1] = static_cast<float>(v2.y);
+    }
+#pragma unroll
+    for (int hh = 0; hh < REP; ++hh) {
+        const float p = fast_exp2(sc[hh] - st.m[hh]);
+        st.l[hh] += p;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) st.acc[hh][d] = fmaf(p, v[d], st.acc[hh][d]);
     }
 }
 
 // Merge lane l's state with lane l ^ MASK's for MASK = M, 2M, ... 32.
 template <int LPR, int REP, int MASK>
-__device__ __forceinline__ void attn_merge_groups(AttnState<LPR, REP>& st, int rep) {
+__device__ __forceinline__ void attn_merge_groups(AttnState<LPR, REP>& st) {
     if constexpr (MASK < kWave) {
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
-            if (hh >= rep) break;
             const float mo = xor_lanes<MASK>(st.m[hh]);
             const float lo = xor_lanes<MASK>(st.l[hh]);
             const float mn = fmaxf(st.m[hh], mo);
@@ -144,7 +154,7 @@ __device__ __forceinline__ void attn_merge_groups(AttnState<LPR, REP>& st, int r
             }
             st.m[hh] = mn;
         }
-        attn_merge_groups<LPR, REP, MASK * 2>(st, rep);
+        attn_merge_groups<LPR, REP, MASK * 2>(st);
     }
 }
 
@@ -294,36 +304,62 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     const bool has_new = pvalid && p >= t0 && p < t1;
     const int tnew = has_new ? p : -1;
 
-    // request the K/V rows of the first chunk now: they do not depend on q (row p is patched from LDS later)
+    // this KV head's cache
     const uint16_t* kbase = a.kc + static_cast<int64_t>(kvh) * S * HD;
     const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * S * HD;
     const int tb0 = t0 + wave * RPI;
     const int npass_all = (t1 - t0 + STEP - 1) / STEP;
+    // PRE: q heads kvh*rep + hh (and, in the workgroup holding p, the new k) are normed and rotated; wave w
+    // takes heads w, w+8, ... With head_dim 128 (one pair per lane) the operands of the wave's first head are
+    // requested before the K/V rows (loads return in order), so its RMSNorm and RoPE run while the rows are in
+    // flight.
+    const int prow = pvalid ? p : (p < 0 ? 0 : S - 1);  // RoPE table row
+    const int nh = PRE ? rep + (has_new ? 1 : 0) : 0;
+    auto head_src = [&](int hh) {
+        return a.q + static_cast<int64_t>(hh == rep ? a.NQ + kvh : kvh * rep + hh) * HD;
+    };
+    uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
+    float f_c = 0.0f, f_sn = 0.0f;
+    if (PRE && HALF == kWave && wave < nh) {  // wave-uniform
+        const uint16_t* src = head_src(wave);
+        const uint16_t* wn = wave == rep ? a.k_norm : a.q_norm;
+        f_x1 = ldg(src + lane);
+        f_x2 = ldg(src + lane + HALF);
+        f_w1 = ldg(wn + lane);
+        f_w2 = ldg(wn + lane + HALF);
+        f_c = ldg(a.cos_t + static_cast<int64_t>(prow) * HALF + lane);
+        f_sn = ldg(a.sin_t + static_cast<int64_t>(prow) * HALF + lane);
+    }
+    // the K/V rows of the first chunk: they do not depend on q (row p is patched from LDS later)
     AttnRows<LPR> rows;
     rows.load(kbase, vbase, tb0, t1, npass_all < kAttnPassMax ? npass_all : kAttnPassMax);
 
     f16x2 qv[REP][4];
     if (PRE) {
-        // q heads kvh*rep + hh (and, in the workgroup holding p, the new k): wave w takes heads w, w+8, ...
         // Lane l reduces elements l, l+64, ... in that order (the order of qk_norm_rope_append).
-        const int prow = pvalid ? p : (p < 0 ? 0 : S - 1);  // RoPE table row
-        const int nh = rep + (has_new ? 1 : 0);
         for (int hh = wave; hh < nh; hh += kAttnWaves) {
             const bool isk = hh == rep;
-            const uint16_t* src = a.q + static_cast<int64_t>(isk ? a.NQ + kvh : kvh * rep + hh) * HD;
+            const uint16_t* src = head_src(hh);
             const uint16_t* wn = isk ? a.k_norm : a.q_norm;
             uint16_t* dst = isk ? s_kv[0] : s_q[hh];
             const float* cr = a.cos_t + static_cast<int64_t>(prow) * HALF;
             const float* sr = a.sin_t + static_cast<int64_t>(prow) * HALF;
-            if (HALF == kWave) {  // one pair per lane: every operand loaded up front
-                const float x1 = f16_bits_to_f32(ldg(src + lane)), x2 = f16_bits_to_f32(ldg(src + lane + HALF));
-                const float w1 = f16_bits_to_f32(ldg(wn + lane)), w2 = f16_bits_to_f32(ldg(wn + lane + HALF));
-                const float c = ldg(cr + lane), sn = ldg(sr + lane);
+            if (HALF == kWave) {  // one pair per lane
+                if (hh != wave) {  // a later head of this wave (rep 8 with the new k): its operands now
+                    f_x1 = ldg(src + lane);
+                    f_x2 = ldg(src + lane + HALF);
+                    f_w1 = ldg(wn + lane);
+                    f_w2 = ldg(wn + lane + HALF);
+                    f_c = ldg(cr + lane);
+                    f_sn = ldg(sr + lane);
+                }
+                const float x1 = f16_bits_to_f32(f_x1), x2 = f16_bits_to_f32(f_x2);
+                const float w1 = f16_bits_to_f32(f_w1), w2 = f16_bits_to_f32(f_w2);
                 const float inv = rsqrtf(wave_sum_bcast(fmaf(x2, x2, x1 * x1)) / static_cast<float>(HD) + a.eps);
                 const float xa = f16_bits_to_f32(f32_to_f16_bits(x1 * inv * w1));
                 const float xb = f16_bits_to_f32(f32_to_f16_bits(x2 * inv * w2));
                 float o1, o2;
-                rope_pair(xa, xb, c, sn, o1, o2);
+                rope_pair(xa, xb, f_c, f_sn, o1, o2);
                 dst[lane] = f32_to_f16_bits(o1);
                 dst[lane + HALF] = f32_to_f16_bits(o2);
             } else {
@@ -387,33 +423,68 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
 #pragma unroll
         for (int d = 0; d < 8; ++d) st.acc[hh][d] = 0.0f;
     }
-    const u32x4* knew = reinterpret_cast<const u32x4*>(s_kv[0]);
-    const u32x4* vnew = reinterpret_cast<const u32x4*>(s_kv[1]);
+    // the new timestep's K / V (PRE, the workgroup holding p): taken from LDS instead of the rows read before
+    // the append
+    u32x4 knew = u32x4{0u, 0u, 0u, 0u}, vnew = knew;
+    if (PRE && has_new) {  // workgroup-uniform
+        knew = reinterpret_cast<const u32x4*>(s_kv[0])[u];
+        vnew = reinterpret_cast<const u32x4*>(s_kv[1])[u];
+    }
+    // Per chunk of up to kAttnPassMax passes: the scores of every pass first (independent of each other), then
+    // the running max moves once to cover them all (acc, l rescaled once), then the rows enter the sums. The
+    // online-softmax recurrence of the reference with the chunk's rows as one step. Passes go in pairs: one
+    // uniform branch per pair; the second pass of a pair past the chunk scores -inf.
     for (int c0 = 0; c0 < npass_all; c0 += kAttnPassMax) {
-        if (c0 > 0) {
-            const int left = npass_all - c0;
-            rows.load(kbase, vbase, tb0 + c0 * STEP, t1, left < kAttnPassMax ? left : kAttnPassMax);
+        const int left = npass_all - c0;
+        const int np = left < kAttnPassMax ? left : kAttnPassMax;
+        if (c0 > 0) rows.load(kbase, vbase, tb0 + c0 * STEP, t1, np);
+        float sc[kAttnPassMax][REP];
+#pragma unroll
+        for (int i = 0; i < kAttnPassMax; i += 2) {
+            if (i < np) {
+#pragma unroll
+                for (int j = i; j < i + 2; ++j) {
+                    const int t = tb0 + (c0 + j) * STEP + g;
+                    const u32x4 kk = (PRE && t == tnew) ? knew : rows.k[j];
+                    attn_scores<LPR, REP>(sc[j], qv, j < np && t < t1, kk, a.scale_log2);
+                }
+            } else {
+#pragma unroll
+                for (int j = i; j < i + 2; ++j)
+#pragma unroll
+                    for (int hh = 0; hh < REP; ++hh) sc[j][hh] = -__builtin_inff();
+            }
         }
 #pragma unroll
-        for (int i = 0; i < kAttnPassMax; ++i) {
-            if (c0 + i >= npass_all) break;
-            const int t = tb0 + (c0 + i) * STEP + g;
-            u32x4 kk = rows.k[i], vv = rows.v[i];
-            if (PRE && t == tnew) {
-                kk = knew[u];
-                vv = vnew[u];
+        for (int hh = 0; hh < REP; ++hh) {
+            float mn = st.m[hh];
+#pragma unroll
+            for (int j = 0; j < kAttnPassMax; ++j) mn = fmaxf(mn, sc[j][hh]);
+            const float corr = fast_exp2(st.m[hh] - mn);
+            st.l[hh] *= corr;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) st.acc[hh][d] *= corr;
+            st.m[hh] = mn;
+        }
+#pragma unroll
+        for (int i = 0; i < kAttnPassMax; i += 2) {
+            if (i < np) {
+#pragma unroll
+                for (int j = i; j < i + 2; ++j) {
+                    const int t = tb0 + (c0 + j) * STEP + g;
+                    const u32x4 vv = (PRE && t == tnew) ? vnew : rows.v[j];
+                    attn_accumulate<LPR, REP>(st, sc[j], vv);
+                }
             }
-            attn_pass<LPR, REP>(st, qv, rep, t < t1, kk, vv, a.scale_log2);
         }
     }
 
     // merge lane groups (same u, different timesteps) inside the wave: partner lane l ^ MASK for MASK = LPR,
     // 2*LPR, ... 32 (VALU lane exchanges, not the LDS crossbar)
-    attn_merge_groups<LPR, REP, LPR>(st, rep);
+    attn_merge_groups<LPR, REP, LPR>(st);
     if (g == 0) {
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
-            if (hh >= rep) break;
             if (u == 0) {
                 s_state[wave][hh][0] = st.m[hh];
                 s_state[wave][hh][1] = st.l[hh];
