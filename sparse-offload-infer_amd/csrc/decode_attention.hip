@@ -22,8 +22,10 @@
 //     lanes; softmax runs in the log2 domain (scores pre-multiplied by
 //     scale*log2(e), v_exp_f32) with the online max/sum recurrence of the
 //     reference (m0 = -1e30) taken one chunk of passes at a time: the
-//     chunk's scores first, one rescale, then its rows enter the sums;
-//   * lane groups, then waves (in wave order) are merged with the standard
+//     chunk's scores first, one rescale, then its rows enter the sums; the
+//     lane groups of a wave share one running max (a wave max per chunk);
+//   * so a wave's lane groups are merged by plain sums (a reduce-scatter of
+//     lane swaps), then the waves (in wave order) with the standard
 //     (m, l, acc) rescaling;
 //   * short contexts (at most 8 passes: 256 timesteps at head_dim 128) run
 //     ONE workgroup per KV head, which writes the output itself; longer ones
@@ -136,25 +138,77 @@ __device__ __forceinline__ void attn_accumulate(AttnState<LPR, REP>& st, const f
     }
 }
 
-// Merge lane l's state with lane l ^ MASK's for MASK = M, 2M, ... 32.
-template <int LPR, int REP, int MASK>
-__device__ __forceinline__ void attn_merge_groups(AttnState<LPR, REP>& st) {
-    if constexpr (MASK < kWave) {
+// a + b of lane pairs swapped across 16-lane rows (ROWS = 16) or wave halves (ROWS = 32) by
+// v_permlane16_swap / v_permlane32_swap on two values (swap16 / swap32: the upper row of each pair of VDST
+// trades places with the lower row of VSRC0): with vdst = x, vsrc = y, lanes of the lower row of each pair end
+// with x of both rows, lanes of the upper row with y of both, summed in row order.
+template <int ROWS>
+__device__ __forceinline__ float swap_sum(float x, float y) {
+    float a = x, b = y;
+    if constexpr (ROWS == 16) {
+        swap16(a, b);
+    } else {
+        swap32(a, b);
+    }
+    return a + b;
+}
+
+// The wave's state into s_row (= s_state[wave]): its lane groups share the running max, so l and acc are plain
+// sums over the groups. Groups inside a 16-lane row are summed by lane exchanges first (LPR < 16); the rows
+// are then summed by a reduce-scatter of swap_sum: level 16 leaves row r with dims (2i + (r & 1)) of its 8,
+// level 32 with dims r and 4 + r, each summed over the 4 rows in a fixed order (wave halves: dims 2i + half).
+template <int LPR, int REP, int HD>
+__device__ __forceinline__ void attn_wave_state(AttnState<LPR, REP>& st, float (*s_row)[HD + 2], int lane) {
+    if constexpr (LPR < 16) {
 #pragma unroll
-        for (int hh = 0; hh < REP; ++hh) {
-            const float mo = xor_lanes<MASK>(st.m[hh]);
-            const float lo = xor_lanes<MASK>(st.l[hh]);
-            const float mn = fmaxf(st.m[hh], mo);
-            const float ca = fast_exp2(st.m[hh] - mn), cb = fast_exp2(mo - mn);
-            st.l[hh] = st.l[hh] * ca + lo * cb;
+        for (int mask = LPR; mask < 16; mask *= 2) {
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const float ao = xor_lanes<MASK>(st.acc[hh][d]);
-                st.acc[hh][d] = st.acc[hh][d] * ca + ao * cb;
+            for (int hh = 0; hh < REP; ++hh) {
+                if (mask == 1) st.l[hh] += xor_lanes<1>(st.l[hh]);
+                if (mask == 2) st.l[hh] += xor_lanes<2>(st.l[hh]);
+                if (mask == 4) st.l[hh] += xor_lanes<4>(st.l[hh]);
+                if (mask == 8) st.l[hh] += xor_lanes<8>(st.l[hh]);
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    if (mask == 1) st.acc[hh][d] += xor_lanes<1>(st.acc[hh][d]);
+                    if (mask == 2) st.acc[hh][d] += xor_lanes<2>(st.acc[hh][d]);
+                    if (mask == 4) st.acc[hh][d] += xor_lanes<4>(st.acc[hh][d]);
+                    if (mask == 8) st.acc[hh][d] += xor_lanes<8>(st.acc[hh][d]);
+                }
             }
-            st.m[hh] = mn;
         }
-        attn_merge_groups<LPR, REP, MASK * 2>(st);
+    }
+    const int u = lane % LPR;
+#pragma unroll
+    for (int hh = 0; hh < REP; ++hh) {
+        if constexpr (LPR <= 16) {
+            const float l2 = swap_sum<16>(st.l[hh], st.l[hh]);
+            const float l4 = swap_sum<32>(l2, l2);
+            float b[4], c[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[i] = swap_sum<16>(st.acc[hh][2 * i], st.acc[hh][2 * i + 1]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) c[i] = swap_sum<32>(b[2 * i], b[2 * i + 1]);
+            const int r = lane >> 4;
+            if ((lane & 15) < LPR) {
+                s_row[hh][2 + 8 * u + r] = c[0];
+                s_row[hh][2 + 8 * u + 4 + r] = c[1];
+            }
+            if (lane == 0) {
+                s_row[hh][0] = st.m[hh];
+                s_row[hh][1] = l4;
+            }
+        } else {  // LPR == 32: two groups, the wave halves
+            const float l2 = swap_sum<32>(st.l[hh], st.l[hh]);
+            const int half = lane >> 5;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                s_row[hh][2 + 8 * u + 2 * i + half] = swap_sum<32>(st.acc[hh][2 * i], st.acc[hh][2 * i + 1]);
+            if (lane == 0) {
+                s_row[hh][0] = st.m[hh];
+                s_row[hh][1] = l2;
+            }
+        }
     }
 }
 
@@ -180,17 +234,24 @@ struct AttnRows {
     }
 };
 
-// Merged state element i of query head hh over the waves (i = 0: M, 1: l,
-// 2 + d: acc[d]), in wave order.
+// The waves' states of query head hh combined: M = the largest m, w[s] = 2^(m_s - M) (wave order).
 template <int REP, int HD>
-__device__ __forceinline__ float wave_merged(const float (*s_state)[REP][HD + 2], int hh, int i) {
+__device__ __forceinline__ float wave_weights(const float (*s_state)[REP][HD + 2], int hh, float (&w)[kAttnWaves]) {
     float M = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, s_state[w][hh][0]);
-    if (i == 0) return M;
+    for (int s = 0; s < kAttnWaves; ++s) M = fmaxf(M, s_state[s][hh][0]);
+#pragma unroll
+    for (int s = 0; s < kAttnWaves; ++s) w[s] = fast_exp2(s_state[s][hh][0] - M);
+    return M;
+}
+
+// sum_s w[s] * (state element e of wave s), e = 1: l, e = 2 + d: acc[d]; in wave order.
+template <int REP, int HD>
+__device__ __forceinline__ float wave_sum(const float (*s_state)[REP][HD + 2], int hh, int e,
+                                          const float (&w)[kAttnWaves]) {
     float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) v += s_state[w][hh][i] * fast_exp2(s_state[w][hh][0] - M);
+    for (int s = 0; s < kAttnWaves; ++s) v = fmaf(s_state[s][hh][e], w[s], v);
     return v;
 }
 
@@ -318,11 +379,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     auto head_src = [&](int hh) {
         return a.q + static_cast<int64_t>(hh == rep ? a.NQ + kvh : kvh * rep + hh) * HD;
     };
+    // (unconditional loads: a wave without a head reads head 0's, unused; a load inside a branch would be waited
+    // for before the branch ends, ahead of the rows)
     uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
     float f_c = 0.0f, f_sn = 0.0f;
-    if (PRE && HALF == kWave && wave < nh) {  // wave-uniform
-        const uint16_t* src = head_src(wave);
-        const uint16_t* wn = wave == rep ? a.k_norm : a.q_norm;
+    if constexpr (PRE && HALF == kWave) {
+        const int fh = wave < nh ? wave : 0;
+        const uint16_t* src = head_src(fh);
+        const uint16_t* wn = fh == rep ? a.k_norm : a.q_norm;
         f_x1 = ldg(src + lane);
         f_x2 = ldg(src + lane + HALF);
         f_w1 = ldg(wn + lane);
@@ -333,6 +397,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     // the K/V rows of the first chunk: they do not depend on q (row p is patched from LDS later)
     AttnRows<LPR> rows;
     rows.load(kbase, vbase, tb0, t1, npass_all < kAttnPassMax ? npass_all : kAttnPassMax);
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits for a load moves above the row requests
 
     f16x2 qv[REP][4];
     if (PRE) {
@@ -460,6 +525,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
             float mn = st.m[hh];
 #pragma unroll
             for (int j = 0; j < kAttnPassMax; ++j) mn = fmaxf(mn, sc[j][hh]);
+            mn = wave_max_bcast(mn);  // one running max for all the wave's lane groups
             const float corr = fast_exp2(st.m[hh] - mn);
             st.l[hh] *= corr;
 #pragma unroll
@@ -479,34 +545,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         }
     }
 
-    // merge lane groups (same u, different timesteps) inside the wave: partner lane l ^ MASK for MASK = LPR,
-    // 2*LPR, ... 32 (VALU lane exchanges, not the LDS crossbar)
-    attn_merge_groups<LPR, REP, LPR>(st);
-    if (g == 0) {
-#pragma unroll
-        for (int hh = 0; hh < REP; ++hh) {
-            if (u == 0) {
-                s_state[wave][hh][0] = st.m[hh];
-                s_state[wave][hh][1] = st.l[hh];
-            }
-#pragma unroll
-            for (int d = 0; d < 8; ++d) s_state[wave][hh][2 + 8 * u + d] = st.acc[hh][d];
-        }
-    }
+    // the wave's state (its lane groups summed) into LDS
+    attn_wave_state<LPR, REP, HD>(st, s_state[wave], lane);
     __syncthreads();
 
     if (ns == 1) {  // one workgroup holds the whole context: out = acc / l (the split combine with one state)
         for (int i = tid; i < rep * HD; i += kAttnThreads) {
             const int hh = i / HD, d = i % HD;
-            const float lsum = wave_merged<REP, HD>(s_state, hh, 1);
-            const float acc = wave_merged<REP, HD>(s_state, hh, 2 + d);
+            float w[kAttnWaves];
+            wave_weights<REP, HD>(s_state, hh, w);
+            const float lsum = wave_sum<REP, HD>(s_state, hh, 1, w);
+            const float acc = wave_sum<REP, HD>(s_state, hh, 2 + d, w);
             stg(a.out + static_cast<int64_t>(kvh * rep + hh) * HD + d, f32_to_f16_bits(acc / lsum));
         }
         return;
     }
-    for (int hh = 0; hh < rep; ++hh) {  // the split's state: [M, l, acc] per query head
-        float* o = a.part + (static_cast<int64_t>(kvh * rep + hh) * a.nsplit + split) * (HD + 2);
-        for (int i = tid; i < HD + 2; i += kAttnThreads) stg(o + i, wave_merged<REP, HD>(s_state, hh, i));
+    for (int i = tid; i < rep * (HD + 2); i += kAttnThreads) {  // the split's state: [M, l, acc] per query head
+        const int hh = i / (HD + 2), e = i % (HD + 2);
+        float w[kAttnWaves];
+        const float M = wave_weights<REP, HD>(s_state, hh, w);
+        const float v = e == 0 ? M : wave_sum<REP, HD>(s_state, hh, e, w);
+        stg(a.part + (static_cast<int64_t>(kvh * rep + hh) * a.nsplit + split) * (HD + 2) + e, v);
     }
     // arrival: the last of the ns splits of this KV head combines its query heads
     arrive_release();
