@@ -153,6 +153,24 @@ __device__ __forceinline__ float swap_sum(float x, float y) {
     return a + b;
 }
 
+// Max over the lane groups of a wave (lane exchanges across masks LPR .. 32; the lanes of a group hold the
+// same value): every lane gets it.
+template <int LPR>
+__device__ __forceinline__ float groups_max(float v) {
+    if constexpr (LPR <= 1) v = fmaxf(v, xor_lanes<1>(v));
+    if constexpr (LPR <= 2) v = fmaxf(v, xor_lanes<2>(v));
+    if constexpr (LPR <= 4) v = fmaxf(v, xor_lanes<4>(v));
+    if constexpr (LPR <= 8) v = fmaxf(v, xor_lanes<8>(v));
+    if constexpr (LPR <= 16) {
+        float a = v, b = v;
+        swap16(a, b);
+        v = fmaxf(a, b);
+    }
+    float a = v, b = v;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
+
 // The wave's state into s_row (= s_state[wave]): its lane groups share the running max, so l and acc are plain
 // sums over the groups. Groups inside a 16-lane row are summed by lane exchanges first (LPR < 16); the rows
 // are then summed by a reduce-scatter of swap_sum: level 16 leaves row r with dims (2i + (r & 1)) of its 8,
@@ -379,12 +397,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     auto head_src = [&](int hh) {
         return a.q + static_cast<int64_t>(hh == rep ? a.NQ + kvh : kvh * rep + hh) * HD;
     };
-    // (unconditional loads: a wave without a head reads head 0's, unused; a load inside a branch would be waited
-    // for before the branch ends, ahead of the rows)
     uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
     float f_c = 0.0f, f_sn = 0.0f;
-    if constexpr (PRE && HALF == kWave) {
-        const int fh = wave < nh ? wave : 0;
+    if (PRE && HALF == kWave && wave < nh) {  // wave-uniform
+        const int fh = wave;
         const uint16_t* src = head_src(fh);
         const uint16_t* wn = fh == rep ? a.k_norm : a.q_norm;
         f_x1 = ldg(src + lane);
@@ -397,7 +413,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     // the K/V rows of the first chunk: they do not depend on q (row p is patched from LDS later)
     AttnRows<LPR> rows;
     rows.load(kbase, vbase, tb0, t1, npass_all < kAttnPassMax ? npass_all : kAttnPassMax);
-    __builtin_amdgcn_sched_barrier(0);  // nothing that waits for a load moves above the row requests
+    // the operands pass through an empty asm here, so no conversion of them (and no wait for them) is placed
+    // above the row requests
+    if constexpr (PRE && HALF == kWave)
+        asm volatile("" : "+v"(f_x1), "+v"(f_x2), "+v"(f_w1), "+v"(f_w2), "+v"(f_c), "+v"(f_sn));
 
     f16x2 qv[REP][4];
     if (PRE) {
@@ -525,7 +544,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
             float mn = st.m[hh];
 #pragma unroll
             for (int j = 0; j < kAttnPassMax; ++j) mn = fmaxf(mn, sc[j][hh]);
-            mn = wave_max_bcast(mn);  // one running max for all the wave's lane groups
+            mn = groups_max<LPR>(mn);  // one running max for all the wave's lane groups
             const float corr = fast_exp2(st.m[hh] - mn);
             st.l[hh] *= corr;
 #pragma unroll
