@@ -696,6 +696,37 @@ def bench_kernels(dev, gen):
         del Ws, Ss
         torch.cuda.empty_cache()
 
+    # --- the resident DIP schedule's two MLP launches: gate|up GEMV with RMSNorm and SwiGLU that also stores the
+    # gate of every channel; the rule-A selection + down as one dense GEMV over the transposed down_proj^T ---
+    N = 2 * I
+    n_cp = cold_copies(N * (row + 4 * G))
+    Ws = [torch.randint(0, 256, (N, row), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n_cp)]
+    Ss = [(torch.rand(N, G, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n_cp)]
+    d = torch.randn(H, generator=gen, device=dev).half()
+    nw = torch.ones(H, dtype=f16, device=dev)
+    g_all, h_all = torch.empty(I, dtype=f16, device=dev), torch.empty(I, dtype=f16, device=dev)
+    t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_rmsnorm_swiglu_gate_into(W, S, x, d, nw, 1e-6, None, g_all,
+                                                                                  h_all, H, GS), list(zip(Ws, Ss)))
+    res["gate_up_swiglu_gate_12288x2048"] = entry(N * (row + 4 * G) + 3 * 2 * H + 2 * 2 * I, t["mean_us"],
+                                                  kernel="gemv_int4_norm (RMSNorm on load, SwiGLU epilogue storing "
+                                                         "gate and h of every channel)")
+    del Ws, Ss
+    torch.cuda.empty_cache()
+    n_cp = cold_copies(H * (I // 2 + 4 * I // GS))
+    Wd = [torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, device=dev, generator=gen) for _ in range(n_cp)]
+    Sd = [(torch.rand(H // GS, I, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n_cp)]
+    g_all.copy_(torch.randn(I, generator=gen, device=dev).half())
+    h_all.copy_(torch.randn(I, generator=gen, device=dev).half())
+    yd = torch.empty(H, dtype=f16, device=dev)
+    for k in (768, 3072):
+        t = time_graph_per_launch(lambda W, S: _C.dip_select_dense_down_into(g_all, h_all, k, W, S, None, None, yd, GS),
+                                  list(zip(Wd, Sd)))
+        res[f"dip_dense_down_k{k}"] = entry(H * I // 2 + 4 * (H // GS) * I + 4 * I + 2 * H, t["mean_us"],
+                                            kernel="dip_dense_down (rule-A selection in every workgroup + the down "
+                                                   "as one GEMV over the transposed down_proj^T, 1 launch)")
+    del Wd, Sd
+    torch.cuda.empty_cache()
+
     # --- host gathers from pinned memory (R8: the reference's staged vs per-row forms), wall clock incl. sync ---
     host = torch.randint(0, 256, (I, row), dtype=torch.uint8, generator=torch.Generator().manual_seed(5)).pin_memory()
     staging = torch.empty(I * row, dtype=torch.uint8).pin_memory()

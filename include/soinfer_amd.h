@@ -501,15 +501,16 @@ int soi_gemv_dip_cached_down(const uint8_t* cache_Wq, const float* cache_scale, 
  * down_proj^T's quantized values stored TRANSPOSED: Wt [H, n/2] (row col holds
  * q_T[0..n-1, col] packed like any INT4 row) and St [num_groups, n] (St[g, c]
  * = s_T[c, g]). Every workgroup computes the selection itself while its rows
- * load, then a GEMV of its 16 output columns with the coefficients h * s
+ * load, then a GEMV of its 8 output columns with the coefficients h * s
  * (fp32, carried as exact binary16 hi + lo pairs under a power-of-two scale).
  * Reads all n channels' rows (the bytes of a dense down projection), needs
  * no workspace; sums the reference's terms in another order (tolerance of
  * the sparse accumulate). out_indices[k] / out_count, when not null, receive
  * the selection exactly as the top-k function writes it (computed after y;
- * leave them null when not needed). n a multiple of 32 in [32, 16384],
- * 1 <= k <= n, group_size a multiple of 16, num_groups = ceil(H / group_size),
- * Wt 16-byte aligned. No reference counterpart as a single entry point.
+ * leave them null when not needed). n a multiple of 32 in [32, 24576],
+ * 1 <= k <= n, group_size a multiple of 8, num_groups = ceil(H / group_size),
+ * Wt and St 16-byte aligned, gate and h 8-byte aligned. No reference
+ * counterpart as a single entry point: it replaces the pair cited above.
  * ------------------------------------------------------------------------ */
 int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
                               const uint8_t* Wt, const float* St, int32_t* out_indices, int32_t* out_count,

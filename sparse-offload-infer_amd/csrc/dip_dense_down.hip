@@ -48,7 +48,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kDdWaves = 8;  // = output rows per workgroup (one per wave)
 constexpr int kDdThreads = kDdWaves * kWave;
 constexpr int kDdChannelsPerPass = kDdThreads * 4;        // one 4-channel group per thread
-constexpr int kDdMaxNC = 8;                               // 4-channel groups per thread (= chunks per lane)
+constexpr int kDdMaxNC = 12;                              // 4-channel groups per thread (= chunks per lane)
 constexpr int kDdMaxChannels = kDdChannelsPerPass * kDdMaxNC;
 constexpr int kDdMaxChunks = kDdMaxChannels / 32;         // 32-channel chunks
 constexpr int kXcds = 8;                                  // accelerator complex dies, each with its own L2
@@ -316,7 +316,11 @@ extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h
         case 5: SOI_DD(5); break;
         case 6: SOI_DD(6); break;
         case 7: SOI_DD(7); break;
-        default: SOI_DD(8); break;
+        case 8: SOI_DD(8); break;
+        case 9: SOI_DD(9); break;
+        case 10: SOI_DD(10); break;
+        case 11: SOI_DD(11); break;
+        default: SOI_DD(12); break;
     }
 #undef SOI_DD
     return launch_status(what);

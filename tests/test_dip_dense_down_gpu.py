@@ -93,7 +93,8 @@ def test_rmsnorm_swiglu_gate_equals_gate_up_and_swiglu(C):
 @pytest.mark.parametrize("I,H,k,ties", [(6144, 2048, 3072, False), (6144, 2048, 768, True), (6144, 2048, 1536, False),
                                         (6144, 2048, 6144, False), (6144, 2048, 1, False), (1024, 256, 333, True),
                                         (8192, 1024, 4096, True), (9728, 2048, 4864, False), (96, 384, 50, False),
-                                        (3008, 2176, 1111, False)])
+                                        (3008, 2176, 1111, False), (17408, 5120, 8704, False),
+                                        (24576, 1024, 12288, True)])
 def test_dense_down_matches_oracle_and_topk(C, ops, I, H, k, ties):
     """Selection = the oracle's rule A = the top-k kernel; y = the binary64 sum over it within the sparse-down
     tolerance, the same without the index outputs, and close to the sparse accumulate on the same (idx, h)."""
@@ -216,3 +217,9 @@ def test_dense_down_rejections(C, ops):
     S_odd = torch.zeros(H // 128, I - 8, device="cuda")
     with pytest.raises(RuntimeError, match="multiple of 32"):
         C.dip_select_dense_down_into(g_odd, g_odd, 10, W_odd, S_odd, None, None, y, 128)
+    n_big = 24576 + 32  # past the 12 four-channel groups per thread
+    g_big = torch.zeros(n_big, dtype=torch.float16, device="cuda")
+    W_big = torch.zeros(H, n_big // 2, dtype=torch.uint8, device="cuda")
+    S_big = torch.zeros(H // 128, n_big, device="cuda")
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        C.dip_select_dense_down_into(g_big, g_big, 10, W_big, S_big, None, None, y, 128)
