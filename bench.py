@@ -457,17 +457,20 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
     # "dip": the fastest resident DIP schedule (dense-up: gate|up GEMV + one-launch selection and down);
     # "dip_indexed_up": the four-launch schedule the cache-aware engines reproduce bit for bit
+    # "*_offload": copies on copy streams two layers ahead of the kernels; "*_offload_serial": each layer's copy
+    # stream-ordered right before its kernels
     modes = ("dense", "dip", "dip_indexed_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
-             "cached_dip_offload")
+             "cached_dip_offload", "dense_offload_serial", "dip_offload_serial", "cached_dip_offload_serial")
     no_hot = [[] for _ in range(c.layers)]
     for mode in modes:
+        kind = mode.replace("_serial", "")
         base = {"dip_indexed_up": "dip", "cached_dip_staged": "cached_dip",
-                "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(mode, mode)
+                "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(kind, kind)
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
-                             hot_channels=(no_hot if mode == "dip_offload" else hot) if base == "cached_dip" else None,
+                             hot_channels=(no_hot if kind == "dip_offload" else hot) if base == "cached_dip" else None,
                              max_new_tokens=n_new, dip_dense_up=mode == "dip",
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
-                             offload=mode.endswith("_offload"))
+                             offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"))
         eng.capture()
         eng.generate(prompt[:8], 8)  # warm up the graphs
         torch.cuda.synchronize()
@@ -494,14 +497,18 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
     out["cached_dip_tokens_equal_dip"] = toks["dip_indexed_up"] == toks["cached_dip"] == toks["cached_dip_staged"]
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
-    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip_indexed_up"), ("cached_dip_offload", "dip_indexed_up")):
+    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip_indexed_up"), ("cached_dip_offload", "dip_indexed_up"),
+                 ("dense_offload_serial", "dense"), ("dip_offload_serial", "dip_indexed_up"),
+                 ("cached_dip_offload_serial", "dip_indexed_up")):
         assert toks[a] == toks[b], f"{a} must generate the same tokens as {b}"
     out["offload_tokens_equal_resident"] = True
     out["offload_note"] = ("*_offload: every layer's dense weights (q|k|v, o, gate|up and down for dense, gate for "
-                           "DIP) streamed from a pinned host arena into a device slot by one hipMemcpyAsync per layer "
-                           "before the layer runs (the reference's streamed configuration); DIP reads its selected "
-                           "up / down^T rows from the host arena in place (dip_offload: no cache, cached_dip_offload: "
-                           "20% hot cache in HBM)")
+                           "DIP) streamed from a pinned host arena into one of two device slots by one hipMemcpyAsync "
+                           "per layer on a copy stream, two layers ahead of the kernels (read-done fences; the first "
+                           "two layers' copies overlap the LM head): the reference's streamed configuration with "
+                           "WeightPipeline's prefetch; *_offload_serial: each copy stream-ordered right before its "
+                           "layer. DIP reads its selected up / down^T rows from the host arena in place (dip_offload: "
+                           "no cache, cached_dip_offload: 20% hot cache in HBM)")
     out["cached_dip"]["miss_path"] = "direct: misses read in place from the pinned host arena inside the GEMVs"
     out["cached_dip_staged"]["miss_path"] = "staged: device gathers of the misses into staging, then descriptors"
     out["dip_indexed_up"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse "

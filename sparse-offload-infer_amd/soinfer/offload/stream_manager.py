@@ -45,13 +45,19 @@ class CopySlot:
 
 
 class StreamManager:
-    """num_buffers copy slots (2 for double buffering, 3 for triple)."""
+    """num_buffers copy slots (2 for double buffering, 3 for triple). shared_stream=True gives every slot the same
+    copy stream (an addition to the reference's interface): the copies then run one after another in the order
+    they were queued instead of splitting the host link between concurrent transfers."""
 
-    def __init__(self, num_buffers: int = 2):
+    def __init__(self, num_buffers: int = 2, shared_stream: bool = False):
         if int(num_buffers) < 1:
             raise ValueError(f"StreamManager needs at least one buffer, got {num_buffers}")
         self.num_buffers = int(num_buffers)
-        self.slots = [CopySlot(torch.cuda.Stream()) for _ in range(self.num_buffers)]
+        if shared_stream:
+            one = torch.cuda.Stream()
+            self.slots = [CopySlot(one) for _ in range(self.num_buffers)]
+        else:
+            self.slots = [CopySlot(torch.cuda.Stream()) for _ in range(self.num_buffers)]
 
     def _slot(self, buf_idx: int) -> CopySlot:
         if not 0 <= buf_idx < self.num_buffers:

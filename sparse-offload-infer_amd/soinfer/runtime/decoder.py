@@ -43,6 +43,7 @@ import torch
 from .. import _C
 from .. import ops
 from ..offload.hot_cache import HotCache
+from ..offload.stream_manager import StreamManager
 from ..offload.weight_store import PinnedWeightStore, plan_bytes
 from ..quant import formats, pack
 
@@ -191,9 +192,13 @@ class DecodeEngine:
     resident) or "cached_dip" (hot channels resident, the rest in pinned host memory; miss_path "direct" reads
     the misses in place inside the up / down kernels, "staged" gathers them into device staging first).
     offload=True keeps the dense weights of every layer (q|k|v, o, and gate|up + down for dense or gate for
-    cached DIP) in a pinned host arena and copies each layer's block into one of two device slots right before
-    the layer runs (hipMemcpyAsync on the compute stream, captured in the graph): the reference's streamed
-    configuration (WeightPipeline, generate.py:85-138). Scales, norms, embedding and LM head stay in HBM.
+    cached DIP) in a pinned host arena and copies each layer's block into one of two device slots: the
+    reference's streamed configuration (WeightPipeline, generate.py:85-138). With overlap_copy=True (default)
+    the copies run on a StreamManager's copy streams, two layers ahead of the kernels: layer l + 2's block goes
+    into slot l % 2 as soon as layer l's kernels are done with it (read-done fence), layer l's kernels wait for
+    its block to land, and a generation step starts the copies of layers 0 and 1 before the LM head, so they
+    overlap it. overlap_copy=False copies each block stream-ordered right before its layer. Scales, norms,
+    embedding and LM head stay in HBM.
 
     All buffers are allocated here; decode steps launch only this package's kernels on the current stream
     and are captured into HIP graphs by capture()."""
@@ -201,7 +206,7 @@ class DecodeEngine:
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
                  dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
-                 down_copy: bool = True):
+                 down_copy: bool = True, overlap_copy: bool = True):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         if offload and mode == "dip":
@@ -276,6 +281,7 @@ class DecodeEngine:
             self.gu_il = [(L.gu_Wq.index_select(0, perm.to(L.gu_Wq.device)).contiguous(),
                            L.gu_scale.index_select(0, perm).contiguous()) for L in w.layers]
         self.offload = offload
+        self.overlap_copy = bool(overlap_copy) and offload
         if not offload:
             packed = [t for L in w.layers for t in (L.qkv_Wq, L.o_Wq, L.gu_Wq, L.down_Wq)]
             if any(t.device != dev for t in packed):
@@ -362,16 +368,52 @@ class DecodeEngine:
                 views[name] = slot[off:off + n].view(t.shape)
                 off += n
             self._slot_views.append(views)
+        if self.overlap_copy:
+            self.copies = StreamManager(2, shared_stream=True)
+            self._fork = torch.cuda.Event()
+            self._step_open = False
+
+    def _prefetch(self, l: int):
+        off, n = self._blocks[l]
+        self.copies.prefetch(l % 2, self.slots[l % 2][:n], self.wstore.arena[off:off + n])
+
+    def _begin_step(self):
+        """Overlapped offload: start a step's copies of layers 0 and 1. The copy streams first wait for an event
+        of the current stream (everything before this point, the previous step included), so a captured step
+        holds its copies as graph branches; the slots' read-done fences start over."""
+        if not self.overlap_copy or self._step_open:
+            return
+        self._fork.record()
+        for slot in self.copies.slots:
+            slot.stream.wait_event(self._fork)  # (the slots share one stream: a repeated wait is harmless)
+            slot.has_reader = False
+        for l in range(min(2, self.c.layers)):
+            self._prefetch(l)
+        self._step_open = True
+
+    def _layer_done(self, l: int):
+        """Overlapped offload: layer l's kernels are issued; its slot takes layer l + 2's block once they finish."""
+        if not self.overlap_copy:
+            return
+        self.copies.mark_read_done(l % 2)
+        if l + 2 < self.c.layers:
+            self._prefetch(l + 2)
+        if l == self.c.layers - 1:
+            self._step_open = False
 
     def _layer(self, l: int, L: LayerWeights):
-        """Layer l's weights for this step. With offload, first copies the layer's block from the pinned arena
-        into slot l % 2 (stream-ordered before the layer's kernels) and returns views of the slot with the
+        """Layer l's weights for this step. With offload, the layer's block from the pinned arena lands in slot
+        l % 2 first (overlapped: the current stream waits for the copy started earlier; otherwise the copy is
+        issued here, stream-ordered before the layer's kernels), and views of the slot come back with the
         resident scales and norms."""
         if not self.offload:
             return L, (self.gu_il[l] if hasattr(self, "gu_il") else None)
         off, n = self._blocks[l]
-        slot = self.slots[l % 2]
-        slot[:n].copy_(self.wstore.arena[off:off + n], non_blocking=True)
+        if self.overlap_copy:
+            self._begin_step()
+            self.copies.wait(l % 2)
+        else:
+            self.slots[l % 2][:n].copy_(self.wstore.arena[off:off + n], non_blocking=True)
         v = self._slot_views[l % 2]
         Ls = LayerWeights(L.in_norm, L.post_norm, L.q_norm, L.k_norm, v["qkv_Wq"], L.qkv_scale, v["o_Wq"], L.o_scale,
                           v.get("gu_Wq", L.gu_Wq), L.gu_scale, v.get("down_Wq", L.down_Wq), L.down_scale,
@@ -473,6 +515,7 @@ class DecodeEngine:
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
             _C.residual_rmsnorm_(self.x, self.o, L.post_norm, self.h, eps)
             self._mlp(l, L)
+            self._layer_done(l)
             if self.layer_hook is not None:
                 self.layer_hook(l)
         _C.residual_rmsnorm_(self.x, self.down, self.w.final_norm, self.hn, eps)
@@ -505,6 +548,7 @@ class DecodeEngine:
                 _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
             _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
             self._mlp_fused(l, L, gu_il, cur, other)
+            self._layer_done(l)
             cur, other = other, cur
             if self.layer_hook is not None:
                 self.layer_hook(l)
@@ -566,6 +610,14 @@ class DecodeEngine:
         _C.gemv_f16_into(self.w.lm_head, self.hn, self.logits)
         _C.argmax_f16_into(self.logits, self.token, self.log, self.log_len, self.argmax_ws)
 
+    def _gen_step(self):
+        """One generation step: LM head + argmax of the previous step, then the layers (an overlapped offload
+        starts the copies of layers 0 and 1 first, so they run under the head)."""
+        if self.offload:
+            self._begin_step()
+        self._head()
+        self._layers()
+
     # ---- graphs ----
     def capture(self):
         """Capture the prompt step (layers) and the generation step (head + layers) as HIP graphs."""
@@ -574,7 +626,7 @@ class DecodeEngine:
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):  # warm up outside capture (first-launch costs)
             self._layers()
-            self._head()
+            self._gen_step()
         torch.cuda.current_stream(self.device).wait_stream(s)
         torch.cuda.synchronize(self.device)
         self._graph_layers = torch.cuda.CUDAGraph()
@@ -582,8 +634,7 @@ class DecodeEngine:
             self._layers()
         self._graph_gen = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self._graph_gen):
-            self._head()
-            self._layers()
+            self._gen_step()
         self.pos.copy_(saved[0])
         self.log_len.copy_(saved[1])
         self.token.copy_(saved[2])
@@ -611,8 +662,7 @@ class DecodeEngine:
             if use_graph:
                 self._graph_gen.replay()
             else:
-                self._head()
-                self._layers()
+                self._gen_step()
 
     def generate(self, prompt_ids, n_new: int, use_graph: bool = True, eos_token_id: Optional[int] = None):
         """Greedy decoding: returns prompt_ids + the n_new generated tokens (cut after eos_token_id, as the

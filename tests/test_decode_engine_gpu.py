@@ -163,12 +163,15 @@ def test_offloaded_dense_weights_bit_identical(dec, fused):
              ("cached_offload", dip, want_dip, dict(dip_k=k, hot_channels=hot)))
     for name, ref, want, kw in cases:
         mode = "dense" if name == "dense" else "cached_dip"
-        eng = dec.DecodeEngine(tiny, mode, max_new_tokens=6, fused=fused, offload=True, **kw)
-        assert eng.wstore.bytes_used == eng.wstore.bytes_total and eng.wstore.arena.is_pinned()
-        for use_graph in (False, True, True):
-            assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"{name} graph={use_graph}"
-            assert torch.equal(eng.x_final, ref.x_final), f"{name} graph={use_graph}: hidden state differs"
-            _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+        for overlap in (True, False):  # copies two layers ahead on copy streams / stream-ordered before the layer
+            eng = dec.DecodeEngine(tiny, mode, max_new_tokens=6, fused=fused, offload=True, overlap_copy=overlap,
+                                   **kw)
+            assert eng.wstore.bytes_used == eng.wstore.bytes_total and eng.wstore.arena.is_pinned()
+            for use_graph in (False, True, True):
+                tag = f"{name} overlap={overlap} graph={use_graph}"
+                assert eng.generate(prompt, 6, use_graph=use_graph) == want, tag
+                assert torch.equal(eng.x_final, ref.x_final), f"{tag}: hidden state differs"
+                _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
 
 
 def test_engine_rejects_bad_arguments(dec, tiny):
