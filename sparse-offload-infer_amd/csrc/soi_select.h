@@ -138,9 +138,10 @@ __device__ __forceinline__ bool radix_pass(const uint32_t (&key)[E], uint32_t* h
 // tau of rule A over the workgroup's keys: NW waves, E keys per lane (0 = NaN
 // or padding), local_max = this lane's fmaxf over its values starting from
 // 0.0f. Zeroes s_hist (radix_hist_offset<Values>(kPasses) words) itself; s_max
-// holds NW floats. Returns tau = lo after the 24 steps; `found` is false when
-// fewer than k keys are nonzero (then every step goes left, as the
-// reference's counts do).
+// holds NW floats. Returns tau = lo after the 24 steps, or, for binary16
+// values, a threshold that selects exactly the same values (see below);
+// `found` is false when fewer than k keys are nonzero (then every step goes
+// left, as the reference's counts do).
 template <int E, int NW, class Values>
 __device__ __forceinline__ float rule_a_tau(const uint32_t (&key)[E], float local_max, uint32_t* s_hist, float* s_max,
                                             int k, int tid) {
@@ -165,10 +166,18 @@ __device__ __forceinline__ float rule_a_tau(const uint32_t (&key)[E], float loca
 #pragma unroll
     for (int w = 0; w < NW; ++w) total_max = fmaxf(total_max, s_max[w]);
     const float vk = Values::value_of(prefix | (NPASS == 2 ? 0x8000u : 0u));
-    // 24 steps of mid = fl(0.5f * fl(lo + hi)), lo = mid if v_(k) >= mid else hi = mid. Both possible next
-    // sums are formed while the comparison resolves (the same fp32 operations, fewer dependent steps).
     float lo = 0.0f;
     float hi = total_max + 1e-3f;
+    if constexpr (NPASS == 2) {
+        // binary16 values: the 24 steps below keep lo <= v_(k) <= hi, and each halves hi - lo and adds at most
+        // hi0 * 2^-24 of rounding (mid = fl(0.5 * fl(lo + hi)), lo + hi <= 2 hi0), so at the end
+        // v_(k) - lo <= 3 * hi0 * 2^-24. When v_(k) is a normal binary16 >= hi0 * 2^-11, every smaller binary16
+        // lies at least v_(k) * 2^-11 > 3 * hi0 * 2^-24 below it, none lies in [lo, v_(k)), and "v >= tau" selects
+        // exactly the values "v >= v_(k)" selects: v_(k) stands for tau without the replay.
+        if (found && vk >= 0x1p-14f && vk >= hi * 0x1p-11f) return vk;
+    }
+    // 24 steps of mid = fl(0.5f * fl(lo + hi)), lo = mid if v_(k) >= mid else hi = mid. Both possible next
+    // sums are formed while the comparison resolves (the same fp32 operations, fewer dependent steps).
     float sum = lo + hi;
 #pragma unroll
     for (int it = 0; it < kBisectionSteps; ++it) {

@@ -215,6 +215,36 @@ def test_topk_rule_a_random(n, k):
     assert np.array_equal(np.sort(O.topk_rule_b(v, k)), np.sort(idx))
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_binary16_threshold_shortcut_selects_the_same_values(seed):
+    """The selection kernels skip the 24-step replay for binary16 values when v_(k) is a normal binary16 with
+    v_(k) >= (max + 1e-3) * 2^-11 and use v_(k) itself as the threshold: after the replay lo <= v_(k) and
+    v_(k) - lo <= 3 * hi0 * 2^-24, while the binary16 values below v_(k) are at least v_(k) * 2^-11 away, so no
+    binary16 value lies in [lo, v_(k)). Checked here against the oracle's tau (the reference's 24 steps) over gates
+    spanning many magnitudes, k from 1 to n, and every finite binary16 value as a candidate."""
+    r = _rng(100 + seed)
+    every_f16 = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    taken = 0
+    for trial in range(300):
+        scale = 10.0 ** r.uniform(-6, 4)
+        n = int(r.integers(1, 200))
+        v = np.abs((r.standard_normal(n) * scale).astype(np.float16)).astype(np.float32)
+        if trial % 5 == 0:
+            v = np.round(v * 4) / 4  # ties
+            v = v.astype(np.float16).astype(np.float32)
+        k = int(r.integers(1, n + 1))
+        vk = np.sort(v)[::-1][k - 1]
+        hi0 = np.float32(np.float32(v.max()) + np.float32(1e-3))
+        if not (vk >= np.float32(2.0 ** -14) and vk >= np.float32(hi0 * np.float32(2.0 ** -11))):
+            continue
+        taken += 1
+        tau = O.topk_tau_rule_a(v, k)
+        assert tau <= vk
+        assert not np.any((every_f16 >= tau) & (every_f16 < vk)), (trial, float(tau), float(vk))
+        assert np.array_equal(v >= tau, v >= vk)
+    assert taken > 100
+
+
 def test_topk_rule_a_fp16_gates_ties():
     # |fp16 gate| values tie often; rule A must still return k ascending indices with v >= tau
     r = _rng(9)
