@@ -659,7 +659,7 @@ def bench_kernels(dev, gen):
     out = torch.empty(NQ, HD, dtype=f16, device=dev)
     ws_at = torch.zeros(_C.decode_attention_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
     ws_step = torch.zeros(_C.decode_attention_step_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
-    for L in (192, 2048):
+    for L in (192, 512, 2048):
         pos = torch.tensor([L - 1], dtype=i32, device=dev)
         nb = 4096 * L + 8192
         t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_at(q, kc, vc, pos, out, ws_at),

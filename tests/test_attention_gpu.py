@@ -28,7 +28,7 @@ def _qkv(NQ, NKV, hd, S, seed):
     return q, k, v
 
 
-@pytest.mark.parametrize("L", [1, 2, 17, 63, 64, 65, 300, 1000, 2047, 2048])
+@pytest.mark.parametrize("L", [1, 2, 17, 63, 64, 65, 300, 1000, 1024, 1025, 2047, 2048])
 def test_qwen_shape_matches_oracle(ops, L):
     q, k, v = _qkv(16, 8, 128, 2048, seed=L)
     ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), L)
