@@ -622,6 +622,7 @@ class DecodeEngine:
     def capture(self):
         """Capture the prompt step (layers) and the generation step (head + layers) as HIP graphs."""
         saved = (self.pos.clone(), self.log_len.clone(), self.token.clone())
+        self._step_open = False  # a step's copies always start inside the step that uses them
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):  # warm up outside capture (first-launch costs)
@@ -643,6 +644,7 @@ class DecodeEngine:
     def reset(self):
         self.pos.zero_()
         self.log_len.zero_()
+        self._step_open = False
 
     def prefill(self, prompt_ids, use_graph: bool = True):
         prompt = torch.as_tensor(list(prompt_ids), dtype=torch.int32, device=self.device)
