@@ -807,8 +807,30 @@ def cpu_baseline(layer0):
         for W, (_, _, x, _) in zip(pre, qs):
             cpu_path.gemv_mv_predequantized(W, x)
 
+    # the other hot-path operators' CPU oracles of the reference's tests (oracle/cpu_path.py) at the BASELINE
+    # shapes: top-k over |gate| I = 6144, k = 3072; gather of 3072 1 KB rows; sparse down over 3072 selected rows
+    # of down^T (pre-dequantized, and with the dequantize of the selected rows); attention at L = 192 and 2048
+    gen = torch.Generator().manual_seed(11)
+    I, H, kk = 6144, 2048, 3072
+    abs_g = torch.randn(I, generator=gen).half().float().abs()
+    rows = torch.randint(0, 256, (I, H // 2), dtype=torch.uint8, generator=gen)
+    sel = torch.sort(torch.randperm(I, generator=gen)[:kk]).values
+    q_d = torch.randint(-7, 8, (kk, H), dtype=torch.int8, generator=gen)
+    s_d = torch.rand(kk, H // GS, generator=gen) * 0.01
+    h_sel = torch.randn(kk, generator=gen).half()
+    Wd_sel = cpu_path.dequantize_group(q_d, s_d, H, GS)
+    qa = torch.randn(16, 128, generator=gen).half()
+    kc, vc = torch.randn(8, 2048, 128, generator=gen).half(), torch.randn(8, 2048, 128, generator=gen).half()
+    others = (("topk_I6144_k3072", lambda: cpu_path.topk_indices(abs_g, kk)),
+              ("gather_rows_k3072", lambda: cpu_path.gather_rows(rows, sel)),
+              ("sparse_down_k3072_predequantized", lambda: cpu_path.sparse_accumulate_ref(h_sel, Wd_sel)),
+              ("sparse_down_k3072_with_dequantize",
+               lambda: cpu_path.sparse_accumulate_ref(h_sel, cpu_path.dequantize_group(q_d, s_d, H, GS))),
+              ("attention_L192", lambda: cpu_path.decode_attention_ref(qa, kc, vc, 192)),
+              ("attention_L2048", lambda: cpu_path.decode_attention_ref(qa, kc, vc, 2048)))
+
     saved = torch.get_num_threads()
-    figures = {}
+    figures, other_figures = {}, {}
     try:
         for threads in (cores, 1):
             torch.set_num_threads(threads)
@@ -816,6 +838,9 @@ def cpu_baseline(layer0):
                 med, p90 = _time_passes(fn)
                 figures[f"{name}_{threads}t"] = {"median_ms": round(med * 1e3, 3), "p90_ms": round(p90 * 1e3, 3),
                                                  "GBps": round(pass_bytes / med / 1e9, 4)}
+            for name, fn in others:
+                med, p90 = _time_passes(fn)
+                other_figures[f"{name}_{threads}t"] = {"median_us": round(med * 1e6, 1), "p90_us": round(p90 * 1e6, 1)}
     finally:
         torch.set_num_threads(saved)
 
@@ -830,13 +855,16 @@ def cpu_baseline(layer0):
     return {"value": main_fig["GBps"], "unit": "GB/s", "cores": cores, "kind": "port",
             "median_ms_per_pass": main_fig["median_ms"], "p90_ms_per_pass": main_fig["p90_ms"],
             "single_thread_value": figures["dequant_mv_1t"]["GBps"], "figures": figures,
-            "c_oracle_binary64_GBps": checker,
+            "c_oracle_binary64_GBps": checker, "other_operators": other_figures,
             "sample": f"the reference's CPU GEMV path (formats.dequantize of the int8 codes and fp32 scales, then "
                       f"fp32 torch.mv, fp16 out; tests/test_m4_kernels.py:157-165, restated in oracle/cpu_path.py) "
                       f"over layer 0's 7 INT4 g128 GEMVs ({pass_bytes} algorithmic bytes per pass), 20 warmup + 100 "
                       f"timed passes, median, torch.set_num_threads({cores}); GB/s = algorithmic INT4 bytes / "
                       f"time, as the GPU figure. Also: 1 thread, the matmul alone on pre-dequantized fp32, and "
-                      f"the C oracle's binary64 GEMV (the tests' checker, not the baseline). Host: {_cpu_model()}, "
+                      f"the C oracle's binary64 GEMV (the tests' checker, not the baseline). other_operators: the "
+                      f"reference tests' CPU oracles of the other path operators (torch.topk, index_select, "
+                      f"h @ W_dequant, decode_attention_ref; oracle/cpu_path.py) at the BASELINE shapes, 20 warmup + "
+                      f"100 timed calls, median and p90 in us. Host: {_cpu_model()}, "
                       f"{avail} cores available to the job"}
 
 

@@ -1,4 +1,4 @@
-"""The reference's own CPU path for a quantized GEMV, restated in torch (CPU tensors).
+"""The reference's own CPU paths for the hot-path operators, restated in torch (CPU tensors).
 
 TEST AND BENCH INFRASTRUCTURE ONLY. bench.py's cpu_baseline leg times it as
 the CPU baseline, and tests/ check it. The product never imports it.
@@ -12,12 +12,24 @@ user of the reference runs for a GEMV. This module states them as functions
 of the unpacked int8 codes and fp32 scales, the inputs formats.quantize
 produces.
 
+The other operators' CPU oracles in the reference's tests are restated the
+same way: top-k as torch.topk (tests/test_m7_kernels.py:19-20), gathers as
+index_select (tests/test_gather_rows.py:41), the sparse accumulate as
+(h.float() @ W_dequant.float()).half() (tests/test_m7_sparse_gemv.py:63-71)
+and attention as decode_attention_ref (tests/test_m5_kernels.py:157-170).
+
 Pinned by tests/test_oracle_cpu.py: dequantize_group equals the C oracle's
 soi_ref_dequant_int4 bit for bit (the same binary32 product fl(q*s) per
 element); gemv_dequant_mv is within binary16 rounding of the binary64 oracle
-GEMV and returns the binary16 rounding of a column for a basis vector x.
+GEMV and returns the binary16 rounding of a column for a basis vector x;
+topk_indices gives the rule-A set on distinct values, gather_rows equals
+numpy indexing, sparse_accumulate_ref is within binary16 rounding of the
+binary64 sparse accumulate, decode_attention_ref within the attention
+tolerance of the binary64 attention.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -40,3 +52,33 @@ def gemv_dequant_mv(q: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, orig_
 def gemv_mv_predequantized(W: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """The matmul half alone, on an fp32 W [N, K] dequantized beforehand."""
     return torch.mv(W, x[: W.shape[1]].float()).half()
+
+
+def topk_indices(abs_g: torch.Tensor, k: int) -> torch.Tensor:
+    """The reference test's top-k: torch.topk over fp32 |gate| (tests/test_m7_kernels.py:19-20), indices only."""
+    return torch.topk(abs_g, k).indices
+
+
+def gather_rows(matrix: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """matrix.index_select(0, indices) (tests/test_gather_rows.py:41): the rows' bytes."""
+    return matrix.index_select(0, indices)
+
+
+def sparse_accumulate_ref(h_sel: torch.Tensor, W_dequant_sel: torch.Tensor) -> torch.Tensor:
+    """fp16 [H] = (h.float() @ W_dequant.float()).half() over the selected rows of down^T
+    (tests/test_m7_sparse_gemv.py:63-71)."""
+    return (h_sel.float() @ W_dequant_sel.float()).half()
+
+
+def decode_attention_ref(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cur_len: int) -> torch.Tensor:
+    """Per query head: softmax(K q / sqrt(hd)) V over the first cur_len timesteps of its KV head, in fp32, fp16
+    out (tests/test_m5_kernels.py:157-170)."""
+    nq, hd = q.shape
+    rep = nq // k_cache.shape[0]
+    scale = 1.0 / math.sqrt(hd)
+    out = torch.empty_like(q)
+    for h in range(nq):
+        kv = h // rep
+        scores = torch.mv(k_cache[kv, :cur_len].float(), q[h].float()) * scale
+        out[h] = torch.mv(v_cache[kv, :cur_len].float().t(), torch.softmax(scores, dim=0)).half()
+    return out

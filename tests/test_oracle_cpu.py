@@ -477,3 +477,51 @@ def test_cpu_path_basis_vector_gives_f16_column():
         e[k] = 1.0
         y = cpu_path.gemv_dequant_mv(torch.from_numpy(q), torch.from_numpy(s), e, 256, 128)
         assert np.array_equal(y.numpy(), Wd[:, k].astype(np.float16))
+
+
+def test_cpu_path_topk_is_rule_a_on_distinct_values():
+    """torch.topk (the reference test's top-k oracle) picks the rule-A set when the values are distinct."""
+    from oracle import cpu_path
+
+    r = _rng(31)
+    v = (r.random(6144) * 10).astype(np.float32)
+    for k in (1, 768, 3072, 6144):
+        got = set(cpu_path.topk_indices(torch.from_numpy(v), k).tolist())
+        assert got == set(O.topk_rule_a(v, k).tolist())
+
+
+def test_cpu_path_gather_equals_numpy_indexing():
+    from oracle import cpu_path
+
+    r = _rng(32)
+    m = r.integers(0, 256, (500, 64), dtype=np.uint8)
+    idx = np.sort(r.permutation(500)[:123]).astype(np.int64)
+    got = cpu_path.gather_rows(torch.from_numpy(m), torch.from_numpy(idx)).numpy()
+    assert np.array_equal(got, O.gather_rows(m, idx)) and np.array_equal(got, m[idx])
+
+
+def test_cpu_path_sparse_accumulate_within_f16_rounding_of_oracle():
+    from oracle import cpu_path
+
+    g = torch.Generator().manual_seed(33)
+    k, H, gs = 300, 2048, 128
+    w = (torch.randn(k, H, generator=g) * 0.02).numpy()
+    q, s = O.quantize_group(w, gs)
+    h = torch.randn(k, generator=g).half()
+    Wd = cpu_path.dequantize_group(torch.from_numpy(q), torch.from_numpy(s), H, gs)
+    y = cpu_path.sparse_accumulate_ref(h, Wd)
+    ref = O.sparse_accumulate_f64(O.pack_int4(q), s, h.numpy(), H, gs)
+    assert np.abs(y.double().numpy() - ref).max() <= 1e-3 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("L", [1, 17, 300])
+def test_cpu_path_attention_within_tolerance_of_oracle(L):
+    from oracle import cpu_path
+
+    g = torch.Generator().manual_seed(34 + L)
+    q = torch.randn(16, 128, generator=g).half()
+    kc = torch.randn(8, 320, 128, generator=g).half()
+    vc = torch.randn(8, 320, 128, generator=g).half()
+    out = cpu_path.decode_attention_ref(q, kc, vc, L)
+    ref = O.decode_attention_f64(q.numpy(), kc.numpy(), vc.numpy(), L)
+    assert np.abs(out.double().numpy() - ref).max() <= 1e-3 * np.abs(ref).max()
