@@ -516,6 +516,30 @@ int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h, int64_t n
                               const uint8_t* Wt, const float* St, int32_t* out_indices, int32_t* out_count,
                               uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Residual update in the producer's epilogue: the projection whose output is
+ * added to the residual stream (o_proj: python/soinfer/runtime/generate.py:172
+ * `h2 = residual + o`; down: generate.py:182 / 310 `residual2 + down`) also
+ * writes res_out[i] = res[i] + y[i], one binary16 addition (the fp32 sum
+ * rounded once), the value soi_gemv_w4a16_rmsnorm / soi_residual_rmsnorm
+ * compute from (res, delta = y). The next RMSNorm-fused GEMV then reads
+ * res_out alone (delta null, x_out null) with bit-identical results.
+ *   soi_gemv_w4a16_residual: soi_gemv_w4a16_group_lop3 (same y) plus
+ *     res_out[N] = res + y; res and res_out are [N] and must not overlap y.
+ *   soi_dip_select_dense_down_residual: soi_dip_select_dense_down (same y,
+ *     index list and count) plus res_out[H] = res + y.
+ * res_out may be res itself (each element is read, then written, by the one
+ * lane that owns its row). No reference counterpart as single entry points:
+ * each replaces a projection plus the add cited above.
+ * ------------------------------------------------------------------------ */
+int soi_gemv_w4a16_residual(const uint8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y,
+                            const uint16_t* res, uint16_t* res_out, int64_t N, int64_t K, int64_t group_size,
+                            int64_t num_groups, void* stream);
+int soi_dip_select_dense_down_residual(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
+                                       const uint8_t* Wt, const float* St, int32_t* out_indices,
+                                       int32_t* out_count, uint16_t* y, const uint16_t* res, uint16_t* res_out,
+                                       int64_t H, int64_t group_size, int64_t num_groups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -778,6 +778,27 @@ void gemv_w4a16_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x, tor
                  n);
 }
 
+void gemv_w4a16_residual_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor x, torch::Tensor y,
+                              torch::Tensor res, torch::Tensor res_out, int64_t K, int64_t group_size) {
+    const char* n = "gemv_w4a16_residual_into";
+    need(Wq, torch::kUInt8, x, n, "Wq");
+    need(scale, torch::kFloat32, x, n, "scale");
+    need(x, torch::kFloat16, x, n, "x");
+    need(y, torch::kFloat16, x, n, "y");
+    need(res, torch::kFloat16, x, n, "res");
+    need(res_out, torch::kFloat16, x, n, "res_out");
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4 && x.numel() == K, n, ": Wq / x shape mismatch");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0) && y.numel() == Wq.size(0), n,
+                ": scale / y shape mismatch");
+    TORCH_CHECK(res.numel() == Wq.size(0) && res_out.numel() == Wq.size(0), n, ": res and res_out must have N values");
+    TORCH_CHECK(res_out.data_ptr() != y.data_ptr() && res.data_ptr() != y.data_ptr(), n,
+                ": res / res_out must not alias y");
+    const at::DeviceGuard guard(x.device());
+    check_status(soi_gemv_w4a16_residual(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(), h16(x), h16m(y), h16(res),
+                                         h16m(res_out), Wq.size(0), K, group_size, scale.size(1), cur_stream(x)),
+                 n);
+}
+
 void gemv_w4a16_indexed_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor idx, torch::Tensor x,
                              torch::Tensor y, int64_t K, int64_t group_size) {
     const char* n = "gemv_w4a16_indexed_into";
@@ -1108,7 +1129,8 @@ void gemv_w4a16_rmsnorm_swiglu_gate_into(torch::Tensor Wq, torch::Tensor scale, 
 
 void dip_select_dense_down_into(torch::Tensor gate, torch::Tensor h, int64_t k, torch::Tensor Wt, torch::Tensor St,
                                 c10::optional<torch::Tensor> idx_out, c10::optional<torch::Tensor> count_out,
-                                torch::Tensor y, int64_t group_size) {
+                                torch::Tensor y, int64_t group_size, c10::optional<torch::Tensor> res,
+                                c10::optional<torch::Tensor> res_out) {
     const char* n = "dip_select_dense_down_into";
     need(gate, torch::kFloat16, gate, n, "gate");
     need(h, torch::kFloat16, gate, n, "h");
@@ -1132,7 +1154,20 @@ void dip_select_dense_down_into(torch::Tensor gate, torch::Tensor h, int64_t k, 
         need_numel(*count_out, 1, n, "count_out");
         cp = count_out->data_ptr<int32_t>();
     }
+    TORCH_CHECK(res.has_value() == res_out.has_value(), n, ": res and res_out go together");
     const at::DeviceGuard guard(gate.device());
+    if (res.has_value()) {
+        need(*res, torch::kFloat16, gate, n, "res");
+        need(*res_out, torch::kFloat16, gate, n, "res_out");
+        TORCH_CHECK(res->numel() == H && res_out->numel() == H, n, ": res and res_out must have H values");
+        TORCH_CHECK(res_out->data_ptr() != y.data_ptr() && res->data_ptr() != y.data_ptr(), n,
+                    ": res / res_out must not alias y");
+        check_status(soi_dip_select_dense_down_residual(h16(gate), h16(h), I, k, Wt.data_ptr<uint8_t>(),
+                                                        St.data_ptr<float>(), ip, cp, h16m(y), h16(*res),
+                                                        h16m(*res_out), H, group_size, St.size(0), cur_stream(gate)),
+                     n);
+        return;
+    }
     check_status(soi_dip_select_dense_down(h16(gate), h16(h), I, k, Wt.data_ptr<uint8_t>(), St.data_ptr<float>(), ip,
                                            cp, h16m(y), H, group_size, St.size(0), cur_stream(gate)),
                  n);
@@ -1393,6 +1428,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("decode_attention_step", &decode_attention_step,
           "q/k norm + RoPE + KV append + attention in one launch (device position)");
     m.def("gemv_w4a16_into", &gemv_w4a16_into, "INT4 GEMV into a caller buffer");
+    m.def("gemv_w4a16_residual_into", &gemv_w4a16_residual_into,
+          "INT4 GEMV into a caller buffer that also writes res_out = res + y (binary16)");
     m.def("gemv_w4a16_indexed_into", &gemv_w4a16_indexed_into, "index-driven INT4 GEMV into a caller buffer");
     m.def("gemv_w4a16_indexed_accumulate_into", &gemv_w4a16_indexed_accumulate_into,
           "index-driven sparse down accumulate into a caller buffer");
@@ -1422,7 +1459,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "DIP selection + down projection over resident transposed down^T values in one launch (index outputs "
           "optional)",
           py::arg("gate"), py::arg("h"), py::arg("k"), py::arg("Wt"), py::arg("St"), py::arg("idx_out"),
-          py::arg("count_out"), py::arg("y"), py::arg("group_size"));
+          py::arg("count_out"), py::arg("y"), py::arg("group_size"), py::arg("res") = py::none(),
+          py::arg("res_out") = py::none());
     m.def("gemv_w4a16_indexed_accumulate_gated_into", &gemv_w4a16_indexed_accumulate_gated_into,
           "sparse down over selected rows with the SiLU gating computed on the fly");
     m.def("dip_select_gated_down_into", &dip_select_gated_down_into,

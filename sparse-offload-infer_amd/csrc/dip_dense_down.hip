@@ -62,6 +62,8 @@ struct DdArgs {
     int32_t* out_idx;      // [k] or null
     int32_t* out_count;    // [1] or null
     uint16_t* y;           // [H]
+    const uint16_t* res;   // [H] or null: the residual stream that y is added to
+    uint16_t* res_out;     // [H] or null: res + y, rounded once to binary16
     int n, k, H, gs;
 };
 
@@ -136,6 +138,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
             wv[i] = __builtin_nontemporal_load((row < a.H && c < chunks) ? rp + c : z4);
         }
     }
+    // the residual element of the row (a zero word when there is none; a select, so the load is not branched)
+    const uint16_t rv = ldg(a.res_out && row < a.H ? a.res + row : reinterpret_cast<const uint16_t*>(g_zero16));
 
     // 2. |gate| (NaN past the end: key 0, never counted or selected), the coefficients h * St[g] (fp32,
     // unmasked) and their largest magnitude, handed to the other waves through the selection's first barrier
@@ -257,7 +261,11 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     }
     {
         const float t = wave_sum_bcast(acc);
-        if (lane == 0 && row < a.H) stg(a.y + row, f32_to_f16_bits(__builtin_ldexpf(t, -e)));
+        if (lane == 0 && row < a.H) {
+            const uint16_t yb = f32_to_f16_bits(__builtin_ldexpf(t, -e));
+            stg(a.y + row, yb);
+            if (a.res_out) stg(a.res_out + row, static_cast<uint16_t>(add_f16x2(rv, yb)));
+        }
     }
 
     // 7. the index list when asked for (after y), by wave 0: workgroup b writes positions [b*win, (b+1)*win)
@@ -285,11 +293,10 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 
 using namespace soi;
 
-extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
-                                         const uint8_t* Wt, const float* St, int32_t* out_indices,
-                                         int32_t* out_count, uint16_t* y, int64_t H, int64_t group_size,
-                                         int64_t num_groups, void* stream) {
-    const char* what = "soi_dip_select_dense_down";
+static int dense_down(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k, const uint8_t* Wt,
+                      const float* St, int32_t* out_indices, int32_t* out_count, uint16_t* y, const uint16_t* res,
+                      uint16_t* res_out, int64_t H, int64_t group_size, int64_t num_groups, void* stream,
+                      const char* what) {
     const int64_t n = num_channels;
     SOI_REQUIRE(n >= 32 && n <= kDdMaxChannels && n % 32 == 0, "%s: num_channels must be a multiple of 32 in [32, %d]",
                 what, kDdMaxChannels);
@@ -302,7 +309,7 @@ extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h
     SOI_REQUIRE(aligned16(Wt) && aligned16(St), "%s: Wt and St must be 16-byte aligned", what);
     SOI_REQUIRE((reinterpret_cast<uintptr_t>(gate) & 7u) == 0 && (reinterpret_cast<uintptr_t>(h) & 7u) == 0,
                 "%s: gate and h must be 8-byte aligned", what);
-    DdArgs a{gate, h, Wt, St, out_indices, out_count, y, static_cast<int>(n), static_cast<int>(k),
+    DdArgs a{gate, h, Wt, St, out_indices, out_count, y, res, res_out, static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(H), static_cast<int>(group_size)};
     const dim3 grid(static_cast<unsigned>(ceil_div64(H, kDdWaves))), block(kDdThreads);
     const int64_t nc = ceil_div64(n, kDdChannelsPerPass);
@@ -324,4 +331,23 @@ extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h
     }
 #undef SOI_DD
     return launch_status(what);
+}
+
+extern "C" int soi_dip_select_dense_down(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
+                                         const uint8_t* Wt, const float* St, int32_t* out_indices,
+                                         int32_t* out_count, uint16_t* y, int64_t H, int64_t group_size,
+                                         int64_t num_groups, void* stream) {
+    return dense_down(gate, h, num_channels, k, Wt, St, out_indices, out_count, y, nullptr, nullptr, H, group_size,
+                      num_groups, stream, "soi_dip_select_dense_down");
+}
+
+extern "C" int soi_dip_select_dense_down_residual(const uint16_t* gate, const uint16_t* h, int64_t num_channels,
+                                                  int64_t k, const uint8_t* Wt, const float* St,
+                                                  int32_t* out_indices, int32_t* out_count, uint16_t* y,
+                                                  const uint16_t* res, uint16_t* res_out, int64_t H,
+                                                  int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_dip_select_dense_down_residual";
+    SOI_REQUIRE(res && res_out, "%s: null pointer", what);
+    return dense_down(gate, h, num_channels, k, Wt, St, out_indices, out_count, y, res, res_out, H, group_size,
+                      num_groups, stream, what);
 }

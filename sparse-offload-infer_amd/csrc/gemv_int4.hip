@@ -491,6 +491,21 @@ extern "C" int soi_gemv_w4a16_group_lop3(const uint8_t* Wq, const float* scale, 
     return dense_int4<true>(Wq, scale, x, y, N, K, group_size, num_groups, stream, "soi_gemv_w4a16_group_lop3");
 }
 
+extern "C" int soi_gemv_w4a16_residual(const uint8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y,
+                                       const uint16_t* res, uint16_t* res_out, int64_t N, int64_t K,
+                                       int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_w4a16_residual";
+    int st = check_int4_common(K, group_size, num_groups, what);
+    if (st) return st;
+    SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: N out of range", what);
+    if (N == 0) return SOI_OK;
+    SOI_REQUIRE(Wq && scale && x && y && res && res_out, "%s: null pointer", what);
+    const int64_t row_bytes = ceil_div64(K, 8) * 4;
+    const bool vec = (K % 32 == 0) && aligned16(Wq) && aligned16(x);
+    DenseRows rows{Wq, scale, row_bytes, num_groups};
+    return launch_int4<true>(rows, N, x, StoreYAdd{y, res, res_out}, K, group_size, vec, as_stream(stream), what);
+}
+
 extern "C" int soi_gemv_dip_fused_up(const uint8_t* cache_Wq, const float* cache_scale, int64_t cache_rows,
                                      const uint8_t* staging_Wq, const float* staging_scale, int64_t staging_rows,
                                      const int32_t* desc, int64_t k, const uint16_t* x, uint16_t* y, int64_t K,

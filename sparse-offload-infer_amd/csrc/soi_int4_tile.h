@@ -213,6 +213,29 @@ struct StoreY {
     }
 };
 
+// StoreYAdd: StoreY, and res_out[row] = res[row] + y[row] as one binary16 addition
+// (the residual update the next RMSNorm would otherwise do on load, with the same
+// rounding). res[row] is requested before the tile's weights.
+struct StoreYAdd {
+    static constexpr bool kSwiglu = false;
+    static constexpr bool kPrefetch = true;
+    uint16_t* y;
+    const uint16_t* res;
+    uint16_t* res_out;
+    struct Pre {
+        uint16_t r;
+    };
+    template <int R>
+    __device__ __forceinline__ Pre prefetch(int64_t row0, int r_lane, int64_t N) const {
+        return {ldg(res + (row0 + r_lane < N ? row0 + r_lane : N - 1))};
+    }
+    __device__ __forceinline__ void store(int64_t row, float total, bool valid, Pre p) const {
+        const uint16_t yb = valid ? f32_to_f16_bits(total) : uint16_t(0x7e00u);
+        stg(y + row, yb);
+        stg(res_out + row, static_cast<uint16_t>(add_f16x2(p.r, yb)));
+    }
+};
+
 // SiluIdxY requests its gate value before the tile's weight loads: the tile's
 // R channels are read with wave-uniform (scalar) loads, the lane's one is
 // selected and gate[c] is requested right away, instead of two dependent

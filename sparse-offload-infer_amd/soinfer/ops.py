@@ -39,6 +39,18 @@ def gemv_w4a16_group_lop3(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch
     return _C.gemv_w4a16_group_lop3(Wq_packed, scale, x, K, group_size)
 
 
+def gemv_w4a16_residual(Wq_packed: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, res: torch.Tensor, K: int,
+                        group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The projection that feeds a residual add (reference generate.py:172 `h2 = residual + o`, :182 `residual2 +
+    down`) with the add in its epilogue: returns (y, res_out), y as gemv_w4a16_group_lop3 gives it and
+    res_out = res + y rounded once to binary16 (res: [N] fp16)."""
+    N = Wq_packed.shape[0]
+    y = torch.empty(N, dtype=torch.float16, device=x.device)
+    res_out = torch.empty(N, dtype=torch.float16, device=x.device)
+    _C.gemv_w4a16_residual_into(Wq_packed, scale, x, y, res, res_out, K, group_size)
+    return y, res_out
+
+
 def _check_aligned16(what: str, K: int, W: torch.Tensor, x: torch.Tensor) -> None:
     """The batched and grouped kernels read Wq and x with 16-byte loads when K % 32 == 0; a misaligned
     problem there would only come back as NaN rows, so it is rejected before launch."""
@@ -236,6 +248,19 @@ def dip_select_dense_down(gate: torch.Tensor, h: torch.Tensor, k: int, Wt: torch
     cnt = torch.empty(1, dtype=torch.int32, device=gate.device) if with_indices else None
     _C.dip_select_dense_down_into(gate, h, k, Wt, St, idx, cnt, y, group_size)
     return y, idx, cnt
+
+
+def dip_select_dense_down_residual(gate: torch.Tensor, h: torch.Tensor, k: int, Wt: torch.Tensor, St: torch.Tensor,
+                                   group_size: int, res: torch.Tensor, with_indices: bool = True):
+    """dip_select_dense_down with the residual add (reference generate.py:310 `residual2 + down_out`) in the
+    same launch: returns (y, res_out, indices, count), res_out = res + y rounded once to binary16."""
+    H = Wt.shape[0]
+    y = torch.empty(H, dtype=torch.float16, device=gate.device)
+    res_out = torch.empty(H, dtype=torch.float16, device=gate.device)
+    idx = torch.empty(k, dtype=torch.int32, device=gate.device) if with_indices else None
+    cnt = torch.empty(1, dtype=torch.int32, device=gate.device) if with_indices else None
+    _C.dip_select_dense_down_into(gate, h, k, Wt, St, idx, cnt, y, group_size, res, res_out)
+    return y, res_out, idx, cnt
 
 
 def gather_rows_device(src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor) -> None:
