@@ -163,8 +163,10 @@ __global__ __launch_bounds__(64) SOI_GEMV_OCCUPANCY void gemv_int4_batched_occ_k
 // eps) with the same wave reduction (so all agree bit for bit); workgroup 0
 // also writes x_out = a + d and h_out = rmsnorm(a + d, w) when given. a, d,
 // w, x_out, h_out: fp16 [K], K % 32 == 0, 16-byte aligned; x_out and h_out
-// must not alias a or d (other workgroups are still reading them).
-template <int R, bool CHUNK_SCALE, bool FULL, bool ONEPASS, class EP>
+// must not alias a or d (other workgroups are still reading them). OP: 0 the
+// general form, 1 the one-pass form (K == 2048) with d, 2 the one-pass form
+// without d (its lanes load only a and w).
+template <int R, bool CHUNK_SCALE, bool FULL, int OP, class EP>
 __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int64_t N, const uint16_t* __restrict__ a,
                                                             const uint16_t* __restrict__ d,
                                                             const uint16_t* __restrict__ w, float eps,
@@ -174,19 +176,18 @@ __global__ __launch_bounds__(64) void gemv_int4_norm_kernel(DenseRows rows, int6
     const u32x4* a4 = reinterpret_cast<const u32x4*>(a);
     const u32x4* d4 = reinterpret_cast<const u32x4*>(d);
     const u32x4* w4 = reinterpret_cast<const u32x4*>(w);
-    if constexpr (ONEPASS) {
+    if constexpr (OP != 0) {
         // K == 2048: lane l's 32 elements are exactly its GEMV chunk. Its a / d / w chunks are requested here, the
         // tile then issues the weight loads, and the add + RMSNorm run while those are in flight (RegNormX).
         static_assert(FULL, "the one-pass norm form needs the full tile");
         RegNormX xs;
-        const u32x4* e4 = d ? d4 : a4;  // unconditional loads (a branch around a load makes the wave wait there)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             xs.t[i] = ldg(a4 + 4 * lane + i);
             xs.g[i] = ldg(w4 + 4 * lane + i);
-            xs.e[i] = ldg(e4 + 4 * lane + i);
+            if constexpr (OP == 1) xs.e[i] = ldg(d4 + 4 * lane + i);  // compile-time choice: no branch at run time
         }
-        xs.has_d = d != nullptr;
+        xs.has_d = OP == 1;
         xs.eps = eps;
         xs.K = K;
         xs.x_out = blockIdx.x == 0 ? x_out : nullptr;
@@ -641,10 +642,11 @@ extern "C" int soi_gemv_w4a16_rmsnorm_gate_up(const uint8_t* Wq, const float* sc
 #define SOI_N(CS, FL, OP)                                                                                          \
     hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, OP, SplitGUY>), grid, dim3(64), 0, s, rows, N, x, delta,   \
                        norm_weight, eps, x_out, h_out, ep, Ki, gi)
-    if (one) SOI_N(true, true, true);
-    else if (cs && full_k) SOI_N(true, true, false);
-    else if (cs) SOI_N(true, false, false);
-    else SOI_N(false, false, false);
+    if (one && delta) SOI_N(true, true, 1);
+    else if (one) SOI_N(true, true, 2);
+    else if (cs && full_k) SOI_N(true, true, 0);
+    else if (cs) SOI_N(true, false, 0);
+    else SOI_N(false, false, 0);
 #undef SOI_N
     return launch_status(what);
 }
@@ -679,10 +681,11 @@ static int rmsnorm_impl(const uint8_t* Wq, const float* scale, const uint16_t* x
 #define SOI_N(CS, FL, OP)                                                                                          \
     hipLaunchKernelGGL((gemv_int4_norm_kernel<8, CS, FL, OP, SwigluY>), grid, dim3(64), 0, s, rows, N, x, delta,    \
                        norm_weight, eps, x_out, h_out, ep, Ki, gi)
-        if (one) SOI_N(true, true, true);
-        else if (cs && full_k) SOI_N(true, true, false);
-        else if (cs) SOI_N(true, false, false);
-        else SOI_N(false, false, false);
+        if (one && delta) SOI_N(true, true, 1);
+        else if (one) SOI_N(true, true, 2);
+        else if (cs && full_k) SOI_N(true, true, 0);
+        else if (cs) SOI_N(true, false, 0);
+        else SOI_N(false, false, 0);
 #undef SOI_N
         return launch_status(what);
     }
@@ -695,11 +698,12 @@ static int rmsnorm_impl(const uint8_t* Wq, const float* scale, const uint16_t* x
 #define SOI_N(RR, CS, FL, OP)                                                                                      \
     hipLaunchKernelGGL((gemv_int4_norm_kernel<RR, CS, FL, OP, StoreY>), grid, dim3(64), 0, s, rows, N, x, delta,   \
                        norm_weight, eps, x_out, h_out, ep, Ki, gi)
-#define SOI_NR(RR)                                \
-    if (full && one) SOI_N(RR, true, true, true); \
-    else if (full) SOI_N(RR, true, true, false);  \
-    else if (cs) SOI_N(RR, true, false, false);   \
-    else SOI_N(RR, false, false, false)
+#define SOI_NR(RR)                                      \
+    if (full && one && delta) SOI_N(RR, true, true, 1); \
+    else if (full && one) SOI_N(RR, true, true, 2);     \
+    else if (full) SOI_N(RR, true, true, 0);            \
+    else if (cs) SOI_N(RR, true, false, 0);             \
+    else SOI_N(RR, false, false, 0)
     switch (R) {
         case 8: SOI_NR(8); break;
         case 4: SOI_NR(4); break;
