@@ -659,6 +659,9 @@ def bench_kernels(dev, gen):
     out = torch.empty(NQ, HD, dtype=f16, device=dev)
     ws_at = torch.zeros(_C.decode_attention_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
     ws_step = torch.zeros(_C.decode_attention_step_workspace_bytes(NQ, NKV, HD, S), dtype=torch.uint8, device=dev)
+    WO = [torch.randint(0, 256, (2048, 1024), dtype=torch.uint8, device=dev, generator=gen) for _ in range(2)]
+    SO = [torch.rand(2048, 16, device=dev, generator=gen) * 0.01 + 1e-3 for _ in range(2)]
+    o_y = torch.empty(2048, dtype=f16, device=dev)
     for L in (192, 512, 2048):
         pos = torch.tensor([L - 1], dtype=i32, device=dev)
         nb = 4096 * L + 8192
@@ -669,6 +672,26 @@ def bench_kernels(dev, gen):
                                                                           1e-6, ws_step), list(zip(KC, VC)))
         res[f"attention_step_L{L}"] = entry(nb + 2 * (NQ + 2 * NKV) * HD, t["mean_us"],
                                             kernel="attn_kernel with q/k norm + RoPE + KV append (1 launch)")
+        # the engine's pair: attention step, then the o projection (2048 x 2048 INT4) on its output; deferred:
+        # the split states combined by the o projection while its weights load
+        args = [(kc, vc, W, Sc) for (kc, vc), (W, Sc) in zip(zip(KC, VC), zip(WO * len(KC), SO * len(KC)))]
+        t = time_graph_per_launch(lambda kc, vc, W, Sc: (
+            _C.decode_attention_step(qkv, qn, qn, cos_t, sin_t, pos, kc, vc, out, 1e-6, ws_step),
+            _C.gemv_w4a16_into(W, Sc, out.view(-1), o_y, NQ * HD, GS)), args)
+        nbo = nb + 2 * (NQ + 2 * NKV) * HD + 2048 * 1024 + 2048 * 16 * 4 + 2 * 2048
+        res[f"attention_step_o_L{L}"] = entry(nbo, t["mean_us"], kernel="attn_kernel step + o GEMV (2 launches)")
+        t = time_graph_per_launch(lambda kc, vc, W, Sc: (
+            _C.decode_attention_step_deferred(qkv, qn, qn, cos_t, sin_t, pos, kc, vc, out, 1e-6, ws_step),
+            _C.gemv_w4a16_attn_combine_into(W, Sc, ws_step, out, pos, NKV, S, o_y, GS)), args)
+        res[f"attention_step_deferred_o_L{L}"] = entry(
+            nbo, t["mean_us"], kernel="attn_kernel step leaving split states + o GEMV combining them on load "
+                                      "(2 launches)")
+        t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_step_deferred(qkv, qn, qn, cos_t, sin_t, pos, kc,
+                                                                                   vc, out, 1e-6, ws_step),
+                                  list(zip(KC, VC)))
+        res[f"attention_step_deferred_L{L}"] = entry(
+            nb + 2 * (NQ + 2 * NKV) * HD, t["mean_us"],
+            kernel="attn_kernel step leaving a split context's states to the o projection (1 launch)")
     del KC, VC
     torch.cuda.empty_cache()
 

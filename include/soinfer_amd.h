@@ -293,6 +293,37 @@ int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const
                               int64_t head_dim, float eps, float scale, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Deferred combine. soi_decode_attention_step_deferred: soi_decode_attention_step
+ * (same arguments, same KV append) except that a context long enough to split
+ * across workgroups (more than 8 passes of the kernel: 256 timesteps at
+ * head_dim 128) leaves `out` unwritten and its per-split softmax states in the
+ * workspace; a shorter one writes `out` itself as before.
+ * soi_gemv_w4a16_attn_combine: y[N] = the INT4 GEMV (soi_gemv_w4a16_group_lop3
+ * arithmetic) of that step's attention output x [NQ * head_dim], with x
+ * finished on load: `out` when the context did not split, else the split
+ * states combined with the step's own combine arithmetic. y is bit-identical
+ * to soi_decode_attention_step followed by soi_gemv_w4a16_group_lop3 on its
+ * out. The workspace, pos, NQ, NKV, head_dim and max_seq are the step's;
+ * attn_out is its `out`. With res and res_out (both or neither) it also writes
+ * res_out = res + y (one binary16 add, as soi_gemv_w4a16_residual). Limits:
+ * the step's fast form (head_dim a power of two in [8, 256], at most 8 query
+ * heads per KV head), NQ * head_dim a multiple of 32 and at most 2048,
+ * group_size a multiple of 8, Wq / attn_out / workspace 16-byte aligned.
+ * No reference counterpart as single entry points: the pair replaces
+ * decode_attention (csrc/kernels/decode_attention.cu:17-63) followed by the
+ * o_proj GEMV (python/soinfer/runtime/generate.py:169-171), moving the split
+ * combine out of the attention launch into the GEMV's load phase, where it
+ * overlaps the weight loads instead of adding a cross-workgroup step. */
+int soi_decode_attention_step_deferred(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                                       const float* cos_table, const float* sin_table, const int32_t* pos,
+                                       uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, int64_t NQ, int64_t NKV,
+                                       int64_t max_seq, int64_t head_dim, float eps, float scale, void* workspace,
+                                       size_t workspace_bytes, void* stream);
+int soi_gemv_w4a16_attn_combine(const uint8_t* Wq, const float* scale, const void* workspace,
+                                size_t workspace_bytes, const uint16_t* attn_out, const int32_t* pos, int64_t NQ,
+                                int64_t NKV, int64_t head_dim, int64_t max_seq, uint16_t* y, const uint16_t* res,
+                                uint16_t* res_out, int64_t N, int64_t group_size, int64_t num_groups, void* stream);
+
 /* --------------------------------------------------------------------------
  * Decoder-step glue (binary16 in/out, fp32 math).
  *

@@ -705,10 +705,10 @@ int64_t decode_attention_step_workspace_bytes(int64_t NQ, int64_t NKV, int64_t h
     return static_cast<int64_t>(soi_decode_attention_step_workspace_bytes(NQ, NKV, head_dim, max_seq));
 }
 
-void decode_attention_step(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm, torch::Tensor cos_table,
-                           torch::Tensor sin_table, torch::Tensor pos, torch::Tensor k_cache, torch::Tensor v_cache,
-                           torch::Tensor out, double eps, torch::Tensor workspace_buf) {
-    const char* n = "decode_attention_step";
+static void attention_step_impl(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm,
+                                torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor pos,
+                                torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor out, double eps,
+                                torch::Tensor workspace_buf, bool deferred, const char* n) {
     need(qkv, torch::kFloat16, qkv, n, "qkv");
     need(q_norm, torch::kFloat16, qkv, n, "q_norm");
     need(k_norm, torch::kFloat16, qkv, n, "k_norm");
@@ -729,11 +729,64 @@ void decode_attention_step(torch::Tensor qkv, torch::Tensor q_norm, torch::Tenso
                 ": RoPE tables must be [max_seq_len, head_dim/2]");
     need_numel(pos, 1, n, "pos");
     const at::DeviceGuard guard(qkv.device());
-    check_status(soi_decode_attention_step(h16(qkv), h16(q_norm), h16(k_norm), cos_table.data_ptr<float>(),
-                                           sin_table.data_ptr<float>(), pos.data_ptr<int32_t>(), h16m(k_cache),
-                                           h16m(v_cache), h16m(out), NQ, NKV, S, hd, static_cast<float>(eps),
-                                           1.0f / std::sqrt(static_cast<float>(hd)), workspace_buf.data_ptr<uint8_t>(),
-                                           workspace_buf.numel(), cur_stream(qkv)),
+    auto fn = deferred ? soi_decode_attention_step_deferred : soi_decode_attention_step;
+    check_status(fn(h16(qkv), h16(q_norm), h16(k_norm), cos_table.data_ptr<float>(), sin_table.data_ptr<float>(),
+                    pos.data_ptr<int32_t>(), h16m(k_cache), h16m(v_cache), h16m(out), NQ, NKV, S, hd,
+                    static_cast<float>(eps), 1.0f / std::sqrt(static_cast<float>(hd)),
+                    workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), cur_stream(qkv)),
+                 n);
+}
+
+void decode_attention_step(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm, torch::Tensor cos_table,
+                           torch::Tensor sin_table, torch::Tensor pos, torch::Tensor k_cache, torch::Tensor v_cache,
+                           torch::Tensor out, double eps, torch::Tensor workspace_buf) {
+    attention_step_impl(qkv, q_norm, k_norm, cos_table, sin_table, pos, k_cache, v_cache, out, eps, workspace_buf,
+                        false, "decode_attention_step");
+}
+
+void decode_attention_step_deferred(torch::Tensor qkv, torch::Tensor q_norm, torch::Tensor k_norm,
+                                    torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor pos,
+                                    torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor out, double eps,
+                                    torch::Tensor workspace_buf) {
+    attention_step_impl(qkv, q_norm, k_norm, cos_table, sin_table, pos, k_cache, v_cache, out, eps, workspace_buf,
+                        true, "decode_attention_step_deferred");
+}
+
+void gemv_w4a16_attn_combine_into(torch::Tensor Wq, torch::Tensor scale, torch::Tensor workspace_buf,
+                                  torch::Tensor attn_out, torch::Tensor pos, int64_t num_kv_heads,
+                                  int64_t max_seq_len, torch::Tensor y, int64_t group_size,
+                                  c10::optional<torch::Tensor> res, c10::optional<torch::Tensor> res_out) {
+    const char* n = "gemv_w4a16_attn_combine_into";
+    need(Wq, torch::kUInt8, attn_out, n, "Wq");
+    need(scale, torch::kFloat32, attn_out, n, "scale");
+    need(workspace_buf, torch::kUInt8, attn_out, n, "workspace");
+    need(attn_out, torch::kFloat16, attn_out, n, "attn_out");
+    need(pos, torch::kInt32, attn_out, n, "pos");
+    need(y, torch::kFloat16, attn_out, n, "y");
+    need_numel(pos, 1, n, "pos");
+    TORCH_CHECK(attn_out.dim() == 2, n, ": attn_out must be 2D [num_q_heads, head_dim]");
+    const int64_t NQ = attn_out.size(0), hd = attn_out.size(1), K = NQ * hd;
+    TORCH_CHECK(Wq.dim() == 2 && Wq.size(1) == ((K + 7) / 8) * 4, n, ": Wq must be [N, ceil(K/8)*4], K = NQ * head_dim");
+    TORCH_CHECK(scale.dim() == 2 && scale.size(0) == Wq.size(0) && y.numel() == Wq.size(0), n,
+                ": scale / y shape mismatch");
+    TORCH_CHECK(res.has_value() == res_out.has_value(), n, ": res and res_out go together");
+    const uint16_t* rp = nullptr;
+    uint16_t* rop = nullptr;
+    if (res.has_value()) {
+        need(*res, torch::kFloat16, attn_out, n, "res");
+        need(*res_out, torch::kFloat16, attn_out, n, "res_out");
+        TORCH_CHECK(res->numel() == Wq.size(0) && res_out->numel() == Wq.size(0), n,
+                    ": res and res_out must have N values");
+        TORCH_CHECK(res_out->data_ptr() != y.data_ptr() && res->data_ptr() != y.data_ptr(), n,
+                    ": res / res_out must not alias y");
+        rp = h16(*res);
+        rop = h16m(*res_out);
+    }
+    const at::DeviceGuard guard(attn_out.device());
+    check_status(soi_gemv_w4a16_attn_combine(Wq.data_ptr<uint8_t>(), scale.data_ptr<float>(),
+                                             workspace_buf.data_ptr<uint8_t>(), workspace_buf.numel(), h16(attn_out),
+                                             pos.data_ptr<int32_t>(), NQ, num_kv_heads, hd, max_seq_len, h16m(y), rp,
+                                             rop, Wq.size(0), group_size, scale.size(1), cur_stream(attn_out)),
                  n);
 }
 
@@ -1427,6 +1480,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "workspace of decode_attention_step");
     m.def("decode_attention_step", &decode_attention_step,
           "q/k norm + RoPE + KV append + attention in one launch (device position)");
+    m.def("decode_attention_step_deferred", &decode_attention_step_deferred,
+          "decode_attention_step that leaves a split context's states for gemv_w4a16_attn_combine_into");
+    m.def("gemv_w4a16_attn_combine_into", &gemv_w4a16_attn_combine_into,
+          "INT4 GEMV of the attention output that combines a deferred step's split states on load",
+          py::arg("Wq"), py::arg("scale"), py::arg("workspace"), py::arg("attn_out"), py::arg("pos"),
+          py::arg("num_kv_heads"), py::arg("max_seq_len"), py::arg("y"), py::arg("group_size"),
+          py::arg("res") = py::none(), py::arg("res_out") = py::none());
     m.def("gemv_w4a16_into", &gemv_w4a16_into, "INT4 GEMV into a caller buffer");
     m.def("gemv_w4a16_residual_into", &gemv_w4a16_residual_into,
           "INT4 GEMV into a caller buffer that also writes res_out = res + y (binary16)");

@@ -36,6 +36,7 @@
 // Other shapes use a simple one-wave-per-head kernel with the same math.
 #include "soi_device.h"
 #include "soi_host.h"
+#include "soi_int4_tile.h"
 
 namespace soi {
 
@@ -348,6 +349,7 @@ struct AttnArgs {
     uint32_t* counters;
     uint16_t* out;
     int rep, NQ, NKV, S, L_arg, nsplit;
+    int defer;  // 1: a split context leaves its states in the workspace (no arrival, no combine, out unwritten)
     float eps, scale_log2;
 };
 
@@ -592,6 +594,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         const float v = e == 0 ? M : wave_sum<REP, HD>(s_state, hh, e, w);
         stg(a.part + (static_cast<int64_t>(kvh * rep + hh) * a.nsplit + split) * (HD + 2) + e, v);
     }
+    if (a.defer) return;  // the consumer combines the states (gemv_attn_combine_kernel)
     // arrival: the last of the ns splits of this KV head combines its query heads
     arrive_release();
     if (tid == 0) {
@@ -769,6 +772,234 @@ static int check_attention(const uint16_t* q, const uint16_t* k_cache, const uin
     return SOI_OK;
 }
 
+
+// ---- o projection that finishes a deferred attention step ----
+// With AttnArgs::defer a split context leaves out unwritten and its per-split
+// states [m, l, acc] in the workspace; the INT4 GEMV that consumes the
+// attention output (the o projection) combines them while its weight rows
+// load. Workgroup = 8 waves, 1 row per wave; thread t owns x[4t .. 4t+3]
+// (K = NQ * hd <= 2048, one query head per thread): it requests the states of
+// its head (the first kOcBatch splits) before the tile's weight loads,
+// combines them with the arithmetic of combine_kv (M over all splits, then l
+// and acc summed in split order, x = fp16(acc / l)) into LDS, and every wave
+// reads its x chunks from there. An unsplit context (ns = 1) wrote out
+// itself, and x is that vector. So y equals the plain GEMV of the attention
+// output bit for bit.
+constexpr int kOcWaves = 8;
+constexpr int kOcThreads = kOcWaves * kWave;
+constexpr int kOcRows = 1;  // 8 rows per workgroup: 256 workgroups (one per CU) for a 2048-row projection
+constexpr int kOcBatch = 16;
+constexpr int kOcMaxK = 4 * kOcThreads;
+
+struct OcArgs {
+    const float* part;         // [NQ, nsplit, hd + 2]
+    const uint16_t* attn_out;  // [K] (written by an unsplit step)
+    const int32_t* pos;
+    int HD, NKV, S, step, nsplit;
+};
+
+__device__ __forceinline__ int attn_splits(const OcArgs& a, int L) {
+    int tps, ns;
+    split_plan(L, a.NKV, a.step, tps, ns);
+    return ns;
+}
+
+// The split states of thread t's four x elements (ns > 1), combined into the LDS copy of x by finish().
+struct AttnCombineState {
+    int ns;   // splits of the current context
+    int i0;   // first x element of the thread (clamped to K - 4; live = 4t < K)
+    bool live;
+    f32x2 ml[kOcBatch];  // (m, l) of each split
+    f32x4 va[kOcBatch];  // acc[d0 .. d0+3] of each split
+
+    __device__ __forceinline__ const float* rec(const OcArgs& a, int s) const {
+        const int h = i0 / a.HD;
+        return a.part + (static_cast<int64_t>(h) * a.nsplit + (s < ns ? s : 0)) * (a.HD + 2);
+    }
+    // Unconditional loads (clamped addresses): a branch around them would make the wave wait at its end.
+    __device__ __forceinline__ void prefetch(const OcArgs& a, int K, int nsplits) {
+        ns = nsplits;
+        const int t4 = 4 * static_cast<int>(threadIdx.x);
+        live = t4 < K;
+        i0 = live ? t4 : K - 4;
+        const int d0 = i0 % a.HD;
+#pragma unroll
+        for (int s = 0; s < kOcBatch; ++s) {
+            const float* r = rec(a, s);
+            ml[s] = ldg(reinterpret_cast<const f32x2*>(r));
+            const f32x2 a01 = ldg(reinterpret_cast<const f32x2*>(r + 2 + d0));  // 8-byte aligned only
+            const f32x2 a23 = ldg(reinterpret_cast<const f32x2*>(r + 4 + d0));
+            va[s] = f32x4{a01.x, a01.y, a23.x, a23.y};
+        }
+    }
+    // x[i0 .. i0+3] into s_x, then a workgroup barrier.
+    __device__ __forceinline__ void finish(const OcArgs& a, uint16_t* s_x) const {
+        float M = kNegBig;  // max is exact: any order gives combine_kv's M
+#pragma unroll
+        for (int s = 0; s < kOcBatch; ++s)
+            if (s < ns) M = fmaxf(M, ml[s].x);
+        for (int s = kOcBatch; s < ns; ++s) M = fmaxf(M, ldg(rec(a, s)));
+        float lsum = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int d0 = i0 % a.HD;
+#pragma unroll
+        for (int s = 0; s < kOcBatch; ++s) {
+            if (s < ns) {
+                const float w = fast_exp2(ml[s].x - M);
+                lsum = fmaf(ml[s].y, w, lsum);
+                acc[0] = fmaf(va[s].x, w, acc[0]);
+                acc[1] = fmaf(va[s].y, w, acc[1]);
+                acc[2] = fmaf(va[s].z, w, acc[2]);
+                acc[3] = fmaf(va[s].w, w, acc[3]);
+            }
+        }
+        for (int s = kOcBatch; s < ns; ++s) {  // long contexts with few KV heads: further splits
+            const float* r = rec(a, s);
+            const float w = fast_exp2(ldg(r) - M);
+            lsum = fmaf(ldg(r + 1), w, lsum);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = fmaf(ldg(r + 2 + d0 + j), w, acc[j]);
+        }
+        u32x2 xo;
+        xo.x = static_cast<uint32_t>(f32_to_f16_bits(acc[0] / lsum)) |
+               (static_cast<uint32_t>(f32_to_f16_bits(acc[1] / lsum)) << 16);
+        xo.y = static_cast<uint32_t>(f32_to_f16_bits(acc[2] / lsum)) |
+               (static_cast<uint32_t>(f32_to_f16_bits(acc[3] / lsum)) << 16);
+        if (live) *reinterpret_cast<u32x2*>(s_x + i0) = xo;
+        __syncthreads();
+    }
+};
+
+// x chunk c (32 elements) from the LDS copy of x (zeros for a chunk past K).
+template <bool FULL>
+__device__ __forceinline__ void lds_x_chunk(const uint16_t* s_x, int c, bool cv, f16x2 xv[16]) {
+    const bool ok = FULL || cv;
+    const u32x4* p = reinterpret_cast<const u32x4*>(s_x + 32 * (ok ? c : 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32x4 t = p[i];
+        if (!ok) t = u32x4{0u, 0u, 0u, 0u};
+        xv[4 * i + 0] = as_f16x2(t.x);
+        xv[4 * i + 1] = as_f16x2(t.y);
+        xv[4 * i + 2] = as_f16x2(t.z);
+        xv[4 * i + 3] = as_f16x2(t.w);
+    }
+}
+
+// General form (several passes, or K < 2048): x is final in LDS before the tile starts.
+struct AttnLdsX {
+    static constexpr bool kSinglePass = false;
+    const uint16_t* s_x;
+    const uint16_t* b;
+    __device__ __forceinline__ const uint16_t* base() const { return b; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int, int c, bool cv, f16x2 xv[16]) const {
+        lds_x_chunk<FULL>(s_x, c, cv, xv);
+    }
+};
+
+// One-pass form (K == 2048, lane l's chunk is x[32l .. 32l+31]): the position and the lane's chunk of the
+// step's out are requested before the tile's weight loads; load() runs after them: an unsplit context takes
+// the chunk as x, a split one requests its states then (held by value: they stay in registers), combines
+// them into LDS and reads the chunk from there.
+struct AttnOnePassX {
+    static constexpr bool kSinglePass = true;
+    OcArgs oa;
+    uint16_t* s_x;
+    int p;        // pos[0]
+    u32x4 xc[4];  // x[32l .. 32l+31] of out
+    __device__ __forceinline__ const uint16_t* base() const { return oa.attn_out; }
+    template <bool VEC, bool FULL>
+    __device__ __forceinline__ void load(int K, int c, bool cv, f16x2 xv[16]) const {
+        const int L = p < 0 ? 1 : (p >= oa.S ? oa.S : p + 1);  // cur_len_of
+        const int ns = attn_splits(oa, L);
+        if (ns == 1) {  // uniform over the grid
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[4 * i + 0] = as_f16x2(xc[i].x);
+                xv[4 * i + 1] = as_f16x2(xc[i].y);
+                xv[4 * i + 2] = as_f16x2(xc[i].z);
+                xv[4 * i + 3] = as_f16x2(xc[i].w);
+            }
+            return;
+        }
+        AttnCombineState st;
+        st.prefetch(oa, K, ns);
+        st.finish(oa, s_x);
+        lds_x_chunk<FULL>(s_x, c, cv, xv);
+    }
+};
+
+template <bool ONEPASS, bool CS, bool FULL, class EP>
+__global__ __launch_bounds__(kOcThreads) void gemv_attn_combine_kernel(DenseRows rows, int64_t N, OcArgs oa, EP ep,
+                                                                       int K, int gs) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[kOcMaxK];
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kOcWaves + (threadIdx.x >> 6)) * kOcRows;
+    if constexpr (ONEPASS) {
+        AttnOnePassX xs;
+        xs.oa = oa;
+        xs.s_x = s_x;
+        xs.p = ldg(oa.pos);
+        const u32x4* o4 = reinterpret_cast<const u32x4*>(oa.attn_out) + 4 * (threadIdx.x & (kWave - 1));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xs.xc[i] = ldg(o4 + i);
+        gemv_int4_tile<kOcRows, 1, true, CS, true, FULL>(rows, N, xs, ep, K, gs, row0);
+    } else {
+        const int ns = attn_splits(oa, cur_len_of(0, oa.pos, oa.S));
+        if (ns == 1) {  // the step wrote out itself (uniform over the grid): the plain GEMV of it
+            gemv_int4_tile<kOcRows, 1, true, CS, true, FULL>(rows, N, PlainX{oa.attn_out}, ep, K, gs, row0);
+            return;
+        }
+        AttnCombineState st;
+        st.prefetch(oa, K, ns);
+        st.finish(oa, s_x);
+        gemv_int4_tile<kOcRows, 1, true, CS, true, FULL>(rows, N, AttnLdsX{s_x, oa.attn_out}, ep, K, gs, row0);
+    }
+}
+
+template <class EP>
+static int launch_attn_combine(const uint8_t* Wq, const float* scale, const void* workspace, size_t workspace_bytes,
+                               const uint16_t* attn_out, const int32_t* pos, int64_t NQ, int64_t NKV,
+                               int64_t head_dim, int64_t max_seq, const EP& ep, int64_t N, int64_t group_size,
+                               int64_t num_groups, void* stream, const char* what) {
+    SOI_REQUIRE(NQ >= 1 && NKV >= 1 && NQ % NKV == 0, "%s: num_q_heads must be a positive multiple of num_kv_heads",
+                what);
+    SOI_REQUIRE(max_seq >= 1 && max_seq <= (int64_t(1) << 30), "%s: max_seq_len out of range", what);
+    const AttnPlan p = plan_attention(NQ, NKV, head_dim, max_seq);
+    SOI_REQUIRE(p.fast, "%s: head_dim %lld / GQA ratio %lld not supported by the deferred attention step", what,
+                (long long)head_dim, (long long)(NQ / NKV));
+    const int64_t K = NQ * head_dim;
+    SOI_REQUIRE(K % 32 == 0 && K <= kOcMaxK, "%s: num_q_heads * head_dim must be a multiple of 32 and at most %d",
+                what, kOcMaxK);
+    SOI_REQUIRE(group_size >= 8 && group_size % 8 == 0, "%s: group_size must be a positive multiple of 8", what);
+    SOI_REQUIRE(num_groups == ceil_div64(K, group_size), "%s: num_groups must be ceil(K / group_size)", what);
+    SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: N out of range", what);
+    SOI_REQUIRE(Wq && scale && workspace && attn_out && pos, "%s: null pointer", what);
+    SOI_REQUIRE(aligned16(Wq) && aligned16(attn_out) && aligned16(workspace),
+                "%s: Wq, attn_out and workspace must be 16-byte aligned", what);
+    const size_t need = attn_partial_bytes(NQ, head_dim, p);
+    if (workspace_bytes < need) {
+        set_last_error("%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+        return SOI_ERR_WORKSPACE;
+    }
+    if (N == 0) return SOI_OK;
+    OcArgs oa{static_cast<const float*>(workspace), attn_out, pos, static_cast<int>(head_dim),
+              static_cast<int>(NKV), static_cast<int>(max_seq), p.step, p.cap};
+    const DenseRows rows{Wq, scale, (K / 8) * 4, num_groups};
+    const dim3 grid(static_cast<unsigned>(ceil_div64(N, kOcWaves * kOcRows)));
+    hipStream_t st = as_stream(stream);
+    const bool one = K == 32 * kWave, cs = group_size % 32 == 0;  // one 64-chunk pass
+    const bool full = N % (kOcWaves * kOcRows) == 0 && K % (32 * kWave) == 0;
+    const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size);
+#define SOI_OC(O, C, F) \
+    hipLaunchKernelGGL((gemv_attn_combine_kernel<O, C, F, EP>), grid, dim3(kOcThreads), 0, st, rows, N, oa, ep, Ki, gi)
+    if (one && cs && full) SOI_OC(true, true, true);
+    else if (cs && full) SOI_OC(false, true, true);
+    else if (cs) SOI_OC(false, true, false);
+    else SOI_OC(false, false, false);
+#undef SOI_OC
+    return launch_status(what);
+}
+
 }  // namespace soi
 
 using namespace soi;
@@ -809,12 +1040,11 @@ extern "C" size_t soi_decode_attention_step_workspace_bytes(int64_t NQ, int64_t 
     return soi_decode_attention_workspace_bytes(NQ, NKV, head_dim, max_seq);
 }
 
-extern "C" int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
-                                         const float* cos_table, const float* sin_table, const int32_t* pos,
-                                         uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, int64_t NQ,
-                                         int64_t NKV, int64_t max_seq, int64_t head_dim, float eps, float scale,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
-    const char* what = "soi_decode_attention_step";
+static int attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                          const float* cos_table, const float* sin_table, const int32_t* pos, uint16_t* k_cache,
+                          uint16_t* v_cache, uint16_t* out, int64_t NQ, int64_t NKV, int64_t max_seq,
+                          int64_t head_dim, float eps, float scale, void* workspace, size_t workspace_bytes,
+                          void* stream, bool defer, const char* what) {
     int st = check_attention(qkv, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, what);
     if (st) return st;
     SOI_REQUIRE(q_norm && k_norm && cos_table && sin_table && pos, "%s: null pointer", what);
@@ -847,8 +1077,44 @@ extern "C" int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_
     a.NKV = static_cast<int>(NKV);
     a.S = static_cast<int>(max_seq);
     a.nsplit = p.cap;
+    a.defer = defer ? 1 : 0;
     a.eps = eps;
     a.scale_log2 = scale * kLog2e;
     launch_attn_kernel(p, true, dim3(static_cast<unsigned>(NKV), static_cast<unsigned>(p.cap)), as_stream(stream), a);
     return launch_status(what);
+}
+
+extern "C" int soi_decode_attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                                         const float* cos_table, const float* sin_table, const int32_t* pos,
+                                         uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, int64_t NQ,
+                                         int64_t NKV, int64_t max_seq, int64_t head_dim, float eps, float scale,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    return attention_step(qkv, q_norm, k_norm, cos_table, sin_table, pos, k_cache, v_cache, out, NQ, NKV, max_seq,
+                          head_dim, eps, scale, workspace, workspace_bytes, stream, false, "soi_decode_attention_step");
+}
+
+extern "C" int soi_decode_attention_step_deferred(const uint16_t* qkv, const uint16_t* q_norm,
+                                                  const uint16_t* k_norm, const float* cos_table,
+                                                  const float* sin_table, const int32_t* pos, uint16_t* k_cache,
+                                                  uint16_t* v_cache, uint16_t* out, int64_t NQ, int64_t NKV,
+                                                  int64_t max_seq, int64_t head_dim, float eps, float scale,
+                                                  void* workspace, size_t workspace_bytes, void* stream) {
+    return attention_step(qkv, q_norm, k_norm, cos_table, sin_table, pos, k_cache, v_cache, out, NQ, NKV, max_seq,
+                          head_dim, eps, scale, workspace, workspace_bytes, stream, true,
+                          "soi_decode_attention_step_deferred");
+}
+
+extern "C" int soi_gemv_w4a16_attn_combine(const uint8_t* Wq, const float* scale, const void* workspace,
+                                           size_t workspace_bytes, const uint16_t* attn_out, const int32_t* pos,
+                                           int64_t NQ, int64_t NKV, int64_t head_dim, int64_t max_seq, uint16_t* y,
+                                           const uint16_t* res, uint16_t* res_out, int64_t N, int64_t group_size,
+                                           int64_t num_groups, void* stream) {
+    const char* what = "soi_gemv_w4a16_attn_combine";
+    SOI_REQUIRE(y, "%s: null pointer", what);
+    SOI_REQUIRE(!res == !res_out, "%s: res and res_out go together", what);
+    if (res)
+        return launch_attn_combine(Wq, scale, workspace, workspace_bytes, attn_out, pos, NQ, NKV, head_dim, max_seq,
+                                   StoreYAdd{y, res, res_out}, N, group_size, num_groups, stream, what);
+    return launch_attn_combine(Wq, scale, workspace, workspace_bytes, attn_out, pos, NQ, NKV, head_dim, max_seq,
+                               StoreY{y}, N, group_size, num_groups, stream, what);
 }

@@ -43,7 +43,6 @@
 
 namespace soi {
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kDdWaves = 8;  // = output rows per workgroup (one per wave)
 constexpr int kDdThreads = kDdWaves * kWave;

@@ -201,7 +201,10 @@ class DecodeEngine:
     embedding and LM head stay in HBM. With fused layers and residual_epilogue=True (default) the projections
     that feed a residual add (o in every mode, down in the dense and dense-up schedules) write the updated
     residual stream themselves, one binary16 add as the next RMSNorm-fused GEMV would do on load (results bit
-    for bit those of residual_epilogue=False, which leaves the add to the consumer).
+    for bit those of residual_epilogue=False, which leaves the add to the consumer). With
+    defer_attention_combine=True (default, fused layers) a context long enough to split the attention across
+    workgroups leaves its split states to the o projection, which combines them while its weight rows load
+    (bit-identical to False, where the attention launch's last workgroup per KV head combines them).
 
     All buffers are allocated here; decode steps launch only this package's kernels on the current stream
     and are captured into HIP graphs by capture()."""
@@ -209,7 +212,8 @@ class DecodeEngine:
     def __init__(self, w: DecoderWeights, mode: str = "dense", dip_k: Optional[int] = None,
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
                  dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
-                 down_copy: bool = True, overlap_copy: bool = True, residual_epilogue: bool = True):
+                 down_copy: bool = True, overlap_copy: bool = True, residual_epilogue: bool = True,
+                 defer_attention_combine: bool = True):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         if offload and mode == "dip":
@@ -262,6 +266,11 @@ class DecodeEngine:
         # one-launch attention (its workspace ends in counters that must start at zero: buf() zero-fills)
         step_ws = _C.decode_attention_step_workspace_bytes(c.q_heads, c.kv_heads, hd, c.max_seq)
         self.step_ws = buf(step_ws, torch.uint8) if (fused and step_ws > 0) else None
+        # a context that splits across attention workgroups: the o projection combines the split states on load
+        # (soi_gemv_w4a16_attn_combine) instead of the attention launch's last workgroup per KV head
+        K_o = c.q_heads * hd
+        self.defer_combine = bool(defer_attention_combine) and self.step_ws is not None and K_o % 32 == 0 and \
+            K_o <= 2048
         self.counts = None  # optional per-layer channel selection counts (eager calibration only)
 
         if mode != "dense":
@@ -551,21 +560,28 @@ class DecodeEngine:
                 _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, self.down, L.in_norm, eps, other, None,
                                            self.qkv, H, gs, False)
                 cur, other = other, cur
+            attn = self.attn.view(c.q_heads, c.head_dim)
             if self.step_ws is not None:
-                _C.decode_attention_step(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos,
-                                         self.k_cache[l], self.v_cache[l], self.attn.view(c.q_heads, c.head_dim),
-                                         eps, self.step_ws)
+                step = _C.decode_attention_step_deferred if self.defer_combine else _C.decode_attention_step
+                step(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.k_cache[l],
+                     self.v_cache[l], attn, eps, self.step_ws)
             else:
                 _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
                                        self.k_cache[l], self.v_cache[l], eps)
                 _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
             K_o = c.q_heads * c.head_dim
-            if fold:
+            res = (cur, other) if fold else (None, None)
+            if self.defer_combine:
+                _C.gemv_w4a16_attn_combine_into(L.o_Wq, L.o_scale, self.step_ws, attn, self.pos, c.kv_heads,
+                                                c.max_seq, self.o, gs, *res)
+            elif fold:
                 _C.gemv_w4a16_residual_into(L.o_Wq, L.o_scale, self.attn, self.o, cur, other, K_o, gs)
+            else:
+                _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, K_o, gs)
+            if fold:
                 cur, other = other, cur
                 self._mlp_fused(l, L, gu_il, cur, None, None, other if down_res and l < last else None)
             else:
-                _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, K_o, gs)
                 self._mlp_fused(l, L, gu_il, cur, self.o, other, None)
             self._layer_done(l)
             if not fold or (down_res and l < last):
@@ -600,156 +616,6 @@ class DecodeEngine:
         assert res_out is None
         gW, gS = L.gate(I)
         _C.gemv_w4a16_rmsnorm_into(gW, gS, x, delta, L.post_norm, eps, x_out, self.h, gate, H, gs, False)
-        _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
-        self._count_selection(l)
-        if self.mode == "dip":
-            uW, uS = L.up(I)
-            _C.gemv_w4a16_indexed_into(uW, uS, self.idx, self.h, self.u_sel, H, gs)
-            _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
-            _C.gemv_w4a16_indexed_accumulate_into(L.down_T_Wq, L.down_T_scale, self.idx, self.h_sel, self.down, H,
-                                                  gs, self.sd_ws)
-            return
-        cache = self.caches[l]
-        _, uS = L.up(I)
-        if self.miss_path == "direct":
-            _C.gemv_dip_cached_up_into(cache.up_Wq, cache.up_scale, self.host_up[l], uS, cache.slot_of, self.idx,
-                                       self.h, self.u_sel, H, gs)
-            _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
-            _C.gemv_dip_cached_down_into(cache.down_Wq, cache.down_scale, self.host_down[l], L.down_T_scale,
-                                         cache.slot_of, self.idx, self.h_sel, self.down, H, gs, self.sd_ws)
-            return
-        self._fetch_misses(l, L, uS)
-        _C.gemv_dip_fused_up_into(cache.up_Wq, cache.up_scale, self.st_up, self.st_up_s, self.desc, self.h,
-                                  self.u_sel, H, gs)
-        _C.silu_mul_indexed_into(gate, self.idx, self.u_sel, self.h_sel)
-        _C.gemv_dip_fused_down_into(cache.down_Wq, cache.down_scale, self.st_dn, self.st_dn_s, self.desc,
-                                    self.h_sel, self.down, H, gs, self.sd_ws)
-
-    def _dense_down(self, l: int, gate: torch.Tensor, h: torch.Tensor, res: Optional[torch.Tensor] = None,
-                    res_out: Optional[torch.Tensor] = None):
-        """Selection + down of the dense-up schedule (h: fp16(silu(gate) * up) of every channel); the index list
-        is written only for the eager consumers that read it (calibration counts, the layer hook). With res_out
-        the launch also writes res + down there."""
-        Wt, St = self.down_tt[l]
-        want = self.counts is not None or self.layer_hook is not None
-        _C.dip_select_dense_down_into(gate, h, self.k, Wt, St, self.idx if want else None,
-                                      self.cnt if want else None, self.down, self.c.group_size,
-                                      res if res_out is not None else None, res_out)
-        self._count_selection(l)
-
-    def _count_selection(self, l: int):
-        """Calibration: add this layer's selected channels to its frequency counts."""
-        if self.counts is not None:
-            self.counts[l].index_add_(0, self.idx.long(), torch.ones(self.k, dtype=self.counts[l].dtype,
-                                                                     device=self.device))
-
-    def _fetch_misses(self, l: int, L: LayerWeights, uS: torch.Tensor):
-        """Descriptors for this layer's selection, then the miss rows into staging: packed rows from pinned
-        host memory (device gather through the host mapping), scale rows from HBM."""
-        I = self.c.intermediate
-        cache = self.caches[l]
-        _C.build_dip_descriptors_into(self.idx, cache.slot_of, self.desc, self.miss_ch, self.miss_cnt)
-        _C.gather_rows_device_counted(self.host_up_ptr[l], I, self.st_up.shape[1], self.miss_ch, self.miss_cnt,
-                                      self.st_up)
-        _C.gather_rows_device_counted(self.host_down_ptr[l], I, self.st_dn.shape[1], self.miss_ch, self.miss_cnt,
-                                      self.st_dn)
-        _C.gather_rows_device_counted(uS.data_ptr(), I, uS.shape[1] * 4, self.miss_ch, self.miss_cnt,
-                                      self.st_up_s.view(torch.uint8))
-        _C.gather_rows_device_counted(L.down_T_scale.data_ptr(), I, L.down_T_scale.shape[1] * 4, self.miss_ch,
-                                      self.miss_cnt, self.st_dn_s.view(torch.uint8))
-
-    def _layers(self):
-        """Embedding of the device token, all layers at the device position, final norm; pos += 1."""
-        if self.fused:
-            self._layers_fused()
-            return
-        c, eps = self.c, self.c.rms_eps
-        H, gs = c.hidden, c.group_size
-        _C.embed_lookup_into(self.w.embed, self.token, self.x)
-        for l, L in enumerate(self.w.layers):
-            L, _ = self._layer(l, L)
-            if l == 0:
-                _C.rmsnorm_into(self.x, L.in_norm, self.h, eps)
-            else:
-                _C.residual_rmsnorm_(self.x, self.down, L.in_norm, self.h, eps)
-            _C.gemv_w4a16_into(L.qkv_Wq, L.qkv_scale, self.h, self.qkv, H, gs)
-            _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
-                                   self.k_cache[l], self.v_cache[l], eps)
-            _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
-            _C.gemv_w4a16_into(L.o_Wq, L.o_scale, self.attn, self.o, c.q_heads * c.head_dim, gs)
-            _C.residual_rmsnorm_(self.x, self.o, L.post_norm, self.h, eps)
-            self._mlp(l, L)
-            self._layer_done(l)
-            if self.layer_hook is not None:
-                self.layer_hook(l)
-        _C.residual_rmsnorm_(self.x, self.down, self.w.final_norm, self.hn, eps)
-        self._x_final = self.x
-        _C.advance_position(self.pos, 1)
-
-    def _layers_fused(self):
-        """Same computation with the residual adds moved into the producers' epilogues (the o projection, and
-        the down projection of the dense and dense-up schedules, also write residual + output into the other
-        of two residual buffers, one binary16 add as the RMSNorm-on-load would do), the RMSNorm done inside
-        the following GEMV, and the SiLU gating in the up / gate|up GEMV epilogue."""
-        c, eps = self.c, self.c.rms_eps
-        H, gs = c.hidden, c.group_size
-        cur, other = self.x, self.x2
-        down_res = self.mode == "dense" or self.dip_dense_up  # the down launch writes the next residual too
-        last = len(self.w.layers) - 1
-        _C.embed_lookup_into(self.w.embed, self.token, cur)
-        for l, L in enumerate(self.w.layers):
-            L, gu_il = self._layer(l, L)
-            if l == 0 or down_res:
-                _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, None, L.in_norm, eps, None, None, self.qkv,
-                                           H, gs, False)
-            else:
-                _C.gemv_w4a16_rmsnorm_into(L.qkv_Wq, L.qkv_scale, cur, self.down, L.in_norm, eps, other, None,
-                                           self.qkv, H, gs, False)
-                cur, other = other, cur
-            if self.step_ws is not None:
-                _C.decode_attention_step(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos,
-                                         self.k_cache[l], self.v_cache[l], self.attn.view(c.q_heads, c.head_dim),
-                                         eps, self.step_ws)
-            else:
-                _C.qk_norm_rope_append(self.qkv, L.q_norm, L.k_norm, self.cos_t, self.sin_t, self.pos, self.q,
-                                       self.k_cache[l], self.v_cache[l], eps)
-                _C.decode_attention_at(self.q, self.k_cache[l], self.v_cache[l], self.pos, self.attn, self.attn_ws)
-            _C.gemv_w4a16_residual_into(L.o_Wq, L.o_scale, self.attn, self.o, cur, other, c.q_heads * c.head_dim,
-                                        gs)
-            cur, other = other, cur
-            res_out = other if down_res and l < last else None
-            self._mlp_fused(l, L, gu_il, cur, res_out)
-            self._layer_done(l)
-            if res_out is not None:
-                cur, other = other, cur
-            if self.layer_hook is not None:
-                self.layer_hook(l)
-        _C.final_norm_advance(cur, self.down, self.w.final_norm, self.hn, eps, self.pos)
-        self._x_final = cur
-
-    def _mlp_fused(self, l: int, L: LayerWeights, gu_il, x: torch.Tensor, res_out: Optional[torch.Tensor]):
-        """Layer l's MLP on the residual x (RMSNorm on load); the output lands in self.down. With res_out
-        (dense and dense-up schedules only) the down launch also writes x + down there."""
-        c, eps = self.c, self.c.rms_eps
-        H, I, gs = c.hidden, c.intermediate, c.group_size
-        if self.mode == "dense":
-            gW, gS = gu_il
-            _C.gemv_w4a16_rmsnorm_into(gW, gS, x, None, L.post_norm, eps, None, None, self.mlp_h, H, gs, True)
-            if res_out is not None:
-                _C.gemv_w4a16_residual_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, x, res_out, I, gs)
-            else:
-                _C.gemv_w4a16_into(L.down_Wq, L.down_scale, self.mlp_h, self.down, I, gs)
-            return
-        gate = self.gu[:I]
-        if self.dip_dense_up:
-            gW, gS = gu_il
-            _C.gemv_w4a16_rmsnorm_swiglu_gate_into(gW, gS, x, None, L.post_norm, eps, None, gate, self.gu[I:],
-                                                   H, gs)
-            self._dense_down(l, gate, self.gu[I:], x, res_out)
-            return
-        assert res_out is None
-        gW, gS = L.gate(I)
-        _C.gemv_w4a16_rmsnorm_into(gW, gS, x, None, L.post_norm, eps, None, self.h, gate, H, gs, False)
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         self._count_selection(l)
         uW, uS = L.up(I)
