@@ -668,6 +668,11 @@ def bench_kernels(dev, gen):
         t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_at(q, kc, vc, pos, out, ws_at),
                                   list(zip(KC, VC)))
         res[f"attention_L{L}"] = entry(nb, t["mean_us"], kernel="attn_kernel, device position (1 launch)")
+        t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_into(q, kc, vc, L, out, ws_at),
+                                  list(zip(KC, VC)))
+        res[f"attention_host_L{L}"] = entry(
+            nb, t["mean_us"], kernel="attn_kernel, host length (the reference operator's form): a split context "
+                                     "leaves its states to attn_combine_kernel (2 launches)")
         t = time_graph_per_launch(lambda kc, vc: _C.decode_attention_step(qkv, qn, qn, cos_t, sin_t, pos, kc, vc, out,
                                                                           1e-6, ws_step), list(zip(KC, VC)))
         res[f"attention_step_L{L}"] = entry(nb + 2 * (NQ + 2 * NKV) * HD, t["mean_us"],

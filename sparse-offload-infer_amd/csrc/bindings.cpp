@@ -794,6 +794,26 @@ int64_t decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, int64_t head_d
     return static_cast<int64_t>(soi_decode_attention_workspace_bytes(NQ, NKV, head_dim, cur_len));
 }
 
+void decode_attention_into(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, int64_t cur_len,
+                           torch::Tensor out, torch::Tensor workspace_buf) {
+    const char* n = "decode_attention_into";
+    need(q, torch::kFloat16, q, n, "q");
+    need(k_cache, torch::kFloat16, q, n, "k_cache");
+    need(v_cache, torch::kFloat16, q, n, "v_cache");
+    need(out, torch::kFloat16, q, n, "out");
+    need(workspace_buf, torch::kUInt8, q, n, "workspace");
+    TORCH_CHECK(q.dim() == 2 && k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes() &&
+                    q.size(1) == k_cache.size(2) && out.sizes() == q.sizes(),
+                n, ": q / out [num_q_heads, head_dim], caches [num_kv_heads, max_seq_len, head_dim]");
+    const int64_t NQ = q.size(0), NKV = k_cache.size(0), S = k_cache.size(1), hd = k_cache.size(2);
+    TORCH_CHECK(cur_len >= 1 && cur_len <= S, n, ": cur_len out of range for max_seq_len");
+    const at::DeviceGuard guard(q.device());
+    check_status(soi_decode_attention(h16(q), h16(k_cache), h16(v_cache), h16m(out), NQ, NKV, S, hd, cur_len,
+                                      1.0f / std::sqrt(static_cast<float>(hd)), workspace_buf.data_ptr<uint8_t>(),
+                                      workspace_buf.numel(), cur_stream(q)),
+                 n);
+}
+
 void decode_attention_at(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor pos,
                          torch::Tensor out, torch::Tensor workspace_buf) {
     const char* n = "decode_attention_at";
@@ -1462,6 +1482,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "index-driven down accumulate over resident weights");
     m.def("gather_rows_device", &gather_rows_device, "device-resident row gather");
     m.def("decode_attention", &decode_attention, "batch-1 GQA decode attention");
+    m.def("decode_attention_into", &decode_attention_into,
+          "decode attention over a host length into a caller buffer, with a caller workspace");
     m.def("topk_threshold_select", &topk_threshold_select, "deterministic threshold top-k");
     m.def("gather_rows_staged", &gather_rows_staged, "pinned-host row gather, staged");
     m.def("gather_rows_naive", &gather_rows_naive, "pinned-host row gather, per row");

@@ -29,9 +29,12 @@
 //     (m, l, acc) rescaling;
 //   * short contexts (at most 8 passes: 256 timesteps at head_dim 128) run
 //     ONE workgroup per KV head, which writes the output itself; longer ones
-//     split the timesteps (about 128 workgroups), each split writes its state
+//     split the timesteps (64 or 128 workgroups), each split writes its state
 //     to the workspace and the last split of a KV head to arrive (a device
-//     counter) combines them in split order. Fixed order throughout:
+//     counter) combines them in split order; or (host length, and the
+//     deferred step whose states the o projection combines) the splits only
+//     write their states and a later launch combines them with the same
+//     arithmetic. Fixed order throughout:
 //     deterministic, and all forms give identical bytes for the same length.
 // Other shapes use a simple one-wave-per-head kernel with the same math.
 #include "soi_device.h"
@@ -609,6 +612,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep, rep, a.nsplit, ns, s_cm, s_cl);
 }
 
+// Second launch of the standalone forms: workgroup kvh combines the split states of its query heads with
+// combine_kv (the arithmetic of the in-launch combine), after an attn_kernel launch with defer set. An unsplit
+// context wrote out itself. Across the launch boundary the states need no device fence or arrival counter.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
+                                                                    uint16_t* __restrict__ out,
+                                                                    const int32_t* __restrict__ pos, int L_arg, int S,
+                                                                    int NKV, int rep, int step, int nsplit) {
+    __shared__ float s_cm[8 * kCombineMaxSplits], s_cl[8 * kCombineMaxSplits];
+    int tps, ns;
+    split_plan(cur_len_of(L_arg, pos, S), NKV, step, tps, ns);
+    if (ns == 1) return;  // uniform
+    combine_kv<kAttnThreads, HD>(part, out, static_cast<int>(blockIdx.x) * rep, rep, nsplit, ns, s_cm, s_cl);
+}
+
 // General shapes: one wave per query head, lanes over dims, online softmax.
 __global__ __launch_bounds__(64) void attn_simple_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
@@ -757,7 +775,26 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
     a.L_arg = static_cast<int>(cur_len);
     a.nsplit = nsplit;
     a.scale_log2 = scale_log2;
+    // a host length that splits: the splits leave their states and a second launch combines them (cheaper at
+    // long contexts than the device-scope release, arrival counter and acquire of the in-launch combine: 9.2
+    // against 10.3 us at L = 2048). A device position keeps the in-launch combine: its grid can split at any
+    // length, and a second launch would cost ~1.4 us at the unsplit lengths too.
+    a.defer = (!pos && nsplit > 1) ? 1 : 0;
     launch_attn_kernel(p, false, dim3(static_cast<unsigned>(NKV), static_cast<unsigned>(nsplit)), st, a);
+    if (a.defer) {
+#define SOI_AC(LL)                                                                                             \
+    hipLaunchKernelGGL(attn_combine_kernel<LL * 8>, dim3(static_cast<unsigned>(NKV)), dim3(kAttnThreads), 0, st, \
+                       a.part, out, pos, a.L_arg, a.S, a.NKV, rep, p.step, nsplit)
+        switch (p.lpr) {
+            case 1: SOI_AC(1); break;
+            case 2: SOI_AC(2); break;
+            case 4: SOI_AC(4); break;
+            case 8: SOI_AC(8); break;
+            case 16: SOI_AC(16); break;
+            default: SOI_AC(32); break;
+        }
+#undef SOI_AC
+    }
     return launch_status(what);
 }
 

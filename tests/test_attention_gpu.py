@@ -46,6 +46,22 @@ def test_other_shapes_match_oracle(ops, NQ, NKV, hd, S, L):
     assert_close(out, ref, f"attention {NQ}/{NKV}/{hd} L={L}")
 
 
+def test_caller_buffers_form_equals_allocating_form(ops):
+    """decode_attention_into (caller out and workspace, reused across calls) == decode_attention, bit for bit, on
+    both sides of the split boundary (a split host length combines in a second launch) and for one KV head."""
+    from soinfer import _C
+
+    for NQ, NKV, hd, S in ((16, 8, 128, 2048), (8, 1, 128, 4096)):
+        q, k, v = _qkv(NQ, NKV, hd, S, seed=S + NKV)
+        q, k, v = q.cuda(), k.cuda(), v.cuda()
+        ws = torch.full((_C.decode_attention_workspace_bytes(NQ, NKV, hd, S),), 255, dtype=torch.uint8,
+                        device="cuda")
+        out = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+        for L in (1, 256, 257, 1000, S // 2 + 1, S):
+            _C.decode_attention_into(q, k, v, L, out, ws)
+            assert torch.equal(out, ops.decode_attention(q, k, v, L)), f"NQ={NQ} NKV={NKV} L={L}"
+
+
 def test_large_scores_stable(ops):
     q, k, v = _qkv(16, 8, 128, 256, seed=3)
     q = (q.float() * 8).half()
