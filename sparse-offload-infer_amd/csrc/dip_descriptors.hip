@@ -53,9 +53,38 @@ __global__ __launch_bounds__(kDescThreads) void build_dip_descriptors_kernel(
     if (tid == 0) *miss_count = static_cast<int32_t>(running);
 }
 
-// dst[j,:] = src[idx[j],:]; 16-byte vector copies when rows allow it. With
+// dst[j,:] = src[idx[j],:] (a zero row for an index out of range). With
 // `count` (device), only rows j < count[0] are copied (the grid covers the
 // maximum). src may be device memory or a device mapping of pinned host memory.
+// Host-row form (rows a multiple of 16 bytes, 16-byte aligned, in pinned host
+// memory): workgroup b copies rows 4b .. 4b+3 with 16 lanes per row, each lane
+// 64 contiguous bytes of every KB; PCIe reads run at ~54 GB/s this way against
+// ~48 GB/s with 16 bytes per lane (1 KB rows, measured).
+__global__ __launch_bounds__(64) void gather_rows_vec_kernel(const uint8_t* __restrict__ src, int64_t num_rows,
+                                                             int64_t row_nbytes, const int32_t* __restrict__ idx,
+                                                             const int32_t* __restrict__ count, int64_t k,
+                                                             uint8_t* __restrict__ dst) {
+    const int lane = threadIdx.x, sub = lane & 15;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + (lane >> 4);
+    if (j >= k || (count && j >= ldg(count))) return;  // no barrier below
+    const int32_t r = ldg(idx + j);
+    const bool ok = r >= 0 && r < num_rows;
+    const int64_t n16 = row_nbytes / 16;
+    const u32x4* s = reinterpret_cast<const u32x4*>(src + (ok ? static_cast<int64_t>(r) : 0) * row_nbytes);
+    const u32x4* z = reinterpret_cast<const u32x4*>(g_zero16);
+    u32x4* d = reinterpret_cast<u32x4*>(dst + j * row_nbytes);
+    for (int64_t base = 4 * sub; base < n16; base += 64) {
+        u32x4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ldg((ok && base + i < n16) ? s + base + i : z);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (base + i < n16) stg(d + base + i, v[i]);
+    }
+}
+
+// One workgroup per row: 16-byte vectors (VEC) or bytes. For rows in device
+// memory this is the faster form (3.1 against 3.7 us for 3072 1 KB rows).
 template <bool VEC>
 __global__ __launch_bounds__(256) void gather_rows_device_kernel(const uint8_t* __restrict__ src, int64_t num_rows,
                                                                   int64_t row_nbytes, const int32_t* __restrict__ idx,
@@ -103,7 +132,14 @@ static int launch_gather(const uint8_t* src, int64_t num_rows, int64_t row_nbyte
     SOI_REQUIRE(src && indices && dst, "%s: null pointer", what);
     const bool vec = (row_nbytes % 16 == 0) && aligned16(src) && aligned16(dst);
     hipStream_t st = as_stream(stream);
-    if (vec)
+    // rows in host memory (a device mapping of pinned memory): the wide per-lane form
+    hipPointerAttribute_t attr{};
+    const bool host = hipPointerGetAttributes(&attr, src) == hipSuccess && attr.type == hipMemoryTypeHost;
+    (void)hipGetLastError();  // an unregistered pointer is not an error here
+    if (vec && host)
+        hipLaunchKernelGGL(gather_rows_vec_kernel, dim3(static_cast<unsigned>(ceil_div64(k, 4))), dim3(64), 0, st, src,
+                           num_rows, row_nbytes, indices, count, k, dst);
+    else if (vec)
         hipLaunchKernelGGL(gather_rows_device_kernel<true>, dim3(static_cast<unsigned>(k)), dim3(256), 0, st, src,
                            num_rows, row_nbytes, indices, count, dst);
     else

@@ -316,6 +316,27 @@ def test_counted_gather_from_pinned_host(C):
         C.host_device_pointer(torch.zeros(16, dtype=torch.uint8))  # not pinned
 
 
+@pytest.mark.parametrize("row", [16, 48, 1024, 1040, 2560, 4096])
+def test_counted_gather_from_pinned_host_row_sizes(C, row):
+    """The host-row gather form (16 lanes per row, 64 bytes per lane per KB): every row size that is a multiple of
+    16 bytes, partial last KB included; a row count not a multiple of 4 (the rows per workgroup); out-of-range
+    indices give zero rows; rows at or past the device count stay unwritten."""
+    n, k = 97, 11
+    host = torch.randint(0, 256, (n, row), dtype=torch.uint8, generator=torch.Generator().manual_seed(row))
+    host = host.pin_memory()
+    ptr = C.host_device_pointer(host)
+    idx_l = [96, 0, 5, 5, -1, 97, 50, 1, 2, 3, 4]
+    idx = torch.tensor(idx_l, dtype=torch.int32, device="cuda")
+    dst = torch.full((k, row), 0xAB, dtype=torch.uint8, device="cuda")
+    C.gather_rows_device_counted(ptr, n, row, idx, torch.tensor([9], dtype=torch.int32, device="cuda"), dst)
+    torch.cuda.synchronize()
+    got = dst.cpu()
+    for j, r in enumerate(idx_l[:9]):
+        want = host[r] if 0 <= r < n else torch.zeros(row, dtype=torch.uint8)
+        assert torch.equal(got[j], want), f"row {j} (index {r})"
+    assert (got[9:] == 0xAB).all(), "rows at or past count are not written"
+
+
 # ---------------------------------------------------------------------------
 # fused decode-step GEMVs: each equals the separate ops on the same values
 # ---------------------------------------------------------------------------
