@@ -134,8 +134,9 @@ static int launch_gather(const uint8_t* src, int64_t num_rows, int64_t row_nbyte
     hipStream_t st = as_stream(stream);
     // rows in host memory (a device mapping of pinned memory): the wide per-lane form
     hipPointerAttribute_t attr{};
-    const bool host = hipPointerGetAttributes(&attr, src) == hipSuccess && attr.type == hipMemoryTypeHost;
-    (void)hipGetLastError();  // an unregistered pointer is not an error here
+    const hipError_t qe = hipPointerGetAttributes(&attr, src);
+    if (qe != hipSuccess) (void)hipGetLastError();  // an unregistered pointer is not an error here
+    const bool host = qe == hipSuccess && attr.type == hipMemoryTypeHost;
     if (vec && host)
         hipLaunchKernelGGL(gather_rows_vec_kernel, dim3(static_cast<unsigned>(ceil_div64(k, 4))), dim3(64), 0, st, src,
                            num_rows, row_nbytes, indices, count, k, dst);
