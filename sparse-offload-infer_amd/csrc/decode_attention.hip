@@ -352,7 +352,8 @@ struct AttnArgs {
     uint32_t* counters;
     uint16_t* out;
     int rep, NQ, NKV, S, L_arg, nsplit;
-    int defer;  // 1: a split context leaves its states in the workspace (no arrival, no combine, out unwritten)
+    int defer;       // 1: a split context leaves its states in the workspace (no arrival, no combine, out unwritten)
+    int head_split;  // 1: workgroup x takes query head x / NKV of KV head x % NKV alone (grid NQ x splits)
     float eps, scale_log2;
 };
 
@@ -375,8 +376,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     __shared__ int s_last;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane / LPR, u = lane % LPR;
-    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int split = blockIdx.y;
     const int rep = a.rep, S = a.S;
+    // the query heads of this workgroup: kvh * rep + hq0 + hh, hh < nhq. With head_split the rep workgroups of a
+    // KV head are NKV apart in x, so (NKV a multiple of 8) they run on one XCD and share the K/V rows in its L2
+    const int gx = blockIdx.x;
+    const int kvh = a.head_split ? gx % a.NKV : gx;
+    const int hq0 = a.head_split ? gx / a.NKV : 0;
+    const int nhq = a.head_split ? 1 : rep;
     int p = -1;
     int L;
     if (PRE) {
@@ -404,16 +411,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     // requested before the K/V rows (loads return in order), so its RMSNorm and RoPE run while the rows are in
     // flight.
     const int prow = pvalid ? p : (p < 0 ? 0 : S - 1);  // RoPE table row
-    const int nh = PRE ? rep + (has_new ? 1 : 0) : 0;
+    const int nh = PRE ? nhq + (has_new ? 1 : 0) : 0;
     auto head_src = [&](int hh) {
-        return a.q + static_cast<int64_t>(hh == rep ? a.NQ + kvh : kvh * rep + hh) * HD;
+        return a.q + static_cast<int64_t>(hh == nhq ? a.NQ + kvh : kvh * rep + hq0 + hh) * HD;
     };
     uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
     float f_c = 0.0f, f_sn = 0.0f;
     if (PRE && HALF == kWave && wave < nh) {  // wave-uniform
         const int fh = wave;
         const uint16_t* src = head_src(fh);
-        const uint16_t* wn = fh == rep ? a.k_norm : a.q_norm;
+        const uint16_t* wn = fh == nhq ? a.k_norm : a.q_norm;
         f_x1 = ldg(src + lane);
         f_x2 = ldg(src + lane + HALF);
         f_w1 = ldg(wn + lane);
@@ -433,7 +440,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     if (PRE) {
         // Lane l reduces elements l, l+64, ... in that order (the order of qk_norm_rope_append).
         for (int hh = wave; hh < nh; hh += kAttnWaves) {
-            const bool isk = hh == rep;
+            const bool isk = hh == nhq;
             const uint16_t* src = head_src(hh);
             const uint16_t* wn = isk ? a.k_norm : a.q_norm;
             uint16_t* dst = isk ? s_kv[0] : s_q[hh];
@@ -482,7 +489,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
             for (int i = tid; i < HD; i += kAttnThreads) s_kv[1][i] = ldg(vsrc + i);
         }
         __syncthreads();
-        if (has_new) {  // append k, v at p
+        if (has_new && hq0 == 0) {  // append k, v at p (one workgroup per KV head)
             uint16_t* kd = a.kc + (static_cast<int64_t>(kvh) * S + p) * HD;
             uint16_t* vd = a.vc + (static_cast<int64_t>(kvh) * S + p) * HD;
             for (int i = tid; i < HD; i += kAttnThreads) {
@@ -492,7 +499,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         }
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
-            const u32x4 t = reinterpret_cast<const u32x4*>(s_q[hh < rep ? hh : 0])[u];
+            const u32x4 t = reinterpret_cast<const u32x4*>(s_q[hh < nhq ? hh : 0])[u];
             qv[hh][0] = as_f16x2(t.x);
             qv[hh][1] = as_f16x2(t.y);
             qv[hh][2] = as_f16x2(t.z);
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     } else {
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
-            const int h = kvh * rep + (hh < rep ? hh : 0);
+            const int h = kvh * rep + hq0 + (hh < nhq ? hh : 0);
             const u32x4 t = ldg(reinterpret_cast<const u32x4*>(a.q + static_cast<int64_t>(h) * HD) + u);
             qv[hh][0] = as_f16x2(t.x);
             qv[hh][1] = as_f16x2(t.y);
@@ -580,36 +587,36 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     __syncthreads();
 
     if (ns == 1) {  // one workgroup holds the whole context: out = acc / l (the split combine with one state)
-        for (int i = tid; i < rep * HD; i += kAttnThreads) {
+        for (int i = tid; i < nhq * HD; i += kAttnThreads) {
             const int hh = i / HD, d = i % HD;
             float w[kAttnWaves];
             wave_weights<REP, HD>(s_state, hh, w);
             const float lsum = wave_sum<REP, HD>(s_state, hh, 1, w);
             const float acc = wave_sum<REP, HD>(s_state, hh, 2 + d, w);
-            stg(a.out + static_cast<int64_t>(kvh * rep + hh) * HD + d, f32_to_f16_bits(acc / lsum));
+            stg(a.out + static_cast<int64_t>(kvh * rep + hq0 + hh) * HD + d, f32_to_f16_bits(acc / lsum));
         }
         return;
     }
-    for (int i = tid; i < rep * (HD + 2); i += kAttnThreads) {  // the split's state: [M, l, acc] per query head
+    for (int i = tid; i < nhq * (HD + 2); i += kAttnThreads) {  // the split's state: [M, l, acc] per query head
         const int hh = i / (HD + 2), e = i % (HD + 2);
         float w[kAttnWaves];
         const float M = wave_weights<REP, HD>(s_state, hh, w);
         const float v = e == 0 ? M : wave_sum<REP, HD>(s_state, hh, e, w);
-        stg(a.part + (static_cast<int64_t>(kvh * rep + hh) * a.nsplit + split) * (HD + 2) + e, v);
+        stg(a.part + (static_cast<int64_t>(kvh * rep + hq0 + hh) * a.nsplit + split) * (HD + 2) + e, v);
     }
     if (a.defer) return;  // the consumer combines the states (gemv_attn_combine_kernel)
-    // arrival: the last of the ns splits of this KV head combines its query heads
+    // arrival: the last of the ns splits of this workgroup's heads combines them (one counter per x)
     arrive_release();
     if (tid == 0) {
-        const uint32_t prev = atomicAdd(a.counters + kvh, 1u);
+        const uint32_t prev = atomicAdd(a.counters + gx, 1u);
         const bool last = prev + 1 == static_cast<uint32_t>(ns);
-        if (last) atomicExch(a.counters + kvh, 0u);
+        if (last) atomicExch(a.counters + gx, 0u);
         s_last = last ? 1 : 0;
     }
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' states
-    combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep, rep, a.nsplit, ns, s_cm, s_cl);
+    combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep + hq0, nhq, a.nsplit, ns, s_cm, s_cl);
 }
 
 // Second launch of the standalone forms: workgroup kvh combines the split states of its query heads with
@@ -677,17 +684,20 @@ struct AttnPlan {
     bool fast;
     int lpr, rep_t, step, tps, nsplit;
     int cap;  // the most splits any length <= the planned one can need (device-position grids)
+    bool head_split;  // one query head per workgroup (grid x = NQ); else a KV head's query heads (x = NKV)
+    int gx;
 };
 
 // L: the context length to plan for; with a device position, the largest one (max_seq).
 static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
-    AttnPlan p{false, 0, 0, 0, 0, 0, 0};
+    AttnPlan p{false, 0, 0, 0, 0, 0, 0, false, 0};
     const int64_t rep = NQ / NKV;
     const int64_t lpr = hd / 8;
     const bool pow2 = lpr >= 1 && (lpr & (lpr - 1)) == 0;
     if (hd % 8 == 0 && pow2 && lpr <= 32 && rep <= 8) {
         p.fast = true;
         p.lpr = static_cast<int>(lpr);
+        p.gx = static_cast<int>(NKV);
         p.rep_t = rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
         p.step = static_cast<int>((kWave / lpr) * kAttnWaves);  // timesteps per workgroup pass
         split_plan(L, NKV, p.step, p.tps, p.nsplit);
@@ -699,15 +709,28 @@ static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
     return p;
 }
 
+// A workgroup per query head (grid x = NQ): the query heads of a KV head share its K/V rows through L2 instead
+// of one workgroup's registers, and each workgroup's passes do 1/rep of the score and sum work (the attention
+// step at L = 192: 5.5 -> 4.7 us). Used where the split combine is not in the launch (the deferred step, the
+// host-length form's second launch) or not needed; the in-launch combine keeps a workgroup per KV head, whose
+// arrival and combine cost twice as much with twice the workgroups (10.2 -> 12.0 us at L = 2048, measured).
+// Each query head's arithmetic does not depend on the layout, so both give the same bytes.
+static void use_head_split(AttnPlan& p, int64_t NQ, int64_t NKV) {
+    if (!p.fast || NQ == NKV) return;
+    p.head_split = true;
+    p.gx = static_cast<int>(NQ);
+    p.rep_t = 1;
+}
+
 // Workspace: the split states [NQ, cap, hd + 2] fp32 (256-byte aligned), then
-// the NKV arrival counters (zero before the first call; every call leaves
-// them zero).
+// one arrival counter per workgroup column, at most NQ (zero before the first
+// call; every call leaves them zero).
 static size_t attn_partial_bytes(int64_t NQ, int64_t hd, const AttnPlan& p) {
     const size_t b = static_cast<size_t>(NQ) * p.cap * (hd + 2) * sizeof(float);
     return (b + 255) & ~static_cast<size_t>(255);
 }
-static size_t attn_counter_bytes(int64_t NKV) {
-    return (static_cast<size_t>(NKV) * sizeof(uint32_t) + 255) & ~static_cast<size_t>(255);
+static size_t attn_counter_bytes(int64_t NQ) {
+    return (static_cast<size_t>(NQ) * sizeof(uint32_t) + 255) & ~static_cast<size_t>(255);
 }
 
 static int launch_attn_kernel(const AttnPlan& p, bool pre, dim3 grid, hipStream_t st, const AttnArgs& a) {
@@ -745,7 +768,8 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
     const float scale_log2 = scale * kLog2e;
     const int rep = static_cast<int>(NQ / NKV);
     // host length: plan for cur_len; device position: grid for every length up to max_seq, plan at run time
-    const AttnPlan p = plan_attention(NQ, NKV, head_dim, pos ? max_seq : cur_len);
+    AttnPlan p = plan_attention(NQ, NKV, head_dim, pos ? max_seq : cur_len);
+    if (!pos) use_head_split(p, NQ, NKV);  // the host length combines in a second launch
     const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
     if (!p.fast || !aligned) {
         hipLaunchKernelGGL(attn_simple_kernel, dim3(static_cast<unsigned>(NQ)), dim3(64), 0, st, q, k_cache, v_cache,
@@ -755,12 +779,13 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
     }
     const int nsplit = pos ? p.cap : p.nsplit;
     const size_t pb = attn_partial_bytes(NQ, head_dim, p);
-    const size_t need = pb + attn_counter_bytes(NKV);
+    const size_t need = pb + attn_counter_bytes(NQ);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) {
         set_last_error("%s: 16-byte aligned workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
         return SOI_ERR_WORKSPACE;
     }
     AttnArgs a{};
+    a.head_split = p.head_split ? 1 : 0;
     a.q = q;
     a.pos = pos;
     a.kc = const_cast<uint16_t*>(k_cache);  // read only in this form
@@ -780,7 +805,7 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
     // against 10.3 us at L = 2048). A device position keeps the in-launch combine: its grid can split at any
     // length, and a second launch would cost ~1.4 us at the unsplit lengths too.
     a.defer = (!pos && nsplit > 1) ? 1 : 0;
-    launch_attn_kernel(p, false, dim3(static_cast<unsigned>(NKV), static_cast<unsigned>(nsplit)), st, a);
+    launch_attn_kernel(p, false, dim3(static_cast<unsigned>(p.gx), static_cast<unsigned>(nsplit)), st, a);
     if (a.defer) {
 #define SOI_AC(LL)                                                                                             \
     hipLaunchKernelGGL(attn_combine_kernel<LL * 8>, dim3(static_cast<unsigned>(NKV)), dim3(kAttnThreads), 0, st, \
@@ -1045,7 +1070,7 @@ extern "C" size_t soi_decode_attention_workspace_bytes(int64_t NQ, int64_t NKV, 
     if (NQ <= 0 || NKV <= 0 || head_dim <= 0 || cur_len <= 0 || NQ % NKV) return 0;
     const AttnPlan p = plan_attention(NQ, NKV, head_dim, cur_len);  // covers the device form with max_seq = cur_len
     if (!p.fast) return 0;
-    return attn_partial_bytes(NQ, head_dim, p) + attn_counter_bytes(NKV);
+    return attn_partial_bytes(NQ, head_dim, p) + attn_counter_bytes(NQ);
 }
 
 extern "C" int soi_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -1085,19 +1110,21 @@ static int attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uin
     int st = check_attention(qkv, k_cache, v_cache, out, NQ, NKV, max_seq, head_dim, what);
     if (st) return st;
     SOI_REQUIRE(q_norm && k_norm && cos_table && sin_table && pos, "%s: null pointer", what);
-    const AttnPlan p = plan_attention(NQ, NKV, head_dim, max_seq);
+    AttnPlan p = plan_attention(NQ, NKV, head_dim, max_seq);
+    if (defer) use_head_split(p, NQ, NKV);  // the o projection combines the split states
     if (!p.fast || !aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache)) {
         set_last_error("%s: head_dim %lld / GQA ratio %lld / alignment not supported by the one-launch form", what,
                        (long long)head_dim, (long long)(NQ / NKV));
         return SOI_ERR_UNSUPPORTED;
     }
     const size_t pb = attn_partial_bytes(NQ, head_dim, p);
-    const size_t need = pb + attn_counter_bytes(NKV);
+    const size_t need = pb + attn_counter_bytes(NQ);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) {
         set_last_error("%s: 16-byte aligned workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
         return SOI_ERR_WORKSPACE;
     }
     AttnArgs a{};
+    a.head_split = p.head_split ? 1 : 0;
     a.q = qkv;
     a.q_norm = q_norm;
     a.k_norm = k_norm;
@@ -1117,7 +1144,7 @@ static int attention_step(const uint16_t* qkv, const uint16_t* q_norm, const uin
     a.defer = defer ? 1 : 0;
     a.eps = eps;
     a.scale_log2 = scale * kLog2e;
-    launch_attn_kernel(p, true, dim3(static_cast<unsigned>(NKV), static_cast<unsigned>(p.cap)), as_stream(stream), a);
+    launch_attn_kernel(p, true, dim3(static_cast<unsigned>(p.gx), static_cast<unsigned>(p.cap)), as_stream(stream), a);
     return launch_status(what);
 }
 
