@@ -122,8 +122,12 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
+        gq[m] = ldg(q < groups4 ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
+    }
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        const int q = tid + m * kDdThreads;
         const bool ok = q < groups4;
-        gq[m] = ldg(ok ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
         hq[m] = ldg(ok ? reinterpret_cast<const u32x2*>(a.h) + q : z2);
         sq[m] = ldg(ok ? reinterpret_cast<const u32x4*>(sg) + q : z4);
     }
@@ -140,35 +144,49 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     // the residual element of the row (a zero word when there is none; a select, so the load is not branched)
     const uint16_t rv = ldg(a.res_out && row < a.H ? a.res + row : reinterpret_cast<const uint16_t*>(g_zero16));
 
-    // 2. |gate| (NaN past the end: key 0, never counted or selected), the coefficients h * St[g] (fp32,
-    // unmasked) and their largest magnitude, handed to the other waves through the selection's first barrier
+    // the selection's histograms are zeroed while the loads are in flight
+    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
+
+    // 2. |gate| (NaN past the end: key 0, never counted or selected)
     float gv[NC][4], xc[NC][4];
     uint32_t key[E];
-    float local_max = 0.0f, cmax = 0.0f;
+    float local_max = 0.0f;
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const bool ok = tid + m * kDdThreads < groups4;
-        // vector lanes are copied to scalars before the bit cast: __builtin_bit_cast applied to a lane of an
-        // ext_vector value (sq[m].y) was compiled as a cast of lane 0
         const uint32_t gw[2] = {gq[m].x, gq[m].y};
-        const uint32_t hw[2] = {hq[m].x, hq[m].y};
-        const uint32_t su[4] = {sq[m].x, sq[m].y, sq[m].z, sq[m].w};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const uint32_t gb = ((gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu) | (ok ? 0u : 0x7e00u);
             gv[m][p] = f16_bits_to_f32(static_cast<uint16_t>(gb));
             key[4 * m + p] = F16AbsValues::key_of(gv[m][p]);
             local_max = fmaxf(local_max, gv[m][p]);
-            const uint16_t hb = static_cast<uint16_t>(hw[p >> 1] >> (16 * (p & 1)));
-            xc[m][p] = f16_bits_to_f32(hb) * __builtin_bit_cast(float, su[p]);
-            cmax = fmaxf(cmax, fabsf(xc[m][p]));
         }
     }
-    cmax = wave_max_bcast(cmax);
-    if (lane == 0) s_cmax[wave] = cmax;
 
-    // 3. tau of rule A
-    const float tau = rule_a_tau<E, kDdWaves, F16AbsValues>(key, local_max, s_hist, s_max, a.k, tid);
+    // 3. tau of rule A. After its first radix pass (the h and St values have landed meanwhile): the coefficients
+    // h * St[g] (fp32, unmasked) and their largest magnitude, handed to the other waves through the second pass's
+    // barrier
+    auto coefficients = [&]() {
+        float cmax = 0.0f;
+#pragma unroll
+        for (int m = 0; m < NC; ++m) {
+            // vector lanes are copied to scalars before the bit cast: __builtin_bit_cast applied to a lane of an
+            // ext_vector value (sq[m].y) was compiled as a cast of lane 0
+            const uint32_t hw[2] = {hq[m].x, hq[m].y};
+            const uint32_t su[4] = {sq[m].x, sq[m].y, sq[m].z, sq[m].w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint16_t hb = static_cast<uint16_t>(hw[p >> 1] >> (16 * (p & 1)));
+                xc[m][p] = f16_bits_to_f32(hb) * __builtin_bit_cast(float, su[p]);
+                cmax = fmaxf(cmax, fabsf(xc[m][p]));
+            }
+        }
+        cmax = wave_max_bcast(cmax);
+        if (lane == 0) s_cmax[wave] = cmax;
+    };
+    const float tau =
+        rule_a_tau<E, kDdWaves, F16AbsValues, true>(key, local_max, s_hist, s_max, a.k, tid, coefficients);
 
     // 4. x_g[c] = [|gate_c| >= tau] * h_c * St[g, c] scaled by 2^e (exact; e from the largest |h * s| of all
     // channels, a bound for the selected ones), split into binary16 hi + lo (8-byte LDS stores per group), and

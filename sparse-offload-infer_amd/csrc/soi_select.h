@@ -135,29 +135,47 @@ __device__ __forceinline__ bool radix_pass(const uint32_t (&key)[E], uint32_t* h
     return true;
 }
 
+// Zero the histograms rule_a_tau uses (its ZEROED = true form expects this done before its call, e.g. while
+// the keys' loads are in flight).
+template <int NW, class Values>
+__device__ __forceinline__ void rule_a_zero_hist(uint32_t* s_hist, int tid) {
+    constexpr int kWords = radix_hist_offset<Values>(Values::kPasses);
+    for (int i = tid; i < kWords; i += NW * kWave) s_hist[i] = 0u;
+}
+
+struct NoMid {
+    __device__ __forceinline__ void operator()() const {}
+};
+
 // tau of rule A over the workgroup's keys: NW waves, E keys per lane (0 = NaN
 // or padding), local_max = this lane's fmaxf over its values starting from
-// 0.0f. Zeroes s_hist (radix_hist_offset<Values>(kPasses) words) itself; s_max
-// holds NW floats. Returns tau = lo after the 24 steps, or, for binary16
+// 0.0f. Zeroes s_hist (radix_hist_offset<Values>(kPasses) words) itself
+// unless ZEROED; s_max holds NW floats. mid() runs in every thread after the
+// first radix pass and before the second pass's barrier, which publishes its
+// LDS stores (a barrier of its own replaces that pass when it does not run):
+// work that does not feed the selection, done while its first pass waits.
+// Returns tau = lo after the 24 steps, or, for binary16
 // values, a threshold that selects exactly the same values (see below);
 // `found` is false when fewer than k keys are nonzero (then every step goes
 // left, as the reference's counts do).
-template <int E, int NW, class Values>
+template <int E, int NW, class Values, bool ZEROED = false, class Mid = NoMid>
 __device__ __forceinline__ float rule_a_tau(const uint32_t (&key)[E], float local_max, uint32_t* s_hist, float* s_max,
-                                            int k, int tid) {
+                                            int k, int tid, const Mid& mid = Mid{}) {
     constexpr int NPASS = Values::kPasses;
-    constexpr int kWords = radix_hist_offset<Values>(NPASS);
     const int wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < kWords; i += NW * kWave) s_hist[i] = 0u;
+    if (!ZEROED) rule_a_zero_hist<NW, Values>(s_hist, tid);
     const float wmax = wave_max_bcast(local_max);
     if (lane == 0) s_max[wave] = wmax;
     __syncthreads();
 
     uint32_t prefix = 0u, pmask = 0u, rank = static_cast<uint32_t>(k);
     bool found = radix_pass<Values::shift(0), Values::bits(0)>(key, s_hist, prefix, pmask, rank, lane);
+    mid();
     if (found)
         found = radix_pass<Values::shift(1), Values::bits(1)>(key, s_hist + radix_hist_offset<Values>(1), prefix,
                                                               pmask, rank, lane);
+    else if (!__is_same(Mid, NoMid))
+        __syncthreads();  // found is the same in every wave (all read one histogram)
     if (NPASS == 3 && found)
         found = radix_pass<Values::shift(NPASS == 3 ? 2 : 1), Values::bits(NPASS == 3 ? 2 : 1)>(
             key, s_hist + radix_hist_offset<Values>(NPASS == 3 ? 2 : 1), prefix, pmask, rank, lane);
