@@ -386,8 +386,28 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     const int nhq = a.head_split ? 1 : rep;
     int p = -1;
     int L;
+    // PRE: the position is requested first (a scalar load), then the operands of the wave's first head (a query
+    // head, or the new k), which do not depend on it, so its RMSNorm does not wait for the position. The RoPE
+    // table rows and the K/V rows follow once it is known. (Requesting split 0's first K/V rows before the
+    // position as well measured slower: loads return in order, so the table rows then wait for the K/V rows.)
+    if (PRE) p = ldg(a.pos);
+    const uint16_t* kbase = a.kc + static_cast<int64_t>(kvh) * S * HD;  // this KV head's cache
+    const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * S * HD;
+    auto head_src = [&](int hh) {
+        return a.q + static_cast<int64_t>(hh == nhq ? a.NQ + kvh : kvh * rep + hq0 + hh) * HD;
+    };
+    uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
+    float f_c = 0.0f, f_sn = 0.0f;
+    if (PRE && HALF == kWave && wave <= nhq) {  // wave-uniform; wave nhq's new k is used only next to p
+        const int fh = wave;
+        const uint16_t* src = head_src(fh);
+        const uint16_t* wn = fh == nhq ? a.k_norm : a.q_norm;
+        f_x1 = ldg(src + lane);
+        f_x2 = ldg(src + lane + HALF);
+        f_w1 = ldg(wn + lane);
+        f_w2 = ldg(wn + lane + HALF);
+    }
     if (PRE) {
-        p = ldg(a.pos);
         L = p < 0 ? 1 : (p >= S ? S : p + 1);
     } else {
         L = cur_len_of(a.L_arg, a.pos, S);
@@ -401,30 +421,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     const bool has_new = pvalid && p >= t0 && p < t1;
     const int tnew = has_new ? p : -1;
 
-    // this KV head's cache
-    const uint16_t* kbase = a.kc + static_cast<int64_t>(kvh) * S * HD;
-    const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * S * HD;
     const int tb0 = t0 + wave * RPI;
     const int npass_all = (t1 - t0 + STEP - 1) / STEP;
-    // PRE: q heads kvh*rep + hh (and, in the workgroup holding p, the new k) are normed and rotated; wave w
+    // PRE: q heads kvh*rep + hq0 + hh (and, in the workgroup holding p, the new k) are normed and rotated; wave w
     // takes heads w, w+8, ... With head_dim 128 (one pair per lane) the operands of the wave's first head are
-    // requested before the K/V rows (loads return in order), so its RMSNorm and RoPE run while the rows are in
-    // flight.
+    // in flight already (above), and the table rows are requested before the K/V rows, so its RMSNorm and RoPE
+    // run while the rows are.
     const int prow = pvalid ? p : (p < 0 ? 0 : S - 1);  // RoPE table row
     const int nh = PRE ? nhq + (has_new ? 1 : 0) : 0;
-    auto head_src = [&](int hh) {
-        return a.q + static_cast<int64_t>(hh == nhq ? a.NQ + kvh : kvh * rep + hq0 + hh) * HD;
-    };
-    uint16_t f_x1 = 0, f_x2 = 0, f_w1 = 0, f_w2 = 0;
-    float f_c = 0.0f, f_sn = 0.0f;
     if (PRE && HALF == kWave && wave < nh) {  // wave-uniform
-        const int fh = wave;
-        const uint16_t* src = head_src(fh);
-        const uint16_t* wn = fh == nhq ? a.k_norm : a.q_norm;
-        f_x1 = ldg(src + lane);
-        f_x2 = ldg(src + lane + HALF);
-        f_w1 = ldg(wn + lane);
-        f_w2 = ldg(wn + lane + HALF);
         f_c = ldg(a.cos_t + static_cast<int64_t>(prow) * HALF + lane);
         f_sn = ldg(a.sin_t + static_cast<int64_t>(prow) * HALF + lane);
     }
