@@ -900,8 +900,9 @@ def run_traffic_set(dev, gen):
     """Launches for the HBM counter passes (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, one run each): the
     calibration copy (copy_reference: 11 copies of 512 MiB), then 6 launches each, on separate operand copies
     and each followed by a synchronize, of sparse_down_kernel, dip_select_down_kernel and dip_dense_down_kernel
-    (index list not written) at k = 3072 and of attn_kernel at L = 192 and L = 2048 (host-length form: grids of
-    8 and 8 x 16 workgroups). Prints the algorithmic bytes each launch moves."""
+    (index list not written) at k = 3072 and of attn_kernel at L = 192 and L = 2048 (host-length form, one
+    workgroup per query head: grids of 16 and 16 x 16 workgroups, the latter followed by attn_combine_kernel over
+    the split states). Prints the algorithmic bytes each launch moves."""
     import torch
 
     from soinfer import _C
