@@ -73,18 +73,28 @@ __device__ __forceinline__ int cur_len_of(int L_arg, const int32_t* pos, int S) 
 // the device (the device-position forms, which read L at run time) use this
 // same function, so both give the same partition and bit-identical results.
 // ns <= ceil(kAttnTargetGroups/NKV) and ns <= ceil(L/step) for every L.
-__host__ __device__ __forceinline__ void split_plan(int64_t L, int64_t NKV, int64_t step, int& tps, int& ns) {
+// Every quantity fits in 32 bits (L * NKV < 2^31: plan_attention takes the fast kernels only then) and step and
+// both group targets are powers of two, so the device evaluates the plan with shifts, a mask and one 32-bit
+// division instead of three 64-bit division sequences (on the critical path of the device-position forms and of
+// the o projection's combine).
+constexpr int kAttnMidGroupsLog2 = 6, kAttnTargetGroupsLog2 = 7;
+static_assert((1 << kAttnMidGroupsLog2) == kAttnMidGroups && (1 << kAttnTargetGroupsLog2) == kAttnTargetGroups,
+              "split targets are powers of two");
+__host__ __device__ __forceinline__ void split_plan(int64_t L64, int64_t NKV64, int64_t step64, int& tps, int& ns) {
+    const uint32_t L = static_cast<uint32_t>(L64), NKV = static_cast<uint32_t>(NKV64);
+    const uint32_t step = static_cast<uint32_t>(step64);  // a power of two
     if (L <= kAttnPassMax * step) {
         tps = static_cast<int>(L);
         ns = 1;
         return;
     }
-    const int64_t groups = L * NKV <= kAttnMidRows ? kAttnMidGroups : kAttnTargetGroups;
-    int64_t t = (L * NKV + groups - 1) / groups;
-    t = (t + step - 1) / step * step;
+    const uint32_t rows = L * NKV;
+    const int lg = rows <= static_cast<uint32_t>(kAttnMidRows) ? kAttnMidGroupsLog2 : kAttnTargetGroupsLog2;
+    uint32_t t = (rows + (1u << lg) - 1u) >> lg;  // ceil(rows / groups)
+    t = (t + step - 1u) & ~(step - 1u);           // rounded up to a multiple of step
     if (t < step) t = step;
     tps = static_cast<int>(t);
-    ns = static_cast<int>((L + t - 1) / t);
+    ns = static_cast<int>((L + t - 1u) / t);
 }
 
 // Sum over the LPR lanes of a row group, every lane of the group gets it. Up to
@@ -624,17 +634,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep + hq0, nhq, a.nsplit, ns, s_cm, s_cl);
 }
 
-// Second launch of the standalone forms: workgroup kvh combines the split states of its query heads with
-// combine_kv (the arithmetic of the in-launch combine), after an attn_kernel launch with defer set. An unsplit
-// context wrote out itself. Across the launch boundary the states need no device fence or arrival counter.
+// Second launch of the host-length form: workgroup kvh combines the split states of its query heads with
+// combine_kv (the arithmetic of the in-launch combine), after an attn_kernel launch with defer set; ns is the
+// host's plan. An unsplit context wrote out itself. Across the launch boundary the states need no device fence
+// or arrival counter.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
-                                                                    uint16_t* __restrict__ out,
-                                                                    const int32_t* __restrict__ pos, int L_arg, int S,
-                                                                    int NKV, int rep, int step, int nsplit) {
+                                                                    uint16_t* __restrict__ out, int rep, int nsplit,
+                                                                    int ns) {
     __shared__ float s_cm[8 * kCombineMaxSplits], s_cl[8 * kCombineMaxSplits];
-    int tps, ns;
-    split_plan(cur_len_of(L_arg, pos, S), NKV, step, tps, ns);
     if (ns == 1) return;  // uniform
     combine_kv<kAttnThreads, HD>(part, out, static_cast<int>(blockIdx.x) * rep, rep, nsplit, ns, s_cm, s_cl);
 }
@@ -699,7 +707,7 @@ static AttnPlan plan_attention(int64_t NQ, int64_t NKV, int64_t hd, int64_t L) {
     const int64_t rep = NQ / NKV;
     const int64_t lpr = hd / 8;
     const bool pow2 = lpr >= 1 && (lpr & (lpr - 1)) == 0;
-    if (hd % 8 == 0 && pow2 && lpr <= 32 && rep <= 8) {
+    if (hd % 8 == 0 && pow2 && lpr <= 32 && rep <= 8 && L * NKV < (int64_t(1) << 31)) {
         p.fast = true;
         p.lpr = static_cast<int>(lpr);
         p.gx = static_cast<int>(NKV);
@@ -814,7 +822,7 @@ static int launch_attention(const uint16_t* q, const uint16_t* k_cache, const ui
     if (a.defer) {
 #define SOI_AC(LL)                                                                                             \
     hipLaunchKernelGGL(attn_combine_kernel<LL * 8>, dim3(static_cast<unsigned>(NKV)), dim3(kAttnThreads), 0, st, \
-                       a.part, out, pos, a.L_arg, a.S, a.NKV, rep, p.step, nsplit)
+                       a.part, out, rep, nsplit, nsplit)
         switch (p.lpr) {
             case 1: SOI_AC(1); break;
             case 2: SOI_AC(2); break;
