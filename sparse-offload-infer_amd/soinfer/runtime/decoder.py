@@ -47,6 +47,9 @@ from ..offload.stream_manager import StreamManager
 from ..offload.weight_store import PinnedWeightStore, plan_bytes
 from ..quant import formats, pack
 
+# Generation steps per replay of the chunk graph (decode replays it for each full chunk of the requested steps)
+GRAPH_CHUNK = 4
+
 
 @dataclass(frozen=True)
 class DecoderConfig:
@@ -305,6 +308,7 @@ class DecodeEngine:
         self._x_final = self.x
         self._graph_layers = None
         self._graph_gen = None
+        self._graph_gen_chunk = None  # GRAPH_CHUNK generation steps in one graph
         # eager runs only: called as layer_hook(l) after layer l's MLP has been issued (the MLP output is in
         # self.down; in DIP modes gate is in self.gu[:I] and the selection in self.idx / self.cnt, and the MLP
         # input in self.h except for the fused dense and dense-up schedules); never set while capture() runs
@@ -661,7 +665,9 @@ class DecodeEngine:
 
     # ---- graphs ----
     def capture(self):
-        """Capture the prompt step (layers) and the generation step (head + layers) as HIP graphs."""
+        """Capture the prompt step (layers), the generation step (head + layers) and GRAPH_CHUNK generation steps
+        in a row as HIP graphs (the chunk graph saves a graph boundary per step: about 5 us, 0.7% of a token of the
+        Qwen3-1.7B shape, measured)."""
         saved = (self.pos.clone(), self.log_len.clone(), self.token.clone())
         self._step_open = False  # a step's copies always start inside the step that uses them
         s = torch.cuda.Stream(device=self.device)
@@ -677,6 +683,10 @@ class DecodeEngine:
         self._graph_gen = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self._graph_gen):
             self._gen_step()
+        self._graph_gen_chunk = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._graph_gen_chunk):
+            for _ in range(GRAPH_CHUNK):
+                self._gen_step()
         self.pos.copy_(saved[0])
         self.log_len.copy_(saved[1])
         self.token.copy_(saved[2])
@@ -701,11 +711,14 @@ class DecodeEngine:
     def decode(self, n_new: int, use_graph: bool = True):
         if n_new > self.log.numel():
             raise ValueError("n_new exceeds max_new_tokens")
-        for _ in range(n_new):
-            if use_graph:
-                self._graph_gen.replay()
-            else:
+        if not use_graph:
+            for _ in range(n_new):
                 self._gen_step()
+            return
+        for _ in range(n_new // GRAPH_CHUNK):
+            self._graph_gen_chunk.replay()
+        for _ in range(n_new % GRAPH_CHUNK):
+            self._graph_gen.replay()
 
     def generate(self, prompt_ids, n_new: int, use_graph: bool = True, eos_token_id: Optional[int] = None):
         """Greedy decoding: returns prompt_ids + the n_new generated tokens (cut after eos_token_id, as the

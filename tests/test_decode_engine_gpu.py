@@ -94,6 +94,21 @@ def test_graph_replay_equals_eager(dec, tiny, mode, k, fused):
         _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
 
 
+@pytest.mark.parametrize("mode,k", [("dense", None), ("dip", 128)])
+def test_chunk_graph_and_single_step_replays_compose(dec, tiny, mode, k):
+    """decode(n) replays the GRAPH_CHUNK-step graph n // GRAPH_CHUNK times, then the one-step graph: every split of
+    n (fewer steps than a chunk, whole chunks, chunks plus a remainder) gives the eager run's tokens and state."""
+    prompt = prompt_ids(4, tiny.config.vocab, seed=13)
+    n_max = 2 * dec.GRAPH_CHUNK + 1
+    a = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=n_max)
+    b = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=n_max)
+    for n in (1, dec.GRAPH_CHUNK - 1, dec.GRAPH_CHUNK, dec.GRAPH_CHUNK + 1, n_max):
+        eager = a.generate(prompt, n, use_graph=False)
+        graph = b.generate(prompt, n, use_graph=True)
+        assert graph == eager, f"{mode}: {n} new tokens"
+        assert torch.equal(b.x_final, a.x_final), f"{mode}: {n} new tokens, hidden state"
+
+
 @pytest.mark.parametrize("miss_path", ["direct", "staged"])
 @pytest.mark.parametrize("fused", [True, False])
 def test_cached_dip_bit_identical_to_dip(dec, tiny, fused, miss_path):
