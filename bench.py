@@ -13,11 +13,13 @@ independent GEMVs run as ONE grouped launch per step (4 shape classes).
 value = algorithmic bytes / step time, timed over --steps steps between two
 device synchronisations.
 
-Also reported:
-  roofline        the dominant (and only) launch of a step, timed with HIP events
-                  around back-to-back launches on the launching stream; `traffic` is the
-                  HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter
-                  summary committed under profiles/ (null when absent);
+The last stdout line is the compact result: the headline fields, config,
+roofline (the dominant -- and only -- launch of a step; its average duration
+from two HIP events on the launching stream around the timed steps themselves,
+so it cannot exceed ms_per_step; `traffic` is the HBM bytes per launch from the
+FETCH_SIZE / WRITE_SIZE counter summary committed under profiles/, null when
+absent), decode_tok_s (config 5 per mode) and cpu_baseline. Everything else is
+one 'bench-detail: {...}' line on stderr (and --detail-json PATH):
   batched_per_class  the same GEMVs as one launch per shape class, per class;
   copy_reference  a plain device-to-device copy of 512 MiB (the calibration
                   kernel of the counter runs, and the box's streaming rate), and
@@ -32,7 +34,7 @@ Also reported:
   decode          BASELINE config 5: greedy decode tok/s of the random-init 28-layer Qwen3-1.7B
                   shape, dense vs DIP vs cache-aware DIP at k/I = 0.5 (64-token prompt, 128 tokens);
   cpu_baseline    the reference's CPU GEMV path (dequantize + fp32 torch.mv) on layer 0's GEMVs,
-                  at the job's host cores and one thread.
+                  at the job's host cores and one thread, and the other operators' CPU oracles.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --traffic-set   (only the launches of the HBM counter passes whose summaries are
@@ -455,20 +457,21 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     out, toks = {}, {}
     L0 = w.layers[0]
     attn_w = (L0.qkv_Wq.numel() + 4 * L0.qkv_scale.numel() + L0.o_Wq.numel() + 4 * L0.o_scale.numel())
-    # "dip": the fastest resident DIP schedule (dense-up: gate|up GEMV + one-launch selection and down);
-    # "dip_indexed_up": the four-launch schedule the cache-aware engines reproduce bit for bit
+    # "dip": the indexed schedule (gate GEMV, top-k, up GEMV over the selected rows, sparse down), the one the
+    # cache-aware engines reproduce bit for bit; "dip_dense_up": the same selection with the up GEMV over every
+    # row and the down as one dense GEMV over a transposed down_proj^T (y summed in another order)
     # "*_offload": copies on copy streams two layers ahead of the kernels; "*_offload_serial": each layer's copy
     # stream-ordered right before its kernels
-    modes = ("dense", "dip", "dip_indexed_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
+    modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
              "cached_dip_offload", "dense_offload_serial", "dip_offload_serial", "cached_dip_offload_serial")
     no_hot = [[] for _ in range(c.layers)]
     for mode in modes:
         kind = mode.replace("_serial", "")
-        base = {"dip_indexed_up": "dip", "cached_dip_staged": "cached_dip",
+        base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip",
                 "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(kind, kind)
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
                              hot_channels=(no_hot if kind == "dip_offload" else hot) if base == "cached_dip" else None,
-                             max_new_tokens=n_new, dip_dense_up=mode == "dip",
+                             max_new_tokens=n_new, dip_dense_up=mode == "dip_dense_up",
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
                              offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"))
         eng.capture()
@@ -483,7 +486,7 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=mode == "dip")
+        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=mode == "dip_dense_up")
         per_tok = c.layers * (attn_w + mlp) + w.lm_head.numel() * 2
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
@@ -495,11 +498,11 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         del eng
         torch.cuda.empty_cache()
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
-    out["cached_dip_tokens_equal_dip"] = toks["dip_indexed_up"] == toks["cached_dip"] == toks["cached_dip_staged"]
+    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"] == toks["cached_dip_staged"]
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
-    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip_indexed_up"), ("cached_dip_offload", "dip_indexed_up"),
-                 ("dense_offload_serial", "dense"), ("dip_offload_serial", "dip_indexed_up"),
-                 ("cached_dip_offload_serial", "dip_indexed_up")):
+    for a, b in (("dense_offload", "dense"), ("dip_offload", "dip"), ("cached_dip_offload", "dip"),
+                 ("dense_offload_serial", "dense"), ("dip_offload_serial", "dip"),
+                 ("cached_dip_offload_serial", "dip")):
         assert toks[a] == toks[b], f"{a} must generate the same tokens as {b}"
     out["offload_tokens_equal_resident"] = True
     out["offload_note"] = ("*_offload: every layer's dense weights (q|k|v, o, gate|up and down for dense, gate for "
@@ -511,16 +514,23 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
                            "no cache, cached_dip_offload: 20% hot cache in HBM)")
     out["cached_dip"]["miss_path"] = "direct: misses read in place from the pinned host arena inside the GEMVs"
     out["cached_dip_staged"]["miss_path"] = "staged: device gathers of the misses into staging, then descriptors"
-    out["dip_indexed_up"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse "
-                                         "down (4 launches per MLP)")
-    out["dip_tokens_equal_indexed_up"] = toks["dip"] == toks["dip_indexed_up"]
-    out["dip"]["schedule"] = ("gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the "
+    out["dip"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse "
+                              "down (4 launches per MLP); cached_dip equals it bit for bit")
+    out["dip_dense_up_tokens_equal_dip"] = toks["dip"] == toks["dip_dense_up"]
+    out["dip_dense_up"]["schedule"] = ("gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the "
                               "rule-A selection in every workgroup + the down as a GEMV over the transposed "
-                              "down_proj^T (2 launches per MLP); the selections of dip_indexed_up, y summed in "
+                              "down_proj^T (2 launches per MLP); the selections of dip, y summed in "
                               "another order")
     out["config"] = {"prompt_tokens": n_prompt, "new_tokens": n_new, "dip_k": k, "hot_fraction": 0.2,
                      "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed and LM head",
                      "kv": "fp16, max_seq 2048"}
+    return out
+
+
+def decode_summary(dec: dict) -> dict:
+    """Compact form of the decode record for the result line: tok/s per mode and the equality checks."""
+    out = {m: v["decode_tok_s"] for m, v in dec.items() if isinstance(v, dict) and "decode_tok_s" in v}
+    out.update({k: v for k, v in dec.items() if isinstance(v, bool)})
     return out
 
 
@@ -880,7 +890,10 @@ def cpu_baseline(layer0):
         reps += 1
     checker = round(reps * pass_bytes / (time.perf_counter() - t0) / 1e9, 4)
     main_fig = figures[f"dequant_mv_{cores}t"]
-    return {"value": main_fig["GBps"], "unit": "GB/s", "cores": cores, "kind": "port",
+    short = (f"reference CPU GEMV path (formats.dequantize + fp32 torch.mv, tests/test_m4_kernels.py:157-165; "
+             f"oracle/cpu_path.py) over layer 0's 7 INT4 g128 GEMVs, {pass_bytes} B per pass, median of 100 passes "
+             f"at {cores} threads; {_cpu_model()}")
+    return {"value": main_fig["GBps"], "short_sample": short, "unit": "GB/s", "cores": cores, "kind": "port",
             "median_ms_per_pass": main_fig["median_ms"], "p90_ms_per_pass": main_fig["p90_ms"],
             "single_thread_value": figures["dequant_mv_1t"]["GBps"], "figures": figures,
             "c_oracle_binary64_GBps": checker, "other_operators": other_figures,
@@ -964,6 +977,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the decode-chain, per-shape and top-k tables")
     ap.add_argument("--no-decode", action="store_true", help="skip the DIP MLP and decode tok/s sections")
+    ap.add_argument("--detail-json", default=None, help="also write the result and the detail record to this file")
     ap.add_argument("--traffic-set", action="store_true",
                     help="only the launches of the HBM counter passes (calibration copy, sparse down, fused "
                          "selection + down, dense down, attention at L = 192 and 2048), then exit")
@@ -1015,12 +1029,19 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # the timed region: wall clock between two device synchronisations, and two HIP events on the launching
+    # (current) stream around the same launches, so the dominant kernel's average duration comes from the
+    # very launches ms_per_step times (one launch per step)
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev_a.record()
     for _ in range(args.steps):
         step()
+    ev_b.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    log(f"{args.steps} timed steps: {elapsed / args.steps * 1e3:.4f} ms/step")
+    dom_us = ev_a.elapsed_time(ev_b) * 1e3 / args.steps
+    log(f"{args.steps} timed steps: {elapsed / args.steps * 1e3:.4f} ms/step, {dom_us:.3f} us per launch (events)")
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9  # GB/s
 
@@ -1043,8 +1064,7 @@ def main() -> int:
         m = layers[l][n]
         assert torch.equal(group.ys[i], ops.gemv_w4a16_group_lop3(m[0], m[1], m[2], m[4], GS)), f"grouped {l}.{n}"
 
-    # ---- dominant kernel: the grouped launch (the whole step), HIP events around back-to-back launches ----
-    dom_us = time_back_to_back(group.run, launches=30)
+    # ---- dominant kernel: the grouped launch (the whole step), from the events around the timed steps ----
     achieved = step_bytes / (dom_us * 1e-6) / 1e9
     n_wg = sum(c * (nn // 8) for c, nn in zip(group.class_count, group.class_N))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
@@ -1052,8 +1072,11 @@ def main() -> int:
                 "kernel": f"soi::gemv_int4_grouped_occ_kernel<8,true,true,true> (196 GEMVs in 4 shape classes, "
                           f"{n_wg} workgroups of 64)",
                 "bytes_per_launch": step_bytes, "avg_launch_us": round(dom_us, 3),
-                "timing": "HIP events around 30 back-to-back launches on the launching stream"}
-    log(f"dominant launch: {dom_us:.3f} us")
+                "timing": f"HIP events on the launching stream around the {args.steps} timed steps (one launch "
+                          f"each)"}
+    # after the timed region: 30 more back-to-back launches, for the detail record only
+    dom_b2b_us = time_back_to_back(group.run, launches=30)
+    log(f"dominant launch after the timed region: {dom_b2b_us:.3f} us")
 
     # ---- the same work as one batched launch per shape class (4 launches), per class ----
     per_class = {}
@@ -1095,20 +1118,20 @@ def main() -> int:
                    "group_size": GS},
         "frac_of_hbm_peak": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": roofline,
-        "copy_reference": copy_ref,
-        "batched_per_class": per_class,
-        "step_spread": step_stats,
     }
+    # everything else goes to the detail record (stderr, and --detail-json): the result line stays compact
+    detail = {"dominant_launch_back_to_back_after_timed_us": round(dom_b2b_us, 3), "copy_reference": copy_ref,
+              "batched_per_class": per_class, "step_spread": step_stats}
     if not args.no_extras:
-        result["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
+        detail["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
         log("decode chain done")
         del layers, group
         torch.cuda.empty_cache()
-        result["per_shape_cold"] = bench_shapes(ops, dev, gen)
+        detail["per_shape_cold"] = bench_shapes(ops, dev, gen)
         log("per-shape table done")
-        result["topk_us_I6144"] = bench_topk(ops, dev, gen)
+        detail["topk_us_I6144"] = bench_topk(ops, dev, gen)
         log("top-k done")
-        result["kernels"] = bench_kernels(dev, gen)
+        detail["kernels"] = bench_kernels(dev, gen)
         log("kernel table done")
     if not args.no_decode:
         from soinfer.runtime import decoder as D
@@ -1122,11 +1145,12 @@ def main() -> int:
         calib = torch.randint(0, D.QWEN3_1P7B.vocab, (64,), generator=torch.Generator().manual_seed(1000)).tolist()
         hot = D.calibrate_hot_channels(w, D.QWEN3_1P7B.intermediate // 2, calib, cache_fraction=0.2)
         log("decoder weights and hot sets ready")
-        result["dip_mlp_layer"] = bench_dip_mlp(D, w, hot, dev)
+        detail["dip_mlp_layer"] = bench_dip_mlp(D, w, hot, dev)
         log("DIP MLP done")
-        result["decode"] = bench_decode(D, w, hot, dev)
+        detail["decode"] = bench_decode(D, w, hot, dev)
         del w
         torch.cuda.empty_cache()
+        result["decode_tok_s"] = decode_summary(detail["decode"])
     if not args.no_cpu_baseline:
         g = torch.Generator().manual_seed(1)
         layer0 = []
@@ -1135,8 +1159,18 @@ def main() -> int:
         for _, N, K in LAYER_SHAPES:
             q, s = O.quantize_group((torch.randn(N, K, generator=g) * 0.02).numpy(), GS)
             layer0.append((q, s, O.pack_int4(q), torch.randn(K, generator=g).half().numpy(), K))
-        result["cpu_baseline"] = cpu_baseline(layer0)
+        cpu = cpu_baseline(layer0)
         log("cpu baseline done")
+        detail["cpu_baseline"] = cpu
+        result["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "single_thread_value",
+                                                     "median_ms_per_pass")}
+        result["cpu_baseline"]["sample"] = cpu["short_sample"]
+    result["detail"] = "stderr line 'bench-detail: {...}' (and --detail-json)"
+    dj = json.dumps(detail)
+    print(f"bench-detail: {dj}", file=sys.stderr, flush=True)
+    if args.detail_json:
+        Path(args.detail_json).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.detail_json).write_text(json.dumps({"result": result, "detail": detail}, indent=1))
     print(json.dumps(result))
     return 0
 
