@@ -179,7 +179,10 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
             for (int p = 0; p < 4; ++p) {
                 const uint16_t hb = static_cast<uint16_t>(hw[p >> 1] >> (16 * (p & 1)));
                 xc[m][p] = f16_bits_to_f32(hb) * __builtin_bit_cast(float, su[p]);
-                cmax = fmaxf(cmax, fabsf(xc[m][p]));
+                // finite magnitudes only: an infinite coefficient (h = +-inf) would otherwise set e = 15 and make
+                // every selected coefficient >= 2 overflow in its binary16 hi part; NaN is ignored by fmaxf
+                const float ax = fabsf(xc[m][p]);
+                cmax = ax < __builtin_inff() ? fmaxf(cmax, ax) : cmax;
             }
         }
         cmax = wave_max_bcast(cmax);
@@ -188,9 +191,10 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     const float tau =
         rule_a_tau<E, kDdWaves, F16AbsValues, true>(key, local_max, s_hist, s_max, a.k, tid, coefficients);
 
-    // 4. x_g[c] = [|gate_c| >= tau] * h_c * St[g, c] scaled by 2^e (exact; e from the largest |h * s| of all
-    // channels, a bound for the selected ones), split into binary16 hi + lo (8-byte LDS stores per group), and
-    // the chunk masks: lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m
+    // 4. x_g[c] = [|gate_c| >= tau] * h_c * St[g, c] scaled by 2^e (exact; e from the largest finite |h * s| of
+    // all channels, a bound for the selected finite ones), split into binary16 hi + lo (8-byte LDS stores per
+    // group; an infinite x keeps hi = x and lo = 0, so its products are +-inf as in the fp32 sum, and NaN for
+    // q = 0), and the chunk masks: lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m
     float mx = s_cmax[0];
 #pragma unroll
     for (int w = 1; w < kDdWaves; ++w) mx = fmaxf(mx, s_cmax[w]);
@@ -205,7 +209,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
             const bool sel = gv[m][p] >= tau;  // NaN (and padding) never
             const float xs = sel ? __builtin_ldexpf(xc[m][p], e) : 0.0f;
             hb[p] = f32_to_f16_bits(xs);
-            lb[p] = f32_to_f16_bits(xs - f16_bits_to_f32(hb[p]));  // exact difference
+            const float d = xs - f16_bits_to_f32(hb[p]);  // exact difference (NaN for an infinite xs)
+            lb[p] = f32_to_f16_bits(fabsf(xs) < __builtin_inff() ? d : 0.0f);
             m4 |= (sel ? 1u : 0u) << p;
         }
         const uint32_t cm = or8_lanes(m4 << (4 * (lane & 7)));

@@ -223,3 +223,53 @@ def test_dense_down_rejections(C, ops):
     S_big = torch.zeros(H // 128, n_big, device="cuda")
     with pytest.raises(RuntimeError, match="multiple of 32"):
         C.dip_select_dense_down_into(g_big, g_big, 10, W_big, S_big, None, None, y, 128)
+
+
+def test_dense_down_unselected_infinite_h(C, ops):
+    """An unselected channel whose h overflowed to +-inf (or is NaN) must not change y: the power-of-two scale
+    comes from the finite coefficients only, so y over the selected channels matches the oracle and is finite."""
+    I, H, k = 2048, 512, 1024
+    down, Wt, St = _problem(ops, I, H, seed=901)
+    g = rnd((I,), 902) * 2
+    hv = rnd((I,), 903) * 4
+    absg = np.abs(g.float().numpy())
+    ref_idx = O.topk_rule_a(absg, k)
+    unsel = np.setdiff1d(np.arange(I), ref_idx)
+    hv[int(unsel[0])] = float("inf")
+    hv[int(unsel[len(unsel) // 2])] = float("-inf")
+    hv[int(unsel[-1])] = float("nan")
+    y, idx, cnt = ops.dip_select_dense_down(g.cuda(), hv.cuda(), k, Wt, St, 128)
+    assert int(cnt.item()) == k and np.array_equal(idx.cpu().numpy(), ref_idx)
+    y_ref = O.sparse_accumulate_f64(down["Wq"][ref_idx], down["s"][ref_idx], hv.numpy()[ref_idx], H, 128)
+    assert_close(y, y_ref, "unselected inf / NaN h")
+
+
+@pytest.mark.parametrize("I,H,k", [(1024, 200, 333), (2048, 2056, 1000), (1024, 204, 512), (512, 36, 100)])
+def test_dense_down_group_size_8_ragged_h(C, ops, I, H, k):
+    """group_size 8 with H not a multiple of 128 (grids of 25, 257, 26 and 5 workgroups, not multiples of 8: the
+    identity tile order) and H not a multiple of 8 (a last tile with rows past H): selection and y against the
+    oracle, and nothing written past y[H - 1] or res_out[H - 1]."""
+    gs = 8
+    down = int4_problem(I, H, gs, seed=950 + H)
+    Wt, St = ops.transposed_down_T(down["Wq_d"], down["s_d"], H)
+    assert St.shape == (-(-H // gs), I)
+    g = rnd((I,), 951 + H) * 2
+    u = rnd((I,), 952 + H) * 2
+    gate, up = g.cuda(), u.cuda()
+    h_all = _gated_all(C, gate, up)
+    sentinel = 0x7bff  # fp16 65504, never a value of these sums
+    y_buf = torch.full((H + 24,), sentinel, dtype=torch.int16, device="cuda").view(torch.float16)
+    r_buf = torch.full((H + 24,), sentinel, dtype=torch.int16, device="cuda").view(torch.float16)
+    res = rnd((H,), 953 + H).cuda()
+    idx = torch.empty(k, dtype=torch.int32, device="cuda")
+    cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+    C.dip_select_dense_down_into(gate, h_all, k, Wt, St, idx, cnt, y_buf[:H], gs, res, r_buf[:H])
+    ref_idx = O.topk_rule_a(np.abs(g.float().numpy()), k)
+    assert int(cnt.item()) == k and np.array_equal(idx.cpu().numpy(), ref_idx)
+    h = h_all.index_select(0, idx.long())
+    y_ref = O.sparse_accumulate_f64(down["Wq"][ref_idx], down["s"][ref_idx], h.cpu().numpy(), H, gs)
+    assert_close(y_buf[:H], y_ref, f"gs=8 H={H}")
+    assert torch.equal(r_buf[:H], (res.float() + y_buf[:H].float()).half()), "residual output"
+    tail = torch.full((24,), sentinel, dtype=torch.int16, device="cuda")
+    assert torch.equal(y_buf[H:].view(torch.int16), tail), "y written past H"
+    assert torch.equal(r_buf[H:].view(torch.int16), tail), "res_out written past H"
