@@ -99,3 +99,58 @@ def test_noalloc_replays_from_a_graph(lib):
         assert _call(lib, q["Wq_d"], q["s_d"], h2, y2, 1024, 77, 64) == 0
         torch.cuda.synchronize()
         assert torch.equal(y2, ops.gemv_w4a16_sparse_accumulate(q["Wq_d"], q["s_d"], h2, 1024, 64))
+
+
+_FIRST_CALL_UNDER_CAPTURE = r'''
+import ctypes as C, sys
+import torch
+sys.path[:0] = [sys.argv[1], sys.argv[2], sys.argv[3]]
+import soinfer.ops as ops
+from helpers import int4_problem
+L = C.CDLL(sys.argv[4])
+f = L.soi_gemv_w4a16_sparse_accumulate_noalloc
+f.argtypes = [C.c_void_p] * 4 + [C.c_int64] * 4 + [C.c_void_p]
+f.restype = C.c_int
+L.soi_last_error.restype = C.c_char_p
+H, k, gs = 2048, 1536, 128
+p = int4_problem(k, H, gs, seed=9)
+h = torch.randn(k, generator=torch.Generator().manual_seed(109)).half().cuda()
+y = torch.zeros(H, dtype=torch.float16, device="cuda")
+want = ops.gemv_w4a16_sparse_accumulate(p["Wq_d"], p["s_d"], h, H, gs)
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    rc = f(p["Wq_d"].data_ptr(), p["s_d"].data_ptr(), h.data_ptr(), y.data_ptr(), H, k, gs, p["s_d"].shape[1],
+           torch.cuda.current_stream().cuda_stream)
+if rc != 0:
+    print("FIRST CALL FAILED", L.soi_last_error(), flush=True)
+    sys.exit(3)
+for i in range(3):
+    y.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(y, want):
+        print("REPLAY DIFFERS", i, flush=True)
+        sys.exit(4)
+    _ = torch.zeros(1 << 20, device="cuda").sum()
+    torch.cuda.synchronize()
+print("FIRST-CALL-UNDER-CAPTURE OK", flush=True)
+'''
+
+
+def test_noalloc_first_call_under_capture(lib, tmp_path):
+    """In a fresh process the first call on the device (symbol lookup + the counter-clearing kernel) is made
+    inside a graph capture; every replay equals the workspace form."""
+    import subprocess
+    import sys
+
+    root = Path(__file__).resolve().parent.parent
+    script = tmp_path / "first_call_under_capture.py"
+    script.write_text(_FIRST_CALL_UNDER_CAPTURE)
+    print("running the first-call-under-capture child", flush=True)
+    r = subprocess.run([sys.executable, str(script), str(root / "sparse-offload-infer_amd"), str(root),
+                        str(root / "tests"), str(LIB)], capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0 and "FIRST-CALL-UNDER-CAPTURE OK" in r.stdout, (r.returncode, r.stdout[-2000:],
+                                                                          r.stderr[-2000:])
