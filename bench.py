@@ -462,18 +462,25 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     # row and the down as one dense GEMV over a transposed down_proj^T (y summed in another order)
     # "*_offload": copies on copy streams two layers ahead of the kernels; "*_offload_serial": each layer's copy
     # stream-ordered right before its kernels
-    modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_offload", "dip_offload",
+    # "*_int4_head": the same schedule with the LM head quantized like the linears (INT4 g128 GEMV) instead of
+    # the reference's fp16 head: config 5's "all weights INT4 g128"
+    modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_int4_head", "dip_int4_head",
+             "dip_dense_up_int4_head", "cached_dip_int4_head", "dense_offload", "dip_offload",
              "cached_dip_offload", "dense_offload_serial", "dip_offload_serial", "cached_dip_offload_serial")
     no_hot = [[] for _ in range(c.layers)]
+    Wq_h, S_h = D.quantize_lm_head(w)
+    head_bytes = {False: w.lm_head.numel() * 2, True: Wq_h.numel() + 4 * S_h.numel()}
     for mode in modes:
-        kind = mode.replace("_serial", "")
+        int4_head = mode.endswith("_int4_head")
+        kind = mode.replace("_serial", "").replace("_int4_head", "")
         base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip",
                 "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(kind, kind)
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
                              hot_channels=(no_hot if kind == "dip_offload" else hot) if base == "cached_dip" else None,
-                             max_new_tokens=n_new, dip_dense_up=mode == "dip_dense_up",
+                             max_new_tokens=n_new, dip_dense_up=kind == "dip_dense_up",
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
-                             offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"))
+                             offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"),
+                             int4_head=int4_head)
         eng.capture()
         eng.generate(prompt[:8], 8)  # warm up the graphs
         torch.cuda.synchronize()
@@ -486,8 +493,8 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=mode == "dip_dense_up")
-        per_tok = c.layers * (attn_w + mlp) + w.lm_head.numel() * 2
+        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=kind == "dip_dense_up")
+        per_tok = c.layers * (attn_w + mlp) + head_bytes[int4_head]
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
                      "weight_bytes_per_token": per_tok,
@@ -499,6 +506,8 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         torch.cuda.empty_cache()
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
     out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"] == toks["cached_dip_staged"]
+    out["cached_dip_int4_head_tokens_equal_dip_int4_head"] = toks["dip_int4_head"] == toks["cached_dip_int4_head"]
+    assert out["cached_dip_int4_head_tokens_equal_dip_int4_head"], "cache-aware DIP must equal DIP (INT4 head)"
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
     for a, b in (("dense_offload", "dense"), ("dip_offload", "dip"), ("cached_dip_offload", "dip"),
                  ("dense_offload_serial", "dense"), ("dip_offload_serial", "dip"),
@@ -522,7 +531,8 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
                               "down_proj^T (2 launches per MLP); the selections of dip, y summed in "
                               "another order")
     out["config"] = {"prompt_tokens": n_prompt, "new_tokens": n_new, "dip_k": k, "hot_fraction": 0.2,
-                     "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed and LM head",
+                     "model": "random-init Qwen3-1.7B shape, 28 layers, INT4 g128 linears, fp16 embed; LM head fp16 "
+                              "(the reference's) or INT4 g128 (*_int4_head)",
                      "kv": "fp16, max_seq 2048"}
     return out
 
@@ -718,6 +728,13 @@ def bench_kernels(dev, gen):
     t = time_graph_per_launch(lambda W: _C.gemv_f16_into(W, x, logits), [(W,) for W in LM])
     res["lm_head_fp16_gemv"] = entry(V * H * 2 + 2 * H + 2 * V, t["mean_us"], kernel="gemv_f16")
     del LM
+    # the INT4 g128 head (config 5's "all weights INT4"): the same INT4 GEMV as every linear, 151936 rows
+    n_cp = max(2, cold_copies(V * (row + 4 * G)))
+    LQ = [(torch.randint(0, 256, (V, row), dtype=torch.uint8, device=dev, generator=gen),
+           torch.rand(V, G, device=dev, generator=gen) * 0.01 + 1e-3) for _ in range(n_cp)]
+    t = time_graph_per_launch(lambda W, S: _C.gemv_w4a16_into(W, S, x, logits, H, GS), LQ)
+    res["lm_head_int4_gemv"] = entry(V * (row + 4 * G) + 2 * H + 2 * V, t["mean_us"], kernel="gemv_int4 (StoreY)")
+    del LQ
     tok = torch.empty(1, dtype=i32, device=dev)
     aws = torch.empty(_C.argmax_workspace_bytes(V), dtype=torch.uint8, device=dev)
     t = time_graph_per_launch(lambda: _C.argmax_f16_into(logits, tok, None, None, aws), [()] * 64)

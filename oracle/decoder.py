@@ -120,11 +120,13 @@ class OracleLayer:
 
 
 class OracleDecoder:
-    """Greedy decoder over numpy copies of the weights; mode "dense" or "dip" (rule-A top-k of dip_k)."""
+    """Greedy decoder over numpy copies of the weights; mode "dense" or "dip" (rule-A top-k of dip_k).
+    lm_head_int4 = (packed rows, fp32 scales): the LM head as an INT4 group GEMV instead of the fp16 one."""
 
-    def __init__(self, cfg, embed, lm_head, final_norm, layers, mode="dense", dip_k=None):
+    def __init__(self, cfg, embed, lm_head, final_norm, layers, mode="dense", dip_k=None, lm_head_int4=None):
         self.c, self.embed, self.lm_head, self.final_norm, self.layers = cfg, embed, lm_head, final_norm, layers
         self.mode, self.k = mode, dip_k
+        self.lm_head_int4 = lm_head_int4
         c = cfg
         self.kc = [np.zeros((c.kv_heads, c.max_seq, c.head_dim), np.float16) for _ in range(c.layers)]
         self.vc = [np.zeros((c.kv_heads, c.max_seq, c.head_dim), np.float16) for _ in range(c.layers)]
@@ -171,6 +173,8 @@ class OracleDecoder:
 
     def logits(self) -> np.ndarray:
         xn = rmsnorm(self.x, self.final_norm, self.c.rms_eps)
+        if self.lm_head_int4 is not None:
+            return int4_gemv(self.lm_head_int4[0], self.lm_head_int4[1], xn, self.c.group_size)
         return gemv_f16(self.lm_head, xn)
 
 

@@ -104,12 +104,27 @@ class DecoderWeights:
     lm_head: torch.Tensor  # [V, H] fp16
     final_norm: torch.Tensor  # [H] fp16
     layers: list = field(default_factory=list)
+    # the LM head quantized like every linear (INT4, group config.group_size, fp32 scales): (packed [V, H/2],
+    # scales [V, H/gs]); made on first use by quantize_lm_head
+    lm_head_int4: Optional[tuple] = None
 
 
 def _quant_int4(w: torch.Tensor, gs: int):
     qt = formats.quantize(w, formats.QuantConfig(bits=4, granularity="group", group_size=gs))
     Wq, _ = pack.pack_int4(qt.qweight)
     return Wq.contiguous(), qt.scale.contiguous()
+
+
+def quantize_lm_head(w: "DecoderWeights") -> tuple:
+    """The fp16 LM head quantized with the linears' quantizer (symmetric INT4, group config.group_size, fp32
+    scales; formats.quantize + pack_int4), kept on the weights for later engines. The reference keeps its head
+    in fp16 (loader.py:55, generate.py:489-491); this is the head of a decoder whose weights are all INT4 g128."""
+    if w.lm_head_int4 is None:
+        V, H = w.lm_head.shape
+        rows = 16384  # quantize in row blocks: the fp32 copy of a whole 151936 x 2048 head would be 1.2 GB
+        parts = [_quant_int4(w.lm_head[r:r + rows].float(), w.config.group_size) for r in range(0, V, rows)]
+        w.lm_head_int4 = (torch.cat([p[0] for p in parts]).contiguous(), torch.cat([p[1] for p in parts]).contiguous())
+    return w.lm_head_int4
 
 
 def random_decoder(config: DecoderConfig = QWEN3_1P7B, seed: int = 0, device="cuda", linear_std: float = 0.02,
@@ -208,6 +223,9 @@ class DecodeEngine:
     defer_attention_combine=True (default, fused layers) a context long enough to split the attention across
     workgroups leaves its split states to the o projection, which combines them while its weight rows load
     (bit-identical to False, where the attention launch's last workgroup per KV head combines them).
+    int4_head=True runs the LM head as the INT4 g128 GEMV of the head quantized like the linears
+    (quantize_lm_head: 166 MB read per token instead of the fp16 head's 622 MB); the default is the reference's
+    fp16 head.
 
     All buffers are allocated here; decode steps launch only this package's kernels on the current stream
     and are captured into HIP graphs by capture()."""
@@ -216,7 +234,7 @@ class DecodeEngine:
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
                  dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
                  down_copy: bool = True, overlap_copy: bool = True, residual_epilogue: bool = True,
-                 defer_attention_combine: bool = True):
+                 defer_attention_combine: bool = True, int4_head: bool = False):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
         if offload and mode == "dip":
@@ -275,6 +293,8 @@ class DecodeEngine:
         self.defer_combine = bool(defer_attention_combine) and self.step_ws is not None and K_o % 32 == 0 and \
             K_o <= 2048
         self.counts = None  # optional per-layer channel selection counts (eager calibration only)
+        # LM head: fp16 GEMV (the reference's head), or the INT4 g128 GEMV of the quantized head
+        self.head_q = quantize_lm_head(w) if int4_head else None
 
         if mode != "dense":
             if dip_k is None or not 1 <= dip_k <= I:
@@ -652,7 +672,11 @@ class DecodeEngine:
 
     def _head(self):
         """LM head on the final-normed hidden state and argmax into the device token (and the log)."""
-        _C.gemv_f16_into(self.w.lm_head, self.hn, self.logits)
+        if self.head_q is not None:
+            _C.gemv_w4a16_into(self.head_q[0], self.head_q[1], self.hn, self.logits, self.c.hidden,
+                               self.c.group_size)
+        else:
+            _C.gemv_f16_into(self.w.lm_head, self.hn, self.logits)
         _C.argmax_f16_into(self.logits, self.token, self.log, self.log_len, self.argmax_ws)
 
     def _gen_step(self):

@@ -211,3 +211,44 @@ def test_full_qwen3_shape_first_tokens_match_oracle(dec):
     """28 layers, hidden 2048, 16/8 heads, I=6144, vocab 151936: dense, 2 prompt tokens, 2 new tokens."""
     w = dec.random_decoder(dec.QWEN3_1P7B, seed=0)
     run_against_oracle(dec, w, "dense", None, n_prompt=2, n_new=2, tol=5e-3)
+
+
+def test_int4_head_decode_matches_oracle(dec, tiny):
+    """int4_head=True: the LM head is the INT4 g128 GEMV of the head quantized like the linears; its logits
+    against the oracle decoder with the same quantized head (the quantization itself is the pinned quantizer),
+    dense and DIP, and graph replay == eager."""
+    Wq, S = dec.quantize_lm_head(tiny)
+    V, H = tiny.lm_head.shape
+    assert Wq.shape == (V, H // 2) and S.shape == (V, H // tiny.config.group_size)
+    from oracle import oracle as O
+
+    q_ref, s_ref = O.quantize_group(tiny.lm_head.float().cpu().numpy(), tiny.config.group_size)
+    assert np.array_equal(Wq.cpu().numpy(), O.pack_int4(q_ref)) and np.array_equal(S.cpu().numpy(), s_ref)
+    emb, lm, fn, layers = OD.from_device(tiny)
+    for mode, k, tol in (("dense", None, 5e-3), ("dip", 256, 2e-2)):
+        eng = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=6, int4_head=True)
+        ora = OD.OracleDecoder(tiny.config, emb, lm, fn, layers, mode=mode, dip_k=k,
+                               lm_head_int4=(Wq.cpu().numpy(), S.cpu().numpy()))
+        eng.reset()
+        prompt = prompt_ids(5, tiny.config.vocab)
+        eng.prefill(prompt, use_graph=False)
+        for t in prompt:
+            ora.step(t)
+        for i in range(5):
+            eng._head()
+            logits = eng.logits.float().cpu().numpy().astype(np.float64)
+            ref = ora.logits().astype(np.float64)
+            # the head GEMV itself on the engine's own final-normed state: the per-element GEMV bound
+            from helpers import assert_close
+
+            assert_close(eng.logits, O.gemv_w4_f64(Wq.cpu().numpy(), S.cpu().numpy(), eng.hn.cpu().numpy(), H,
+                                                   tiny.config.group_size), f"{mode} int4 head step {i}")
+            err = np.abs(logits - ref).max()
+            assert err <= tol * np.abs(ref).max(), f"{mode} step {i}: logits error vs oracle decoder"
+            tok = int(eng.token.item())
+            assert tok == OD.argmax_first(eng.logits.cpu().numpy()), "token = first maximum of the logits"
+            eng._layers()
+            ora.step(tok)
+        a = dec.DecodeEngine(tiny, mode, dip_k=k, max_new_tokens=6, int4_head=True)
+        eager = a.generate(prompt, 6, use_graph=False)
+        assert a.generate(prompt, 6, use_graph=True) == eager
