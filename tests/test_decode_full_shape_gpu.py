@@ -151,3 +151,105 @@ def test_config5_first_step_per_layer_matches_oracle(setup):
             assert torch.equal(o["down"], t["down"]), f"{name} layer {l} MLP output"
             assert torch.equal(o["h"], t["h"]), f"{name} layer {l} MLP input"
             assert torch.equal(o["h_sel"], t["h_sel"]), f"{name} layer {l} gated up h"
+
+
+# BASELINE config 5 at its stated lengths: a 64-token prompt, then 128 greedy tokens (positions 0 .. 191)
+N_PROMPT5, N_NEW5 = 64, 128
+
+
+def _prompt5(V):
+    return torch.randint(0, V, (N_PROMPT5,), generator=torch.Generator().manual_seed(7)).tolist()
+
+
+def test_config5_full_length_cached_dip_equals_dip(setup):
+    """64 + 128 tokens through 28 layers: cache-aware DIP (20% calibrated hot cache, misses from pinned host
+    memory, direct and staged) generates DIP's tokens and ends with its final hidden state, bit for bit."""
+    D, w, _, hot = setup
+    prompt = _prompt5(w.config.vocab)
+    dip = D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW5)
+    want = dip.generate(prompt, N_NEW5)
+    x_ref = dip.x_final.clone()
+    assert len(want) == N_PROMPT5 + N_NEW5 and int(dip.pos.item()) == N_PROMPT5 + N_NEW5
+    del dip
+    for path in ("direct", "staged"):
+        eng = D.DecodeEngine(w, "cached_dip", dip_k=DIP_K, hot_channels=hot, max_new_tokens=N_NEW5, miss_path=path)
+        got = eng.generate(prompt, N_NEW5)
+        assert got == want, f"cached DIP ({path}): tokens differ from DIP"
+        assert torch.equal(eng.x_final, x_ref), f"cached DIP ({path}): final hidden state differs from DIP"
+        del eng
+
+
+def test_config5_last_step_per_layer_matches_oracle(setup):
+    """The last step of the 64 + 128 token run (position 191), teacher-forced layer by layer on the engine's own
+    state after 191 positions: q/k norm + RoPE + the attention over the engine's own KV cache of 192 positions
+    against the binary64 oracle attention, the gate GEMV, rule-A selection, gated up values and sparse down
+    against the oracle as in the first-step test. (defer_attention_combine=False so the attention output is in
+    one buffer; the deferred form equals it bit for bit, tests/test_attn_combine_gpu.py.)"""
+    D, w, _, hot = setup
+    from soinfer import _C
+
+    c = w.config
+    I, H, gs, NQ, NKV, hd = c.intermediate, c.hidden, c.group_size, c.q_heads, c.kv_heads, c.head_dim
+    eng = D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW5, defer_attention_combine=False)
+    eng.capture()
+    eng.reset()
+    eng.prefill(_prompt5(c.vocab))
+    eng.decode(N_NEW5 - 1)
+    torch.cuda.synchronize()
+    pos = int(eng.pos.item())
+    assert pos == N_PROMPT5 + N_NEW5 - 1 == 191
+    trace = []
+
+    def hook(l):
+        trace.append({"h": eng.h.clone(), "gate": eng.gu[:I].clone(), "idx": eng.idx.clone(), "cnt": eng.cnt.clone(),
+                      "h_sel": eng.h_sel.clone(), "down": eng.down.clone(), "qkv": eng.qkv.clone(),
+                      "attn": eng.attn.clone()})
+
+    eng._head()
+    eng.layer_hook = hook
+    eng._layers()
+    eng.layer_hook = None
+    torch.cuda.synchronize()
+    assert len(trace) == c.layers
+    p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    for l, t in enumerate(trace):
+        L = w.layers[l]
+        # attention: q from the layer's own qkv by the q/k norm + RoPE op (tested against the oracle separately),
+        # the K/V caches as the engine left them (the appended row at 191 included)
+        q = torch.empty(NQ, hd, dtype=torch.float16, device="cuda")
+        kc, vc = eng.k_cache[l].clone(), eng.v_cache[l].clone()
+        _C.qk_norm_rope_append(t["qkv"], L.q_norm, L.k_norm, eng.cos_t, eng.sin_t, p, q, kc, vc, c.rms_eps)
+        assert torch.equal(kc, eng.k_cache[l]) and torch.equal(vc, eng.v_cache[l]), f"layer {l}: KV row at 191"
+        a_ref = O.decode_attention_f64(q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy(), pos + 1)
+        assert_close(t["attn"].view(NQ, hd), a_ref, f"layer {l} attention at L = {pos + 1}")
+        # MLP
+        h = t["h"].cpu().numpy()
+        gate = t["gate"].cpu().numpy()
+        assert_close(t["gate"], O.gemv_w4_f64(L.gu_Wq[:I].cpu().numpy(), L.gu_scale[:I].cpu().numpy(), h, H, gs),
+                     f"layer {l} gate")
+        idx = t["idx"].cpu().numpy()
+        assert int(t["cnt"].item()) == DIP_K
+        assert np.array_equal(idx, O.topk_rule_a(np.abs(gate.astype(np.float32)), DIP_K)), f"layer {l} selection"
+        u = OD.int4_gemv(L.gu_Wq[I:].cpu().numpy()[idx], L.gu_scale[I:].cpu().numpy()[idx], h, gs)
+        assert_close(t["h_sel"], OD.silu_mul(gate[idx], u).astype(np.float64), f"layer {l} gated up h", tol=2e-3)
+        dW, dS = L.down_T_Wq.cpu().numpy()[idx], L.down_T_scale.cpu().numpy()[idx]
+        assert_close(t["down"], O.sparse_accumulate_f64(dW, dS, t["h_sel"].cpu().numpy(), H, gs),
+                     f"layer {l} sparse down")
+
+
+def test_config5_int4_head_logits_match_oracle(setup):
+    """The INT4 g128 LM head at the full vocabulary (151936 x 2048): logits on the engine's own final-normed
+    state within the GEMV bound of the binary64 oracle, and the token their first maximum."""
+    D, w, prompt, _ = setup
+    c = w.config
+    Wq, S = D.quantize_lm_head(w)
+    eng = D.DecodeEngine(w, "dense", max_new_tokens=4, int4_head=True)
+    eng.reset()
+    eng.prefill(prompt[:2], use_graph=False)
+    for i in range(2):
+        eng._head()
+        torch.cuda.synchronize()
+        ref = O.gemv_w4_f64(Wq.cpu().numpy(), S.cpu().numpy(), eng.hn.cpu().numpy(), c.hidden, c.group_size)
+        assert_close(eng.logits, ref, f"INT4 head step {i}")
+        assert int(eng.token.item()) == OD.argmax_first(eng.logits.cpu().numpy())
+        eng._layers()
