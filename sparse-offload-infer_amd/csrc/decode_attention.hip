@@ -264,7 +264,18 @@ __device__ __forceinline__ float wave_sum(const float (*s_state)[REP][HD + 2], i
 constexpr int kCombineMaxSplits = kAttnTargetGroups;  // nsplit <= kAttnTargetGroups by construction of the plan
 constexpr int kCombineBatch = 32;
 
-template <int NT, int HD>
+// COHERENT: the states were written device-coherent in this launch by workgroups that may run on other XCDs
+// (the in-launch combine after the arrival), so they are read device-coherent too; across a launch boundary
+// plain loads see them.
+template <bool COHERENT>
+__device__ __forceinline__ float part_load(const float* p) {
+    if constexpr (COHERENT)
+        return ld_agent(p);
+    else
+        return ldg(p);
+}
+
+template <int NT, int HD, bool COHERENT = false>
 __device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint16_t* __restrict__ out, int h0, int rep,
                                            int nsplit, int ns, float* s_m, float* s_l) {
     constexpr int stride = HD + 2;
@@ -275,13 +286,13 @@ __device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint1
         const int o = tid < nout ? tid : 0;
         const float* po = part + static_cast<int64_t>(h0 + o / HD) * nsplit * stride + 2 + o % HD;
 #pragma unroll
-        for (int s = 0; s < kCombineBatch; ++s) v[s] = ldg(po + static_cast<int64_t>(s < ns ? s : 0) * stride);
+        for (int s = 0; s < kCombineBatch; ++s) v[s] = part_load<COHERENT>(po + static_cast<int64_t>(s < ns ? s : 0) * stride);
     }
     for (int i = tid; i < rep * ns; i += NT) {
         const int hh = i / ns, sp = i % ns;
         const float* ps = part + (static_cast<int64_t>(h0 + hh) * nsplit + sp) * stride;
-        s_m[hh * kCombineMaxSplits + sp] = ldg(ps);
-        s_l[hh * kCombineMaxSplits + sp] = ldg(ps + 1);
+        s_m[hh * kCombineMaxSplits + sp] = part_load<COHERENT>(ps);
+        s_l[hh * kCombineMaxSplits + sp] = part_load<COHERENT>(ps + 1);
     }
     __syncthreads();  // (m, l) of every split in LDS
     for (int o = tid; o < nout; o += NT) {
@@ -296,7 +307,7 @@ __device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint1
             if (o != tid || b0 > 0) {  // the first batch of the first output is already in v
 #pragma unroll
                 for (int s = 0; s < kCombineBatch; ++s)
-                    v[s] = ldg(po + static_cast<int64_t>(b0 + s < ns ? b0 + s : 0) * stride);
+                    v[s] = part_load<COHERENT>(po + static_cast<int64_t>(b0 + s < ns ? b0 + s : 0) * stride);
             }
 #pragma unroll
             for (int s = 0; s < kCombineBatch; ++s) {
@@ -579,11 +590,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         float w[kAttnWaves];
         const float M = wave_weights<REP, HD>(s_state, hh, w);
         const float v = e == 0 ? M : wave_sum<REP, HD>(s_state, hh, e, w);
-        stg(a.part + (static_cast<int64_t>(kvh * rep + hq0 + hh) * a.nsplit + split) * (HD + 2) + e, v);
+        float* dst = a.part + (static_cast<int64_t>(kvh * rep + hq0 + hh) * a.nsplit + split) * (HD + 2) + e;
+        if (a.defer)
+            stg(dst, v);  // read by the next launch
+        else
+            st_agent(dst, v);  // read in this launch by the last split, possibly on another XCD
     }
     if (a.defer) return;  // the consumer combines the states (gemv_attn_combine_kernel)
-    // arrival: the last of the ns splits of this workgroup's heads combines them (one counter per x)
-    arrive_release();
+    // arrival: the last of the ns splits of this workgroup's heads combines them (one counter per x); the states
+    // go out and come back device-coherent, so no L2 write-back or invalidate is needed (arrive_coherent)
+    arrive_coherent();
     if (tid == 0) {
         const uint32_t prev = atomicAdd(a.counters + gx, 1u);
         const bool last = prev + 1 == static_cast<uint32_t>(ns);
@@ -592,8 +608,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' states
-    combine_kv<kAttnThreads, HD>(a.part, a.out, kvh * rep + hq0, nhq, a.nsplit, ns, s_cm, s_cl);
+    combine_kv<kAttnThreads, HD, true>(a.part, a.out, kvh * rep + hq0, nhq, a.nsplit, ns, s_cm, s_cl);
 }
 
 // Second launch of the host-length form: workgroup kvh combines the split states of its query heads with

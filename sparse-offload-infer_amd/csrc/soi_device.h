@@ -328,27 +328,24 @@ __device__ __forceinline__ int reduce_rows_row(uint32_t lane) {
     return 0;
 }
 
-// Device-scope release by one thread before it signals other workgroups: the
-// fence writes this XCD's L2 back (buffer_wbl2), and the write-back must have
-// completed before the signal can be seen. The documented release sequence
-// waits on vmcnt after buffer_wbl2, but the compiler's wait insertion drops
-// that wait (observed in the gfx950 ISA of these kernels: the signalling
-// atomic or store directly follows buffer_wbl2), so the wait is explicit.
-__device__ __forceinline__ void release_agent() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Device-coherent (agent scope) 4-byte stores and loads (global_store / global_load with sc1): they reach,
+// and read from, the point where the XCDs' accesses are coherent, so data one workgroup writes this way is
+// visible to a workgroup on another XCD that reads it this way once the writer's stores have completed
+// (s_waitcnt) and the reader has observed the writer's signal (a device-scope atomic). That needs no L2
+// write-back (buffer_wbl2) before the signal and no L2 invalidate after it: measured on MI355X, those two
+// fences cost about 3-4 us per arrival, more than the round trips they order.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workgroup arrival, release side: every wave waits until its own stores have
-// completed (reached L2; a workgroup-scope fence does not wait for them), the
-// barrier makes that true for the whole workgroup, and then ONE device-scope
-// release by thread 0 writes the L2 lines back before thread 0 signals (a
-// release in every wave costs one L2 write-back per wave). Thread 0 must
-// perform the signalling atomic right after this returns.
-__device__ __forceinline__ void arrive_release() {
+// Workgroup arrival for data written with st_agent: every wave waits until its own stores have completed, and
+// the barrier makes that true for the whole workgroup; thread 0 then signals with a device-scope atomic.
+__device__ __forceinline__ void arrive_coherent() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) release_agent();
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

@@ -1,7 +1,7 @@
 // Sparse down projection over selected rows of down_proj^T: the work of one
-// (column slice, row chunk) item, shared by sparse_down.hip (one item per
-// workgroup) and the single-launch DIP MLP (dip_mlp.hip, two items per
-// workgroup). See sparse_down.hip for the layout and the arithmetic.
+// (column slice, row chunk) item, shared by the kernels of sparse_down.hip
+// (one item per workgroup). See sparse_down.hip for the layout and the
+// arithmetic.
 #pragma once
 
 #include "soi_device.h"
@@ -58,9 +58,9 @@ constexpr int kDownU = 6;                       // 8-row groups per wave per bat
 // reads g_zero16 instead, so the loads are issued unconditionally).
 constexpr int kRedFloats = kDownWaves * kGroupRows * kSliceChunks * kRedPitch;
 
-// One workgroup's share: rows [r*rpc, min((r+1)*rpc, k)) of slice blockIdx.x,
-// r = blockIdx.y, then the partial row, the arrival and (last workgroup of the
-// slice) the combine. red: kRedFloats floats of LDS; s_last: one LDS word.
+// One workgroup's share: rows [r*rpc, min((r+1)*rpc, k)) of slice `slice`
+// (both from down_item), then the partial row, the arrival and (last workgroup
+// of the slice) the combine. red: kRedFloats floats of LDS; s_last: one LDS word.
 // The work of item (slice, r) by a group of kDownWaves waves; gtid = the
 // thread's index inside its group. Every thread of the workgroup must call it
 // the same number of times (it holds workgroup barriers); a group with no item
@@ -172,16 +172,15 @@ __device__ __forceinline__ void sparse_down_item(const Rows& rows, const HS& hs,
 #pragma unroll
     for (int g = 0; g < kDownWaves * kGroupRows; ++g) part += red[(g * kSliceChunks + tc) * kRedPitch + ti];
     const int64_t col = static_cast<int64_t>(slice) * kSliceCols + tid;
-    if (active && col < H) stg(partial + static_cast<int64_t>(r) * H + col, part);
+    // the partial row goes out device-coherent (the slice's other items may run on other XCDs)
+    if (active && col < H) st_agent(partial + static_cast<int64_t>(r) * H + col, part);
 
-    // arrival: the last of the slice's R items sums the partial rows (arrive_release, with each group's
-    // thread 0 fencing its own signal)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // arrival: the last of the slice's R items sums the partial rows (arrive_coherent: no L2 write-back or
+    // invalidate, the partial rows are written and read device-coherent)
+    arrive_coherent();
     if (tid == 0) {
         bool last = false;
         if (active) {
-            release_agent();
             const uint32_t prev = atomicAdd(counters + slice, 1u);
             last = prev + 1 == static_cast<uint32_t>(R);
             if (last) atomicExch(counters + slice, 0u);
@@ -190,7 +189,6 @@ __device__ __forceinline__ void sparse_down_item(const Rows& rows, const HS& hs,
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other items' partial rows
     if (col >= H) return;
     const float* pc = partial + col;
     float sum = 0.0f;
@@ -198,12 +196,31 @@ __device__ __forceinline__ void sparse_down_item(const Rows& rows, const HS& hs,
     for (; rr + 8 <= R; rr += 8) {
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ldg(pc + static_cast<int64_t>(rr + u) * H);
+        for (int u = 0; u < 8; ++u) v[u] = ld_agent(pc + static_cast<int64_t>(rr + u) * H);
 #pragma unroll
         for (int u = 0; u < 8; ++u) sum += v[u];
     }
-    for (; rr < R; ++rr) sum += ldg(pc + static_cast<int64_t>(rr) * H);
+    for (; rr < R; ++rr) sum += ld_agent(pc + static_cast<int64_t>(rr) * H);
     stg(y + col, f32_to_f16_bits(sum));
+}
+
+// Item (slice, row chunk) of the workgroup in a grid of S x R workgroups. Workgroups are dispatched to the 8
+// XCDs round-robin by linear id; with R a multiple of 8, XCD x takes row chunks x, x + 8, ... of every slice
+// (linear id 8i + x -> slice i % S, chunk x + 8 (i / S)), so the S workgroups reading the same rows share one
+// L2: each row's scale line, index and coefficient are fetched once per chunk instead of once per slice (the
+// identity order put every slice on its own XCD, each fetching every row's 64-byte scale line). Otherwise the
+// identity order.
+__device__ __forceinline__ void down_item(int& slice, int& r) {
+    const int S = static_cast<int>(gridDim.x), R = static_cast<int>(gridDim.y);
+    if (R % 8 == 0) {
+        const int L = static_cast<int>(blockIdx.x) + S * static_cast<int>(blockIdx.y);
+        const int x = L & 7, i = L >> 3;
+        slice = i % S;
+        r = x + 8 * (i / S);
+    } else {
+        slice = static_cast<int>(blockIdx.x);
+        r = static_cast<int>(blockIdx.y);
+    }
 }
 
 // Partition: S = ceil(chunks / 8) slices; each slice's k rows split into R

@@ -17,11 +17,15 @@
 //   * the 32 (wave, row-in-group) partials of each column are summed through
 //     LDS in a fixed order and the workgroup writes one fp32 partial row of
 //     256 columns to the workspace;
-//   * arrival (arrive_release): every wave waits for its partial stores to
-//     complete, then one thread releases them at device scope and counts the
-//     workgroup in on the slice's counter; the last of the slice's R
-//     workgroups acquires, sums the R partial rows of the slice in ascending
-//     r and writes fp16 y, and resets the counter to zero.
+//   * the partial rows are written and read device-coherent (st_agent /
+//     ld_agent); arrival (arrive_coherent): every wave waits for its partial
+//     stores to complete, then one thread counts the workgroup in on the
+//     slice's counter; the last of the slice's R workgroups sums the R partial
+//     rows of the slice in ascending r, writes fp16 y, and resets the counter
+//     to zero (no L2 write-back or invalidate);
+//   * items are placed XCD-aware (down_item): the workgroups of one row chunk
+//     share an XCD, so the chunk's scales, indices and coefficients are
+//     fetched into one L2 once.
 // Fixed partition and fixed order: deterministic, and every row source
 // (gathered rows, hot cache + staging descriptors, resident index list) gives
 // bit-identical results for the same logical rows.
@@ -42,8 +46,9 @@ __global__ __launch_bounds__(kDownThreads) void sparse_down_kernel(Rows rows, co
                                                                     int gs, int rpc, int R) {
     __shared__ float red[kRedFloats];
     __shared__ int s_last;
-    sparse_down_item<U, VEC, CHUNK_SCALE>(rows, hs, y, partial, counters, k, H, gs, rpc, R, red, &s_last,
-                                          static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y),
+    int slice, r;
+    down_item(slice, r);
+    sparse_down_item<U, VEC, CHUNK_SCALE>(rows, hs, y, partial, counters, k, H, gs, rpc, R, red, &s_last, slice, r,
                                           static_cast<int>(threadIdx.x), true);
 }
 
@@ -107,7 +112,9 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
     __shared__ uint16_t s_g[kFusedMaxRpc];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int base_i = wave * kWave * E + lane;
-    const int64_t j0 = static_cast<int64_t>(blockIdx.y) * rpc;
+    int slice, chunk;
+    down_item(slice, chunk);
+    const int64_t j0 = static_cast<int64_t>(chunk) * rpc;
     const int64_t j1 = (j0 + rpc < k) ? j0 + rpc : static_cast<int64_t>(k);
 
     uint32_t raw[E];
@@ -127,7 +134,7 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
         local_max = fmaxf(local_max, val[j]);
     }
     const float tau = rule_a_tau<E, kDownWaves, F16AbsValues>(key, local_max, s_hist, s_max, k, tid);
-    const bool writer = blockIdx.x == 0;
+    const bool writer = slice == 0;
     // only this workgroup's chunk [j0, j1) of the positions is emitted
     const uint32_t total = rule_a_compact<E, kDownWaves>(
         val, tau, s_tot, tid, static_cast<uint32_t>(j0), static_cast<uint32_t>(j1), [&](uint32_t pos, int j) {
@@ -137,12 +144,11 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
             if (writer) stg(out_idx + pos, static_cast<int32_t>(c));
         });
     const int64_t kk = total < static_cast<uint32_t>(k) ? static_cast<int64_t>(total) : static_cast<int64_t>(k);
-    if (writer && blockIdx.y == 0 && tid == 0) stg(out_count, static_cast<int32_t>(kk));
+    if (writer && chunk == 0 && tid == 0) stg(out_count, static_cast<int32_t>(kk));
     __syncthreads();  // s_ch / s_g of the chunk complete
     sparse_down_item<kDownU, VEC, CHUNK_SCALE>(LdsIndexRows{W, S, s_ch, j0, row_bytes, G},
                                                LdsGatedH{s_g, s_ch, up, j0}, y, partial, counters, kk, H, gs, rpc,
-                                               R, red, &s_last, static_cast<int>(blockIdx.x),
-                                               static_cast<int>(blockIdx.y), tid, true);
+                                               R, red, &s_last, slice, chunk, tid, true);
 }
 
 // Workspace: the S arrival counters first (their place depends on H only, so
