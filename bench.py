@@ -812,6 +812,45 @@ def bench_kernels(dev, gen):
     return res
 
 
+def bench_grid_barrier(dev):
+    """The cost of one grid-wide barrier among P co-resident workgroups (csrc/grid_sync.hip: O(P) arrival over
+    8 per-XCD counters and a global one, one polling lane per workgroup, data exchanged device-coherent; and the
+    same with an agent-scope release / acquire pair), against the boundary between two dependent launches of a
+    captured graph, which is what a persistent decode launch would replace by such a barrier. Per barrier:
+    (span of 201 rounds - span of 1 round) / 200, best of 5, from s_memrealtime stamps."""
+    import torch
+
+    from soinfer import _C
+
+    out = {}
+    maxp = _C.grid_barrier_max_workgroups()
+    for fenced in (False, True):
+        for P in (256, 1024):
+            if P > maxp:
+                continue
+            ws = torch.zeros(_C.grid_barrier_bench_workspace_bytes(P), dtype=torch.uint8, device=dev)
+            spans = {}
+            for rounds in (1, 201):
+                best = None
+                for _ in range(5):
+                    _C.grid_barrier_bench(fenced, P, rounds, ws)
+                    torch.cuda.synchronize()
+                    st = ws[4608:4608 + 16 * P].view(torch.int64).view(P, 2).cpu()
+                    span = int((st[:, 1].max() - st[:, 0].min()).item()) * 10  # 100 MHz stamps -> ns
+                    best = span if best is None else min(best, span)
+                spans[rounds] = best
+            err = ws[:4608].view(torch.int32)[1088:1090].tolist()
+            assert err == [0, 0], f"grid barrier: timeout flag / mismatches {err}"
+            out[f"{'fenced_' if fenced else ''}P{P}_us"] = round((spans[201] - spans[1]) / 200 / 1e3, 3)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    out["graph_launch_boundary_us"] = round(graph_time_us(lambda: [_C.advance_position(pos, 1) for _ in range(100)])
+                                            / 100, 3)
+    out["note"] = ("P workgroups of 256 threads; per barrier = (201 rounds - 1 round) / 200. A persistent decode launch "
+                   "would replace each graph launch boundary by one such barrier (plus the device-coherent reload of "
+                   "the exchanged vector), so it cannot beat the launch chain")
+    return out
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -1150,6 +1189,8 @@ def main() -> int:
         log("top-k done")
         detail["kernels"] = bench_kernels(dev, gen)
         log("kernel table done")
+        detail["grid_barrier"] = bench_grid_barrier(dev)
+        log(f"grid barrier: {detail['grid_barrier']}")
     if not args.no_decode:
         from soinfer.runtime import decoder as D
 

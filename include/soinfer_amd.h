@@ -571,6 +571,29 @@ int soi_dip_select_dense_down_residual(const uint16_t* gate, const uint16_t* h, 
                                        int32_t* out_count, uint16_t* y, const uint16_t* res, uint16_t* res_out,
                                        int64_t H, int64_t group_size, int64_t num_groups, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Grid-wide barrier cost (measurement; no counterpart in the reference, whose
+ * decode runs one kernel per op). A persistent decode launch would replace
+ * each dependent launch boundary by a barrier among co-resident workgroups;
+ * this measures the cheapest such barrier on the device: P workgroups of 256
+ * threads run `rounds` rounds of (write 64 words device-coherent, barrier,
+ * read another workgroup's words and count mismatches). Arrival is O(P) over
+ * 8 counters (one per XCD) and a global counter, one lane per workgroup polls
+ * one of 8 generation copies; fenced = 1 adds an agent-scope release before
+ * the arrival and an acquire after the wait (plain data stores and loads).
+ * Workspace (soi_grid_barrier_bench_workspace_bytes(P), 16-byte aligned,
+ * zero-filled before the first call; calls and replays may reuse it):
+ * bytes [0, 4608) the sync block (uint32 word 1088: 1 if a bounded wait gave
+ * up; word 1089: mismatched words), then 2 x P uint64 s_memrealtime stamps
+ * (100 MHz; begin and end of workgroup b at 2b, 2b + 1), then the data.
+ * P must not exceed soi_grid_barrier_max_workgroups() (every workgroup
+ * resident at once); larger P is rejected before any launch.
+ * ------------------------------------------------------------------------ */
+size_t soi_grid_barrier_bench_workspace_bytes(int64_t P);
+int soi_grid_barrier_max_workgroups(int64_t* max_workgroups);
+int soi_grid_barrier_bench(int fenced, int64_t P, int64_t rounds, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,7 +29,7 @@ BUILD = PKG_ROOT / "_build"
 
 ARCH = os.environ.get("SOINFER_HIP_ARCH", "gfx950")
 HIP_SOURCES = ["decoder.hip", "capi.hip", "gemv_int4.hip", "gemv_int8.hip", "topk_select.hip", "dip_descriptors.hip",
-               "sparse_down.hip", "decode_attention.hip", "dip_dense_down.hip"]
+               "sparse_down.hip", "decode_attention.hip", "dip_dense_down.hip", "grid_sync.hip"]
 HIP_LIB = SOINFER / "libsoinfer_hip.so"
 EXT_LIB = SOINFER / ("_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 

@@ -1466,6 +1466,27 @@ void gemv_dip_cached_down_into(torch::Tensor cache_Wq, torch::Tensor cache_scale
                  n);
 }
 
+// ---- grid barrier cost (measurement) ----
+int64_t grid_barrier_bench_workspace_bytes(int64_t P) {
+    return static_cast<int64_t>(soi_grid_barrier_bench_workspace_bytes(P));
+}
+
+int64_t grid_barrier_max_workgroups() {
+    int64_t p = 0;
+    check_status(soi_grid_barrier_max_workgroups(&p), "grid_barrier_max_workgroups");
+    return p;
+}
+
+void grid_barrier_bench(bool fenced, int64_t P, int64_t rounds, torch::Tensor workspace) {
+    const char* n = "grid_barrier_bench";
+    TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == torch::kUInt8 && workspace.is_contiguous(), n,
+                ": workspace must be a contiguous uint8 CUDA tensor");
+    const at::DeviceGuard guard(workspace.device());
+    check_status(soi_grid_barrier_bench(fenced ? 1 : 0, P, rounds, workspace.data_ptr(),
+                                        static_cast<size_t>(workspace.numel()), cur_stream(workspace)),
+                 n);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "soinfer MI355X (gfx950) quantized decode hot path";
     m.def("gemv_w8a16", &gemv_w8a16, "INT8 GEMV");
@@ -1526,6 +1547,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("silu_mul_indexed_into", &silu_mul_indexed_into, "fp16(silu(gate[idx]) * u_sel)");
     m.def("embed_lookup_into", &embed_lookup_into, "embedding row of a device token");
     m.def("advance_position", &advance_position, "pos[0] += delta on the device");
+    m.def("grid_barrier_bench_workspace_bytes", &grid_barrier_bench_workspace_bytes,
+          "workspace bytes of grid_barrier_bench for P workgroups");
+    m.def("grid_barrier_max_workgroups", &grid_barrier_max_workgroups,
+          "most workgroups of the barrier measurement kernel resident at once");
+    m.def("grid_barrier_bench", &grid_barrier_bench,
+          "rounds of a grid-wide barrier among P co-resident workgroups, stamped (measurement)");
     m.def("topk_threshold_select_f16abs_into", &topk_threshold_select_f16abs_into,
           "threshold top-k over |fp16 gate| into caller buffers");
     m.def("host_device_pointer", &host_device_pointer, "device address of pinned host memory");
