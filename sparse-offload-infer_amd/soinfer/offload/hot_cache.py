@@ -18,7 +18,7 @@ the staged H2D gather instead (the reference's offload setting).
 """
 from __future__ import annotations
 
-from collections import OrderedDict
+import heapq
 from dataclasses import dataclass
 from typing import Iterable, Optional, Sequence
 
@@ -43,125 +43,148 @@ class SimulationResult:
         return self.hits / self.total if self.total else 0.0
 
 
-class StaticFrequencyPolicy:
-    """Fixed hot set: the cache_size channels of highest frequency, lower index first on ties."""
+class _TraceSimulator:
+    """Replays a selection trace token by token and counts cache hits. A token is the set of channels one
+    decode step selects (sorted ascending here, whatever order the trace gives); a subclass's _step(t, chans)
+    returns how many of them hit and updates its cache. cache_size <= 0 means no cache (every lookup misses)."""
+
+    name = ""
+
+    def __init__(self, cache_size: int):
+        self.cache_size = int(cache_size)
+
+    def _begin(self) -> None:
+        """Forget the state of a previous replay."""
+
+    def _step(self, t: int, chans: list) -> int:
+        raise NotImplementedError
+
+    def simulate(self, trace: Iterable) -> SimulationResult:
+        self._begin()
+        hits = total = 0
+        for t, selected in enumerate(trace):
+            chans = _sorted_ints(selected)
+            total += len(chans)
+            hits += self._step(t, chans)
+        return SimulationResult(self.name, self.cache_size, hits, total)
+
+
+class StaticFrequencyPolicy(_TraceSimulator):
+    """Fixed hot set: the cache_size channels of highest frequency, lower index first on ties
+    (hot_cache.py:67-95 of the reference)."""
 
     name = "static"
 
     def __init__(self, frequencies: torch.Tensor | Sequence[int], cache_size: int):
         freq = torch.as_tensor(frequencies).to(torch.int64).cpu()
-        n = freq.numel()
-        self.cache_size = min(int(cache_size), n)
-        # stable sort by descending frequency keeps ascending index among equals
-        order = torch.sort(-freq, stable=True).indices
-        self.hot_indices = torch.sort(order[: self.cache_size]).values
+        super().__init__(min(int(cache_size), freq.numel()))
+        # a stable sort on -frequency leaves equal frequencies in ascending channel order
+        ranked = torch.sort(-freq, stable=True).indices
+        self.hot_indices = torch.sort(ranked[: self.cache_size]).values
         self.hot_set = frozenset(self.hot_indices.tolist())
 
-    def simulate(self, trace: Iterable) -> SimulationResult:
-        hits = total = 0
-        for selected in trace:
-            for c in _sorted_ints(selected):
-                total += 1
-                hits += c in self.hot_set
-        return SimulationResult(self.name, self.cache_size, hits, total)
+    def _step(self, t: int, chans: list) -> int:
+        return sum(1 for c in chans if c in self.hot_set)
 
 
-class LRUPolicy:
-    """Least-recently-selected eviction, no calibration (hot_cache.py:98-141).
+class LRUPolicy(_TraceSimulator):
+    """Online cache that evicts the channel selected longest ago; needs no calibration (reference
+    hot_cache.py:98-141).
 
-    A token's selected channels are all looked up against the cache as it stood at the end of the previous
-    token (hits become most recent); only then are the token's misses inserted, in ascending channel order,
-    each evicting the least recently used entry when the cache is full. This is how the device cache behaves
-    per token (descriptors for the whole selection, then one update), and it keeps cross-token reuse visible
-    when one token selects more channels than the cache holds."""
+    Per token, as the device cache works (every selected channel resolved against the cache, then one update):
+    first every channel of the token is looked up in the cache as the previous token left it, each hit
+    refreshing its recency (ascending channel order); then the token's misses go in, ascending, each evicting
+    the least recently used channel while the cache is full. Looking up and inserting channel by channel
+    instead would let a token that selects more channels than the cache holds evict everything the previous
+    token left before it is looked up. Recency is a tick per touch; the eviction order is a heap of (tick,
+    channel) entries, where entries whose channel was touched again since are skipped when they surface."""
 
     name = "lru"
 
-    def __init__(self, cache_size: int):
-        self.cache_size = int(cache_size)
+    def _begin(self) -> None:
+        self._tick = 0
+        self._last = {}  # cached channel -> tick of its latest touch
+        self._heap = []  # (tick, channel); stale entries skipped on pop
 
-    def simulate(self, trace: Iterable) -> SimulationResult:
-        cache: "OrderedDict[int, None]" = OrderedDict()  # first = least recently used
-        hits = total = 0
-        for selected in trace:
-            chans = _sorted_ints(selected)
-            total += len(chans)
-            missed = []
-            for c in chans:
-                if c in cache:
-                    cache.move_to_end(c)
-                    hits += 1
-                else:
-                    missed.append(c)
-            if self.cache_size <= 0:
+    def _touch(self, c: int) -> None:
+        self._tick += 1
+        self._last[c] = self._tick
+        heapq.heappush(self._heap, (self._tick, c))
+
+    def _step(self, t: int, chans: list) -> int:
+        hit = [c for c in chans if c in self._last]
+        for c in hit:
+            self._touch(c)
+        if self.cache_size <= 0:
+            return len(hit)
+        for c in chans:
+            if c in self._last:
                 continue
-            for c in missed:
-                if len(cache) >= self.cache_size:
-                    cache.popitem(last=False)
-                cache[c] = None
-        return SimulationResult(self.name, self.cache_size, hits, total)
+            while len(self._last) >= self.cache_size:
+                tick, old = heapq.heappop(self._heap)
+                if self._last.get(old) == tick:  # the entry is current: old is the least recently used
+                    del self._last[old]
+            self._touch(c)
+        return len(hit)
 
 
-class LFUDecayPolicy:
-    """Lowest-frequency eviction with periodic decay (hot_cache.py:144-187).
+class LFUDecayPolicy(_TraceSimulator):
+    """Online cache that evicts the channel of lowest decayed frequency (reference hot_cache.py:144-187).
 
-    Every selection adds 1 to its channel's frequency (before the lookup); a miss into a full cache evicts
-    the cached channel of lowest frequency, the higher index on ties (the lower index stays, as in
-    StaticFrequencyPolicy). After every decay_every tokens all tracked frequencies are multiplied by
-    decay in (0, 1], so stale popularity fades."""
+    Each selection first adds 1 to its channel's frequency, then looks the channel up; a miss into a full
+    cache replaces the cached channel of lowest frequency (of two equal, the higher index leaves, as the
+    static policy keeps the lower one). Every decay_every tokens every frequency seen so far is multiplied by
+    decay (0 < decay <= 1), so a channel popular long ago loses its claim."""
 
     name = "lfu_decay"
 
     def __init__(self, cache_size: int, decay: float = 0.98, decay_every: int = 50):
-        if not (0.0 < decay <= 1.0):
-            raise ValueError("decay must be in (0, 1]")
-        self.cache_size = int(cache_size)
+        if not 0.0 < decay <= 1.0:
+            raise ValueError(f"LFUDecayPolicy: decay must satisfy 0 < decay <= 1, got {decay}")
+        super().__init__(cache_size)
         self.decay = float(decay)
         self.decay_every = int(decay_every)
 
-    def simulate(self, trace: Iterable) -> SimulationResult:
-        freq: dict = {}
-        cache: set = set()
-        hits = total = 0
-        for step, selected in enumerate(trace):
-            for c in _sorted_ints(selected):
-                total += 1
-                freq[c] = freq.get(c, 0.0) + 1.0
-                if c in cache:
-                    hits += 1
-                    continue
-                if self.cache_size <= 0:
-                    continue
-                if len(cache) >= self.cache_size:
-                    # lowest frequency first; among equal frequencies the highest index goes
-                    cache.remove(min(cache, key=lambda x: (freq[x], -x)))
-                cache.add(c)
-            if self.decay_every > 0 and (step + 1) % self.decay_every == 0:
-                for ch in freq:
-                    freq[ch] *= self.decay
-        return SimulationResult(self.name, self.cache_size, hits, total)
+    def _begin(self) -> None:
+        self._freq = {}  # channel -> decayed selection count
+        self._cached = set()
+
+    def _step(self, t: int, chans: list) -> int:
+        f, cached = self._freq, self._cached
+        n_hit = 0
+        for c in chans:
+            f[c] = f.get(c, 0.0) + 1.0
+            if c in cached:
+                n_hit += 1
+            elif self.cache_size > 0:
+                if len(cached) >= self.cache_size:
+                    cached.remove(min(cached, key=lambda x: (f[x], -x)))
+                cached.add(c)
+        if self.decay_every > 0 and (t + 1) % self.decay_every == 0:
+            for c in f:
+                f[c] *= self.decay
+        return n_hit
 
 
 def compare_policies(trace: Sequence, cache_sizes: Sequence[int], frequencies: Optional[Sequence[int]] = None,
                      **lfu_kwargs) -> list:
-    """Static, LRU and LFU-with-decay over the same trace at each cache size (hot_cache.py:190-218).
+    """For each cache size, the static, LRU and LFU-with-decay results over one trace, in that order
+    (reference hot_cache.py:190-218).
 
-    frequencies (for the static policy) default to the trace's own per-channel selection counts, i.e. the
-    static policy's best case; pass calibration counts to evaluate it on held-out traffic instead."""
-    trace = list(trace)
+    Without frequencies the static policy ranks channels by their counts in the trace itself (its best case);
+    calibration counts from other tokens evaluate it on held-out traffic instead."""
+    tokens = [_sorted_ints(sel) for sel in trace]
     if frequencies is None:
-        counts: dict = {}
-        for selected in trace:
-            for c in _sorted_ints(selected):
-                counts[c] = counts.get(c, 0) + 1
-        n = max(counts) + 1 if counts else 0
-        frequencies = [counts.get(c, 0) for c in range(n)]
-    out = []
+        n = 1 + max((c for tok in tokens for c in tok), default=-1)
+        frequencies = [0] * n
+        for tok in tokens:
+            for c in tok:
+                frequencies[c] += 1
+    results = []
     for size in cache_sizes:
-        out.append(StaticFrequencyPolicy(frequencies, size).simulate(trace))
-        out.append(LRUPolicy(size).simulate(trace))
-        out.append(LFUDecayPolicy(size, **lfu_kwargs).simulate(trace))
-    return out
+        for sim in (StaticFrequencyPolicy(frequencies, size), LRUPolicy(size), LFUDecayPolicy(size, **lfu_kwargs)):
+            results.append(sim.simulate(tokens))
+    return results
 
 
 @dataclass

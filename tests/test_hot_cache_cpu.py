@@ -61,3 +61,28 @@ def test_compare_policies_runs_all_three_per_size():
     assert all(r.total == 8 for r in res)
     # static with the trace's own counts (0:2, 1:4, 2:1, 3:1): size 1 keeps {1} -> 4 hits; size 2 {0, 1} -> 6
     assert (res[0].hits, res[3].hits) == (4, 6)
+
+
+def test_lru_heap_equals_a_list_replay_on_random_traces():
+    """The heap-based LRU against a plain recency list replayed by hand (look up the whole token, then insert its
+    misses ascending, evicting from the front), over random traces with tokens larger than the cache."""
+    import random
+
+    rng = random.Random(5)
+    for size in (0, 1, 3, 8, 20):
+        trace = [rng.sample(range(40), rng.randint(1, 25)) for _ in range(60)]
+        recency, hits = [], 0
+        for tok in trace:
+            tok = sorted(tok)
+            for c in tok:
+                if c in recency:
+                    hits += 1
+                    recency.remove(c)
+                    recency.append(c)
+            for c in tok:
+                if c not in recency and size > 0:
+                    if len(recency) >= size:
+                        recency.pop(0)
+                    recency.append(c)
+        r = HC.LRUPolicy(size).simulate(trace)
+        assert r.hits == hits and r.total == sum(len(t) for t in trace), size
