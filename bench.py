@@ -21,6 +21,7 @@ FETCH_SIZE / WRITE_SIZE counter summary committed under profiles/, null when
 absent), decode_tok_s (config 5 per mode) and cpu_baseline. Everything else is
 one 'bench-detail: {...}' line on stderr (and --detail-json PATH):
   batched_per_class  the same GEMVs as one launch per shape class, per class;
+  int8_batched_per_class  the INT8 g128 GEMVs of the same shapes, one batched launch per class;
   copy_reference  a plain device-to-device copy of 512 MiB (the calibration
                   kernel of the counter runs, and the box's streaming rate), and
                   by_size: the same copy of one gate/up GEMV's bytes, of 64 MB and of a step;
@@ -1147,6 +1148,24 @@ def main() -> int:
                                       "frac_of_hbm": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
         del bt
     log("per-class batched launches done")
+    # the INT8 g128 half of config 2 at the same scale: one batched launch per shape over 28 (down) or 56 distinct
+    # weight copies (the quantized values of one matrix per shape, copied: the bytes, not the values, matter here)
+    int8_per_class = {}
+    for names, N, K in ((("down",), H, I), (("gate", "up"), I, H), (("q", "o"), NQ * HD, H), (("k", "v"), NKV * HD, H)):
+        P = LAYERS * len(names)
+        q8, s8 = make_int8(N, K, gen, dev)
+        Q8 = [q8.clone() for _ in range(P)]
+        S8 = [s8.clone() for _ in range(P)]
+        X8 = [torch.randn(K, generator=gen, device=dev).half() for _ in range(P)]
+        b8 = ops.Int8Batch(Q8, S8, X8, GS)
+        us = time_back_to_back(b8.run, launches=20)
+        nbytes = P * int8_bytes(N, K)
+        int8_per_class["/".join(names)] = {"problems": P, "N": N, "K": K, "bytes": nbytes, "us": round(us, 3),
+                                           "GBps": round(nbytes / us / 1e3, 1),
+                                           "frac_of_hbm": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+        del Q8, S8, X8, b8
+    torch.cuda.empty_cache()
+    log("INT8 per-class batched launches done")
     copy_ref = copy_reference()
     # the same copy at the sizes the kernels here move: one gate/up GEMV's bytes, 64 MB, and a whole step
     copy_ref["by_size"] = {str(nb): copy_reference(nb, reps=30 if nb < (256 << 20) else 10)
@@ -1177,7 +1196,7 @@ def main() -> int:
     }
     # everything else goes to the detail record (stderr, and --detail-json): the result line stays compact
     detail = {"dominant_launch_back_to_back_after_timed_us": round(dom_b2b_us, 3), "copy_reference": copy_ref,
-              "batched_per_class": per_class, "step_spread": step_stats}
+              "batched_per_class": per_class, "int8_batched_per_class": int8_per_class, "step_spread": step_stats}
     if not args.no_extras:
         detail["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
         log("decode chain done")

@@ -99,6 +99,15 @@ int soi_gemv_w4a16_grouped(const uint8_t* const* Wq_ptrs, const float* const* sc
  * ------------------------------------------------------------------------ */
 int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N, int64_t K,
                    int64_t group_size, int64_t num_groups, int64_t scale_row_stride, void* stream);
+/* Batched INT8 form: P independent problems of one shape in ONE launch; Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs
+ * are DEVICE arrays of P device pointers (problem p: Wq [N, K], scale with the row stride above, x [K], y [N]).
+ * Each y is bit-identical to soi_gemv_w8a16 on that problem (same tile for the shape). A problem with a null
+ * pointer is skipped; with K % 16 == 0, one whose Wq or x is not 16-byte aligned gets NaN rows (soinfer.ops.
+ * Int8Batch rejects such problems before launch). No reference counterpart: the per-launch latency floor
+ * amortised over many GEMVs, as soi_gemv_w4a16_batched does for INT4. */
+int soi_gemv_w8a16_batched(const int8_t* const* Wq_ptrs, const float* const* scale_ptrs, const uint16_t* const* x_ptrs,
+                           uint16_t* const* y_ptrs, int64_t P, int64_t N, int64_t K, int64_t group_size,
+                           int64_t num_groups, int64_t scale_row_stride, void* stream);
 
 /* --------------------------------------------------------------------------
  * Deterministic threshold top-k over non-negative values (Dynamic Input

@@ -164,6 +164,26 @@ void gemv_w4a16_batched(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::
                  name);
 }
 
+// P same-shape INT8 GEMVs in one launch; pointer tables built (and validated) by soinfer.ops.Int8Batch.
+void gemv_w8a16_batched(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::Tensor x_ptrs, torch::Tensor y_ptrs,
+                        int64_t N, int64_t K, int64_t group_size, int64_t num_groups, int64_t scale_row_stride) {
+    const char* name = "gemv_w8a16_batched";
+    for (const auto* t : {&Wq_ptrs, &scale_ptrs, &x_ptrs, &y_ptrs}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kInt64 && t->dim() == 1 && t->is_contiguous(), name,
+                    ": pointer tables must be contiguous 1D int64 CUDA tensors");
+        TORCH_CHECK(t->size(0) == Wq_ptrs.size(0), name, ": pointer tables must have the same length");
+        check_same_device(Wq_ptrs, *t, name);
+    }
+    const at::DeviceGuard guard(Wq_ptrs.device());
+    check_status(soi_gemv_w8a16_batched(reinterpret_cast<const int8_t* const*>(Wq_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const float* const*>(scale_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<const uint16_t* const*>(x_ptrs.data_ptr<int64_t>()),
+                                        reinterpret_cast<uint16_t* const*>(y_ptrs.data_ptr<int64_t>()),
+                                        Wq_ptrs.size(0), N, K, group_size, num_groups, scale_row_stride,
+                                        cur_stream(Wq_ptrs)),
+                 name);
+}
+
 void gemv_w4a16_grouped(torch::Tensor Wq_ptrs, torch::Tensor scale_ptrs, torch::Tensor x_ptrs, torch::Tensor y_ptrs,
                         std::vector<int64_t> class_count, std::vector<int64_t> class_N, std::vector<int64_t> class_K,
                         int64_t group_size) {
@@ -1547,6 +1567,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("silu_mul_indexed_into", &silu_mul_indexed_into, "fp16(silu(gate[idx]) * u_sel)");
     m.def("embed_lookup_into", &embed_lookup_into, "embedding row of a device token");
     m.def("advance_position", &advance_position, "pos[0] += delta on the device");
+    m.def("gemv_w8a16_batched", &gemv_w8a16_batched, "P same-shape INT8 GEMVs in one launch (device pointer tables)");
     m.def("grid_barrier_bench_workspace_bytes", &grid_barrier_bench_workspace_bytes,
           "workspace bytes of grid_barrier_bench for P workgroups");
     m.def("grid_barrier_max_workgroups", &grid_barrier_max_workgroups,

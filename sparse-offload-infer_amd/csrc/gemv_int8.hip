@@ -23,13 +23,14 @@
 
 namespace soi {
 
+// Rows row0 .. row0 + R - 1 of one problem, by the calling wave (the single and batched kernels share it, so a
+// batched problem's y is bit-identical to the single launch's).
 template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
-__global__ __launch_bounds__(64) void gemv_int8_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
-                                                       int64_t srow_stride, int64_t N, const uint16_t* __restrict__ x,
-                                                       uint16_t* __restrict__ y, int K, int gs, int G) {
+__device__ __forceinline__ void gemv_int8_rows(const int8_t* __restrict__ W, const float* __restrict__ S,
+                                               int64_t srow_stride, int64_t N, const uint16_t* __restrict__ x,
+                                               uint16_t* __restrict__ y, int K, int gs, int G, int64_t row0) {
     constexpr int SC = CHUNK_SCALE ? 1 : 4;
     const int lane = threadIdx.x;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
     const int chunks = (K + 15) >> 4;
     const uint32_t* zw = g_zero16;
     const float* zf = reinterpret_cast<const float*>(g_zero16);
@@ -146,6 +147,39 @@ __global__ __launch_bounds__(64) void gemv_int8_kernel(const int8_t* __restrict_
     if ((lane & (64 / R - 1)) == 0 && (FULL || row0 + r < N)) stg(y + row0 + r, f32_to_f16_bits(total));
 }
 
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int8_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
+                                                       int64_t srow_stride, int64_t N, const uint16_t* __restrict__ x,
+                                                       uint16_t* __restrict__ y, int K, int gs, int G) {
+    gemv_int8_rows<R, PU, VEC, CHUNK_SCALE, FULL>(W, S, srow_stride, N, x, y, K, gs, G,
+                                                  static_cast<int64_t>(blockIdx.x) * R);
+}
+
+// Batched form: P problems of one shape; workgroup b takes row tile b % tiles of problem b / tiles. The pointer
+// tables live in device memory; a problem with a null pointer writes nothing, and (VEC) one whose W or x is not
+// 16-byte aligned gets NaN rows instead of being read with dwordx4 loads.
+template <int R, int PU, bool VEC, bool CHUNK_SCALE, bool FULL>
+__global__ __launch_bounds__(64) void gemv_int8_batched_kernel(const int8_t* const* __restrict__ Wp,
+                                                               const float* const* __restrict__ Sp,
+                                                               const uint16_t* const* __restrict__ Xp,
+                                                               uint16_t* const* __restrict__ Yp, int64_t srow_stride,
+                                                               int64_t N, int K, int gs, int G, int tiles) {
+    const int b = static_cast<int>(blockIdx.x);
+    const int p = b / tiles;
+    const int64_t row0 = static_cast<int64_t>(b - p * tiles) * R;
+    const int8_t* W = ldg(Wp + p);
+    const float* S = ldg(Sp + p);
+    const uint16_t* x = ldg(Xp + p);
+    uint16_t* y = ldg(Yp + p);
+    if (!W || !S || !x || !y) return;
+    if (VEC && ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15u)) {
+        const int64_t r = row0 + static_cast<int64_t>(threadIdx.x);
+        if (threadIdx.x < R && r < N) stg(y + r, static_cast<uint16_t>(0x7e00u));
+        return;
+    }
+    gemv_int8_rows<R, PU, VEC, CHUNK_SCALE, FULL>(W, S, srow_stride, N, x, y, K, gs, G, row0);
+}
+
 struct Int8Plan {
     int R, PU;
 };
@@ -174,10 +208,8 @@ static Int8Plan plan_int8(int64_t N, int64_t K, bool vec) {
 
 using namespace soi;
 
-extern "C" int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N,
-                              int64_t K, int64_t group_size, int64_t num_groups, int64_t scale_row_stride,
-                              void* stream) {
-    const char* what = "soi_gemv_w8a16";
+static int check_int8(int64_t N, int64_t K, int64_t group_size, int64_t num_groups, int64_t scale_row_stride,
+                      const char* what) {
     SOI_REQUIRE(K >= 1 && K <= (int64_t(1) << 30), "%s: K must be in [1, 2^30]", what);
     SOI_REQUIRE(N >= 0 && N <= (int64_t(1) << 31) - 1, "%s: N out of range", what);
     SOI_REQUIRE(group_size >= 1, "%s: group_size must be >= 1", what);
@@ -188,18 +220,14 @@ extern "C" int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16
                 (long long)ceil_div64(K, group_size), (long long)num_groups);
     SOI_REQUIRE(scale_row_stride == 0 || scale_row_stride == num_groups,
                 "%s: scale_row_stride must be 0 (per-tensor) or num_groups", what);
-    if (N == 0) return SOI_OK;
-    SOI_REQUIRE(Wq && scale && x && y, "%s: null pointer", what);
-    const bool vec = (K % 16 == 0) && aligned16(Wq) && aligned16(x);
-    const bool chunk_scale = (num_groups == 1) || (group_size % 16 == 0);
-    const Int8Plan pl = plan_int8(N, K, vec);
-    const bool full = vec && (N % pl.R == 0) && ((K / 16) % (kWave * pl.PU) == 0);
-    const dim3 grid(static_cast<unsigned>(ceil_div64(N, pl.R)));
-    hipStream_t st = as_stream(stream);
-    const int Ki = static_cast<int>(K), gi = static_cast<int>(group_size), Gi = static_cast<int>(num_groups);
-#define SOI_L(RR, PP, V, CS, FL)                                                                                   \
-    hipLaunchKernelGGL((gemv_int8_kernel<RR, PP, V, CS, FL>), grid, dim3(64), 0, st, Wq, scale, scale_row_stride, N, \
-                       x, y, Ki, gi, Gi)
+    return SOI_OK;
+}
+
+// Launches kernel form F (the single or the batched kernel) with the tile of plan_int8; `launch(kernel_tag)`
+// is called with a functor type per (R, PU, VEC, CHUNK_SCALE, FULL).
+template <class Launch>
+static void dispatch_int8(const Int8Plan& pl, bool vec, bool full, bool chunk_scale, Launch&& launch) {
+#define SOI_L(RR, PP, V, CS, FL) launch.template go<RR, PP, V, CS, FL>()
 #define SOI_CS(RR, PP, V)                                     \
     if (V && full && chunk_scale) SOI_L(RR, PP, V, true, true); \
     else if (chunk_scale) SOI_L(RR, PP, V, true, false);        \
@@ -228,5 +256,79 @@ extern "C" int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16
     }
 #undef SOI_CS
 #undef SOI_L
+}
+
+struct SingleInt8Launch {
+    dim3 grid;
+    hipStream_t st;
+    const int8_t* W;
+    const float* S;
+    int64_t stride, N;
+    const uint16_t* x;
+    uint16_t* y;
+    int K, gs, G;
+    template <int R, int PU, bool V, bool CS, bool FL>
+    void go() const {
+        hipLaunchKernelGGL((gemv_int8_kernel<R, PU, V, CS, FL>), grid, dim3(64), 0, st, W, S, stride, N, x, y, K, gs,
+                           G);
+    }
+};
+
+struct BatchedInt8Launch {
+    int64_t P;
+    hipStream_t st;
+    const int8_t* const* Wp;
+    const float* const* Sp;
+    const uint16_t* const* Xp;
+    uint16_t* const* Yp;
+    int64_t stride, N;
+    int K, gs, G;
+    template <int R, int PU, bool V, bool CS, bool FL>
+    void go() const {
+        const int tiles = static_cast<int>(ceil_div64(N, R));
+        const dim3 grid(static_cast<unsigned>(P * tiles));
+        hipLaunchKernelGGL((gemv_int8_batched_kernel<R, PU, V, CS, FL>), grid, dim3(64), 0, st, Wp, Sp, Xp, Yp, stride,
+                           N, K, gs, G, tiles);
+    }
+};
+
+extern "C" int soi_gemv_w8a16(const int8_t* Wq, const float* scale, const uint16_t* x, uint16_t* y, int64_t N,
+                              int64_t K, int64_t group_size, int64_t num_groups, int64_t scale_row_stride,
+                              void* stream) {
+    const char* what = "soi_gemv_w8a16";
+    int s = check_int8(N, K, group_size, num_groups, scale_row_stride, what);
+    if (s) return s;
+    if (N == 0) return SOI_OK;
+    SOI_REQUIRE(Wq && scale && x && y, "%s: null pointer", what);
+    const bool vec = (K % 16 == 0) && aligned16(Wq) && aligned16(x);
+    const bool chunk_scale = (num_groups == 1) || (group_size % 16 == 0);
+    const Int8Plan pl = plan_int8(N, K, vec);
+    const bool full = vec && (N % pl.R == 0) && ((K / 16) % (kWave * pl.PU) == 0);
+    SingleInt8Launch L{dim3(static_cast<unsigned>(ceil_div64(N, pl.R))), as_stream(stream), Wq, scale,
+                       scale_row_stride, N, x, y, static_cast<int>(K), static_cast<int>(group_size),
+                       static_cast<int>(num_groups)};
+    dispatch_int8(pl, vec, full, chunk_scale, L);
+    return launch_status(what);
+}
+
+extern "C" int soi_gemv_w8a16_batched(const int8_t* const* Wq_ptrs, const float* const* scale_ptrs,
+                                      const uint16_t* const* x_ptrs, uint16_t* const* y_ptrs, int64_t P, int64_t N,
+                                      int64_t K, int64_t group_size, int64_t num_groups, int64_t scale_row_stride,
+                                      void* stream) {
+    const char* what = "soi_gemv_w8a16_batched";
+    int s = check_int8(N, K, group_size, num_groups, scale_row_stride, what);
+    if (s) return s;
+    SOI_REQUIRE(P >= 0 && P <= (int64_t(1) << 20), "%s: P out of range", what);
+    if (N == 0 || P == 0) return SOI_OK;
+    SOI_REQUIRE(Wq_ptrs && scale_ptrs && x_ptrs && y_ptrs, "%s: null pointer table", what);
+    // the tile of the single form for this shape (with aligned operands), so every problem's y equals it
+    const bool vec = K % 16 == 0;
+    const bool chunk_scale = (num_groups == 1) || (group_size % 16 == 0);
+    const Int8Plan pl = plan_int8(N, K, vec);
+    const bool full = vec && (N % pl.R == 0) && ((K / 16) % (kWave * pl.PU) == 0);
+    SOI_REQUIRE(P * ceil_div64(N, pl.R) <= (int64_t(1) << 31) - 1, "%s: grid too large", what);
+    BatchedInt8Launch L{P, as_stream(stream), Wq_ptrs, scale_ptrs, x_ptrs, y_ptrs, scale_row_stride, N,
+                        static_cast<int>(K), static_cast<int>(group_size), static_cast<int>(num_groups)};
+    dispatch_int8(pl, vec, full, chunk_scale, L);
     return launch_status(what);
 }

@@ -101,6 +101,52 @@ class GemvBatch:
         return self.ys
 
 
+class Int8Batch:
+    """P independent INT8 GEMVs of one shape [N, K] in ONE kernel launch (the INT8 counterpart of GemvBatch).
+
+    scales: [N, G] group / per-channel scales, or [1, G] per-tensor (every problem the same kind). y[p] is
+    bit-identical to gemv_w8a16(Wqs[p], scales[p], xs[p], group_size)."""
+
+    def __init__(self, Wqs, scales, xs, group_size: int, ys=None):
+        P = len(Wqs)
+        if not (len(scales) == len(xs) == P and P > 0):
+            raise ValueError("Int8Batch: Wqs, scales and xs must be non-empty lists of equal length")
+        N, K = Wqs[0].shape
+        G = scales[0].shape[1]
+        per_tensor = scales[0].shape[0] == 1 and N != 1
+        dev = Wqs[0].device
+        if ys is None:
+            ys = [torch.empty(N, dtype=torch.float16, device=dev) for _ in range(P)]
+        for W, s, x, y in zip(Wqs, scales, xs, ys):
+            if not (W.dtype == torch.int8 and W.is_contiguous() and tuple(W.shape) == (N, K)):
+                raise RuntimeError("Int8Batch: every Wq must be a contiguous int8 [N, K] tensor")
+            if not (s.dtype == torch.float32 and s.is_contiguous() and tuple(s.shape) == ((1 if per_tensor else N), G)):
+                raise RuntimeError("Int8Batch: every scale must be a contiguous float32 [N or 1, G] tensor, all alike")
+            if not (x.dtype == torch.float16 and x.is_contiguous() and tuple(x.shape) == (K,)):
+                raise RuntimeError("Int8Batch: every x must be a contiguous float16 [K] tensor")
+            if not (y.dtype == torch.float16 and y.is_contiguous() and tuple(y.shape) == (N,)):
+                raise RuntimeError("Int8Batch: every y must be a contiguous float16 [N] tensor")
+            if not all(t.device == dev for t in (W, s, x, y)):
+                raise RuntimeError("Int8Batch: all tensors must be on one device")
+            if K % 16 == 0 and (W.data_ptr() % 16 or x.data_ptr() % 16):
+                raise RuntimeError("Int8Batch: Wq and x must be 16-byte aligned when K % 16 == 0")
+        if G != 1 and (G != -(-K // group_size) or group_size % 4):
+            raise RuntimeError("Int8Batch: G must be 1 or ceil(K / group_size), group_size a multiple of 4")
+        self._keep = (list(Wqs), list(scales), list(xs), list(ys))
+        self.ys = self._keep[3]
+        self.N, self.K, self.group_size, self.G = N, K, group_size, G
+        self.stride = 0 if per_tensor else G
+
+        def table(ts):
+            return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+
+        self._tables = tuple(table(ts) for ts in self._keep)
+
+    def run(self):
+        _C.gemv_w8a16_batched(*self._tables, self.N, self.K, self.group_size, self.G, self.stride)
+        return self.ys
+
+
 class GemvGroup:
     """Independent INT4 GEMVs of up to 8 different shapes executed in ONE kernel launch.
 

@@ -304,3 +304,30 @@ def test_int4_gemv_accumulation_error_bound(ops, xkind):
     # integer dot products: only the (round-to-nearest) scale FMAs and the lane reduction round
     assert (np.abs(y1 - r1) - 0.5 * np.spacing(np.abs(r1).astype(np.float16)).astype(np.float64)).max() <= \
         2e-7 * np.abs(r1).max()
+
+
+@pytest.mark.parametrize("gran,gs", W8 + [("group", 32), ("group", 12)])
+@pytest.mark.parametrize("N,K,P", [(6144, 2048, 3), (2048, 6144, 2), (1024, 2048, 5), (4097, 3072, 2), (7, 96, 4),
+                                   (2049, 100, 3)])
+def test_w8_batched_equals_single(ops, gran, gs, N, K, P):
+    """Int8Batch: P same-shape INT8 GEMVs in one launch, each bit-identical to the single launch (vector and
+    ragged-K tiles, per-tensor / per-channel / group scales, partial last tiles), and within the oracle's tolerance."""
+    if gs and K % gs:
+        pytest.skip("K not a multiple of the group size in this grid")
+    probs = [_int8_problem(N, K, gran, gs or K, seed=17 * p + N + K) for p in range(P)]
+    Ws = [torch.from_numpy(q).cuda() for q, _, _ in probs]
+    Ss = [torch.from_numpy(np.ascontiguousarray(s)).cuda() for _, s, _ in probs]
+    xs = [x.cuda() for _, _, x in probs]
+    ys = ops.Int8Batch(Ws, Ss, xs, gs or K).run()
+    for p in range(P):
+        assert torch.equal(ys[p], ops.gemv_w8a16(Ws[p], Ss[p], xs[p], gs or K)), f"problem {p}"
+    q, s, x = probs[-1]
+    assert_close(ys[-1], O.gemv_w8_f64(q, s, x.numpy(), gs or K), f"int8 batched {gran} {N}x{K}")
+
+
+def test_w8_batched_rejects_mixed_shapes(ops):
+    a = _int8_problem(64, 128, "per_channel", 128, seed=1)
+    b = _int8_problem(32, 128, "per_channel", 128, seed=2)
+    with pytest.raises(RuntimeError, match="Int8Batch"):
+        ops.Int8Batch([torch.from_numpy(a[0]).cuda(), torch.from_numpy(b[0]).cuda()],
+                      [torch.from_numpy(a[1]).cuda(), torch.from_numpy(b[1]).cuda()], [a[2].cuda(), b[2].cuda()], 128)
