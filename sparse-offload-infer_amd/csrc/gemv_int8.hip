@@ -223,8 +223,8 @@ static int check_int8(int64_t N, int64_t K, int64_t group_size, int64_t num_grou
     return SOI_OK;
 }
 
-// Launches kernel form F (the single or the batched kernel) with the tile of plan_int8; `launch(kernel_tag)`
-// is called with a functor type per (R, PU, VEC, CHUNK_SCALE, FULL).
+// Picks the instantiation (R, PU, VEC, CHUNK_SCALE, FULL) of the plan and calls launch.go<...>() with it; the
+// launcher (SingleInt8Launch or BatchedInt8Launch) holds the arguments of its kernel form.
 template <class Launch>
 static void dispatch_int8(const Int8Plan& pl, bool vec, bool full, bool chunk_scale, Launch&& launch) {
 #define SOI_L(RR, PP, V, CS, FL) launch.template go<RR, PP, V, CS, FL>()
