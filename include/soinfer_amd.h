@@ -591,7 +591,9 @@ int soi_dip_select_dense_down_residual(const uint16_t* gate, const uint16_t* h, 
  * one of 8 generation copies; fenced = 1 adds an agent-scope release before
  * the arrival and an acquire after the wait (plain data stores and loads).
  * Workspace (soi_grid_barrier_bench_workspace_bytes(P), 16-byte aligned,
- * zero-filled before the first call; calls and replays may reuse it):
+ * zero-filled before the first call; later calls with the same P and fenced
+ * flag may reuse it, since its counters continue from the last call's, but a
+ * different P needs a fresh zero-filled workspace):
  * bytes [0, 4608) the sync block (uint32 word 1088: 1 if a bounded wait gave
  * up; word 1089: mismatched words), then 2 x P uint64 s_memrealtime stamps
  * (100 MHz; begin and end of workgroup b at 2b, 2b + 1), then the data.
