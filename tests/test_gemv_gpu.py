@@ -271,6 +271,34 @@ def test_batched_table_with_misaligned_x_writes_nan_rows(ops):
     assert torch.isnan(yg[1]).all()
 
 
+def test_grouped_large_table_with_null_and_misaligned_problems(ops):
+    """A grouped launch of the Qwen3 classes through the raw pointer tables (4992 8-row tiles): a problem whose
+    y pointer is null is skipped and leaves the other outputs alone, a misaligned x gives NaN rows, and every
+    other problem, the K = 6144 ones (three passes per row) included, equals the single GEMV bit for bit."""
+    from soinfer import _C
+
+    shapes = [(6144, 2048)] * 5 + [(2048, 6144)] * 3 + [(1024, 2048)] * 3
+    probs = [int4_problem(N, K, 128, seed=300 + i) for i, (N, K) in enumerate(shapes)]
+    xs = [p["x_d"] for p in probs]
+    xs[9] = _offset_view(probs[9]["x_d"])  # misaligned x: NaN rows
+    ys = [torch.full((N,), 7.0, dtype=torch.float16, device="cuda") for N, _ in shapes]
+
+    def table(ts):
+        return torch.tensor([t.data_ptr() if t is not None else 0 for t in ts], dtype=torch.int64, device="cuda")
+
+    yt = [y if i != 6 else None for i, y in enumerate(ys)]  # problem 6: null y, skipped
+    # classes in table order: 5 x (6144, 2048), 3 x (2048, 6144), 3 x (1024, 2048)
+    _C.gemv_w4a16_grouped(table([p["Wq_d"] for p in probs]), table([p["s_d"] for p in probs]), table(xs), table(yt),
+                          [5, 3, 3], [6144, 2048, 1024], [2048, 6144, 2048], 128)
+    for i, p in enumerate(probs):
+        if i == 6:
+            assert (ys[i] == 7.0).all()
+        elif i == 9:
+            assert torch.isnan(ys[i]).all()
+        else:
+            assert torch.equal(ys[i], ops.gemv_w4a16_group_lop3(p["Wq_d"], p["s_d"], p["x_d"], p["K"], 128)), i
+
+
 @pytest.mark.parametrize("xkind", ["normal", "swiglu", "positive"])
 def test_int4_gemv_accumulation_error_bound(ops, xkind):
     """The fp32 accumulation error of the INT4 GEMV over K = 6144 (the down projection), separated from the
