@@ -444,11 +444,12 @@ def bench_dip_mlp(D, w, hot, dev):
     return res
 
 
-def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
+def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep=None):
     """greedy decoding of the random-init 28-layer Qwen3-1.7B-shaped INT4 decoder from a
     seeded 64-token prompt, 128 new tokens, dense vs DIP vs cache-aware DIP at k/I = 0.5 (20% hot cache,
     misses from pinned host memory). One HIP graph per token; decode_tok_s = new tokens / decode time,
-    end_to_end_tok_s = new tokens / (prefill + decode) time (the reference's tokens/sec, bench_m7_pareto.py:87-90)."""
+    end_to_end_tok_s = new tokens / (prefill + decode) time (the reference's tokens/sec, bench_m7_pareto.py:87-90).
+    hot_sweep: {mode name: per-layer hot sets} of further cache-aware DIP runs at other cache sizes."""
     import torch
 
     c = w.config
@@ -468,6 +469,8 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
     modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_int4_head", "dip_int4_head",
              "dip_dense_up_int4_head", "cached_dip_int4_head", "dense_offload", "dip_offload",
              "cached_dip_offload", "dense_offload_serial", "dip_offload_serial", "cached_dip_offload_serial")
+    hot_sweep = hot_sweep or {}
+    modes = modes + tuple(hot_sweep)
     no_hot = [[] for _ in range(c.layers)]
     Wq_h, S_h = D.quantize_lm_head(w)
     head_bytes = {False: w.lm_head.numel() * 2, True: Wq_h.numel() + 4 * S_h.numel()}
@@ -476,8 +479,11 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
         kind = mode.replace("_serial", "").replace("_int4_head", "")
         base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip",
                 "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(kind, kind)
+        mode_hot = hot_sweep.get(mode, no_hot if kind == "dip_offload" else hot)
+        if mode in hot_sweep:
+            kind = base = "cached_dip"
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
-                             hot_channels=(no_hot if kind == "dip_offload" else hot) if base == "cached_dip" else None,
+                             hot_channels=mode_hot if base == "cached_dip" else None,
                              max_new_tokens=n_new, dip_dense_up=kind == "dip_dense_up",
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
                              offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"),
@@ -500,13 +506,16 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128):
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
                      "weight_bytes_per_token": per_tok,
                      "weight_GBps": round(per_tok * n_new / (t2 - t1) / 1e9, 1)}
+        if mode in hot_sweep:
+            out[mode]["hot_fraction"] = round(len(mode_hot[0]) / I, 3)
         if eng.offload:
             out[mode]["streamed_bytes_per_token"] = eng.wstore.bytes_total
             out[mode]["streamed_GBps"] = round(eng.wstore.bytes_total * n_new / (t2 - t1) / 1e9, 1)
         del eng
         torch.cuda.empty_cache()
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
-    out["cached_dip_tokens_equal_dip"] = toks["dip"] == toks["cached_dip"] == toks["cached_dip_staged"]
+    out["cached_dip_tokens_equal_dip"] = all(toks["dip"] == toks[m] for m in ("cached_dip", "cached_dip_staged",
+                                                                              *hot_sweep))
     out["cached_dip_int4_head_tokens_equal_dip_int4_head"] = toks["dip_int4_head"] == toks["cached_dip_int4_head"]
     assert out["cached_dip_int4_head_tokens_equal_dip_int4_head"], "cache-aware DIP must equal DIP (INT4 head)"
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
@@ -1220,11 +1229,20 @@ def main() -> int:
         torch.cuda.empty_cache()
         w = D.random_decoder(D.QWEN3_1P7B, seed=0)
         calib = torch.randint(0, D.QWEN3_1P7B.vocab, (64,), generator=torch.Generator().manual_seed(1000)).tolist()
-        hot = D.calibrate_hot_channels(w, D.QWEN3_1P7B.intermediate // 2, calib, cache_fraction=0.2)
+        from soinfer.offload.hot_cache import StaticFrequencyPolicy
+
+        counts = D.calibrate_channel_counts(w, D.QWEN3_1P7B.intermediate // 2, calib)
+        # hot sets as calibrate_hot_channels builds them (the most frequently selected channels), at the
+        # config's 20% and, for the hot-fraction sweep, 50% and 100% of I
+        hot_sets = {f: [StaticFrequencyPolicy(cnt.cpu(), int(round(f * D.QWEN3_1P7B.intermediate))).hot_indices
+                        .tolist() for cnt in counts] for f in (0.2, 0.5, 1.0)}
+        hot = hot_sets[0.2]
+        del counts
         log("decoder weights and hot sets ready")
         detail["dip_mlp_layer"] = bench_dip_mlp(D, w, hot, dev)
         log("DIP MLP done")
-        detail["decode"] = bench_decode(D, w, hot, dev)
+        detail["decode"] = bench_decode(D, w, hot, dev, hot_sweep={"cached_dip_hot50": hot_sets[0.5],
+                                                                    "cached_dip_hot100": hot_sets[1.0]})
         del w
         torch.cuda.empty_cache()
         result["decode_tok_s"] = decode_summary(detail["decode"])
