@@ -63,7 +63,6 @@ __device__ __forceinline__ T* uniform_ptr(T* p) {
 }
 
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
-__device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
 // ---------------------------------------------------------------------------
 // INT4 (AWQ nibble order) -> binary16, two methods with identical results.
@@ -136,20 +135,6 @@ __device__ __forceinline__ void int4x8_subnormal_scalar(uint32_t w, f16x2 lo[2],
     hi[0] = as_f16x2((u[2] << 4) | (u[3] << 20));
     lo[1] = as_f16x2(u[4] | (u[5] << 16));
     hi[1] = as_f16x2((u[6] << 4) | (u[7] << 20));
-}
-
-// Method "scalar": per-nibble signed bitfield extract and integer -> binary16
-// conversion (v_bfe_i32 + v_cvt_f16_i16). Slower; kept as the independent
-// second derivation of the same exact values.
-__device__ __forceinline__ void dequant_int4x8_scalar(uint32_t w, f16x2 out[4]) {
-    // nibble index holding logical element j
-    constexpr int nib[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int a = __builtin_amdgcn_sbfe(static_cast<int>(w), 4 * nib[2 * p], 4);
-        const int b = __builtin_amdgcn_sbfe(static_cast<int>(w), 4 * nib[2 * p + 1], 4);
-        out[p] = f16x2{static_cast<f16>(static_cast<int16_t>(a)), static_cast<f16>(static_cast<int16_t>(b))};
-    }
 }
 
 // INT8 -> binary16: four signed bytes b0..b3 of a word become (b0,b1),(b2,b3).
@@ -347,8 +332,6 @@ __device__ __forceinline__ void arrive_coherent() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
-
-__device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 // number of set bits of a 64-bit wave mask strictly below this lane
 __device__ __forceinline__ uint32_t mask_prefix(uint64_t m) {

@@ -1,6 +1,6 @@
 // The INT4 dequant-GEMV tile shared by the GEMV kernels (gemv_int4.hip) and
-// the single-launch DIP MLP (dip_mlp.hip): x sources, epilogues and
-// gemv_int4_tile, which computes R rows of y = W x per wave with fp32
+// the o projection that combines split attention states on load
+// (decode_attention.hip): x sources, epilogues and gemv_int4_tile, which computes R rows of y = W x per wave with fp32
 // accumulation in a fixed order. Every kernel built on it returns the same
 // row totals for the same logical rows and x, whatever the tile height.
 #pragma once
@@ -123,20 +123,6 @@ struct NormX {
             xv[4 * i + 2] = as_f16x2(norm_f16x2(t.z, g.z, inv));
             xv[4 * i + 3] = as_f16x2(norm_f16x2(t.w, g.w, inv));
         }
-    }
-};
-
-// RegX: the lane's x chunk already in registers (single-pass shapes: K == 2048,
-// lane l owns chunk l), computed by the caller.
-struct RegX {
-    static constexpr bool kSinglePass = false;
-    const f16x2* v;     // 16 pairs held by this lane
-    const uint16_t* b;  // a K-element vector for unresolvable rows
-    __device__ __forceinline__ const uint16_t* base() const { return b; }
-    template <bool VEC, bool FULL>
-    __device__ __forceinline__ void load(int, int, bool, f16x2 xv[16]) const {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) xv[e] = v[e];
     }
 };
 
