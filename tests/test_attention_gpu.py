@@ -46,6 +46,26 @@ def test_other_shapes_match_oracle(ops, NQ, NKV, hd, S, L):
     assert_close(out, ref, f"attention {NQ}/{NKV}/{hd} L={L}")
 
 
+@pytest.mark.parametrize("L", [4096, 8191, 16384])
+def test_long_context_matches_oracle(ops, L):
+    """Past the BASELINE context (2048): more than 8192 timestep rows per launch switch the split target, and
+    each split then spans several 8-pass load batches. The host-length form against the binary64 oracle, and
+    the device-position form (length read from pos on the device, the engine's form) bit for bit against it."""
+    from soinfer import _C
+
+    S = 16384
+    q, k, v = _qkv(16, 8, 128, S, seed=L)
+    ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), L)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out = ops.decode_attention(qd, kd, vd, L)
+    assert_close(out, ref, f"attention L={L}")
+    ws = torch.zeros(_C.decode_attention_workspace_bytes(16, 8, 128, S), dtype=torch.uint8, device="cuda")
+    pos = torch.tensor([L - 1], dtype=torch.int32, device="cuda")
+    at = torch.empty_like(out)
+    _C.decode_attention_at(qd, kd, vd, pos, at, ws)
+    assert torch.equal(at, out), f"device-position form differs at L={L}"
+
+
 def test_caller_buffers_form_equals_allocating_form(ops):
     """decode_attention_into (caller out and workspace, reused across calls) == decode_attention, bit for bit, on
     both sides of the split boundary (a split host length combines in a second launch) and for one KV head."""
