@@ -50,7 +50,7 @@ def _split(L, NKV, hd):
     (4, 2, 64, 1024, 256, 128, [100, 512, 513, 1024]),                        # several passes: K = 256
     (8, 1, 128, 4096, 1000, 128, [256, 257, 2000, 4096]),                     # one KV head: 64 splits; ragged N
     (16, 8, 128, 2048, 2048, 16, [200, 300, 2048]),                           # per-word scales (gs % 32 != 0)
-    (16, 8, 128, 16384, 2048, 128, [4096, 8193, 16384]),                      # long contexts: many passes per split
+    (16, 8, 128, 16384, 2048, 128, [200, 4096, 8193, 16384]),                 # long contexts: many passes per split
 ])
 def test_deferred_step_and_combine_equal_step_and_gemv(C, ops, NQ, NKV, hd, S, N, gs, lengths):
     K = NQ * hd
