@@ -267,17 +267,21 @@ def bench_decode_chain(ops, layers, step_bytes):
     del chain, graph
     return decode_chain
 
-def mlp_bytes(L, I: int, H: int, k=None, dense_up: bool = False) -> int:
+def mlp_bytes(L, I: int, H: int, k=None, dense_up: bool = False, gated: bool = False) -> int:
     """Algorithmic bytes of one layer's MLP: dense reads gate|up and down; DIP reads gate, k rows of up and
     k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes; the dense-up DIP schedule
     reads every gate|up row and every down^T value (its down is a GEMV over the transposed down_proj^T: unselected
-    channels read with a zero coefficient), and writes then reads gate and h of every channel."""
+    channels read with a zero coefficient), and writes then reads gate and h of every channel; the gated DIP
+    schedule reads every gate|up row and k rows of down^T, and writes gate and up of every channel, then reads
+    the gates and the k selected up values."""
     row = L.gu_Wq.shape[1] + 4 * L.gu_scale.shape[1]
     if k is None:
         return 2 * I * row + L.down_Wq.numel() + 4 * L.down_scale.numel() + 2 * (H + 3 * I + H)
     row_t = L.down_T_Wq.shape[1] + 4 * L.down_T_scale.shape[1]
     if dense_up:
         return 2 * I * row + I * row_t + 2 * (H + 4 * I + H)
+    if gated:
+        return 2 * I * row + k * row_t + 2 * (H + 3 * I + k + H) + 4 * k
     return I * row + k * (row + row_t) + 2 * (H + I + 2 * k + H) + 4 * (I + k)
 
 
@@ -390,6 +394,22 @@ def bench_dip_mlp(D, w, hot, dev):
         if frac == 0.5:
             y_dip = y_unfused
         del eng
+        # gated schedule (the engine's dip_schedule="gated"): gate and up of every channel in one launch with the
+        # RMSNorm on load, then the rule-A selection in each workgroup and the gated sparse down over the selected
+        # down^T rows (2 launches); the same selection and y as the four-launch schedule, bit for bit
+        eng = D.DecodeEngine(w, "dip", dip_k=k, max_new_tokens=1, dip_schedule="gated")
+
+        def gated_mlp():
+            for l, L in enumerate(w.layers):
+                gW, gS = eng.gu_il[l]
+                C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, x, None, nw, eps, None, eng.gu[:I], eng.gu[I:], H,
+                                                  c.group_size)
+                C.dip_select_gated_down_into(eng.gu[:I], eng.gu[I:], k, L.down_T_Wq, L.down_T_scale, eng.idx, eng.cnt,
+                                             eng.down, H, c.group_size, eng.sd_ws)
+        us_g = graph_time_us(gated_mlp) / c.layers
+        assert torch.equal(eng.idx, idx_dip) and torch.equal(eng.down, y_norm), \
+            "the gated schedule must equal the four-launch schedule bit for bit"
+        del eng
         # dense-up schedule (the engine's dip_dense_up): one launch computes gate and h = fp16(silu(gate) * up) of
         # every channel with the RMSNorm on load, a second the rule-A selection in each workgroup and the down
         # projection as a GEMV over the transposed down_proj^T (2 launches); the same selection, y within the
@@ -421,7 +441,11 @@ def bench_dip_mlp(D, w, hot, dev):
             "indexed_up_us": round(us_4, 2), "indexed_up_bytes": nb,
             "indexed_up_schedule": "RMSNorm-fused gate GEMV, top-k, up GEMV over the selected rows with the SiLU "
                                    "epilogue, sparse down (4 launches)",
-            "indexed_up_no_norm_us": round(us_f, 2), "indexed_up_unfused_us": round(us, 2)}
+            "indexed_up_no_norm_us": round(us_f, 2), "indexed_up_unfused_us": round(us, 2),
+            "gated_us": round(us_g, 2), "gated_bytes": mlp_bytes(w.layers[0], I, H, k, gated=True),
+            "gated_schedule": "gate|up GEMV with RMSNorm on load writing gate and up of every channel, then the "
+                              "rule-A selection in every workgroup + the gated sparse down over the selected down^T "
+                              "rows (2 launches); equal to the four-launch schedule bit for bit"}
         res[f"dip_k{k}"]["GBps"] = round(res[f"dip_k{k}"]["bytes"] / us_du / 1e3, 1)
         del eng
     k = I // 2
@@ -466,9 +490,10 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
     # stream-ordered right before its kernels
     # "*_int4_head": the same schedule with the LM head quantized like the linears (INT4 g128 GEMV) instead of
     # the reference's fp16 head: config 5's "all weights INT4 g128"
-    modes = ("dense", "dip", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_int4_head", "dip_int4_head",
-             "dip_dense_up_int4_head", "cached_dip_int4_head", "dense_offload", "dip_offload",
-             "cached_dip_offload", "dense_offload_serial", "dip_offload_serial", "cached_dip_offload_serial")
+    modes = ("dense", "dip", "dip_gated", "dip_dense_up", "cached_dip", "cached_dip_staged", "dense_int4_head",
+             "dip_int4_head", "dip_gated_int4_head", "dip_dense_up_int4_head", "cached_dip_int4_head",
+             "dense_offload", "dip_offload", "cached_dip_offload", "dense_offload_serial", "dip_offload_serial",
+             "cached_dip_offload_serial")
     hot_sweep = hot_sweep or {}
     modes = modes + tuple(hot_sweep)
     no_hot = [[] for _ in range(c.layers)]
@@ -477,14 +502,15 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
     for mode in modes:
         int4_head = mode.endswith("_int4_head")
         kind = mode.replace("_serial", "").replace("_int4_head", "")
-        base = {"dip_dense_up": "dip", "cached_dip_staged": "cached_dip",
+        base = {"dip_dense_up": "dip", "dip_gated": "dip", "cached_dip_staged": "cached_dip",
                 "dense_offload": "dense", "dip_offload": "cached_dip", "cached_dip_offload": "cached_dip"}.get(kind, kind)
         mode_hot = hot_sweep.get(mode, no_hot if kind == "dip_offload" else hot)
         if mode in hot_sweep:
             kind = base = "cached_dip"
         eng = D.DecodeEngine(w, base, dip_k=None if base == "dense" else k,
                              hot_channels=mode_hot if base == "cached_dip" else None,
-                             max_new_tokens=n_new, dip_dense_up=kind == "dip_dense_up",
+                             max_new_tokens=n_new,
+                             dip_schedule={"dip_dense_up": "dense_up", "dip_gated": "gated"}.get(kind),
                              miss_path="staged" if mode == "cached_dip_staged" else "direct",
                              offload=kind.endswith("_offload"), overlap_copy=not mode.endswith("_serial"),
                              int4_head=int4_head)
@@ -500,7 +526,8 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=kind == "dip_dense_up")
+        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=kind == "dip_dense_up",
+                        gated=kind == "dip_gated")
         per_tok = c.layers * (attn_w + mlp) + head_bytes[int4_head]
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
@@ -516,6 +543,9 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
         log(f"decode {mode}: {out[mode]['decode_tok_s']} tok/s")
     out["cached_dip_tokens_equal_dip"] = all(toks["dip"] == toks[m] for m in ("cached_dip", "cached_dip_staged",
                                                                               *hot_sweep))
+    out["dip_gated_tokens_equal_dip"] = toks["dip"] == toks["dip_gated"]
+    assert out["dip_gated_tokens_equal_dip"], "the gated DIP schedule must generate the indexed schedule's tokens"
+    assert toks["dip_int4_head"] == toks["dip_gated_int4_head"], "gated DIP must equal DIP (INT4 head)"
     out["cached_dip_int4_head_tokens_equal_dip_int4_head"] = toks["dip_int4_head"] == toks["cached_dip_int4_head"]
     assert out["cached_dip_int4_head_tokens_equal_dip_int4_head"], "cache-aware DIP must equal DIP (INT4 head)"
     assert out["cached_dip_tokens_equal_dip"], "cache-aware DIP must generate the same tokens as DIP"
@@ -535,6 +565,9 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
     out["cached_dip_staged"]["miss_path"] = "staged: device gathers of the misses into staging, then descriptors"
     out["dip"]["schedule"] = ("RMSNorm-fused gate GEMV, top-k, up GEMV with SiLU epilogue, sparse "
                               "down (4 launches per MLP); cached_dip equals it bit for bit")
+    out["dip_gated"]["schedule"] = ("gate|up GEMV with RMSNorm on load writing gate and up of every channel, then the "
+                                    "rule-A selection in every workgroup + the gated sparse down over the selected "
+                                    "down^T rows (2 launches per MLP); dip's tokens and hidden states bit for bit")
     out["dip_dense_up_tokens_equal_dip"] = toks["dip"] == toks["dip_dense_up"]
     out["dip_dense_up"]["schedule"] = ("gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the "
                               "rule-A selection in every workgroup + the down as a GEMV over the transposed "

@@ -209,6 +209,9 @@ class DecodeEngine:
     """Greedy decoder over DecoderWeights. mode: "dense", "dip" (top dip_k channels per layer, weights
     resident) or "cached_dip" (hot channels resident, the rest in pinned host memory; miss_path "direct" reads
     the misses in place inside the up / down kernels, "staged" gathers them into device staging first).
+    dip_schedule (mode "dip"): "indexed" (default; 4 MLP launches, the schedule cached_dip equals bit for bit),
+    "gated" (2 MLP launches, the same tokens and hidden states as "indexed" bit for bit) or "dense_up" (2 MLP
+    launches, y summed in another order; dip_dense_up=True is the same).
     offload=True keeps the dense weights of every layer (q|k|v, o, and gate|up + down for dense or gate for
     cached DIP) in a pinned host arena and copies each layer's block into one of two device slots: the
     reference's streamed configuration (WeightPipeline, generate.py:85-138). With overlap_copy=True (default)
@@ -234,9 +237,18 @@ class DecodeEngine:
                  hot_channels: Optional[list] = None, max_new_tokens: int = 256, fused: bool = True,
                  dip_dense_up: bool = False, miss_path: str = "direct", offload: bool = False,
                  down_copy: bool = True, overlap_copy: bool = True, residual_epilogue: bool = True,
-                 defer_attention_combine: bool = True, int4_head: bool = False):
+                 defer_attention_combine: bool = True, int4_head: bool = False, dip_schedule: Optional[str] = None):
         if mode not in ("dense", "dip", "cached_dip"):
             raise ValueError(f"unknown mode {mode!r}")
+        if dip_schedule is None:
+            dip_schedule = "dense_up" if dip_dense_up else "indexed"
+        if dip_schedule not in ("indexed", "dense_up", "gated"):
+            raise ValueError(f"unknown dip_schedule {dip_schedule!r}")
+        if dip_dense_up and dip_schedule != "dense_up":
+            raise ValueError("dip_dense_up=True is dip_schedule='dense_up'")
+        if dip_schedule != "indexed" and mode != "dip":
+            raise ValueError(f"dip_schedule {dip_schedule!r} applies to mode 'dip' (weights resident)")
+        dip_dense_up = dip_schedule == "dense_up"
         if offload and mode == "dip":
             raise ValueError("offload streams the dense weights; for DIP with every selected row read from host "
                              "memory use mode 'cached_dip' with empty hot-channel lists")
@@ -246,14 +258,22 @@ class DecodeEngine:
         # direct path, fused layers: the up GEMV also copies the down^T miss rows to staging (False: the down
         # accumulate reads them in place)
         self.down_copy = down_copy
-        if dip_dense_up and mode != "dip":
-            raise ValueError("dip_dense_up applies to mode 'dip' (weights resident)")
-        # DIP schedule for resident weights: one launch computes gate and h = fp16(silu(gate) * up) of every
-        # channel, a second runs the rule-A selection in each of its workgroups and the down projection as a GEMV
-        # over a transposed copy of down_proj^T's quantized values with the masked coefficients (no cross-
-        # workgroup step). The selection equals the four-launch schedule's; y sums the same terms in another order
-        # (within the sparse accumulate's tolerance, not bit for bit).
+        # DIP schedules for resident weights (mode 'dip'):
+        #  * "indexed" (default): RMSNorm-fused gate GEMV, top-k, up GEMV over the selected rows with the SiLU
+        #    epilogue, sparse down over the selected down^T rows (4 MLP launches); the cache-aware modes equal it
+        #    bit for bit;
+        #  * "gated": one launch computes gate and up of every channel (RMSNorm on load), a second runs the rule-A
+        #    selection in each of its workgroups and the sparse down over the selected down^T rows with
+        #    h = fp16(silu(gate) * up) formed on load (2 MLP launches): the same selection, the same h values and
+        #    the same row partition and sums as "indexed", so the same y bit for bit;
+        #  * "dense_up": one launch computes gate and h = fp16(silu(gate) * up) of every channel, a second runs
+        #    the rule-A selection in each of its workgroups and the down projection as a GEMV over a transposed
+        #    copy of down_proj^T's quantized values with the masked coefficients (no cross-workgroup step). The
+        #    selection equals the other schedules'; y sums the same terms in another order (within the sparse
+        #    accumulate's tolerance, not bit for bit).
+        self.dip_schedule = dip_schedule
         self.dip_dense_up = dip_dense_up
+        self.dip_gated = dip_schedule == "gated"
         c = w.config
         self.w, self.c, self.mode, self.fused = w, c, mode, fused
         self.residual_epilogue = bool(residual_epilogue)
@@ -310,7 +330,7 @@ class DecodeEngine:
         if dip_dense_up:
             # down_proj^T's values transposed for the one-launch down (the same quantized values, no rounding)
             self.down_tt = [ops.transposed_down_T(L.down_T_Wq, L.down_T_scale, H) for L in w.layers]
-        if fused and (mode == "dense" or dip_dense_up):
+        if fused and (mode == "dense" or dip_schedule != "indexed"):
             # gate|up rows interleaved by 8-row tiles (gate 4t..4t+3, up 4t..4t+3) for the SwiGLU epilogue
             t = torch.arange(I // 4, device=dev)
             perm = torch.stack([4 * t + i for i in range(4)] + [I + 4 * t + i for i in range(4)], 1).reshape(-1)
@@ -476,6 +496,11 @@ class DecodeEngine:
             _C.silu_mul_into(gate, self.gu[I:], self.mlp_h)  # h of every channel
             self._dense_down(l, gate, self.mlp_h)
             return
+        if self.dip_gated:
+            uW, uS = L.up(I)
+            _C.gemv_w4a16_into(uW, uS, self.h, self.gu[I:], H, gs)
+            self._gated_down(l, L, gate, self.gu[I:])
+            return
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         self._count_selection(l)
         if self.mode == "dip":
@@ -511,6 +536,14 @@ class DecodeEngine:
         _C.dip_select_dense_down_into(gate, h, self.k, Wt, St, self.idx if want else None,
                                       self.cnt if want else None, self.down, self.c.group_size,
                                       res if res_out is not None else None, res_out)
+        self._count_selection(l)
+
+    def _gated_down(self, l: int, L: LayerWeights, gate: torch.Tensor, up: torch.Tensor):
+        """Selection + sparse down of the gated schedule (gate and up of every channel given): h of the selected
+        channels is formed on load, as the indexed up GEMV's SiLU epilogue rounds it."""
+        c = self.c
+        _C.dip_select_gated_down_into(gate, up, self.k, L.down_T_Wq, L.down_T_scale, self.idx, self.cnt, self.down,
+                                      c.hidden, c.group_size, self.sd_ws)
         self._count_selection(l)
 
     def _count_selection(self, l: int):
@@ -638,6 +671,11 @@ class DecodeEngine:
             self._dense_down(l, gate, self.gu[I:], x, res_out)
             return
         assert res_out is None
+        if self.dip_gated:
+            gW, gS = gu_il
+            _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, x, delta, L.post_norm, eps, x_out, gate, self.gu[I:], H, gs)
+            self._gated_down(l, L, gate, self.gu[I:])
+            return
         gW, gS = L.gate(I)
         _C.gemv_w4a16_rmsnorm_into(gW, gS, x, delta, L.post_norm, eps, x_out, self.h, gate, H, gs, False)
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)

@@ -159,6 +159,24 @@ def test_dip_dense_up_schedule(dec, tiny, fused):
 
 
 @pytest.mark.parametrize("fused", [True, False])
+def test_dip_gated_schedule_bit_identical_to_indexed(dec, tiny, fused):
+    """Gate and up of every channel in one launch + the one-launch selection and gated sparse down: the same
+    selection, h values and row partition as the indexed schedule, so the same tokens and hidden state bit for
+    bit, eager and graph replays; the selection indices too."""
+    cfg = tiny.config
+    k = cfg.intermediate // 2
+    prompt = prompt_ids(6, cfg.vocab, seed=19)
+    plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
+    want = plain.generate(prompt, 6, use_graph=True)
+    eng = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused, dip_schedule="gated")
+    for use_graph in (False, True, True):
+        assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"graph={use_graph}"
+        assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
+        assert torch.equal(eng.idx, plain.idx) and torch.equal(eng.cnt, plain.cnt)
+        _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("fused", [True, False])
 def test_offloaded_dense_weights_bit_identical(dec, fused):
     """Dense weights streamed per layer from the pinned arena into two device slots (the reference's streamed
     configuration) give the resident engine's tokens and hidden state bit for bit: dense, DIP with every selected
@@ -192,6 +210,12 @@ def test_offloaded_dense_weights_bit_identical(dec, fused):
 def test_engine_rejects_bad_arguments(dec, tiny):
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "dense", dip_dense_up=True)
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "cached_dip", dip_k=8, hot_channels=[[]] * tiny.config.layers, dip_schedule="gated")
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dip", dip_k=8, dip_schedule="sparse")
+    with pytest.raises(ValueError):
+        dec.DecodeEngine(tiny, "dip", dip_k=8, dip_dense_up=True, dip_schedule="gated")
     with pytest.raises(ValueError):
         dec.DecodeEngine(tiny, "sparse")
     with pytest.raises(ValueError):

@@ -3,9 +3,9 @@
 Counterpart of the reference's DIP / cache-aware DIP comparison (python/soinfer/runtime/generate.py:466-542,
 tests/test_m8_cached_dip_pipeline.py:103-138) at the real shape, k/I = 0.5, with a 20% hot cache calibrated
 from 64 seeded tokens (calibrate_hot_channels, generate.py:579-609):
-  * DIP (indexed up GEMV) and cache-aware DIP with the misses read in place from pinned host memory (direct)
-    or gathered into staging first (staged) generate the same tokens and end with bit-identical hidden states,
-    from HIP-graph replays; DIP with the dense-up schedule (one-launch selection + gated down) sums its down
+  * DIP (indexed up GEMV), DIP with the two-launch gated schedule and cache-aware DIP with the misses read in
+    place from pinned host memory (direct) or gathered into staging first (staged) generate the same tokens and
+    end with bit-identical hidden states, from HIP-graph replays; DIP with the dense-up schedule (one-launch selection + gated down) sums its down
     terms in another order, so its tokens are checked for determinism (graph replay == eager run) only;
   * the first generated step, teacher-forced layer by layer: each layer's gate within 1e-3 of the binary64
     oracle GEMV on the layer's own MLP input, the selection equal to the oracle's rule A on the kernel's own
@@ -45,6 +45,7 @@ def _engines(D, w, hot):
     return {
         "dip": D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW),
         "dip_dense_up": D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW, dip_dense_up=True),
+        "dip_gated": D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW, dip_schedule="gated"),
         "cached_direct": D.DecodeEngine(w, "cached_dip", dip_k=DIP_K, hot_channels=hot, max_new_tokens=N_NEW),
         "cached_staged": D.DecodeEngine(w, "cached_dip", dip_k=DIP_K, hot_channels=hot, max_new_tokens=N_NEW,
                                         miss_path="staged"),
@@ -149,6 +150,11 @@ def test_config5_first_step_per_layer_matches_oracle(setup):
                 continue
             assert torch.equal(o["idx"], t["idx"]) and torch.equal(o["cnt"], t["cnt"]), f"{name} layer {l} idx"
             assert torch.equal(o["down"], t["down"]), f"{name} layer {l} MLP output"
+            if name == "dip_gated":
+                # normalizes on load and forms h inside the down launch: neither the normed input nor h_sel is
+                # stored; its gate of every channel and the up values of the selected ones are
+                assert torch.equal(o["gate"], t["gate"]), f"{name} layer {l} gate"
+                continue
             assert torch.equal(o["h"], t["h"]), f"{name} layer {l} MLP input"
             assert torch.equal(o["h_sel"], t["h_sel"]), f"{name} layer {l} gated up h"
 
@@ -163,7 +169,8 @@ def _prompt5(V):
 
 def test_config5_full_length_cached_dip_equals_dip(setup):
     """64 + 128 tokens through 28 layers: cache-aware DIP (20% calibrated hot cache, misses from pinned host
-    memory, direct and staged) generates DIP's tokens and ends with its final hidden state, bit for bit."""
+    memory, direct and staged) and the gated DIP schedule generate DIP's tokens and end with its final hidden
+    state, bit for bit."""
     D, w, _, hot = setup
     prompt = _prompt5(w.config.vocab)
     dip = D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW5)
@@ -177,6 +184,10 @@ def test_config5_full_length_cached_dip_equals_dip(setup):
         assert got == want, f"cached DIP ({path}): tokens differ from DIP"
         assert torch.equal(eng.x_final, x_ref), f"cached DIP ({path}): final hidden state differs from DIP"
         del eng
+    # the two-launch gated schedule: the same tokens and final hidden state as well
+    eng = D.DecodeEngine(w, "dip", dip_k=DIP_K, max_new_tokens=N_NEW5, dip_schedule="gated")
+    assert eng.generate(prompt, N_NEW5) == want, "gated DIP: tokens differ from DIP"
+    assert torch.equal(eng.x_final, x_ref), "gated DIP: final hidden state differs from DIP"
 
 
 def test_config5_last_step_per_layer_matches_oracle(setup):
