@@ -270,10 +270,10 @@ def bench_decode_chain(ops, layers, step_bytes):
 def mlp_bytes(L, I: int, H: int, k=None, dense_up: bool = False, gated: bool = False) -> int:
     """Algorithmic bytes of one layer's MLP: dense reads gate|up and down; DIP reads gate, k rows of up and
     k rows of down^T (packed + fp32 scales), plus the fp16 vectors it reads and writes; the dense-up DIP schedule
-    reads every gate|up row and every down^T value (its down is a GEMV over the transposed down_proj^T: unselected
-    channels read with a zero coefficient), and writes then reads gate and h of every channel; the gated DIP
-    schedule reads every gate|up row and k rows of down^T, and writes gate and up of every channel, then reads
-    the gates and the k selected up values."""
+    and the gated one with the ordered down read every gate|up row and every down^T value (their downs run over
+    the transposed down_proj^T: unselected channels read and left out), and write then read gate and h of every
+    channel; the gated schedule's row form (gated=True) reads every gate|up row and k rows of down^T, and writes
+    gate and up of every channel, then reads the gates and the k selected up values."""
     row = L.gu_Wq.shape[1] + 4 * L.gu_scale.shape[1]
     if k is None:
         return 2 * I * row + L.down_Wq.numel() + 4 * L.down_scale.numel() + 2 * (H + 3 * I + H)
@@ -406,9 +406,28 @@ def bench_dip_mlp(D, w, hot, dev):
                                                   c.group_size)
                 C.dip_select_gated_down_into(eng.gu[:I], eng.gu[I:], k, L.down_T_Wq, L.down_T_scale, eng.idx, eng.cnt,
                                              eng.down, H, c.group_size, eng.sd_ws)
-        us_g = graph_time_us(gated_mlp) / c.layers
+        us_gr = graph_time_us(gated_mlp) / c.layers
         assert torch.equal(eng.idx, idx_dip) and torch.equal(eng.down, y_norm), \
             "the gated schedule must equal the four-launch schedule bit for bit"
+        us_g = us_gr
+        if eng.dip_gated_tr:  # the engine's form where the shape fits: the down over the transposed copy
+            def gated_tr_mlp():
+                for l, L in enumerate(w.layers):
+                    gW, gS = eng.gu_il[l]
+                    Wt, St = eng.down_tt[l]
+                    C.gemv_w4a16_rmsnorm_swiglu_gate_into(gW, gS, x, None, nw, eps, None, eng.gu[:I], eng.gu[I:], H,
+                                                          c.group_size)
+                    C.dip_select_down_ordered_into(eng.gu[:I], eng.gu[I:], k, Wt, St, None, None, eng.down,
+                                                   c.group_size)
+            eng.down.zero_()
+            us_g = graph_time_us(gated_tr_mlp) / c.layers  # as the engine runs it: no index outputs
+            assert torch.equal(eng.down, y_norm), "the ordered down must equal the four-launch schedule bit for bit"
+            Wt, St = eng.down_tt[c.layers - 1]
+            C.dip_select_down_ordered_into(eng.gu[:I], eng.gu[I:], k, Wt, St, eng.idx, eng.cnt, eng.down,
+                                           c.group_size)
+            torch.cuda.synchronize()
+            assert torch.equal(eng.idx, idx_dip) and torch.equal(eng.down, y_norm), \
+                "the ordered down's selection must equal the four-launch schedule's"
         del eng
         # dense-up schedule (the engine's dip_dense_up): one launch computes gate and h = fp16(silu(gate) * up) of
         # every channel with the RMSNorm on load, a second the rule-A selection in each workgroup and the down
@@ -442,10 +461,14 @@ def bench_dip_mlp(D, w, hot, dev):
             "indexed_up_schedule": "RMSNorm-fused gate GEMV, top-k, up GEMV over the selected rows with the SiLU "
                                    "epilogue, sparse down (4 launches)",
             "indexed_up_no_norm_us": round(us_f, 2), "indexed_up_unfused_us": round(us, 2),
-            "gated_us": round(us_g, 2), "gated_bytes": mlp_bytes(w.layers[0], I, H, k, gated=True),
-            "gated_schedule": "gate|up GEMV with RMSNorm on load writing gate and up of every channel, then the "
-                              "rule-A selection in every workgroup + the gated sparse down over the selected down^T "
-                              "rows (2 launches); equal to the four-launch schedule bit for bit"}
+            "gated_us": round(us_g, 2), "gated_row_form_us": round(us_gr, 2),
+            "gated_bytes": mlp_bytes(w.layers[0], I, H, k, dense_up=True),
+            "gated_row_form_bytes": mlp_bytes(w.layers[0], I, H, k, gated=True),
+            "gated_schedule": "gate|up GEMV with RMSNorm on load writing gate and h of every channel, then the "
+                              "rule-A selection in every workgroup + the down in the sparse accumulate's order over "
+                              "the transposed down_proj^T (gated_row_form_us: gate and up stored, then the selection "
+                              "+ gated sparse down over the selected down^T rows); 2 launches, equal to the "
+                              "four-launch schedule bit for bit"}
         res[f"dip_k{k}"]["GBps"] = round(res[f"dip_k{k}"]["bytes"] / us_du / 1e3, 1)
         del eng
     k = I // 2
@@ -526,8 +549,7 @@ def bench_decode(D, w, hot, dev, n_prompt: int = 64, n_new: int = 128, hot_sweep
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         toks[mode] = eng.log[:n_new].tolist()
-        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=kind == "dip_dense_up",
-                        gated=kind == "dip_gated")
+        mlp = mlp_bytes(L0, I, c.hidden, None if base == "dense" else k, dense_up=kind in ("dip_dense_up", "dip_gated"))
         per_tok = c.layers * (attn_w + mlp) + head_bytes[int4_head]
         out[mode] = {"decode_tok_s": round(n_new / (t2 - t1), 1), "ms_per_token": round((t2 - t1) / n_new * 1e3, 4),
                      "end_to_end_tok_s": round(n_new / (t2 - t0), 1), "prefill_ms": round((t1 - t0) * 1e3, 2),
@@ -829,6 +851,12 @@ def bench_kernels(dev, gen):
         res[f"dip_dense_down_k{k}"] = entry(H * I // 2 + 4 * (H // GS) * I + 4 * I + 2 * H, t["mean_us"],
                                             kernel="dip_dense_down (rule-A selection in every workgroup + the down "
                                                    "as one GEMV over the transposed down_proj^T, 1 launch)")
+        t = time_graph_per_launch(lambda W, S: _C.dip_select_down_ordered_into(g_all, h_all, k, W, S, None, None, yd,
+                                                                                GS), list(zip(Wd, Sd)))
+        res[f"dip_select_down_ordered_k{k}"] = entry(
+            H * I // 2 + 4 * (H // GS) * I + 4 * I + 2 * H, t["mean_us"],
+            kernel="dip_down_ordered (rule-A selection in every workgroup + the sparse down of the selected channels "
+                   "in its own order, over the transposed down_proj^T, 1 launch)")
     del Wd, Sd
     torch.cuda.empty_cache()
 

@@ -480,6 +480,31 @@ int soi_dip_select_gated_down(const uint16_t* gate, const uint16_t* up, int64_t 
                               const uint8_t* Wq_T, const float* scale_T, int64_t num_rows, int32_t* out_indices,
                               int32_t* out_count, uint16_t* y, int64_t H, int64_t group_size, int64_t num_groups,
                               void* workspace, size_t workspace_bytes, void* stream);
+/* soi_dip_select_down_ordered: the DIP selection and the sparse down of one
+ *   MLP in ONE launch from the binary16 gates and h = fp16(silu(gate) * up) of
+ *   every channel (as soi_gemv_w4a16_rmsnorm_swiglu_gate writes them), over
+ *   the transposed copy of down_proj^T that soi_dip_select_dense_down reads
+ *   (Wt [H, n/2], St [H/gs, n]). Indices, count and y equal
+ *   soi_topk_threshold_select_f16abs followed by
+ *   soi_gemv_w4a16_indexed_accumulate over h_sel = h[indices] (so also
+ *   soi_dip_select_gated_down on the same gate and up) bit for bit, with no
+ *   workspace and no cross-workgroup step: every output column replays the
+ *   sparse accumulate's partition and summation order (its row chunks of the
+ *   plan for (H, k), the 32 fma chains of each chunk, their sums in order).
+ *   Replaces the reference's topk_threshold_select (csrc/bindings.cpp:507-518)
+ *   and gemv_w4a16_sparse_accumulate (csrc/bindings.cpp:311-339) of one MLP.
+ *   Optional res / res_out (res_out null, or both given): res_out[H] = res +
+ *   y, one binary16 add. out_indices / out_count may be null. Requires
+ *   num_channels a multiple of 32 up to 24576, group_size a multiple of 8,
+ *   gate / h 8-byte and Wt / St 16-byte aligned, and a shape inside the
+ *   kernel's limits: soi_dip_select_down_ordered_lds_bytes(H, num_channels,
+ *   k) > 0 (the plan has at most 64 row chunks and the tables fit in 144 KB
+ *   of LDS; H = 2048 with n = 6144 fits for every k). */
+size_t soi_dip_select_down_ordered_lds_bytes(int64_t H, int64_t num_channels, int64_t k);
+int soi_dip_select_down_ordered(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
+                                const uint8_t* Wt, const float* St, int32_t* out_indices, int32_t* out_count,
+                                uint16_t* y, const uint16_t* res, uint16_t* res_out, int64_t H, int64_t group_size,
+                                int64_t num_groups, void* stream);
 
 /* --------------------------------------------------------------------------
  * Hot-cache GEMVs that read the misses in place (cache-aware DIP without a

@@ -1220,6 +1220,55 @@ void gemv_w4a16_rmsnorm_swiglu_gate_into(torch::Tensor Wq, torch::Tensor scale, 
                  n);
 }
 
+void dip_select_down_ordered_into(torch::Tensor gate, torch::Tensor h, int64_t k, torch::Tensor Wt,
+                                           torch::Tensor St, c10::optional<torch::Tensor> idx_out,
+                                           c10::optional<torch::Tensor> count_out, torch::Tensor y, int64_t group_size,
+                                           c10::optional<torch::Tensor> res, c10::optional<torch::Tensor> res_out) {
+    const char* n = "dip_select_down_ordered_into";
+    need(gate, torch::kFloat16, gate, n, "gate");
+    need(h, torch::kFloat16, gate, n, "h");
+    need(Wt, torch::kUInt8, gate, n, "Wt");
+    need(St, torch::kFloat32, gate, n, "St");
+    need(y, torch::kFloat16, gate, n, "y");
+    const int64_t I = gate.numel(), H = y.numel();
+    TORCH_CHECK(h.numel() == I, n, ": gate and h must have the same length");
+    TORCH_CHECK(k >= 1 && k <= I, n, ": k must be in [1, n]");
+    TORCH_CHECK(Wt.dim() == 2 && Wt.size(0) == H && Wt.size(1) == I / 2, n, ": Wt must be [H, n/2]");
+    TORCH_CHECK(St.dim() == 2 && St.size(1) == I, n, ": St must be [num_groups, n]");
+    int32_t* ip = nullptr;
+    int32_t* cp = nullptr;
+    if (idx_out.has_value()) {
+        need(*idx_out, torch::kInt32, gate, n, "idx_out");
+        need_numel(*idx_out, k, n, "idx_out");
+        ip = idx_out->data_ptr<int32_t>();
+    }
+    if (count_out.has_value()) {
+        need(*count_out, torch::kInt32, gate, n, "count_out");
+        need_numel(*count_out, 1, n, "count_out");
+        cp = count_out->data_ptr<int32_t>();
+    }
+    TORCH_CHECK(res.has_value() == res_out.has_value(), n, ": res and res_out go together");
+    const uint16_t* rp = nullptr;
+    uint16_t* rop = nullptr;
+    if (res.has_value()) {
+        need(*res, torch::kFloat16, gate, n, "res");
+        need(*res_out, torch::kFloat16, gate, n, "res_out");
+        TORCH_CHECK(res->numel() == H && res_out->numel() == H, n, ": res and res_out must have H values");
+        TORCH_CHECK(res_out->data_ptr() != y.data_ptr() && res->data_ptr() != y.data_ptr(), n,
+                    ": res / res_out must not alias y");
+        rp = h16(*res);
+        rop = h16m(*res_out);
+    }
+    const at::DeviceGuard guard(gate.device());
+    check_status(soi_dip_select_down_ordered(h16(gate), h16(h), I, k, Wt.data_ptr<uint8_t>(), St.data_ptr<float>(),
+                                             ip, cp, h16m(y), rp, rop, H, group_size, St.size(0), cur_stream(gate)),
+                 n);
+}
+
+int64_t dip_select_down_ordered_lds_bytes(int64_t H, int64_t num_channels, int64_t k) {
+    return static_cast<int64_t>(soi_dip_select_down_ordered_lds_bytes(H, num_channels, k));
+}
+
 void dip_select_dense_down_into(torch::Tensor gate, torch::Tensor h, int64_t k, torch::Tensor Wt, torch::Tensor St,
                                 c10::optional<torch::Tensor> idx_out, c10::optional<torch::Tensor> count_out,
                                 torch::Tensor y, int64_t group_size, c10::optional<torch::Tensor> res,
@@ -1585,6 +1634,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows, both halves written");
     m.def("gemv_w4a16_rmsnorm_swiglu_gate_into", &gemv_w4a16_rmsnorm_swiglu_gate_into,
           "INT4 GEMV of rmsnorm(x + delta) over interleaved gate|up rows: SwiGLU output and the gate half");
+    m.def("dip_select_down_ordered_into", &dip_select_down_ordered_into,
+          "DIP selection + sparse down over the transposed down^T values in one launch, in the sparse accumulate's "
+          "order (equal to top-k + the sparse down of h[idx] bit for bit); optional residual add",
+          py::arg("gate"), py::arg("h"), py::arg("k"), py::arg("Wt"), py::arg("St"), py::arg("idx_out"),
+          py::arg("count_out"), py::arg("y"), py::arg("group_size"), py::arg("res") = py::none(),
+          py::arg("res_out") = py::none());
+    m.def("dip_select_down_ordered_lds_bytes", &dip_select_down_ordered_lds_bytes,
+          "LDS bytes the ordered down needs for (H, n, k); 0 outside its limits");
     m.def("dip_select_dense_down_into", &dip_select_dense_down_into,
           "DIP selection + down projection over resident transposed down^T values in one launch (index outputs "
           "optional)",

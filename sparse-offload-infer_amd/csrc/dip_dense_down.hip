@@ -38,6 +38,7 @@
 // The index list of the selection is written only when asked for, after y,
 // from the same chunk masks and counts.
 #include "soi_device.h"
+#include "soi_down.h"
 #include "soi_host.h"
 #include "soi_select.h"
 
@@ -311,6 +312,269 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The selection + down in the sparse accumulate's own order, over the
+// transposed copy (soi_dip_select_down_ordered).
+//
+// y equals the top-k launch followed by the sparse down over the selected
+// channels' h values (soi_gemv_w4a16_indexed_accumulate with h_sel =
+// h[idx]) bit for bit, with no cross-workgroup step: each wave owns one
+// output column, as in the dense down above, and replays the sparse down's
+// summation for it. That kernel (soi_down.h) splits the k selected positions
+// into R row chunks of rpc positions (down_plan for (H, k)); inside chunk r,
+// the sub-partial g = 8w + rs of its (wave w, row lane rs) is the fma chain
+// acc = fma(coef_p, q_p, acc) over the positions p = r*rpc + g + 32i <
+// min((r+1)*rpc, kept) in ascending i, from acc = 0; the chunk's partial is
+// 0 + sub_0 + sub_1 + ... + sub_31 in that order, and y = 0 + partial_0 + ...
+// + partial_{R-1}. Here coef_p = fl(h_c * St[g, c]) with c the p-th kept
+// channel, and q_p the exact INT4 value of channel c in the column's
+// transposed row: the same products in the same order.
+//   1. the thread of 4-channel group q requests gate, h and St[g] of its
+//      channels, every lane its row chunks (as the dense down);
+//   2. rule A's threshold over |gate| (the coefficients fl(h * s) are formed
+//      after the first radix pass);
+//   3. the chunk masks [|gate| >= tau] and each wave's packed row go to LDS
+//      (one barrier); each thread finds the positions of its selected
+//      channels from the chunk prefix counts and writes (coef, location of
+//      the channel's nibble in a row) per position p < k (one barrier);
+//   4. thread t runs chain (r, g) = (t / 32, t % 32) (then t + 512, ...) for
+//      all 8 rows of the workgroup: one position-table read feeds 8 row-byte
+//      reads (a signed bitfield extract gives q) and 8 accumulators; then each
+//      wave's ordered sums: lane r sums chunk r's 32 sub-partials, and the
+//      chunk partials are summed in order; y and optionally res + y (one
+//      binary16 add) are stored.
+// Limits: R <= 64 row chunks, and the tables (8k + 4n + 8 * R * 128 bytes)
+// within kOdMaxLds of LDS.
+// ---------------------------------------------------------------------------
+constexpr int kOdMaxR = 64;
+constexpr int kOdMaxLds = 144 * 1024;
+
+struct OdArgs {
+    const uint16_t* gate;  // [n]
+    const uint16_t* h;     // [n] fp16(silu(gate) * up)
+    const uint8_t* W;      // [H, n/2]
+    const float* S;        // [G, n]
+    int32_t* out_idx;      // [k] or null
+    int32_t* out_count;    // [1] or null
+    uint16_t* y;           // [H]
+    const uint16_t* res;   // [H] or null
+    uint16_t* res_out;     // [H] or null: res + y, rounded once to binary16
+    int n, k, H, gs, rpc, R;
+    int pos_bytes;  // LDS: position table (8 bytes per position, rounded to 16); then 8 packed rows of n / 2 bytes
+};
+
+template <int NC>
+__global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) {
+    constexpr int E = 4 * NC;
+    __shared__ uint32_t s_hist[radix_hist_offset<F16AbsValues>(F16AbsValues::kPasses)];
+    __shared__ float s_max[kDdWaves];
+    __shared__ uint32_t s_bits[kDdMaxChunks];
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    const int n = a.n;
+    u32x2* s_pos = reinterpret_cast<u32x2*>(s_dyn);  // per position: coef bits, byte of the row | nibble shift << 16
+    uint8_t* s_row = s_dyn + a.pos_bytes;            // row w (packed, n / 2 bytes) at w * n / 2
+    float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * (n >> 1));  // [wave][R][32]
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+    const int chunks = n >> 5;  // n % 32 == 0 (checked on the host)
+    const int groups4 = n >> 2;
+    const int nb = gridDim.x, b = blockIdx.x;
+    const int tile = (nb % kXcds == 0) ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+    const int row = tile * kDdWaves + wave;
+    const int g = (tile * kDdWaves) / a.gs;
+    const u32x4* z4 = reinterpret_cast<const u32x4*>(g_zero16);
+    const u32x2* z2 = reinterpret_cast<const u32x2*>(g_zero16);
+
+    // 1. gate first, then h and St[g], then the row chunks (loads return in order)
+    u32x2 gq[NC], hq[NC];
+    u32x4 sq[NC];
+    const float* sg = a.S + static_cast<int64_t>(g) * n;
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        const int q = tid + m * kDdThreads;
+        gq[m] = ldg(q < groups4 ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
+    }
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        const int q = tid + m * kDdThreads;
+        const bool ok = q < groups4;
+        hq[m] = ldg(ok ? reinterpret_cast<const u32x2*>(a.h) + q : z2);
+        sq[m] = ldg(ok ? reinterpret_cast<const u32x4*>(sg) + q : z4);
+    }
+    u32x4 wv[NC];
+    {
+        const u32x4* rp = reinterpret_cast<const u32x4*>(a.W + static_cast<int64_t>(row < a.H ? row : 0) * (n >> 1));
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + i * kWave;
+            wv[i] = __builtin_nontemporal_load((row < a.H && c < chunks) ? rp + c : z4);
+        }
+    }
+    const uint16_t rv = ldg(a.res_out && row < a.H ? a.res + row : reinterpret_cast<const uint16_t*>(g_zero16));
+    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
+
+    // 2. |gate| keys (NaN past the end: key 0, never counted or selected) and rule A's threshold; after the first
+    // radix pass, the coefficients fl(h * St[g])
+    float gv[NC][4], xc[NC][4];
+    uint32_t key[E];
+    float local_max = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        const bool ok = tid + m * kDdThreads < groups4;
+        const uint32_t gw[2] = {gq[m].x, gq[m].y};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t gb = ((gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu) | (ok ? 0u : 0x7e00u);
+            gv[m][p] = f16_bits_to_f32(static_cast<uint16_t>(gb));
+            key[4 * m + p] = F16AbsValues::key_of(gv[m][p]);
+            local_max = fmaxf(local_max, gv[m][p]);
+        }
+    }
+    auto coefficients = [&]() {
+#pragma unroll
+        for (int m = 0; m < NC; ++m) {
+            // vector lanes copied to scalars before any bit cast (see the dense down)
+            const uint32_t hw[2] = {hq[m].x, hq[m].y};
+            const uint32_t su[4] = {sq[m].x, sq[m].y, sq[m].z, sq[m].w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                xc[m][p] = f16_bits_to_f32(static_cast<uint16_t>(hw[p >> 1] >> (16 * (p & 1)))) *
+                           __builtin_bit_cast(float, su[p]);
+        }
+    };
+    const float tau =
+        rule_a_tau<E, kDdWaves, F16AbsValues, true>(key, local_max, s_hist, s_max, a.k, tid, coefficients);
+
+    // 3. chunk masks (lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m) and the wave's packed row
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        const int q = tid + m * kDdThreads;
+        uint32_t m4 = 0u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) m4 |= (gv[m][p] >= tau ? 1u : 0u) << p;  // NaN (and padding) never
+        const uint32_t cm = or8_lanes(m4 << (4 * (lane & 7)));
+        if (q < groups4 && (lane & 7) == 0) s_bits[q >> 3] = cm;
+    }
+    {
+        uint8_t* my_row = s_row + wave * (n >> 1);
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + i * kWave;
+            if (c < chunks) *reinterpret_cast<u32x4*>(my_row + 16 * c) = wv[i];
+        }
+    }
+    __syncthreads();
+
+    // kept channels of the earlier chunks, chunk by chunk in index order (lane l: chunks l + 64i)
+    const uint32_t k = static_cast<uint32_t>(a.k);
+    uint32_t total = 0u;
+    uint32_t before[NC], bits[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + i * kWave;
+        bits[i] = c < chunks ? s_bits[c] : 0u;
+        const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(bits[i]));
+        const uint32_t incl = wave_prefix_u32(cnt);
+        before[i] = total + incl - cnt;
+        total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+    }
+    const uint32_t kk = total < k ? total : k;
+    // the position table: group q = tid + 512m lies in chunk (tid >> 3) + 64m, whose counts this wave's lane
+    // 8 * wave + (lane >> 3) holds at index m; the group's channels sit at bits 4 (lane & 7) .. + 3 of its mask
+    {
+        const int src = 8 * wave + (lane >> 3);
+        const uint32_t sh = 4u * static_cast<uint32_t>(lane & 7);
+#pragma unroll
+        for (int m = 0; m < NC; ++m) {
+            const uint32_t cb = static_cast<uint32_t>(__shfl(static_cast<int>(bits[m]), src, kWave));
+            uint32_t pos = static_cast<uint32_t>(__shfl(static_cast<int>(before[m]), src, kWave)) +
+                           static_cast<uint32_t>(__builtin_popcount(cb & ((1u << sh) - 1u)));
+            const uint32_t ch0 = 4u * static_cast<uint32_t>(tid + m * kDdThreads);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                if ((cb >> (sh + p)) & 1u) {
+                    if (pos < k) {
+                        // AWQ order: logical element j of a word sits at nibble (j >> 1) + 4 (j & 1)
+                        const uint32_t ch = ch0 + static_cast<uint32_t>(p);
+                        const uint32_t j = ch & 7u, nib = (j >> 1) + 4u * (j & 1u);
+                        const uint32_t loc = (4u * (ch >> 3) + (nib >> 1)) | ((4u * (nib & 1u)) << 16);
+                        s_pos[pos] = u32x2{__builtin_bit_cast(uint32_t, xc[m][p]), loc};
+                    }
+                    ++pos;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. the chains: thread t takes chain (r, gsub) = (t / 32, t % 32), then t + 512, ..., for all 8 rows of the
+    // workgroup at once (sparse-down wave gsub >> 3 and row lane gsub & 7 read positions r * rpc + gsub + 32i)
+    const int R = a.R, rpc = a.rpc;
+    for (int cn = tid; cn < R * 32; cn += kDdThreads) {
+        const int r = cn >> 5, gsub = cn & 31;
+        const int j0 = r * rpc;
+        const int j1 = j0 + rpc < static_cast<int>(kk) ? j0 + rpc : static_cast<int>(kk);
+        float acc[kDdWaves];
+#pragma unroll
+        for (int w = 0; w < kDdWaves; ++w) acc[w] = 0.0f;
+        int p = j0 + gsub;
+        u32x2 e = s_pos[p < j1 ? p : 0];  // s_pos[0] exists (k >= 1); read but unused when the chain is empty
+        for (; p < j1; p += 32) {
+            const int pn = p + 32;
+            const u32x2 en = s_pos[pn < j1 ? pn : p];  // the next entry, requested before the current one is used
+            const float cf = __builtin_bit_cast(float, e.x);
+            const int off = static_cast<int>(e.y & 0xffffu), sh = static_cast<int>(e.y >> 16);
+#pragma unroll
+            for (int w = 0; w < kDdWaves; ++w) {
+                // the nibble as a signed 4-bit value (v_bfe_i32 sign-extends): the exact INT4 value q
+                const int qv = __builtin_amdgcn_sbfe(static_cast<int>(s_row[w * (n >> 1) + off]), sh, 4);
+                acc[w] = fmaf(cf, static_cast<float>(qv), acc[w]);
+            }
+            e = en;
+        }
+#pragma unroll
+        for (int w = 0; w < kDdWaves; ++w) s_sub[(w * R + r) * 32 + gsub] = acc[w];
+    }
+    __syncthreads();
+    const float* my_sub = s_sub + wave * R * 32;
+    float part = 0.0f;
+    if (lane < R) {
+#pragma unroll 8
+        for (int s2 = 0; s2 < 32; ++s2) part += my_sub[lane * 32 + s2];
+    }
+    float sum = 0.0f;
+    for (int r = 0; r < R; ++r)
+        sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), r));
+    if (lane == 0 && row < a.H) {
+        const uint16_t yb = f32_to_f16_bits(sum);
+        stg(a.y + row, yb);
+        if (a.res_out) stg(a.res_out + row, static_cast<uint16_t>(add_f16x2(rv, yb)));
+    }
+
+    // 5. the index list when asked for (after y), by wave 0: workgroup b writes positions [b*win, (b+1)*win)
+    if (b == 0 && tid == 0 && a.out_count) stg(a.out_count, static_cast<int32_t>(kk));
+    if (!a.out_idx || wave != 0) return;  // wave-uniform
+    const uint32_t win = (kk + nb - 1) / nb;
+    const uint32_t lo = b * win;
+    const uint32_t hi = lo + win < kk ? lo + win : kk;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + i * kWave;
+        const int keep = before[i] >= k ? 0
+                         : (before[i] + static_cast<uint32_t>(__builtin_popcount(bits[i])) <= k
+                                ? 32
+                                : nth_set_bit(bits[i], k - before[i]) + 1);
+        uint32_t x = keep >= 32 ? bits[i] : (bits[i] & ((1u << keep) - 1u));
+        uint32_t pos = before[i];
+        if (c >= chunks || pos >= hi || pos + static_cast<uint32_t>(__builtin_popcount(x)) <= lo) continue;
+        while (x != 0u) {
+            if (pos >= lo && pos < hi) stg(a.out_idx + pos, static_cast<int32_t>(32 * c + __builtin_ctz(x)));
+            ++pos;
+            x &= x - 1u;
+        }
+    }
+}
+
 }  // namespace soi
 
 using namespace soi;
@@ -372,4 +636,77 @@ extern "C" int soi_dip_select_dense_down_residual(const uint16_t* gate, const ui
     SOI_REQUIRE(res && res_out, "%s: null pointer", what);
     return dense_down(gate, h, num_channels, k, Wt, St, out_indices, out_count, y, res, res_out, H, group_size,
                       num_groups, stream, what);
+}
+
+// LDS of the ordered down for (H, n, k): the position table, the 8 packed rows and the chains' sub-partials;
+// 0 when the shape is outside the kernel's limits.
+static size_t ordered_lds(int64_t H, int64_t n, int64_t k, DownPlan* plan) {
+    if (H < 1 || n < 32 || n % 32 != 0 || n > kDdMaxChannels || k < 1 || k > n) return 0;
+    const DownPlan p = down_plan(H, k);
+    if (p.R > kOdMaxR) return 0;
+    const size_t pos = (static_cast<size_t>(k) * 8 + 15) / 16 * 16;
+    const size_t lds = pos + static_cast<size_t>(kDdWaves) * static_cast<size_t>(n / 2) +
+                       static_cast<size_t>(kDdWaves) * static_cast<size_t>(p.R) * 32 * sizeof(float);
+    if (lds > static_cast<size_t>(kOdMaxLds)) return 0;
+    if (plan) *plan = p;
+    return lds;
+}
+
+extern "C" size_t soi_dip_select_down_ordered_lds_bytes(int64_t H, int64_t num_channels, int64_t k) {
+    return ordered_lds(H, num_channels, k, nullptr);
+}
+
+extern "C" int soi_dip_select_down_ordered(const uint16_t* gate, const uint16_t* h, int64_t num_channels, int64_t k,
+                                           const uint8_t* Wt, const float* St, int32_t* out_indices,
+                                           int32_t* out_count, uint16_t* y, const uint16_t* res, uint16_t* res_out,
+                                           int64_t H, int64_t group_size, int64_t num_groups, void* stream) {
+    const char* what = "soi_dip_select_down_ordered";
+    const int64_t n = num_channels;
+    SOI_REQUIRE(n >= 32 && n <= kDdMaxChannels && n % 32 == 0, "%s: num_channels must be a multiple of 32 in [32, %d]",
+                what, kDdMaxChannels);
+    SOI_REQUIRE(k >= 1 && k <= n, "%s: k must be in [1, num_channels]", what);
+    SOI_REQUIRE(H >= 1 && H <= (int64_t(1) << 24), "%s: H out of range", what);
+    SOI_REQUIRE(group_size >= kDdWaves && group_size % kDdWaves == 0, "%s: group_size must be a positive multiple of %d",
+                what, kDdWaves);
+    SOI_REQUIRE(num_groups == ceil_div64(H, group_size), "%s: num_groups must be ceil(H / group_size)", what);
+    SOI_REQUIRE(gate && h && Wt && St && y, "%s: null pointer", what);
+    SOI_REQUIRE(!res_out || res, "%s: res_out needs res", what);
+    SOI_REQUIRE(aligned16(Wt) && aligned16(St), "%s: Wt and St must be 16-byte aligned", what);
+    SOI_REQUIRE((reinterpret_cast<uintptr_t>(gate) & 7u) == 0 && (reinterpret_cast<uintptr_t>(h) & 7u) == 0,
+                "%s: gate and h must be 8-byte aligned", what);
+    DownPlan p{};
+    const size_t lds = ordered_lds(H, n, k, &p);
+    SOI_REQUIRE(lds > 0, "%s: H = %lld, k = %lld: the sparse down's plan has more than %d row chunks or the tables "
+                "need more than %d bytes of LDS; use the top-k kernel and the sparse down", what, (long long)H,
+                (long long)k, kOdMaxR, kOdMaxLds);
+    OdArgs a{gate, h, Wt, St, out_indices, out_count, y, res, res_out, static_cast<int>(n), static_cast<int>(k),
+             static_cast<int>(H), static_cast<int>(group_size), static_cast<int>(p.rpc), static_cast<int>(p.R),
+             static_cast<int>((static_cast<size_t>(k) * 8 + 15) / 16 * 16)};
+    const dim3 grid(static_cast<unsigned>(ceil_div64(H, kDdWaves))), block(kDdThreads);
+    const int64_t nc = ceil_div64(n, kDdChannelsPerPass);
+    hipStream_t st = as_stream(stream);
+    const unsigned sh = static_cast<unsigned>(lds);
+#define SOI_OD(NN)                                                                                             \
+    do {                                                                                                       \
+        SOI_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&dip_down_ordered_kernel<NN>),           \
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sh)),     \
+                    what);                                                                                     \
+        hipLaunchKernelGGL((dip_down_ordered_kernel<NN>), grid, block, sh, st, a);                             \
+    } while (0)
+    switch (nc) {
+        case 1: SOI_OD(1); break;
+        case 2: SOI_OD(2); break;
+        case 3: SOI_OD(3); break;
+        case 4: SOI_OD(4); break;
+        case 5: SOI_OD(5); break;
+        case 6: SOI_OD(6); break;
+        case 7: SOI_OD(7); break;
+        case 8: SOI_OD(8); break;
+        case 9: SOI_OD(9); break;
+        case 10: SOI_OD(10); break;
+        case 11: SOI_OD(11); break;
+        default: SOI_OD(12); break;
+    }
+#undef SOI_OD
+    return launch_status(what);
 }

@@ -262,10 +262,14 @@ class DecodeEngine:
         #  * "indexed" (default): RMSNorm-fused gate GEMV, top-k, up GEMV over the selected rows with the SiLU
         #    epilogue, sparse down over the selected down^T rows (4 MLP launches); the cache-aware modes equal it
         #    bit for bit;
-        #  * "gated": one launch computes gate and up of every channel (RMSNorm on load), a second runs the rule-A
-        #    selection in each of its workgroups and the sparse down over the selected down^T rows with
-        #    h = fp16(silu(gate) * up) formed on load (2 MLP launches): the same selection, the same h values and
-        #    the same row partition and sums as "indexed", so the same y bit for bit;
+        #  * "gated" (2 MLP launches, the same y as "indexed" bit for bit): where the shape fits
+        #    (dip_select_down_ordered_lds_bytes > 0), one launch computes gate and h = fp16(silu(gate) * up) of
+        #    every channel (RMSNorm on load; the rounding of the indexed up GEMV's SiLU epilogue), and a second
+        #    runs the rule-A selection in each of its workgroups and the down over a transposed copy of
+        #    down_proj^T, each output column replaying the sparse accumulate's partition and order, with no
+        #    cross-workgroup step and the residual add in its epilogue; otherwise the first launch stores gate
+        #    and up, and the second runs the selection and the sparse down over the selected down^T rows with h
+        #    formed on load;
         #  * "dense_up": one launch computes gate and h = fp16(silu(gate) * up) of every channel, a second runs
         #    the rule-A selection in each of its workgroups and the down projection as a GEMV over a transposed
         #    copy of down_proj^T's quantized values with the masked coefficients (no cross-workgroup step). The
@@ -274,6 +278,8 @@ class DecodeEngine:
         self.dip_schedule = dip_schedule
         self.dip_dense_up = dip_dense_up
         self.dip_gated = dip_schedule == "gated"
+        self.dip_gated_tr = self.dip_gated and dip_k is not None and 1 <= dip_k <= w.config.intermediate and \
+            _C.dip_select_down_ordered_lds_bytes(w.config.hidden, w.config.intermediate, dip_k) > 0
         c = w.config
         self.w, self.c, self.mode, self.fused = w, c, mode, fused
         self.residual_epilogue = bool(residual_epilogue)
@@ -327,7 +333,7 @@ class DecodeEngine:
             if hot_channels is None or len(hot_channels) != c.layers:
                 raise ValueError("cached_dip needs one hot-channel list per layer")
             self._setup_cache(hot_channels)
-        if dip_dense_up:
+        if dip_dense_up or self.dip_gated_tr:
             # down_proj^T's values transposed for the one-launch down (the same quantized values, no rounding)
             self.down_tt = [ops.transposed_down_T(L.down_T_Wq, L.down_T_scale, H) for L in w.layers]
         if fused and (mode == "dense" or dip_schedule != "indexed"):
@@ -499,7 +505,11 @@ class DecodeEngine:
         if self.dip_gated:
             uW, uS = L.up(I)
             _C.gemv_w4a16_into(uW, uS, self.h, self.gu[I:], H, gs)
-            self._gated_down(l, L, gate, self.gu[I:])
+            if self.dip_gated_tr:
+                _C.silu_mul_into(gate, self.gu[I:], self.mlp_h)  # h of every channel
+                self._gated_down(l, L, gate, self.mlp_h)
+            else:
+                self._gated_down(l, L, gate, self.gu[I:])
             return
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)
         self._count_selection(l)
@@ -538,12 +548,23 @@ class DecodeEngine:
                                       res if res_out is not None else None, res_out)
         self._count_selection(l)
 
-    def _gated_down(self, l: int, L: LayerWeights, gate: torch.Tensor, up: torch.Tensor):
-        """Selection + sparse down of the gated schedule (gate and up of every channel given): h of the selected
-        channels is formed on load, as the indexed up GEMV's SiLU epilogue rounds it."""
+    def _gated_down(self, l: int, L: LayerWeights, gate: torch.Tensor, hu: torch.Tensor,
+                    res: Optional[torch.Tensor] = None, res_out: Optional[torch.Tensor] = None):
+        """Selection + sparse down of the gated schedule. Over the transposed copy (hu = h of every channel) the
+        index list is written only for the eager consumers that read it, and with res_out the launch also writes
+        res + down there; over the selected rows (hu = up of every channel) h of the selected channels is formed
+        on load, as the indexed up GEMV's SiLU epilogue rounds it."""
         c = self.c
-        _C.dip_select_gated_down_into(gate, up, self.k, L.down_T_Wq, L.down_T_scale, self.idx, self.cnt, self.down,
-                                      c.hidden, c.group_size, self.sd_ws)
+        if self.dip_gated_tr:
+            Wt, St = self.down_tt[l]
+            want = self.counts is not None or self.layer_hook is not None
+            _C.dip_select_down_ordered_into(gate, hu, self.k, Wt, St, self.idx if want else None,
+                                            self.cnt if want else None, self.down, c.group_size,
+                                            res if res_out is not None else None, res_out)
+        else:
+            assert res_out is None
+            _C.dip_select_gated_down_into(gate, hu, self.k, L.down_T_Wq, L.down_T_scale, self.idx, self.cnt,
+                                          self.down, c.hidden, c.group_size, self.sd_ws)
         self._count_selection(l)
 
     def _count_selection(self, l: int):
@@ -605,7 +626,8 @@ class DecodeEngine:
         H, gs = c.hidden, c.group_size
         cur, other = self.x, self.x2
         fold = self.residual_epilogue
-        down_res = fold and (self.mode == "dense" or self.dip_dense_up)  # the down launch writes the residual
+        # the down launch writes the residual
+        down_res = fold and (self.mode == "dense" or self.dip_dense_up or self.dip_gated_tr)
         last = len(self.w.layers) - 1
         _C.embed_lookup_into(self.w.embed, self.token, cur)
         for l, L in enumerate(self.w.layers):
@@ -670,12 +692,17 @@ class DecodeEngine:
                                                    H, gs)
             self._dense_down(l, gate, self.gu[I:], x, res_out)
             return
-        assert res_out is None
         if self.dip_gated:
             gW, gS = gu_il
-            _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, x, delta, L.post_norm, eps, x_out, gate, self.gu[I:], H, gs)
-            self._gated_down(l, L, gate, self.gu[I:])
+            if self.dip_gated_tr:  # gate and h of every channel, as the dense-up schedule's first launch
+                _C.gemv_w4a16_rmsnorm_swiglu_gate_into(gW, gS, x, delta, L.post_norm, eps, x_out, gate,
+                                                       self.gu[I:], H, gs)
+            else:  # gate and up of every channel
+                _C.gemv_w4a16_rmsnorm_gate_up_into(gW, gS, x, delta, L.post_norm, eps, x_out, gate, self.gu[I:],
+                                                   H, gs)
+            self._gated_down(l, L, gate, self.gu[I:], x, res_out)
             return
+        assert res_out is None
         gW, gS = L.gate(I)
         _C.gemv_w4a16_rmsnorm_into(gW, gS, x, delta, L.post_norm, eps, x_out, self.h, gate, H, gs, False)
         _C.topk_threshold_select_f16abs_into(gate, self.k, self.idx, self.cnt)

@@ -160,9 +160,10 @@ def test_dip_dense_up_schedule(dec, tiny, fused):
 
 @pytest.mark.parametrize("fused", [True, False])
 def test_dip_gated_schedule_bit_identical_to_indexed(dec, tiny, fused):
-    """Gate and up of every channel in one launch + the one-launch selection and gated sparse down: the same
-    selection, h values and row partition as the indexed schedule, so the same tokens and hidden state bit for
-    bit, eager and graph replays; the selection indices too."""
+    """Gate and up of every channel in one launch + the one-launch selection and gated sparse down (here over
+    the transposed copy, with the residual add in its epilogue): the same selection, h values and summation
+    order as the indexed schedule, so the same tokens and hidden state bit for bit, eager and graph replays.
+    (The index list is written only for eager consumers that read it; the kernels' own tests compare it.)"""
     cfg = tiny.config
     k = cfg.intermediate // 2
     prompt = prompt_ids(6, cfg.vocab, seed=19)
@@ -172,8 +173,8 @@ def test_dip_gated_schedule_bit_identical_to_indexed(dec, tiny, fused):
     for use_graph in (False, True, True):
         assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"graph={use_graph}"
         assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
-        assert torch.equal(eng.idx, plain.idx) and torch.equal(eng.cnt, plain.cnt)
         _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
+    assert eng.dip_gated_tr
 
 
 @pytest.mark.parametrize("fused", [True, False])
