@@ -37,6 +37,8 @@
 //      stores y.
 // The index list of the selection is written only when asked for, after y,
 // from the same chunk masks and counts.
+#include <mutex>
+
 #include "soi_device.h"
 #include "soi_down.h"
 #include "soi_host.h"
@@ -652,6 +654,27 @@ static size_t ordered_lds(int64_t H, int64_t n, int64_t k, DownPlan* plan) {
     return lds;
 }
 
+// The ordered kernels may take more than 64 KB of dynamic LDS: the limit is raised to kOdMaxLds once per device
+// and instantiation (the first call on a device; launches below the limit need nothing more).
+constexpr int kOdMaxDevices = 64;
+static std::mutex g_od_mu;
+static bool g_od_attr[kOdMaxDevices][kDdMaxNC + 1] = {};
+
+template <int NN>
+static int ordered_lds_limit(const char* what) {
+    int dev = -1;
+    SOI_HIP_TRY(hipGetDevice(&dev), what);
+    SOI_REQUIRE(dev >= 0 && dev < kOdMaxDevices, "%s: device %d out of range", what, dev);
+    std::lock_guard<std::mutex> lock(g_od_mu);
+    if (!g_od_attr[dev][NN]) {
+        SOI_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&dip_down_ordered_kernel<NN>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, kOdMaxLds),
+                    what);
+        g_od_attr[dev][NN] = true;
+    }
+    return SOI_OK;
+}
+
 extern "C" size_t soi_dip_select_down_ordered_lds_bytes(int64_t H, int64_t num_channels, int64_t k) {
     return ordered_lds(H, num_channels, k, nullptr);
 }
@@ -688,9 +711,8 @@ extern "C" int soi_dip_select_down_ordered(const uint16_t* gate, const uint16_t*
     const unsigned sh = static_cast<unsigned>(lds);
 #define SOI_OD(NN)                                                                                             \
     do {                                                                                                       \
-        SOI_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&dip_down_ordered_kernel<NN>),           \
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sh)),     \
-                    what);                                                                                     \
+        const int ls = ordered_lds_limit<NN>(what);                                                            \
+        if (ls) return ls;                                                                                     \
         hipLaunchKernelGGL((dip_down_ordered_kernel<NN>), grid, block, sh, st, a);                             \
     } while (0)
     switch (nc) {

@@ -159,22 +159,26 @@ def test_dip_dense_up_schedule(dec, tiny, fused):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-def test_dip_gated_schedule_bit_identical_to_indexed(dec, tiny, fused):
-    """Gate and up of every channel in one launch + the one-launch selection and gated sparse down (here over
-    the transposed copy, with the residual add in its epilogue): the same selection, h values and summation
-    order as the indexed schedule, so the same tokens and hidden state bit for bit, eager and graph replays.
-    (The index list is written only for eager consumers that read it; the kernels' own tests compare it.)"""
+@pytest.mark.parametrize("ordered", [True, False])
+def test_dip_gated_schedule_bit_identical_to_indexed(dec, tiny, fused, ordered):
+    """The gated schedule's two MLP launches, in both forms: gate and h of every channel + the selection and the
+    ordered down over the transposed copy (residual add in its epilogue), and the row form the engine falls back
+    to outside that kernel's limits (gate and up of every channel + the selection and gated sparse down over the
+    selected rows; forced here). The same selection, h values and summation order as the indexed schedule, so
+    the same tokens and hidden state bit for bit, eager and graph replays. (The ordered form writes the index list
+    only for eager consumers that read it; the kernels' own tests compare it.)"""
     cfg = tiny.config
     k = cfg.intermediate // 2
     prompt = prompt_ids(6, cfg.vocab, seed=19)
     plain = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused)
     want = plain.generate(prompt, 6, use_graph=True)
     eng = dec.DecodeEngine(tiny, "dip", dip_k=k, max_new_tokens=6, fused=fused, dip_schedule="gated")
+    assert eng.dip_gated_tr  # this shape fits the ordered down
+    eng.dip_gated_tr = ordered
     for use_graph in (False, True, True):
         assert eng.generate(prompt, 6, use_graph=use_graph) == want, f"graph={use_graph}"
         assert torch.equal(eng.x_final, plain.x_final), f"graph={use_graph}: hidden state differs"
         _ = torch.zeros(1 << 20, device="cuda").sum()  # unrelated eager work between replays
-    assert eng.dip_gated_tr
 
 
 @pytest.mark.parametrize("fused", [True, False])
