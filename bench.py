@@ -11,7 +11,9 @@ fp16 x + fp16 y), each weight resident in HBM and touched once per step
 (751 MB > the 256 MB Infinity Cache, so reads come from HBM). The 196
 independent GEMVs run as ONE grouped launch per step (4 shape classes).
 value = algorithmic bytes / step time, timed over --steps steps between two
-device synchronisations.
+device synchronisations, after --ramp-ms (default 250) of untimed steps and
+--warmup steps (the loaded steady state: the first hundred or so launches
+after set-up run up to ~10% slower).
 
 The last stdout line is the compact result: the headline fields, config,
 roofline (the dominant -- and only -- launch of a step; its average duration
@@ -37,7 +39,7 @@ one 'bench-detail: {...}' line on stderr (and --detail-json PATH):
   cpu_baseline    the reference's CPU GEMV path (dequantize + fp32 torch.mv) on layer 0's GEMVs,
                   at the job's host cores and one thread, and the other operators' CPU oracles.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS]
        python bench.py --traffic-set   (only the launches of the HBM counter passes whose summaries are
                                         committed under profiles/; prints their algorithmic bytes)
 """
@@ -1101,6 +1103,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ramp-ms", type=float, default=250.0,
+                    help="untimed streaming of the weight set before the warmup steps (ms of wall time)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the decode-chain, per-shape and top-k tables")
     ap.add_argument("--no-decode", action="store_true", help="skip the DIP MLP and decode tok/s sections")
@@ -1153,6 +1157,26 @@ def main() -> int:
     for _ in range(3):
         step()
     torch.cuda.synchronize()
+    # the same number of steps before the ramp (detail record only: the cold-start rate)
+    ev_c0, ev_c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev_c0.record()
+    for _ in range(args.steps):
+        step()
+    ev_c1.record()
+    ev_c1.synchronize()
+    cold_us = ev_c0.elapsed_time(ev_c1) * 1e3 / args.steps
+    # load ramp: the first launches after set-up run slower than the loaded steady state (the same 50 steps after
+    # 5 / 50 / 200 / 1000 warmup steps: 130.9 / 129.0 / 119.0 / 116.8 us per launch, one box), so the weight set
+    # is streamed for --ramp-ms of wall time (untimed) before the W warmup steps
+    ramp_steps = 0
+    t_ramp = time.perf_counter()
+    while (time.perf_counter() - t_ramp) * 1e3 < args.ramp_ms:
+        for _ in range(16):
+            step()
+        torch.cuda.synchronize()
+        ramp_steps += 16
+    log(f"{args.steps} steps before the ramp: {cold_us:.3f} us per launch (events); load ramp: {ramp_steps} untimed "
+        f"steps in {(time.perf_counter() - t_ramp) * 1e3:.0f} ms")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -1260,12 +1284,13 @@ def main() -> int:
                                "Qwen3-1.7B-shaped decoder (q,k,v,o,gate,up,down; each GEMV its own x), HBM-resident; "
                                "all 196 GEMVs in one grouped launch per step",
                    "bytes_per_step": step_bytes, "layers": LAYERS, "hidden": H, "intermediate": I,
-                   "group_size": GS},
+                   "group_size": GS, "ramp": f"{ramp_steps} untimed steps ({args.ramp_ms:g} ms) before the warmup"},
         "frac_of_hbm_peak": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": roofline,
     }
     # everything else goes to the detail record (stderr, and --detail-json): the result line stays compact
-    detail = {"dominant_launch_back_to_back_after_timed_us": round(dom_b2b_us, 3), "copy_reference": copy_ref,
+    detail = {"dominant_launch_back_to_back_after_timed_us": round(dom_b2b_us, 3),
+              "dominant_launch_before_ramp_us": round(cold_us, 3), "copy_reference": copy_ref,
               "batched_per_class": per_class, "int8_batched_per_class": int8_per_class, "step_spread": step_stats}
     if not args.no_extras:
         detail["decode_chain"] = bench_decode_chain(ops, layers, step_bytes)
