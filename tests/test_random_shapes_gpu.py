@@ -11,7 +11,11 @@ same cases every run), each within the operator's documented limits.
   * the ordered down (selection + the sparse accumulate's order over the transposed copy) where its limits
     allow, bit-identical to the row form;
   * decode attention: query / KV head counts, head sizes (fast and general kernels), cache sizes and lengths
-    against the binary64 softmax attention.
+    against the binary64 softmax attention;
+  * INT8 GEMV (per-tensor, per-channel, group scales) against the binary64 oracle;
+  * the cache-aware chain: a random selection and hot set, build_dip_descriptors equal to the oracle (exact),
+    then the descriptor-driven up and down (hot rows from the cache copy, misses from a staging copy)
+    bit-identical to the index-driven GEMVs over the resident rows, and within the oracle's tolerance.
 """
 import numpy as np
 import pytest
@@ -156,3 +160,62 @@ def test_decode_attention(ops, NQ, NKV, hd, S, L):
     ref = O.decode_attention_f64(q.numpy(), k.numpy(), v.numpy(), L)
     out = ops.decode_attention(q.cuda(), k.cuda(), v.cuda(), L)
     assert_close(out, ref, f"attention {NQ}/{NKV} hd={hd} S={S} L={L}")
+
+
+INT8 = _cases(606, 16, lambda r: (int(r.integers(1, 3001)), int(r.integers(1, 4097)),
+                                  str(r.choice(["per_tensor", "per_channel", "group"])),
+                                  int(r.choice([8, 16, 32, 64, 128]))))
+
+
+@pytest.mark.parametrize("N,K,gran,gs", INT8)
+def test_int8_gemv(ops, N, K, gran, gs):
+    g = torch.Generator().manual_seed(N + K)
+    if gran == "group":
+        K = max(gs, K // gs * gs)  # group scales: K a multiple of the group size
+    w = (torch.randn(N, K, generator=g)).numpy()
+    q, sc = O.quantize_group(w, gs, bits=8) if gran == "group" else O.quantize_simple(w, gran, bits=8)
+    q = q[:, :K].copy()
+    x = torch.randn(K, generator=g).half()
+    gsz = gs if gran == "group" else K
+    ref = O.gemv_w8_f64(q, sc, x.numpy(), gsz)
+    y = ops.gemv_w8a16(torch.from_numpy(q).cuda(), torch.from_numpy(np.ascontiguousarray(sc)).cuda(), x.cuda(), gsz)
+    assert_close(y, ref, f"int8 {gran} {N}x{K} gs={gsz}")
+
+
+CACHED = _cases(707, 12, lambda r: (int(r.integers(32, 8193)), int(r.integers(8, 3001)), float(r.uniform(0.0, 1.0)),
+                                    float(r.uniform(0.0, 1.0)), int(r.choice([32, 64, 128]))))
+
+
+@pytest.mark.parametrize("I,H,kf,hot,gs", CACHED)
+def test_cache_aware_chain(ops, I, H, kf, hot, gs):
+    k = max(1, min(I, int(round(kf * I))))
+    r = np.random.default_rng(I + H)
+    up = int4_problem(I, H, gs, seed=I * 5 + H)        # up_proj: I rows of H
+    dn = int4_problem(I, H, gs, seed=I * 5 + H + 1)    # down_proj^T: I rows of H
+    Hp = up["K"]
+    sel = np.sort(r.choice(I, size=k, replace=False)).astype(np.int32)
+    hot_ch = np.sort(r.choice(I, size=int(round(hot * I)), replace=False)).astype(np.int32)
+    slot_of = np.full(I, -1, np.int32)
+    slot_of[hot_ch] = np.arange(hot_ch.size, dtype=np.int32)
+    d_ref, m_ref, mc_ref = O.build_dip_descriptors(sel, slot_of)
+    sel_d = torch.from_numpy(sel).cuda()
+    desc, miss, mc = ops.build_dip_descriptors(sel_d, torch.from_numpy(slot_of).cuda())
+    assert int(mc.item()) == mc_ref and np.array_equal(desc.cpu().numpy(), d_ref), f"I={I} k={k}: descriptors"
+    assert np.array_equal(miss.cpu().numpy()[:mc_ref], m_ref[:mc_ref]), f"I={I} k={k}: miss list"
+    hot_t = torch.from_numpy(hot_ch).long().cuda()
+    miss_t = torch.from_numpy(m_ref[:mc_ref]).long().cuda()
+    for name, p in (("up", up), ("down", dn)):
+        W, S = p["Wq_d"], p["s_d"]
+        cW, cS = W.index_select(0, hot_t).contiguous(), S.index_select(0, hot_t).contiguous()
+        sW, sS = W.index_select(0, miss_t).contiguous(), S.index_select(0, miss_t).contiguous()
+        if name == "up":
+            y = ops.gemv_dip_fused_up(cW, cS, sW, sS, desc, up["x_d"], Hp, gs)
+            assert torch.equal(y, ops.gemv_w4a16_indexed(W, S, sel_d, up["x_d"], Hp, gs)), f"I={I} k={k}: up"
+            assert_close(y, O.gemv_w4_f64(up["Wq"][sel], up["s"][sel], up["x"], Hp, gs), f"I={I} k={k}: up", floor=5e-5)
+        else:
+            h = torch.from_numpy(r.standard_normal(k).astype(np.float32)).half()
+            y = ops.gemv_dip_fused_down(cW, cS, sW, sS, desc, h.cuda(), Hp, gs)
+            assert torch.equal(y, ops.gemv_w4a16_indexed_accumulate(W, S, sel_d, h.cuda(), Hp, gs)), \
+                f"I={I} k={k}: down"
+            assert_close(y, O.sparse_accumulate_f64(dn["Wq"][sel], dn["s"][sel], h.numpy(), Hp, gs),
+                         f"I={I} k={k}: down")
