@@ -257,10 +257,13 @@ __device__ __forceinline__ float wave_sum(const float (*s_state)[REP][HD + 2], i
 
 // out[h,d] = (sum_s acc_s[d] 2^(m_s-M)) / (sum_s l_s 2^(m_s-M)) over the ns
 // split states of the KV head's query heads h0 .. h0+rep-1, M = max_s m_s.
-// Thread o takes output (o / HD, o % HD). Its first kCombineBatch split values
-// are requested before the (m, l) pairs, which go to LDS, so both arrive in
-// one memory round trip (more only past 32 splits or 512 outputs); every sum
-// runs over the splits in ascending order: deterministic.
+// Thread o takes output (o / HD, o % HD). Its first B split values are
+// requested before the (m, l) pairs, which go to LDS, so both arrive in one
+// memory round trip (more only past B splits or 512 outputs); every sum runs
+// over the splits in ascending order: deterministic. B = 8, 16 or 32, the
+// smallest that holds ns (a wave-uniform choice): a batch longer than ns
+// repeats split 0's loads, and repeated loads of one address queue behind
+// each other.
 constexpr int kCombineMaxSplits = kAttnTargetGroups;  // nsplit <= kAttnTargetGroups by construction of the plan
 constexpr int kCombineBatch = 32;
 
@@ -275,18 +278,18 @@ __device__ __forceinline__ float part_load(const float* p) {
         return ldg(p);
 }
 
-template <int NT, int HD, bool COHERENT = false>
-__device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint16_t* __restrict__ out, int h0, int rep,
-                                           int nsplit, int ns, float* s_m, float* s_l) {
+template <int NT, int HD, bool COHERENT, int B>
+__device__ __forceinline__ void combine_kv_b(const float* __restrict__ part, uint16_t* __restrict__ out, int h0,
+                                             int rep, int nsplit, int ns, float* s_m, float* s_l) {
     constexpr int stride = HD + 2;
     const int tid = threadIdx.x;
     const int nout = rep * HD;
-    float v[kCombineBatch];
+    float v[B];
     {
         const int o = tid < nout ? tid : 0;
         const float* po = part + static_cast<int64_t>(h0 + o / HD) * nsplit * stride + 2 + o % HD;
 #pragma unroll
-        for (int s = 0; s < kCombineBatch; ++s) v[s] = part_load<COHERENT>(po + static_cast<int64_t>(s < ns ? s : 0) * stride);
+        for (int s = 0; s < B; ++s) v[s] = part_load<COHERENT>(po + static_cast<int64_t>(s < ns ? s : 0) * stride);
     }
     for (int i = tid; i < rep * ns; i += NT) {
         const int hh = i / ns, sp = i % ns;
@@ -303,14 +306,14 @@ __device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint1
         float M = kNegBig;
         for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, sm[sp]);
         float lsum = 0.0f, acc = 0.0f;
-        for (int b0 = 0; b0 < ns; b0 += kCombineBatch) {
+        for (int b0 = 0; b0 < ns; b0 += B) {
             if (o != tid || b0 > 0) {  // the first batch of the first output is already in v
 #pragma unroll
-                for (int s = 0; s < kCombineBatch; ++s)
+                for (int s = 0; s < B; ++s)
                     v[s] = part_load<COHERENT>(po + static_cast<int64_t>(b0 + s < ns ? b0 + s : 0) * stride);
             }
 #pragma unroll
-            for (int s = 0; s < kCombineBatch; ++s) {
+            for (int s = 0; s < B; ++s) {
                 if (b0 + s >= ns) break;
                 const float w = fast_exp2(sm[b0 + s] - M);
                 lsum = fmaf(sl[b0 + s], w, lsum);
@@ -319,6 +322,17 @@ __device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint1
         }
         stg(out + static_cast<int64_t>(h0 + hh) * HD + o % HD, f32_to_f16_bits(acc / lsum));
     }
+}
+
+template <int NT, int HD, bool COHERENT = false>
+__device__ __forceinline__ void combine_kv(const float* __restrict__ part, uint16_t* __restrict__ out, int h0, int rep,
+                                           int nsplit, int ns, float* s_m, float* s_l) {
+    if (ns <= 8)
+        combine_kv_b<NT, HD, COHERENT, 8>(part, out, h0, rep, nsplit, ns, s_m, s_l);
+    else if (ns <= 16)
+        combine_kv_b<NT, HD, COHERENT, 16>(part, out, h0, rep, nsplit, ns, s_m, s_l);
+    else
+        combine_kv_b<NT, HD, COHERENT, kCombineBatch>(part, out, h0, rep, nsplit, ns, s_m, s_l);
 }
 
 struct AttnArgs {
@@ -831,7 +845,9 @@ static int check_attention(const uint16_t* q, const uint16_t* k_cache, const uin
 // attention output (the o projection) combines them while its weight rows
 // load. Workgroup = 8 waves, 1 row per wave; thread t owns x[4t .. 4t+3]
 // (K = NQ * hd <= 2048, one query head per thread): it requests the states of
-// its head (the first kOcBatch splits) before the tile's weight loads,
+// its head (the first 8 or 16 splits: the smaller batch that holds the
+// context's splits, since a longer batch repeats split 0's loads and repeated
+// loads of one address queue behind each other) before the tile's weight loads,
 // combines them with the arithmetic of combine_kv (M over all splits, then l
 // and acc summed in split order, x = fp16(acc / l)) into LDS, and every wave
 // reads its x chunks from there. An unsplit context (ns = 1) wrote out
@@ -856,13 +872,15 @@ __device__ __forceinline__ int attn_splits(const OcArgs& a, int L) {
     return ns;
 }
 
-// The split states of thread t's four x elements (ns > 1), combined into the LDS copy of x by finish().
+// The split states of thread t's four x elements (ns > 1), combined into the LDS copy of x by finish(); the
+// first B splits are held in registers.
+template <int B>
 struct AttnCombineState {
     int ns;   // splits of the current context
     int i0;   // first x element of the thread (clamped to K - 4; live = 4t < K)
     bool live;
-    f32x2 ml[kOcBatch];  // (m, l) of each split
-    f32x4 va[kOcBatch];  // acc[d0 .. d0+3] of each split
+    f32x2 ml[B];  // (m, l) of each split
+    f32x4 va[B];  // acc[d0 .. d0+3] of each split
 
     __device__ __forceinline__ const float* rec(const OcArgs& a, int s) const {
         const int h = i0 / a.HD;
@@ -876,25 +894,26 @@ struct AttnCombineState {
         i0 = live ? t4 : K - 4;
         const int d0 = i0 % a.HD;
 #pragma unroll
-        for (int s = 0; s < kOcBatch; ++s) {
+        for (int s = 0; s < B; ++s) {
             const float* r = rec(a, s);
             ml[s] = ldg(reinterpret_cast<const f32x2*>(r));
             const f32x2 a01 = ldg(reinterpret_cast<const f32x2*>(r + 2 + d0));  // 8-byte aligned only
             const f32x2 a23 = ldg(reinterpret_cast<const f32x2*>(r + 4 + d0));
             va[s] = f32x4{a01.x, a01.y, a23.x, a23.y};
         }
+        __builtin_amdgcn_sched_barrier(0);  // every state load requested before the first use
     }
     // x[i0 .. i0+3] into s_x, then a workgroup barrier.
     __device__ __forceinline__ void finish(const OcArgs& a, uint16_t* s_x) const {
         float M = kNegBig;  // max is exact: any order gives combine_kv's M
 #pragma unroll
-        for (int s = 0; s < kOcBatch; ++s)
+        for (int s = 0; s < B; ++s)
             if (s < ns) M = fmaxf(M, ml[s].x);
-        for (int s = kOcBatch; s < ns; ++s) M = fmaxf(M, ldg(rec(a, s)));
+        for (int s = B; s < ns; ++s) M = fmaxf(M, ldg(rec(a, s)));
         float lsum = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const int d0 = i0 % a.HD;
 #pragma unroll
-        for (int s = 0; s < kOcBatch; ++s) {
+        for (int s = 0; s < B; ++s) {
             if (s < ns) {
                 const float w = fast_exp2(ml[s].x - M);
                 lsum = fmaf(ml[s].y, w, lsum);
@@ -904,7 +923,7 @@ struct AttnCombineState {
                 acc[3] = fmaf(va[s].w, w, acc[3]);
             }
         }
-        for (int s = kOcBatch; s < ns; ++s) {  // long contexts with few KV heads: further splits
+        for (int s = B; s < ns; ++s) {  // long contexts with few KV heads: further splits
             const float* r = rec(a, s);
             const float w = fast_exp2(ldg(r) - M);
             lsum = fmaf(ldg(r + 1), w, lsum);
@@ -920,6 +939,23 @@ struct AttnCombineState {
         __syncthreads();
     }
 };
+
+// The context's split states combined into the LDS copy of x (ns > 1; the batch choice is wave-uniform). The
+// two branches start with different (empty) asm statements: with identical first instructions the compiler
+// hoists split 0's loads above the branch and waits for them there, a round trip before the other loads.
+__device__ __forceinline__ void attn_combine_into(const OcArgs& a, int K, int ns, uint16_t* s_x) {
+    if (ns <= 8) {
+        asm volatile("; combine batch 8" ::: "memory");
+        AttnCombineState<8> st;
+        st.prefetch(a, K, ns);
+        st.finish(a, s_x);
+    } else {
+        asm volatile("; combine batch 16" ::: "memory");
+        AttnCombineState<kOcBatch> st;
+        st.prefetch(a, K, ns);
+        st.finish(a, s_x);
+    }
+}
 
 // x chunk c (32 elements) from the LDS copy of x (zeros for a chunk past K).
 template <bool FULL>
@@ -974,9 +1010,7 @@ struct AttnOnePassX {
             }
             return;
         }
-        AttnCombineState st;
-        st.prefetch(oa, K, ns);
-        st.finish(oa, s_x);
+        attn_combine_into(oa, K, ns, s_x);
         lds_x_chunk<FULL>(s_x, c, cv, xv);
     }
 };
@@ -1001,9 +1035,7 @@ __global__ __launch_bounds__(kOcThreads) void gemv_attn_combine_kernel(DenseRows
             gemv_int4_tile<kOcRows, 1, true, CS, true, FULL>(rows, N, PlainX{oa.attn_out}, ep, K, gs, row0);
             return;
         }
-        AttnCombineState st;
-        st.prefetch(oa, K, ns);
-        st.finish(oa, s_x);
+        attn_combine_into(oa, K, ns, s_x);
         gemv_int4_tile<kOcRows, 1, true, CS, true, FULL>(rows, N, AttnLdsX{s_x, oa.attn_out}, ep, K, gs, row0);
     }
 }
