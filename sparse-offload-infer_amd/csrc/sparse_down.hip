@@ -97,7 +97,7 @@ struct LdsGatedH {
     }
 };
 
-template <int E, bool VEC, bool CHUNK_SCALE>
+template <int E, int U, bool VEC, bool CHUNK_SCALE>
 __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int n, int k, int32_t* __restrict__ out_idx,
     int32_t* __restrict__ out_count, const uint8_t* __restrict__ W, const float* __restrict__ S, int64_t row_bytes,
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
     const int64_t kk = total < static_cast<uint32_t>(k) ? static_cast<int64_t>(total) : static_cast<int64_t>(k);
     if (writer && chunk == 0 && tid == 0) stg(out_count, static_cast<int32_t>(kk));
     __syncthreads();  // s_ch / s_g of the chunk complete
-    sparse_down_item<kDownU, VEC, CHUNK_SCALE>(LdsIndexRows{W, S, s_ch, j0, row_bytes, G},
+    sparse_down_item<U, VEC, CHUNK_SCALE>(LdsIndexRows{W, S, s_ch, j0, row_bytes, G},
                                                LdsGatedH{s_g, s_ch, up, j0}, y, partial, counters, kk, H, gs, rpc,
                                                R, red, &s_last, slice, chunk, tid, true);
 }
@@ -180,14 +180,24 @@ static int launch_sparse_down_on(const Rows& rows, int64_t k, const HS& h, uint1
     const bool cs = (gs % 32) == 0;
     const int Hi = static_cast<int>(H), gi = static_cast<int>(gs), ri = static_cast<int>(p.rpc),
               Ri = static_cast<int>(p.R);
-#define SOI_D(V, CS)                                                                                           \
-    hipLaunchKernelGGL((sparse_down_kernel<kDownU, V, CS, Rows, HS>), grid, dim3(kDownThreads), 0, st, rows, h, y, \
+    // 8-row groups per wave per batch: as many as a chunk gives each wave (rpc / 32), in steps of 2, 3 and 6; a
+    // batch slot past the chunk loads the zero buffer, and those repeated loads of one address cost time
+    const int64_t gpw = p.rpc / (static_cast<int64_t>(kDownWaves) * kGroupRows);
+#define SOI_D(U, V, CS)                                                                                        \
+    hipLaunchKernelGGL((sparse_down_kernel<U, V, CS, Rows, HS>), grid, dim3(kDownThreads), 0, st, rows, h, y,  \
                        partial, counters, k, Hi, gi, ri, Ri)
+#define SOI_DU(V, CS)                                                                                          \
+    do {                                                                                                       \
+        if (gpw <= 2) SOI_D(2, V, CS);                                                                         \
+        else if (gpw <= 3) SOI_D(3, V, CS);                                                                    \
+        else SOI_D(kDownU, V, CS);                                                                             \
+    } while (0)
     if (vec) {
-        if (cs) SOI_D(true, true); else SOI_D(true, false);
+        if (cs) SOI_DU(true, true); else SOI_DU(true, false);
     } else {
-        if (cs) SOI_D(false, true); else SOI_D(false, false);
+        if (cs) SOI_DU(false, true); else SOI_DU(false, false);
     }
+#undef SOI_DU
 #undef SOI_D
     return launch_status(what);
 }
@@ -437,14 +447,22 @@ extern "C" int soi_dip_select_gated_down(const uint16_t* gate, const uint16_t* u
     const int ni = static_cast<int>(num_channels), ki = static_cast<int>(k), Hi = static_cast<int>(H),
               gi = static_cast<int>(group_size), ri = static_cast<int>(p.rpc), Ri = static_cast<int>(p.R);
     hipStream_t st = as_stream(stream);
-#define SOI_F(EE)                                                                                                  \
-    hipLaunchKernelGGL((dip_select_down_kernel<EE, true, true>), grid, dim3(kDownThreads), 0, st, gate, up, ni, ki, \
-                       out_indices, out_count, Wq_T, scale_T, row_bytes, num_groups, y, partial, counters, Hi, gi, ri, \
-                       Ri)
-    if (E <= 8) SOI_F(8);
-    else if (E <= 16) SOI_F(16);
-    else if (E <= 24) SOI_F(24);
-    else SOI_F(32);
+#define SOI_F(EE, UU)                                                                                              \
+    hipLaunchKernelGGL((dip_select_down_kernel<EE, UU, true, true>), grid, dim3(kDownThreads), 0, st, gate, up, ni, \
+                       ki, out_indices, out_count, Wq_T, scale_T, row_bytes, num_groups, y, partial, counters, Hi, gi, \
+                       ri, Ri)
+#define SOI_FU(EE)                                                                                                 \
+    do {                                                                                                           \
+        if (gpw <= 2) SOI_F(EE, 2);                                                                                \
+        else if (gpw <= 3) SOI_F(EE, 3);                                                                           \
+        else SOI_F(EE, kDownU);                                                                                    \
+    } while (0)
+    const int64_t gpw = p.rpc / (static_cast<int64_t>(kDownWaves) * kGroupRows);  // as in launch_sparse_down_on
+    if (E <= 8) SOI_FU(8);
+    else if (E <= 16) SOI_FU(16);
+    else if (E <= 24) SOI_FU(24);
+    else SOI_FU(32);
+#undef SOI_FU
 #undef SOI_F
     return launch_status(what);
 }
