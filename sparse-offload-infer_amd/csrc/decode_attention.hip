@@ -224,12 +224,20 @@ struct AttnRows {
         constexpr int RPI = kWave / LPR;
         const int lane = threadIdx.x & 63;
         const int g = lane / LPR, u = lane % LPR;
+        // pairs of passes past npass are not requested (one wave-uniform branch per pair, as the pass loop
+        // takes them): a clamped request would repeat row t1 - 1, and repeated loads of one address queue
+        // behind each other
 #pragma unroll
-        for (int i = 0; i < kAttnPassMax; ++i) {
-            const int t = tb0 + i * kAttnWaves * RPI + g;
-            const int tl = (i < npass && t < t1) ? t : t1 - 1;
-            k[i] = ldg(reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(tl) * HD) + u);
-            v[i] = ldg(reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(tl) * HD) + u);
+        for (int i = 0; i < kAttnPassMax; i += 2) {
+            if (i < npass) {
+#pragma unroll
+                for (int j = i; j < i + 2; ++j) {
+                    const int t = tb0 + j * kAttnWaves * RPI + g;
+                    const int tl = (j < npass && t < t1) ? t : t1 - 1;
+                    k[j] = ldg(reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(tl) * HD) + u);
+                    v[j] = ldg(reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(tl) * HD) + u);
+                }
+            }
         }
     }
 };
