@@ -345,11 +345,18 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 //      wave's ordered sums: lane r sums chunk r's 32 sub-partials, and the
 //      chunk partials are summed in order; y and optionally res + y (one
 //      binary16 add) are stored.
-// Limits: R <= 64 row chunks, and the tables (8k + 4n + 8 * R * 128 bytes)
-// within kOdMaxLds of LDS.
+// Limits: R <= 64 row chunks, and the tables (8k + 8 * 1024 * ceil(n / 2048)
+// + 8 * R * 128 bytes) within kOdMaxLds of LDS.
 // ---------------------------------------------------------------------------
 constexpr int kOdMaxR = 64;
 constexpr int kOdMaxLds = 144 * 1024;
+
+// The 4-bit field of b at bit sh, sign-extended (v_bfe_i32): the exact INT4
+// value q, as a float. The builtin's result type is unsigned, so it is read as
+// int before the conversion (an unsigned conversion would turn -1 into 2^32).
+__device__ __forceinline__ float s4_field(int b, int sh) {
+    return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(b, sh, 4)));
+}
 
 struct OdArgs {
     const uint16_t* gate;  // [n]
@@ -362,7 +369,7 @@ struct OdArgs {
     const uint16_t* res;   // [H] or null
     uint16_t* res_out;     // [H] or null: res + y, rounded once to binary16
     int n, k, H, gs, rpc, R;
-    int pos_bytes;  // LDS: position table (8 bytes per position, rounded to 16); then 8 packed rows of n / 2 bytes
+    int pos_bytes;  // LDS: position table (8 bytes per position, rounded to 16); then 8 packed rows, NC KB apart
 };
 
 template <int NC>
@@ -374,8 +381,11 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
     const int n = a.n;
     u32x2* s_pos = reinterpret_cast<u32x2*>(s_dyn);  // per position: coef bits, byte of the row | nibble shift << 16
-    uint8_t* s_row = s_dyn + a.pos_bytes;            // row w (packed, n / 2 bytes) at w * n / 2
-    float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * (n >> 1));  // [wave][R][32]
+    // row w (packed, n / 2 bytes) at w * RS: a compile-time stride, so each row read takes its row's offset
+    // in the LDS instruction's immediate field instead of an address add
+    constexpr int RS = NC * (kDdChannelsPerPass / 2);
+    uint8_t* s_row = s_dyn + a.pos_bytes;
+    float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * RS);  // [wave][R][32]
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
     const int chunks = n >> 5;  // n % 32 == 0 (checked on the host)
@@ -458,7 +468,7 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
         if (q < groups4 && (lane & 7) == 0) s_bits[q >> 3] = cm;
     }
     {
-        uint8_t* my_row = s_row + wave * (n >> 1);
+        uint8_t* my_row = s_row + wave * RS;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = lane + i * kWave;
@@ -519,20 +529,32 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
         float acc[kDdWaves];
 #pragma unroll
         for (int w = 0; w < kDdWaves; ++w) acc[w] = 0.0f;
+        // two positions per step (p, then p + 32: the chain's order), both entries and all 16 row bytes
+        // requested before the first fma
         int p = j0 + gsub;
-        u32x2 e = s_pos[p < j1 ? p : 0];  // s_pos[0] exists (k >= 1); read but unused when the chain is empty
-        for (; p < j1; p += 32) {
-            const int pn = p + 32;
-            const u32x2 en = s_pos[pn < j1 ? pn : p];  // the next entry, requested before the current one is used
+        for (; p + 32 < j1; p += 64) {
+            const u32x2 e0 = s_pos[p], e1 = s_pos[p + 32];
+            const int o0 = static_cast<int>(e0.y & 0xffffu), h0 = static_cast<int>(e0.y >> 16);
+            const int o1 = static_cast<int>(e1.y & 0xffffu), h1 = static_cast<int>(e1.y >> 16);
+            int b0[kDdWaves], b1[kDdWaves];
+#pragma unroll
+            for (int w = 0; w < kDdWaves; ++w) {
+                b0[w] = s_row[w * RS + o0];
+                b1[w] = s_row[w * RS + o1];
+            }
+            const float c0 = __builtin_bit_cast(float, e0.x), c1 = __builtin_bit_cast(float, e1.x);
+#pragma unroll
+            for (int w = 0; w < kDdWaves; ++w) acc[w] = fmaf(c0, s4_field(b0[w], h0), acc[w]);
+#pragma unroll
+            for (int w = 0; w < kDdWaves; ++w) acc[w] = fmaf(c1, s4_field(b1[w], h1), acc[w]);
+        }
+        if (p < j1) {
+            const u32x2 e = s_pos[p];
             const float cf = __builtin_bit_cast(float, e.x);
             const int off = static_cast<int>(e.y & 0xffffu), sh = static_cast<int>(e.y >> 16);
 #pragma unroll
-            for (int w = 0; w < kDdWaves; ++w) {
-                // the nibble as a signed 4-bit value (v_bfe_i32 sign-extends): the exact INT4 value q
-                const int qv = __builtin_amdgcn_sbfe(static_cast<int>(s_row[w * (n >> 1) + off]), sh, 4);
-                acc[w] = fmaf(cf, static_cast<float>(qv), acc[w]);
-            }
-            e = en;
+            for (int w = 0; w < kDdWaves; ++w)
+                acc[w] = fmaf(cf, s4_field(s_row[w * RS + off], sh), acc[w]);
         }
 #pragma unroll
         for (int w = 0; w < kDdWaves; ++w) s_sub[(w * R + r) * 32 + gsub] = acc[w];
@@ -647,7 +669,8 @@ static size_t ordered_lds(int64_t H, int64_t n, int64_t k, DownPlan* plan) {
     const DownPlan p = down_plan(H, k);
     if (p.R > kOdMaxR) return 0;
     const size_t pos = (static_cast<size_t>(k) * 8 + 15) / 16 * 16;
-    const size_t lds = pos + static_cast<size_t>(kDdWaves) * static_cast<size_t>(n / 2) +
+    const size_t row_stride = static_cast<size_t>(ceil_div64(n, kDdChannelsPerPass)) * (kDdChannelsPerPass / 2);
+    const size_t lds = pos + static_cast<size_t>(kDdWaves) * row_stride +
                        static_cast<size_t>(kDdWaves) * static_cast<size_t>(p.R) * 32 * sizeof(float);
     if (lds > static_cast<size_t>(kOdMaxLds)) return 0;
     if (plan) *plan = p;
