@@ -346,7 +346,7 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 //      chunk partials are summed in order; y and optionally res + y (one
 //      binary16 add) are stored.
 // Limits: R <= 64 row chunks, and the tables (8k + 8 * 1024 * ceil(n / 2048)
-// + 8 * R * 128 bytes) within kOdMaxLds of LDS.
+// + 8 * 128 * (R | 1) bytes) within kOdMaxLds of LDS.
 // ---------------------------------------------------------------------------
 constexpr int kOdMaxR = 64;
 constexpr int kOdMaxLds = 144 * 1024;
@@ -385,7 +385,9 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     // in the LDS instruction's immediate field instead of an address add
     constexpr int RS = NC * (kDdChannelsPerPass / 2);
     uint8_t* s_row = s_dyn + a.pos_bytes;
-    float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * RS);  // [wave][R][32]
+    // sub-partials [wave][g][P], P = R | 1 (odd): the chains' stores (32 values of g, stride P) and the sums'
+    // loads (R consecutive chunks for each g) both fall in distinct LDS banks
+    float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * RS);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
     const int chunks = n >> 5;  // n % 32 == 0 (checked on the host)
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
 
     // 4. the chains: thread t takes chain (r, gsub) = (t / 32, t % 32), then t + 512, ..., for all 8 rows of the
     // workgroup at once (sparse-down wave gsub >> 3 and row lane gsub & 7 read positions r * rpc + gsub + 32i)
-    const int R = a.R, rpc = a.rpc;
+    const int R = a.R, rpc = a.rpc, P = a.R | 1;
     for (int cn = tid; cn < R * 32; cn += kDdThreads) {
         const int r = cn >> 5, gsub = cn & 31;
         const int j0 = r * rpc;
@@ -557,14 +559,14 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
                 acc[w] = fmaf(cf, s4_field(s_row[w * RS + off], sh), acc[w]);
         }
 #pragma unroll
-        for (int w = 0; w < kDdWaves; ++w) s_sub[(w * R + r) * 32 + gsub] = acc[w];
+        for (int w = 0; w < kDdWaves; ++w) s_sub[(w * 32 + gsub) * P + r] = acc[w];
     }
     __syncthreads();
-    const float* my_sub = s_sub + wave * R * 32;
+    const float* my_sub = s_sub + wave * 32 * P;
     float part = 0.0f;
     if (lane < R) {
 #pragma unroll 8
-        for (int s2 = 0; s2 < 32; ++s2) part += my_sub[lane * 32 + s2];
+        for (int s2 = 0; s2 < 32; ++s2) part += my_sub[s2 * P + lane];
     }
     float sum = 0.0f;
     for (int r = 0; r < R; ++r)
@@ -671,7 +673,7 @@ static size_t ordered_lds(int64_t H, int64_t n, int64_t k, DownPlan* plan) {
     const size_t pos = (static_cast<size_t>(k) * 8 + 15) / 16 * 16;
     const size_t row_stride = static_cast<size_t>(ceil_div64(n, kDdChannelsPerPass)) * (kDdChannelsPerPass / 2);
     const size_t lds = pos + static_cast<size_t>(kDdWaves) * row_stride +
-                       static_cast<size_t>(kDdWaves) * static_cast<size_t>(p.R) * 32 * sizeof(float);
+                       static_cast<size_t>(kDdWaves) * 32 * static_cast<size_t>(p.R | 1) * sizeof(float);
     if (lds > static_cast<size_t>(kOdMaxLds)) return 0;
     if (plan) *plan = p;
     return lds;
