@@ -399,7 +399,9 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     const u32x4* z4 = reinterpret_cast<const u32x4*>(g_zero16);
     const u32x2* z2 = reinterpret_cast<const u32x2*>(g_zero16);
 
-    // 1. gate first, then h and St[g], then the row chunks (loads return in order)
+    // 1. gate first, then h and St[g], then the row chunks (loads return in order). Every wave requests its gate
+    // words before any wave requests the rest (the barrier): the workgroup's 72 KB (n = 6144) of requests return
+    // through the CU roughly in request order, and the first radix pass needs every wave's gate
     u32x2 gq[NC], hq[NC];
     u32x4 sq[NC];
     const float* sg = a.S + static_cast<int64_t>(g) * n;
@@ -408,6 +410,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
         const int q = tid + m * kDdThreads;
         gq[m] = ldg(q < groups4 ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
     }
+    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
+    __syncthreads();  // also orders the zeroed histograms before the first radix pass
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
@@ -425,25 +429,26 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
         }
     }
     const uint16_t rv = ldg(a.res_out && row < a.H ? a.res + row : reinterpret_cast<const uint16_t*>(g_zero16));
-    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
 
     // 2. |gate| keys (NaN past the end: key 0, never counted or selected) and rule A's threshold; after the first
-    // radix pass, the coefficients fl(h * St[g])
-    float gv[NC][4], xc[NC][4];
+    // radix pass, the coefficients fl(h * St[g]). The key of |g| is its binary16 pattern with the sign bit set
+    // (F16AbsValues::key_of of the value, formed from the bits), and the largest key gives the largest value
+    float xc[NC][4];
     uint32_t key[E];
-    float local_max = 0.0f;
+    uint32_t key_max = 0u;
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const bool ok = tid + m * kDdThreads < groups4;
         const uint32_t gw[2] = {gq[m].x, gq[m].y};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const uint32_t gb = ((gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu) | (ok ? 0u : 0x7e00u);
-            gv[m][p] = f16_bits_to_f32(static_cast<uint16_t>(gb));
-            key[4 * m + p] = F16AbsValues::key_of(gv[m][p]);
-            local_max = fmaxf(local_max, gv[m][p]);
+            const uint32_t gb = (gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu;
+            const uint32_t kv = (ok && gb <= 0x7c00u) ? (gb | 0x8000u) : 0u;
+            key[4 * m + p] = kv;
+            key_max = kv > key_max ? kv : key_max;
         }
     }
+    const float local_max = F16AbsValues::value_of(key_max);
     auto coefficients = [&]() {
 #pragma unroll
         for (int m = 0; m < NC; ++m) {
@@ -456,8 +461,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
                            __builtin_bit_cast(float, su[p]);
         }
     };
-    const float tau =
-        rule_a_tau<E, kDdWaves, F16AbsValues, true>(key, local_max, s_hist, s_max, a.k, tid, coefficients);
+    const float tau = rule_a_tau<E, kDdWaves, F16AbsValues, true, decltype(coefficients), true>(
+        key, local_max, s_hist, s_max, a.k, tid, coefficients);
 
     // 3. chunk masks (lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m) and the wave's packed row
 #pragma unroll
@@ -465,7 +470,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
         const int q = tid + m * kDdThreads;
         uint32_t m4 = 0u;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) m4 |= (gv[m][p] >= tau ? 1u : 0u) << p;  // NaN (and padding) never
+        for (int p = 0; p < 4; ++p)  // |g| >= tau; key 0 (NaN, padding) never
+            m4 |= (key[4 * m + p] != 0u && F16AbsValues::value_of(key[4 * m + p]) >= tau ? 1u : 0u) << p;
         const uint32_t cm = or8_lanes(m4 << (4 * (lane & 7)));
         if (q < groups4 && (lane & 7) == 0) s_bits[q >> 3] = cm;
     }

@@ -150,7 +150,9 @@ struct NoMid {
 // tau of rule A over the workgroup's keys: NW waves, E keys per lane (0 = NaN
 // or padding), local_max = this lane's fmaxf over its values starting from
 // 0.0f. Zeroes s_hist (radix_hist_offset<Values>(kPasses) words) itself
-// unless ZEROED; s_max holds NW floats. mid() runs in every thread after the
+// unless ZEROED; with SYNCED the caller zeroed it and ran a barrier after, so
+// the first radix pass's barrier also publishes s_max (no barrier of its own
+// between the keys and the first pass); s_max holds NW floats. mid() runs in every thread after the
 // first radix pass and before the second pass's barrier, which publishes its
 // LDS stores (a barrier of its own replaces that pass when it does not run):
 // work that does not feed the selection, done while its first pass waits.
@@ -158,15 +160,15 @@ struct NoMid {
 // values, a threshold that selects exactly the same values (see below);
 // `found` is false when fewer than k keys are nonzero (then every step goes
 // left, as the reference's counts do).
-template <int E, int NW, class Values, bool ZEROED = false, class Mid = NoMid>
+template <int E, int NW, class Values, bool ZEROED = false, class Mid = NoMid, bool SYNCED = false>
 __device__ __forceinline__ float rule_a_tau(const uint32_t (&key)[E], float local_max, uint32_t* s_hist, float* s_max,
                                             int k, int tid, const Mid& mid = Mid{}) {
     constexpr int NPASS = Values::kPasses;
     const int wave = tid >> 6, lane = tid & 63;
-    if (!ZEROED) rule_a_zero_hist<NW, Values>(s_hist, tid);
+    if (!ZEROED && !SYNCED) rule_a_zero_hist<NW, Values>(s_hist, tid);
     const float wmax = wave_max_bcast(local_max);
     if (lane == 0) s_max[wave] = wmax;
-    __syncthreads();
+    if (!SYNCED) __syncthreads();
 
     uint32_t prefix = 0u, pmask = 0u, rank = static_cast<uint32_t>(k);
     bool found = radix_pass<Values::shift(0), Values::bits(0)>(key, s_hist, prefix, pmask, rank, lane);
