@@ -118,7 +118,10 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     const u32x4* z4 = reinterpret_cast<const u32x4*>(g_zero16);
     const u32x2* z2 = reinterpret_cast<const u32x2*>(g_zero16);
 
-    // 1. requested first (loads return in order): gate / h / St[g] of the thread's groups q = tid + 512m
+    // 1. requested first (loads return in order): gate / h / St[g] of the thread's groups q = tid + 512m. Every
+    // wave requests its gate words before any wave requests the rest (the barrier, which also orders the zeroed
+    // histograms before the first radix pass): the requests return through the CU roughly in request order, and
+    // the first radix pass needs every wave's gate
     u32x2 gq[NC], hq[NC];
     u32x4 sq[NC];
     const float* sg = a.S + static_cast<int64_t>(g) * n;
@@ -127,6 +130,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
         const int q = tid + m * kDdThreads;
         gq[m] = ldg(q < groups4 ? reinterpret_cast<const u32x2*>(a.gate) + q : z2);
     }
+    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
+    __syncthreads();
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
@@ -147,25 +152,25 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
     // the residual element of the row (a zero word when there is none; a select, so the load is not branched)
     const uint16_t rv = ldg(a.res_out && row < a.H ? a.res + row : reinterpret_cast<const uint16_t*>(g_zero16));
 
-    // the selection's histograms are zeroed while the loads are in flight
-    rule_a_zero_hist<kDdWaves, F16AbsValues>(s_hist, tid);
-
-    // 2. |gate| (NaN past the end: key 0, never counted or selected)
-    float gv[NC][4], xc[NC][4];
+    // 2. |gate| keys (NaN past the end: key 0, never counted or selected): the binary16 pattern of |g| with the
+    // sign bit set (F16AbsValues::key_of of the value, formed from the bits); the largest key gives the largest
+    // value
+    float xc[NC][4];
     uint32_t key[E];
-    float local_max = 0.0f;
+    uint32_t key_max = 0u;
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const bool ok = tid + m * kDdThreads < groups4;
         const uint32_t gw[2] = {gq[m].x, gq[m].y};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const uint32_t gb = ((gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu) | (ok ? 0u : 0x7e00u);
-            gv[m][p] = f16_bits_to_f32(static_cast<uint16_t>(gb));
-            key[4 * m + p] = F16AbsValues::key_of(gv[m][p]);
-            local_max = fmaxf(local_max, gv[m][p]);
+            const uint32_t gb = (gw[p >> 1] >> (16 * (p & 1))) & 0x7fffu;
+            const uint32_t kv = (ok && gb <= 0x7c00u) ? (gb | 0x8000u) : 0u;
+            key[4 * m + p] = kv;
+            key_max = kv > key_max ? kv : key_max;
         }
     }
+    const float local_max = F16AbsValues::value_of(key_max);
 
     // 3. tau of rule A. After its first radix pass (the h and St values have landed meanwhile): the coefficients
     // h * St[g] (fp32, unmasked) and their largest magnitude, handed to the other waves through the second pass's
@@ -191,8 +196,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
         cmax = wave_max_bcast(cmax);
         if (lane == 0) s_cmax[wave] = cmax;
     };
-    const float tau =
-        rule_a_tau<E, kDdWaves, F16AbsValues, true>(key, local_max, s_hist, s_max, a.k, tid, coefficients);
+    const float tau = rule_a_tau<E, kDdWaves, F16AbsValues, true, decltype(coefficients), true>(
+        key, local_max, s_hist, s_max, a.k, tid, coefficients);
 
     // 4. x_g[c] = [|gate_c| >= tau] * h_c * St[g, c] scaled by 2^e (exact; e from the largest finite |h * s| of
     // all channels, a bound for the selected finite ones), split into binary16 hi + lo (8-byte LDS stores per
@@ -209,7 +214,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
         uint16_t hb[4], lb[4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const bool sel = gv[m][p] >= tau;  // NaN (and padding) never
+            // |g| >= tau; key 0 (NaN, padding) never
+            const bool sel = key[4 * m + p] != 0u && F16AbsValues::value_of(key[4 * m + p]) >= tau;
             const float xs = sel ? __builtin_ldexpf(xc[m][p], e) : 0.0f;
             hb[p] = f32_to_f16_bits(xs);
             const float d = xs - f16_bits_to_f32(hb[p]);  // exact difference (NaN for an infinite xs)

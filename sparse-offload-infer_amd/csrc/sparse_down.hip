@@ -126,6 +126,9 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
         const int i = base_i + j * kWave;
         raw[j] = ldg(gate + (i < n ? i : n - 1));
     }
+    // the histograms are zeroed and published while the gates are in flight (rule A's SYNCED form)
+    rule_a_zero_hist<kDownWaves, F16AbsValues>(s_hist, tid);
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const int i = base_i + j * kWave;
@@ -133,7 +136,8 @@ __global__ __launch_bounds__(kDownThreads) void dip_select_down_kernel(
         key[j] = F16AbsValues::key_of(val[j]);
         local_max = fmaxf(local_max, val[j]);
     }
-    const float tau = rule_a_tau<E, kDownWaves, F16AbsValues>(key, local_max, s_hist, s_max, k, tid);
+    const float tau =
+        rule_a_tau<E, kDownWaves, F16AbsValues, true, NoMid, true>(key, local_max, s_hist, s_max, k, tid);
     const bool writer = slice == 0;
     // only this workgroup's chunk [j0, j1) of the positions is emitted
     const uint32_t total = rule_a_compact<E, kDownWaves>(

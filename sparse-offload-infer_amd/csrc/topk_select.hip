@@ -234,6 +234,9 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(const Values 
         const int i = base_i + j * kWave;
         val[j] = v.load(i < n ? i : n - 1);
     }
+    // the histograms are zeroed and published while the values are in flight (rule A's SYNCED form)
+    rule_a_zero_hist<kRadixWaves, Values>(s_hist, tid);
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const int i = base_i + j * kWave;
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(const Values 
         key[j] = Values::key_of(val[j]);
         local_max = fmaxf(local_max, val[j]);
     }
-    const float tau = rule_a_tau<E, kRadixWaves, Values>(key, local_max, s_hist, s_max, k, tid);
+    const float tau = rule_a_tau<E, kRadixWaves, Values, true, NoMid, true>(key, local_max, s_hist, s_max, k, tid);
     const uint32_t total = rule_a_compact<E, kRadixWaves>(val, tau, s_tot, tid, [&](uint32_t pos, int j) {
         if (pos < static_cast<uint32_t>(k)) out_idx[pos] = base_i + j * kWave;
     });
