@@ -470,7 +470,9 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     const float tau = rule_a_tau<E, kDdWaves, F16AbsValues, true, decltype(coefficients), true>(
         key, local_max, s_hist, s_max, a.k, tid, coefficients);
 
-    // 3. chunk masks (lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m) and the wave's packed row
+    // 3. chunk masks (lanes 8j .. 8j+7 hold the 8 groups of chunk (tid >> 3) + 64m, and each of them keeps the
+    // chunk's mask for the position table) and the wave's packed row
+    uint32_t cmask[NC];
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
         const int q = tid + m * kDdThreads;
@@ -478,8 +480,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
 #pragma unroll
         for (int p = 0; p < 4; ++p)  // |g| >= tau; key 0 (NaN, padding) never
             m4 |= (key[4 * m + p] != 0u && F16AbsValues::value_of(key[4 * m + p]) >= tau ? 1u : 0u) << p;
-        const uint32_t cm = or8_lanes(m4 << (4 * (lane & 7)));
-        if (q < groups4 && (lane & 7) == 0) s_bits[q >> 3] = cm;
+        cmask[m] = or8_lanes(m4 << (4 * (lane & 7)));
+        if (q < groups4 && (lane & 7) == 0) s_bits[q >> 3] = cmask[m];
     }
     {
         uint8_t* my_row = s_row + wave * RS;
@@ -491,43 +493,48 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     }
     __syncthreads();
 
-    // kept channels of the earlier chunks, chunk by chunk in index order (lane l: chunks l + 64i)
+    // kept channels of the earlier chunks, chunk by chunk in index order (lane l: chunks l + 64i; all NC words
+    // requested at once: lane + 64i < 64 NC <= kDdMaxChunks, words past the chunks read but not used)
     const uint32_t k = static_cast<uint32_t>(a.k);
     uint32_t total = 0u;
     uint32_t before[NC], bits[NC];
 #pragma unroll
+    for (int i = 0; i < NC; ++i) bits[i] = s_bits[lane + i * kWave];
+#pragma unroll
     for (int i = 0; i < NC; ++i) {
         const int c = lane + i * kWave;
-        bits[i] = c < chunks ? s_bits[c] : 0u;
+        bits[i] = c < chunks ? bits[i] : 0u;
         const uint32_t cnt = static_cast<uint32_t>(__builtin_popcount(bits[i]));
         const uint32_t incl = wave_prefix_u32(cnt);
         before[i] = total + incl - cnt;
         total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
     }
     const uint32_t kk = total < k ? total : k;
-    // the position table: group q = tid + 512m lies in chunk (tid >> 3) + 64m, whose counts this wave's lane
-    // 8 * wave + (lane >> 3) holds at index m; the group's channels sit at bits 4 (lane & 7) .. + 3 of its mask
+    // the position table: group q = tid + 512m lies in chunk (tid >> 3) + 64m, whose count of earlier kept
+    // channels this wave's lane 8 * wave + (lane >> 3) holds at index m; the group's channels sit at bits
+    // 4 (lane & 7) .. + 3 of the chunk's mask
     {
         const int src = 8 * wave + (lane >> 3);
         const uint32_t sh = 4u * static_cast<uint32_t>(lane & 7);
 #pragma unroll
         for (int m = 0; m < NC; ++m) {
-            const uint32_t cb = static_cast<uint32_t>(__shfl(static_cast<int>(bits[m]), src, kWave));
+            const uint32_t cb = cmask[m];
             uint32_t pos = static_cast<uint32_t>(__shfl(static_cast<int>(before[m]), src, kWave)) +
                            static_cast<uint32_t>(__builtin_popcount(cb & ((1u << sh) - 1u)));
-            const uint32_t ch0 = 4u * static_cast<uint32_t>(tid + m * kDdThreads);
+            // AWQ order: logical element j of a word sits at nibble (j >> 1) + 4 (j & 1). The group's channels
+            // 4t .. 4t + 3 (t = q) are elements 4 (t & 1) + p of word t >> 1: nibble 2 (t & 1) + (p >> 1) + 4 (p & 1),
+            // i.e. byte 4 (t >> 1) + (t & 1) + 2 (p & 1) of the row, shift 4 (p >> 1)
+            const uint32_t t = static_cast<uint32_t>(tid + m * kDdThreads);
+            const uint32_t byte0 = 4u * (t >> 1) + (t & 1u);
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                if ((cb >> (sh + p)) & 1u) {
-                    if (pos < k) {
-                        // AWQ order: logical element j of a word sits at nibble (j >> 1) + 4 (j & 1)
-                        const uint32_t ch = ch0 + static_cast<uint32_t>(p);
-                        const uint32_t j = ch & 7u, nib = (j >> 1) + 4u * (j & 1u);
-                        const uint32_t loc = (4u * (ch >> 3) + (nib >> 1)) | ((4u * (nib & 1u)) << 16);
-                        s_pos[pos] = u32x2{__builtin_bit_cast(uint32_t, xc[m][p]), loc};
-                    }
-                    ++pos;
+                const bool on = ((cb >> (sh + static_cast<uint32_t>(p))) & 1u) != 0u;
+                if (on && pos < k) {
+                    const uint32_t loc = (byte0 + 2u * static_cast<uint32_t>(p & 1)) |
+                                         ((4u * static_cast<uint32_t>(p >> 1)) << 16);
+                    s_pos[pos] = u32x2{__builtin_bit_cast(uint32_t, xc[m][p]), loc};
                 }
+                pos += on ? 1u : 0u;
             }
         }
     }
