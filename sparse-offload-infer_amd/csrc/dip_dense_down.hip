@@ -352,10 +352,11 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 //      chunk partials are summed in order; y and optionally res + y (one
 //      binary16 add) are stored.
 // Limits: R <= 64 row chunks, and the tables (8k + 8 * 1024 * ceil(n / 2048)
-// + 8 * 128 * (R | 1) bytes) within kOdMaxLds of LDS.
+// + 8 * 144 * R bytes) within kOdMaxLds of LDS.
 // ---------------------------------------------------------------------------
 constexpr int kOdMaxR = 64;
 constexpr int kOdMaxLds = 144 * 1024;
+constexpr int kOdSubPitch = 36;  // floats per (wave, chunk) row of sub-partials: 32 + 4 of padding
 
 // The 4-bit field of b at bit sh, sign-extended (v_bfe_i32): the exact INT4
 // value q, as a float. The builtin's result type is unsigned, so it is read as
@@ -391,8 +392,8 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
     // in the LDS instruction's immediate field instead of an address add
     constexpr int RS = NC * (kDdChannelsPerPass / 2);
     uint8_t* s_row = s_dyn + a.pos_bytes;
-    // sub-partials [wave][g][P], P = R | 1 (odd): the chains' stores (32 values of g, stride P) and the sums'
-    // loads (R consecutive chunks for each g) both fall in distinct LDS banks
+    // sub-partials [wave][r][kOdSubPitch]: lane r of the in-order sums reads its chunk's 32 values as 8 16-byte
+    // words, and the 36-float pitch puts the lanes' words in distinct LDS banks
     float* s_sub = reinterpret_cast<float*>(s_dyn + a.pos_bytes + kDdWaves * RS);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
 
     // 4. the chains: thread t takes chain (r, gsub) = (t / 32, t % 32), then t + 512, ..., for all 8 rows of the
     // workgroup at once (sparse-down wave gsub >> 3 and row lane gsub & 7 read positions r * rpc + gsub + 32i)
-    const int R = a.R, rpc = a.rpc, P = a.R | 1;
+    const int R = a.R, rpc = a.rpc;
     for (int cn = tid; cn < R * 32; cn += kDdThreads) {
         const int r = cn >> 5, gsub = cn & 31;
         const int j0 = r * rpc;
@@ -578,14 +579,17 @@ __global__ __launch_bounds__(kDdThreads) void dip_down_ordered_kernel(OdArgs a) 
                 acc[w] = fmaf(cf, s4_field(s_row[w * RS + off], sh), acc[w]);
         }
 #pragma unroll
-        for (int w = 0; w < kDdWaves; ++w) s_sub[(w * 32 + gsub) * P + r] = acc[w];
+        for (int w = 0; w < kDdWaves; ++w) s_sub[(w * R + r) * kOdSubPitch + gsub] = acc[w];
     }
     __syncthreads();
-    const float* my_sub = s_sub + wave * 32 * P;
     float part = 0.0f;
     if (lane < R) {
-#pragma unroll 8
-        for (int s2 = 0; s2 < 32; ++s2) part += my_sub[s2 * P + lane];
+        const float4* src = reinterpret_cast<const float4*>(s_sub + (wave * R + lane) * kOdSubPitch);
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = src[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part = (((part + v[j].x) + v[j].y) + v[j].z) + v[j].w;
     }
     float sum = 0.0f;
     for (int r = 0; r < R; ++r)
@@ -692,7 +696,7 @@ static size_t ordered_lds(int64_t H, int64_t n, int64_t k, DownPlan* plan) {
     const size_t pos = (static_cast<size_t>(k) * 8 + 15) / 16 * 16;
     const size_t row_stride = static_cast<size_t>(ceil_div64(n, kDdChannelsPerPass)) * (kDdChannelsPerPass / 2);
     const size_t lds = pos + static_cast<size_t>(kDdWaves) * row_stride +
-                       static_cast<size_t>(kDdWaves) * 32 * static_cast<size_t>(p.R | 1) * sizeof(float);
+                       static_cast<size_t>(kDdWaves) * static_cast<size_t>(p.R) * kOdSubPitch * sizeof(float);
     if (lds > static_cast<size_t>(kOdMaxLds)) return 0;
     if (plan) *plan = p;
     return lds;
