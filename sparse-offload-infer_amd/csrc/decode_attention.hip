@@ -438,6 +438,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
         f_c = ldg(a.cos_t + static_cast<int64_t>(prow) * HALF + lane);
         f_sn = ldg(a.sin_t + static_cast<int64_t>(prow) * HALF + lane);
     }
+    // without PRE the query heads are requested first: loads return in order, and the first pass's scores need
+    // them, so they do not wait behind every pass's K/V rows
+    u32x4 qraw[REP];
+    if (!PRE) {
+#pragma unroll
+        for (int hh = 0; hh < REP; ++hh) {
+            const int h = kvh * rep + hq0 + (hh < nhq ? hh : 0);
+            qraw[hh] = ldg(reinterpret_cast<const u32x4*>(a.q + static_cast<int64_t>(h) * HD) + u);
+        }
+    }
     // the K/V rows of the first chunk: they do not depend on q (row p is patched from LDS later)
     AttnRows<LPR> rows;
     rows.load(kbase, vbase, tb0, t1, npass_all < kAttnPassMax ? npass_all : kAttnPassMax);
@@ -518,8 +528,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(const AttnArgs a) {
     } else {
 #pragma unroll
         for (int hh = 0; hh < REP; ++hh) {
-            const int h = kvh * rep + hq0 + (hh < nhq ? hh : 0);
-            const u32x4 t = ldg(reinterpret_cast<const u32x4*>(a.q + static_cast<int64_t>(h) * HD) + u);
+            const u32x4 t = qraw[hh];
             qv[hh][0] = as_f16x2(t.x);
             qv[hh][1] = as_f16x2(t.y);
             qv[hh][2] = as_f16x2(t.z);
