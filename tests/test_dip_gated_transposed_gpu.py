@@ -6,6 +6,8 @@ followed by the gated sparse down:
   * indices, count and y equal the row form bit for bit: the Qwen3-1.7B MLP shape at k = 1 .. n, fp16 gates
     with boundary ties, tie-heavy gates (more than k channels at the threshold), NaN gates (fewer than k kept),
     ragged H with per-word scales, small n, and column counts whose plan has up to 64 row chunks;
+  * channel counts past the row form's reach (up to 24576, the largest packed-row stride): y and the selection
+    equal the indexed schedule's three launches;
   * y does not depend on whether the index outputs are requested; res_out = res + y as one binary16 add;
   * y also equals the indexed schedule's three launches (top-k, indexed up GEMV with the SiLU epilogue, sparse
     down) on the same gate and up, and lies within the sparse-down tolerance of the binary64 oracle;
@@ -130,6 +132,36 @@ def test_other_shapes_equal_row_form(C, ops, I, H, gs, ks):
     for k in ks:
         gate, up = rnd((I,), 50 + k, 0.9).cuda(), rnd((I,), 60 + k).cuda()
         _check(C, gate, up, k, down, Wt, St, H, gs, f"I={I} H={H} gs={gs} k={k}")
+
+
+@pytest.mark.parametrize("I,H,gs,ks", [
+    (24576, 2048, 128, [512, 2048]),         # 12 packed-row KB per wave: the largest row stride the kernel takes
+    (20480, 512, 64, [1000]),                # 10 KB rows, gs 64
+    (10240, 1024, 128, [5120]),              # 5 KB rows
+])
+def test_wide_rows_equal_indexed_schedule(C, ops, I, H, gs, ks):
+    """Channel counts past the row form's reach (it takes n <= 6144): y and the selection against the indexed
+    schedule's three launches (top-k, SiLU gating of the selected channels, indexed sparse down) and y against the
+    binary64 oracle on the same selection."""
+    down, Wt, St = _problem(ops, I, H, seed=I + H, gs=gs)
+    for k in ks:
+        assert C.dip_select_down_ordered_lds_bytes(H, I, k) > 0, (I, H, k)
+        gate, up = rnd((I,), 70 + k, 0.9).cuda(), rnd((I,), 80 + k).cuda()
+        ti, tc, ty, _ = _transposed(C, gate, up, k, Wt, St, H, gs)
+        idx3 = torch.empty(k, dtype=torch.int32, device="cuda")
+        cnt3 = torch.empty(1, dtype=torch.int32, device="cuda")
+        C.topk_threshold_select_f16abs_into(gate, k, idx3, cnt3)
+        assert int(tc.item()) == int(cnt3.item()) == k
+        assert torch.equal(ti, idx3), f"I={I} k={k}: indices"
+        h_sel = torch.empty(k, dtype=torch.float16, device="cuda")
+        C.silu_mul_indexed_into(gate, idx3, up.index_select(0, idx3.long()), h_sel)
+        y3 = torch.empty(H, dtype=torch.float16, device="cuda")
+        ws = torch.zeros(C.sparse_accumulate_workspace_bytes(H, k), dtype=torch.uint8, device="cuda")
+        C.gemv_w4a16_indexed_accumulate_into(down["Wq_d"], down["s_d"], idx3, h_sel, y3, H, gs, ws)
+        assert torch.equal(ty, y3), f"I={I} H={H} k={k}: differs from the indexed schedule"
+        sel = idx3.cpu().numpy()
+        ref = O.sparse_accumulate_f64(down["Wq"][sel], down["s"][sel], h_sel.cpu().numpy(), H, gs)
+        assert_close(ty, ref, f"I={I} H={H} k={k} vs oracle")
 
 
 def test_outside_limits_rejected(C, ops):
