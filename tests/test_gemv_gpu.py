@@ -42,6 +42,7 @@ SHAPES = [
     (512, 4096, 128), (512, 4099, 128),  # reference test shapes (4099 pads to 4224)
     (6144, 2048, 128), (2048, 6144, 128), (2048, 2048, 128), (1024, 2048, 128),  # Qwen3-1.7B
     (2049, 6144, 128), (1000, 5120, 128),  # multi-pass tiles with a ragged last tile / a pass count of 2.5
+    (2560, 9728, 128), (4096, 12288, 64),  # 4-row multi-pass tiles (Qwen3-4B / 8B down), two load batches
     (37, 512, 32), (64, 256, 64), (33, 200, 8), (17, 1000, 40),  # non-32-multiple groups
     (1, 8, 8), (3, 100, 16),  # tiny / unaligned rows
 ]
