@@ -16,7 +16,10 @@
 // of one column group (tiles placed XCD-aware, below). Thread t owns the
 // 4-channel groups t + 512m (m < NC = n / 2048 rounded up); lane l of every
 // wave owns the 32-channel chunks l + 64i (i < NC) of its row.
-//   1. it requests the gate / h / St[g] values of its groups, then every
+//   1. it requests the gate values of its groups, zeroes its share of the
+//      selection's histograms and meets one barrier (every wave's gate
+//      requests precede the rest: the CU returns them roughly in request
+//      order), then requests the h / St[g] values of its groups and every
 //      packed chunk of its row;
 //   2. it forms every channel's coefficient h_c * St[g, c] in fp32 and their
 //      largest magnitude (handed over through the selection's first barrier);
@@ -337,8 +340,10 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 // + partial_{R-1}. Here coef_p = fl(h_c * St[g, c]) with c the p-th kept
 // channel, and q_p the exact INT4 value of channel c in the column's
 // transposed row: the same products in the same order.
-//   1. the thread of 4-channel group q requests gate, h and St[g] of its
-//      channels, every lane its row chunks (as the dense down);
+//   1. the thread of 4-channel group q requests the gate words of its
+//      channels; one barrier (after the histograms are zeroed) so every
+//      wave's gate requests precede the rest; then h and St[g] of its
+//      channels, and every lane its row chunks (as the dense down);
 //   2. rule A's threshold over |gate| (the coefficients fl(h * s) are formed
 //      after the first radix pass);
 //   3. the chunk masks [|gate| >= tau] and each wave's packed row go to LDS
@@ -346,11 +351,11 @@ __global__ __launch_bounds__(kDdThreads) void dip_dense_down_kernel(DdArgs a) {
 //      channels from the chunk prefix counts and writes (coef, location of
 //      the channel's nibble in a row) per position p < k (one barrier);
 //   4. thread t runs chain (r, g) = (t / 32, t % 32) (then t + 512, ...) for
-//      all 8 rows of the workgroup: one position-table read feeds 8 row-byte
-//      reads (a signed bitfield extract gives q) and 8 accumulators; then each
-//      wave's ordered sums: lane r sums chunk r's 32 sub-partials, and the
-//      chunk partials are summed in order; y and optionally res + y (one
-//      binary16 add) are stored.
+//      all 8 rows of the workgroup, two positions per step: one read of two
+//      table entries feeds 16 row-byte reads (a signed bitfield extract gives
+//      q) and 8 accumulators; then each wave's ordered sums: lane r sums chunk
+//      r's 32 sub-partials, and the chunk partials are summed in order; y and
+//      optionally res + y (one binary16 add) are stored.
 // Limits: R <= 64 row chunks, and the tables (8k + 8 * 1024 * ceil(n / 2048)
 // + 8 * 144 * R bytes) within kOdMaxLds of LDS.
 // ---------------------------------------------------------------------------
