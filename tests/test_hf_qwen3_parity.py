@@ -27,6 +27,10 @@ from oracle import oracle as O
 TOL = 1e-2
 TINY = dict(hidden=256, layers=2, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=1000,
             group_size=128, max_seq=64, rms_eps=1e-6, rope_theta=1_000_000.0)
+# head size 128 (one rotation pair per lane in the attention step, the Qwen3 path), 2 query heads per KV head
+WIDE = dict(hidden=512, layers=2, q_heads=8, kv_heads=4, head_dim=128, intermediate=1024, vocab=2000,
+            group_size=128, max_seq=64, rms_eps=1e-6, rope_theta=1_000_000.0)
+CONFIGS = {"tiny": TINY, "hd128": WIDE}
 
 
 def _hf_model(c, embed, lm_head, final_norm, layers, down_from_transposed=False):
@@ -108,8 +112,9 @@ def _random_oracle_model(c, seed):
     return embed, lm_head, norm(H), layers
 
 
-def test_oracle_decoder_matches_transformers():
-    c = SimpleNamespace(**TINY)
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_oracle_decoder_matches_transformers(name):
+    c = SimpleNamespace(**CONFIGS[name])
     embed, lm_head, final_norm, layers = _random_oracle_model(c, seed=5)
     model = _hf_model(c, embed, lm_head, final_norm, layers)
     ora = OD.OracleDecoder(c, embed, lm_head, final_norm, layers)
@@ -119,17 +124,18 @@ def test_oracle_decoder_matches_transformers():
     for i in range(6):
         ours = ora.logits()
         tok = OD.argmax_first(ours)
-        _compare("oracle", i, ours, _hf_logits(model, seq), tok)
+        _compare(f"oracle {name}", i, ours, _hf_logits(model, seq), tok)
         seq.append(tok)
         ora.step(tok)
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", list(CONFIGS))
 @pytest.mark.parametrize("mode", ["dense", "gated"])
-def test_engine_matches_transformers(cuda, mode):
+def test_engine_matches_transformers(cuda, mode, name):
     from soinfer.runtime import decoder as dec
 
-    cfg = dec.DecoderConfig(**TINY)
+    cfg = dec.DecoderConfig(**CONFIGS[name])
     w = dec.random_decoder(cfg, seed=3, linear_std=0.05, norm_jitter=0.1)
     embed, lm_head, final_norm, layers = OD.from_device(w)
     model = _hf_model(cfg, embed, lm_head, final_norm, layers, down_from_transposed=mode != "dense")
@@ -143,6 +149,6 @@ def test_engine_matches_transformers(cuda, mode):
     for i in range(6):
         eng._head()
         tok = int(eng.token.item())
-        _compare(f"engine {mode}", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
+        _compare(f"engine {mode} {name}", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
         seq.append(tok)
         eng._layers()
