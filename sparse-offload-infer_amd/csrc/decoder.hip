@@ -610,7 +610,9 @@ extern "C" int soi_gemv_f16(const uint16_t* W, const uint16_t* x, uint16_t* y, i
         hipLaunchKernelGGL(gemv_f16_simple_kernel, dim3(static_cast<unsigned>(N)), dim3(64), 0, st, W, x, y, Ki);
         return launch_status(what);
     }
-    constexpr int R = 4;
+    // one row per wave (151936 single-wave workgroups for the LM head): 90.2-91.5 us for the 622.6 MB head against
+    // 92.9-93.5 us with 2 rows and 94.1-95.6 us with 4 (4 passes each, back to back on cold copies, bit-identical)
+    constexpr int R = 1;
     const int64_t chunks = K / 8;
     const int64_t passes = ceil_div64(chunks, kWave);
     const dim3 grid(static_cast<unsigned>(ceil_div64(N, R)));
