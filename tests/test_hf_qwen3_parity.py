@@ -30,7 +30,10 @@ TINY = dict(hidden=256, layers=2, q_heads=4, kv_heads=2, head_dim=64, intermedia
 # head size 128 (one rotation pair per lane in the attention step, the Qwen3 path), 2 query heads per KV head
 WIDE = dict(hidden=512, layers=2, q_heads=8, kv_heads=4, head_dim=128, intermediate=1024, vocab=2000,
             group_size=128, max_seq=64, rms_eps=1e-6, rope_theta=1_000_000.0)
-CONFIGS = {"tiny": TINY, "hd128": WIDE}
+# one KV head shared by 4 query heads, 64-element quantization groups, a hidden size that is not a power of two
+GQA4 = dict(hidden=384, layers=2, q_heads=4, kv_heads=1, head_dim=128, intermediate=768, vocab=1500,
+            group_size=64, max_seq=64, rms_eps=1e-6, rope_theta=1_000_000.0)
+CONFIGS = {"tiny": TINY, "hd128": WIDE, "gqa4_g64": GQA4}
 
 
 def _hf_model(c, embed, lm_head, final_norm, layers, down_from_transposed=False):
