@@ -13,7 +13,8 @@ logits within 1e-2 of max|logit| of transformers' (half the reference's HF bound
 `max rel err < 2e-2`; the difference is the binary16 rounding of every activation here against binary64 there,
 about 1e-3 on this model, while swapping the q and k norm weights moves the oracle's logits by 3-5e-2 and a RoPE
 position off by one by 0.15), and the same greedy token wherever transformers' top-2 margin exceeds twice that
-bound. transformers is in this image; the tests skip where it is not importable.
+bound; the GPU engines also over a 300-token prompt and 4 generated tokens (split attention). transformers is in
+this image; the tests skip where it is not importable.
 """
 from types import SimpleNamespace
 
@@ -153,5 +154,31 @@ def test_engine_matches_transformers(cuda, mode, name):
         eng._head()
         tok = int(eng.token.item())
         _compare(f"engine {mode} {name}", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
+        seq.append(tok)
+        eng._layers()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["dense", "gated"])
+def test_engine_long_context_matches_transformers(cuda, mode):
+    """A 300-token prompt (past one attention workgroup's rows, so the attention step splits the context and
+    combines the splits) and 4 generated tokens on the head-size-128 model, by the same bound."""
+    from soinfer.runtime import decoder as dec
+
+    cfg = dec.DecoderConfig(**dict(WIDE, max_seq=320))
+    w = dec.random_decoder(cfg, seed=13, linear_std=0.05, norm_jitter=0.1)
+    embed, lm_head, final_norm, layers = OD.from_device(w)
+    model = _hf_model(cfg, embed, lm_head, final_norm, layers, down_from_transposed=mode != "dense")
+    if mode == "dense":
+        eng = dec.DecodeEngine(w, "dense", max_new_tokens=4)
+    else:
+        eng = dec.DecodeEngine(w, "dip", dip_k=cfg.intermediate, max_new_tokens=4, dip_schedule="gated")
+    eng.reset()
+    seq = _prompt(300, cfg.vocab, seed=17)
+    eng.prefill(seq, use_graph=False)
+    for i in range(4):
+        eng._head()
+        tok = int(eng.token.item())
+        _compare(f"engine {mode} long context", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
         seq.append(tok)
         eng._layers()
