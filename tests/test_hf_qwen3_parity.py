@@ -13,7 +13,8 @@ logits within 1e-2 of max|logit| of transformers' (half the reference's HF bound
 `max rel err < 2e-2`; the difference is the binary16 rounding of every activation here against binary64 there,
 about 1e-3 on this model, while swapping the q and k norm weights moves the oracle's logits by 3-5e-2 and a RoPE
 position off by one by 0.15), and the same greedy token wherever transformers' top-2 margin exceeds twice that
-bound; the GPU engines also over a 300-token prompt and 4 generated tokens (split attention). transformers is in
+bound; the GPU engines also over a 300-token prompt and 4 generated tokens (split attention), and on two layers
+of the Qwen3-1.7B shape. transformers is in
 this image; the tests skip where it is not importable.
 """
 from types import SimpleNamespace
@@ -180,5 +181,32 @@ def test_engine_long_context_matches_transformers(cuda, mode):
         eng._head()
         tok = int(eng.token.item())
         _compare(f"engine {mode} long context", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
+        seq.append(tok)
+        eng._layers()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["dense", "gated"])
+def test_engine_qwen3_1p7b_width_matches_transformers(cuda, mode):
+    """Two layers of the Qwen3-1.7B shape (hidden 2048, intermediate 6144, 16 query / 8 KV heads of 128, INT4 g128)
+    with a 4096-token vocabulary: 6 prompt + 6 generated tokens, by the same bound."""
+    from soinfer.runtime import decoder as dec
+
+    cfg = dec.DecoderConfig(hidden=2048, layers=2, q_heads=16, kv_heads=8, head_dim=128, intermediate=6144,
+                            vocab=4096, group_size=128, max_seq=64, rms_eps=1e-6, rope_theta=1_000_000.0)
+    w = dec.random_decoder(cfg, seed=19, linear_std=0.03, norm_jitter=0.1)
+    embed, lm_head, final_norm, layers = OD.from_device(w)
+    model = _hf_model(cfg, embed, lm_head, final_norm, layers, down_from_transposed=mode != "dense")
+    if mode == "dense":
+        eng = dec.DecodeEngine(w, "dense", max_new_tokens=6)
+    else:
+        eng = dec.DecodeEngine(w, "dip", dip_k=cfg.intermediate, max_new_tokens=6, dip_schedule="gated")
+    eng.reset()
+    seq = _prompt(6, cfg.vocab, seed=21)
+    eng.prefill(seq, use_graph=False)
+    for i in range(6):
+        eng._head()
+        tok = int(eng.token.item())
+        _compare(f"engine {mode} 1.7B width", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
         seq.append(tok)
         eng._layers()
