@@ -13,8 +13,8 @@ logits within 1e-2 of max|logit| of transformers' (half the reference's HF bound
 `max rel err < 2e-2`; the difference is the binary16 rounding of every activation here against binary64 there,
 about 1e-3 on this model, while swapping the q and k norm weights moves the oracle's logits by 3-5e-2 and a RoPE
 position off by one by 0.15), and the same greedy token wherever transformers' top-2 margin exceeds twice that
-bound; the GPU engines also over a 300-token prompt and 4 generated tokens (split attention), and on two layers
-of the Qwen3-1.7B shape. transformers is in
+bound; the GPU engines also over a 300-token prompt and 4 generated tokens (split attention), on two layers
+of the Qwen3-1.7B shape, and with every weight INT4 g128, the LM head included (int4_head). transformers is in
 this image; the tests skip where it is not importable.
 """
 from types import SimpleNamespace
@@ -208,5 +208,32 @@ def test_engine_qwen3_1p7b_width_matches_transformers(cuda, mode):
         eng._head()
         tok = int(eng.token.item())
         _compare(f"engine {mode} 1.7B width", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
+        seq.append(tok)
+        eng._layers()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["dense", "gated"])
+def test_engine_int4_head_matches_transformers(cuda, mode):
+    """Every weight INT4 g128, the LM head included (int4_head=True): transformers' lm_head is the dequantized
+    INT4 head the engine reads; head-size-128 model, 6 prompt + 6 generated tokens, by the same bound."""
+    from soinfer.runtime import decoder as dec
+
+    cfg = dec.DecoderConfig(**WIDE)
+    w = dec.random_decoder(cfg, seed=23, linear_std=0.05, norm_jitter=0.1)
+    kw = dict(int4_head=True, max_new_tokens=6)
+    eng = (dec.DecodeEngine(w, "dense", **kw) if mode == "dense"
+           else dec.DecodeEngine(w, "dip", dip_k=cfg.intermediate, dip_schedule="gated", **kw))
+    hq, hs = (t.cpu().numpy() for t in dec.quantize_lm_head(w))
+    embed, _, final_norm, layers = OD.from_device(w)
+    head = O.dequant_int4(hq, hs, cfg.hidden, cfg.group_size)
+    model = _hf_model(cfg, embed, head, final_norm, layers, down_from_transposed=mode != "dense")
+    eng.reset()
+    seq = _prompt(6, cfg.vocab, seed=25)
+    eng.prefill(seq, use_graph=False)
+    for i in range(6):
+        eng._head()
+        tok = int(eng.token.item())
+        _compare(f"engine {mode} INT4 head", i, eng.logits.float().cpu().numpy(), _hf_logits(model, seq), tok)
         seq.append(tok)
         eng._layers()
